@@ -1,0 +1,217 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the parity checker and the timed CPU baseline.
+Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
+import this module, and only to check or time against; the product path
+(``kore_amd``) never imports it.
+
+The C functions restate kore.cpp's RoPE / KV-append / attention arithmetic in
+kore's operation order (citations in oracle/kore_oracle.c).  The KV store
+``KV`` mirrors kore's ``Engine::kcache/vcache`` layout ``[layer][pos][kv_dim]``
+(kore.cpp:1260).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_BIN = os.path.join(HERE, "_ref", "kore_ref")
+
+_F = C.POINTER(C.c_float)
+_D = C.POINTER(C.c_double)
+_I = C.POINTER(C.c_int)
+
+
+class _KV(C.Structure):
+    _fields_ = [
+        ("n_layer", C.c_int), ("ctx", C.c_int), ("n_head", C.c_int), ("n_head_kv", C.c_int),
+        ("head_dim", C.c_int), ("window", C.c_int), ("rope_base", C.c_float),
+        ("kcache", _F), ("vcache", _F), ("inv_freq", _F), ("scores", _F),
+    ]
+
+
+def build() -> None:
+    """Compile liboracle.so (gcc) and, when the kore sources are present,
+    oracle/_ref/kore_ref."""
+    subprocess.run(["make", "-s", "-C", HERE, "-B", "all"], check=True)
+    if os.path.exists(os.path.join(os.environ.get("KORE_SRC", "/root/reference"), "kore.cpp")):
+        subprocess.run(["make", "-s", "-C", HERE, "-B", "ref"], check=True)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+        L = C.CDLL(LIB_PATH)
+        L.ko_inv_freq.argtypes = [C.c_int, C.c_float, _F]
+        L.ko_rope_cs.argtypes = [C.c_int, C.c_int, _F, _F, _F]
+        L.ko_inv_sqrt.argtypes = [C.c_int]
+        L.ko_inv_sqrt.restype = C.c_float
+        L.ko_rope_neox.argtypes = [_F, C.c_int, C.c_int, _F, _F]
+        L.ko_attn_decode.argtypes = [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _F, _F]
+        L.ko_hd_dot.argtypes = [_F, _F, C.c_int, C.c_int]
+        L.ko_hd_dot.restype = C.c_float
+        L.ko_hd_fma.argtypes = [_F, _F, C.c_float, C.c_int, C.c_int]
+        L.ko_attn_batch.argtypes = [_F, C.c_int, C.c_int, _F, _F, C.c_int, C.c_int, C.c_int,
+                                    C.c_float, C.c_int, _F, _F]
+        L.ko_kv_init.argtypes = [C.POINTER(_KV), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                 C.c_float, C.c_int]
+        L.ko_kv_free.argtypes = [C.POINTER(_KV)]
+        L.ko_decode.argtypes = [C.POINTER(_KV), C.c_int, C.c_int, _F, _F, _F, _F]
+        L.ko_prefill.argtypes = [C.POINTER(_KV), C.c_int, C.c_int, C.c_int, _F, _F, _F, _F, C.c_int]
+        L.ko_attn_ref64.argtypes = [_F, _F, _F, _I, C.c_int, C.c_int, C.c_int, C.c_int, _D]
+        L.ko_splitmix64.argtypes = [C.c_uint64]
+        L.ko_splitmix64.restype = C.c_uint64
+        L.ko_synth_value.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64]
+        L.ko_synth_value.restype = C.c_float
+        L.ko_synth_is_outlier.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]
+        L.ko_synth_fill.argtypes = [_F, C.c_int, C.c_int, C.c_uint64, C.c_uint64, C.c_uint64,
+                                    C.c_uint64, C.c_uint32, C.c_float]
+        L.ko_cpu_has_fma.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def fptr(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_F)
+
+
+def dptr(a: np.ndarray):
+    assert a.dtype == np.float64 and a.flags.c_contiguous
+    return a.ctypes.data_as(_D)
+
+
+# ---------------------------------------------------------------- functions
+
+def inv_freq(head_dim: int, rope_base: float) -> np.ndarray:
+    out = np.zeros(head_dim // 2, np.float32)
+    lib().ko_inv_freq(head_dim, rope_base, fptr(out))
+    return out
+
+
+def rope_cs(pos: int, head_dim: int, inv_f: np.ndarray):
+    c = np.zeros(head_dim // 2, np.float32)
+    s = np.zeros(head_dim // 2, np.float32)
+    lib().ko_rope_cs(pos, head_dim, fptr(np.ascontiguousarray(inv_f, np.float32)), fptr(c), fptr(s))
+    return c, s
+
+
+def inv_sqrt(head_dim: int) -> float:
+    return float(lib().ko_inv_sqrt(head_dim))
+
+
+def rope_neox(vec: np.ndarray, n_heads: int, head_dim: int, c: np.ndarray, s: np.ndarray) -> np.ndarray:
+    out = np.array(vec, np.float32, copy=True, order="C")
+    lib().ko_rope_neox(fptr(out), n_heads, head_dim, fptr(c), fptr(s))
+    return out
+
+
+def hd_dot(a: np.ndarray, b: np.ndarray, avx2: bool = True) -> float:
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return float(lib().ko_hd_dot(fptr(a), fptr(b), a.size, int(avx2)))
+
+
+def hd_fma(o: np.ndarray, v: np.ndarray, p: float, avx2: bool = True) -> np.ndarray:
+    o = np.array(o, np.float32, copy=True)
+    v = np.ascontiguousarray(v, np.float32)
+    lib().ko_hd_fma(fptr(o), fptr(v), p, o.size, int(avx2))
+    return o
+
+
+def attn_ref64(q_roped: np.ndarray, kc: np.ndarray, vc: np.ndarray, rows, n_head: int,
+               n_head_kv: int, head_dim: int) -> np.ndarray:
+    """Double-precision attention of one query over the given cache rows
+    (kore layout ``[row][kv_dim]``)."""
+    rows = np.ascontiguousarray(np.asarray(rows, np.int32))
+    out = np.zeros(n_head * head_dim, np.float64)
+    lib().ko_attn_ref64(fptr(np.ascontiguousarray(q_roped, np.float32)),
+                        fptr(np.ascontiguousarray(kc, np.float32)),
+                        fptr(np.ascontiguousarray(vc, np.float32)),
+                        rows.ctypes.data_as(_I), rows.size, n_head, n_head_kv, head_dim, dptr(out))
+    return out
+
+
+def splitmix64(x: int) -> int:
+    return int(lib().ko_splitmix64(x & 0xFFFFFFFFFFFFFFFF))
+
+
+def synth(rows: int, dim: int, seed: int, stream: int, row0: int = 0, tensor: int = 0,
+          per_mille: int = 0, outlier_scale: float = 20.0) -> np.ndarray:
+    """Counter-based approximately N(0,1) fp32 inputs, ``[rows][dim]``."""
+    out = np.zeros((rows, dim), np.float32)
+    lib().ko_synth_fill(fptr(out), rows, dim, seed, stream, row0, tensor, per_mille, outlier_scale)
+    return out
+
+
+def cpu_has_fma() -> bool:
+    return bool(lib().ko_cpu_has_fma())
+
+
+class KV:
+    """kore-semantics KV store of the oracle (``[layer][pos][kv_dim]`` fp32,
+    zero-initialised like kore.cpp:1344-1345)."""
+
+    def __init__(self, n_layer: int, ctx: int, n_head: int, n_head_kv: int, head_dim: int,
+                 rope_base: float = 1e6, window: int = 0):
+        self._kv = _KV()
+        rc = lib().ko_kv_init(C.byref(self._kv), n_layer, ctx, n_head, n_head_kv, head_dim,
+                              rope_base, window)
+        if rc != 0:
+            raise ValueError(f"ko_kv_init failed ({rc})")
+        self.n_layer, self.ctx, self.n_head, self.n_head_kv = n_layer, ctx, n_head, n_head_kv
+        self.head_dim, self.window = head_dim, window
+        self.kv_dim = n_head_kv * head_dim
+        self.E = n_head * head_dim
+
+    def close(self):
+        if self._kv.kcache:
+            lib().ko_kv_free(C.byref(self._kv))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def kcache(self) -> np.ndarray:
+        n = self.n_layer * self.ctx * self.kv_dim
+        return np.ctypeslib.as_array(self._kv.kcache, shape=(n,)).reshape(
+            self.n_layer, self.ctx, self.kv_dim)
+
+    def vcache(self) -> np.ndarray:
+        n = self.n_layer * self.ctx * self.kv_dim
+        return np.ctypeslib.as_array(self._kv.vcache, shape=(n,)).reshape(
+            self.n_layer, self.ctx, self.kv_dim)
+
+    def decode(self, layer: int, pos: int, q, k, v) -> np.ndarray:
+        q = np.ascontiguousarray(q, np.float32).reshape(-1)
+        k = np.ascontiguousarray(k, np.float32).reshape(-1)
+        v = np.ascontiguousarray(v, np.float32).reshape(-1)
+        out = np.zeros(self.E, np.float32)
+        rc = lib().ko_decode(C.byref(self._kv), layer, pos, fptr(q), fptr(k), fptr(v), fptr(out))
+        if rc != 0:
+            raise ValueError(f"ko_decode rejected layer={layer} pos={pos} ({rc})")
+        return out
+
+    def prefill(self, layer: int, pos0: int, q, k, v, avx2: bool = True) -> np.ndarray:
+        q = np.ascontiguousarray(q, np.float32).reshape(-1, self.E)
+        k = np.ascontiguousarray(k, np.float32).reshape(-1, self.kv_dim)
+        v = np.ascontiguousarray(v, np.float32).reshape(-1, self.kv_dim)
+        n = q.shape[0]
+        out = np.zeros((n, self.E), np.float32)
+        rc = lib().ko_prefill(C.byref(self._kv), layer, pos0, n, fptr(q), fptr(k), fptr(v),
+                              fptr(out), int(avx2))
+        if rc != 0:
+            raise ValueError(f"ko_prefill rejected layer={layer} pos0={pos0} n={n} ({rc})")
+        return out
