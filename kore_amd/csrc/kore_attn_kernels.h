@@ -1,0 +1,90 @@
+// kore_attn_kernels.h - launch interface of the gfx950 kernels behind the
+// kore_attn C ABI.  Internal to libkore_attn.so.
+//
+// KV-cache layout in HBM (one allocation each for K and V):
+//     [layer][kv_head][slot][head_dim]  fp32
+// i.e. every kv-head of a layer is one contiguous run of `slots` rows of
+// head_dim floats.  kore keeps [layer][pos][kv_head][head_dim]
+// (kore.cpp:1260); the values are identical, only the order of rows
+// differs, so kore_attn_read_kv() gives kore's layout back.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace kore_attn_gpu {
+
+// Single-token decode: RoPE of q and of the new k row, append of the new k/v
+// row, split-K attention over slots [0, n_attend) and the split combine, in
+// one launch.
+struct DecodeArgs {
+    const float *q;       // [n_head][hd]        post-bias, pre-RoPE
+    const float *k;       // [n_head_kv][hd]     post-bias, pre-RoPE
+    const float *v;       // [n_head_kv][hd]
+    const float2 *cs;     // [hd/2] (cos, sin) of this position
+    float *kc, *vc;       // layer base, [n_head_kv][slots][hd]
+    float *out;           // [n_head][hd]
+    float *part_o;        // [n_head][n_split][hd]   split partial outputs
+    float *part_ml;       // [n_head][n_split][2]    split max / sum
+    unsigned *counters;   // [n_groups] zero between launches
+    int slots;            // rows per kv-head in the cache (ctx)
+    int n_attend;         // attended slots [0, n_attend)
+    int new_slot;         // slot receiving the new row
+    int rows_per_split;   // rows of one workgroup
+    int n_split;
+    int n_head_kv;
+    int n_rep;            // q heads per kv head
+    float scale;          // 1/sqrt(hd) as kore computes it (kore.cpp:1411)
+};
+
+// Batched RoPE + append of n_tok rows starting at position pos0
+// (kore.cpp:1535-1538).
+struct AppendArgs {
+    const float *k;       // [n_tok][n_head_kv][hd]
+    const float *v;
+    const float2 *cs;     // table base, row p = position p
+    float *kc, *vc;       // layer base
+    int slots;
+    int pos0;
+    int n_tok;
+    int n_head_kv;
+};
+
+// Batched causal attention of n_tok query rows at positions pos0.. against
+// cache rows [0, pos0 + n_tok) (kore.cpp:1542-1563).  q is pre-RoPE.
+struct PrefillArgs {
+    const float *q;       // [n_tok][n_head][hd]
+    const float2 *cs;     // table base
+    const float *kc, *vc; // layer base
+    float *out;           // [n_tok][n_head][hd]
+    int slots;
+    int pos0;
+    int n_tok;
+    int n_head_kv;
+    int n_rep;
+    int n_strips;         // ceil(n_tok / 32)
+    float scale_log2;     // kore's 1/sqrt(hd) times log2(e)
+};
+
+// Counter-based synthetic inputs (identical bits to the CPU oracle's
+// generator): dst[r*dim + c] for r < rows.
+struct SynthArgs {
+    float *dst;
+    int rows, dim;
+    uint64_t seed, stream, row0, tensor;
+    uint32_t per_mille;
+    float outlier_scale;
+};
+
+// Number of splits / rows per split the decode launch uses for a given
+// attended length (the host sizes the partial buffers from the maximum).
+int decode_rows_per_split(int head_dim, int n_attend, int n_head_kv, int num_cu);
+bool decode_supported(int head_dim, int n_rep);
+bool prefill_supported(int head_dim, int n_rep);
+
+hipError_t launch_decode(const DecodeArgs &a, int head_dim, hipStream_t s);
+hipError_t launch_append(const AppendArgs &a, int head_dim, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
+hipError_t launch_synth(const SynthArgs &a, hipStream_t s);
+
+}  // namespace kore_attn_gpu

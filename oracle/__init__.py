@@ -57,6 +57,7 @@ def lib() -> C.CDLL:
         L.ko_inv_sqrt.argtypes = [C.c_int]
         L.ko_inv_sqrt.restype = C.c_float
         L.ko_rope_neox.argtypes = [_F, C.c_int, C.c_int, _F, _F]
+        L.ko_rope_rows.argtypes = [_F, C.c_int, C.c_int, C.c_int, _I, _F]
         L.ko_attn_decode.argtypes = [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _F, _F]
         L.ko_hd_dot.argtypes = [_F, _F, C.c_int, C.c_int]
         L.ko_hd_dot.restype = C.c_float
@@ -113,6 +114,42 @@ def inv_sqrt(head_dim: int) -> float:
 def rope_neox(vec: np.ndarray, n_heads: int, head_dim: int, c: np.ndarray, s: np.ndarray) -> np.ndarray:
     out = np.array(vec, np.float32, copy=True, order="C")
     lib().ko_rope_neox(fptr(out), n_heads, head_dim, fptr(c), fptr(s))
+    return out
+
+
+def rope_rows(x: np.ndarray, positions, n_heads: int, head_dim: int, inv_f: np.ndarray) -> np.ndarray:
+    """Rows ``x[r]`` rotated at ``positions[r]`` (kore's per-row RoPE)."""
+    out = np.array(x, np.float32, copy=True, order="C").reshape(len(positions), n_heads * head_dim)
+    pos = np.ascontiguousarray(np.asarray(positions, np.int32))
+    lib().ko_rope_rows(fptr(out), out.shape[0], n_heads, head_dim, pos.ctypes.data_as(_I),
+                       fptr(np.ascontiguousarray(inv_f, np.float32)))
+    return out
+
+
+def attn_decode(q_roped: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos: int, n_head: int,
+                n_head_kv: int, head_dim: int) -> np.ndarray:
+    """kore's decode attention block (kore.cpp:1432-1455) over cache rows
+    0..pos in kore layout ``[row][kv_dim]``."""
+    out = np.zeros(n_head * head_dim, np.float32)
+    sc = np.zeros(pos + 1, np.float32)
+    kc = np.ascontiguousarray(kc, np.float32)
+    vc = np.ascontiguousarray(vc, np.float32)
+    lib().ko_attn_decode(fptr(np.ascontiguousarray(q_roped, np.float32)), fptr(kc), fptr(vc), pos,
+                         n_head, n_head_kv, head_dim, inv_sqrt(head_dim), fptr(sc), fptr(out))
+    return out
+
+
+def attn_batch(bq_roped: np.ndarray, pos0: int, kc: np.ndarray, vc: np.ndarray, n_head: int,
+               n_head_kv: int, head_dim: int, avx2: bool = True) -> np.ndarray:
+    """kore's batched causal attention block (kore.cpp:1542-1563)."""
+    bq = np.ascontiguousarray(bq_roped, np.float32).reshape(-1, n_head * head_dim)
+    nb = bq.shape[0]
+    out = np.zeros_like(bq)
+    sc = np.zeros(pos0 + nb, np.float32)
+    kc = np.ascontiguousarray(kc, np.float32)
+    vc = np.ascontiguousarray(vc, np.float32)
+    lib().ko_attn_batch(fptr(bq), nb, pos0, fptr(kc), fptr(vc), n_head, n_head_kv, head_dim,
+                        inv_sqrt(head_dim), int(avx2), fptr(sc), fptr(out))
     return out
 
 

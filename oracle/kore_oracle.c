@@ -54,6 +54,18 @@ void ko_rope_neox(float *vec, int n_heads, int head_dim, const float *c, const f
     }
 }
 
+void ko_rope_rows(float *x, int n_rows, int n_heads, int head_dim, const int *pos,
+                  const float *inv_freq) {
+    const int half = head_dim / 2;
+    float *c = (float *)malloc(sizeof(float) * (size_t)half * 2);
+    if (!c) return;
+    for (int r = 0; r < n_rows; r++) {
+        ko_rope_cs(pos[r], head_dim, inv_freq, c, c + half);
+        ko_rope_neox(x + (size_t)r * n_heads * head_dim, n_heads, head_dim, c, c + half);
+    }
+    free(c);
+}
+
 /* ------------------------------------------------------- decode attention */
 
 /* kore.cpp:1432-1455 generalised to a run of positions t0..t1 stored at

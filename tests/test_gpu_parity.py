@@ -1,0 +1,373 @@
+"""GPU parity: the HIP path through the C ABI against the oracle and kore's
+own golden outputs.
+
+Bar: K/V cache rows bit-identical to kore's (memcmp, as kore_kernels.cpp:760
+checks its threads), attention outputs within max|d| <= 1e-4 * max|ref|
+(kore_kernels.cpp:742).  Every test names its case before it touches the GPU.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.golden import cases as C
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _close(out, ref, what=""):
+    ref = np.asarray(ref, np.float64)
+    err = float(np.max(np.abs(np.asarray(out, np.float64) - ref)))
+    scale = float(np.max(np.abs(ref)))
+    assert err <= TOL * scale, f"{what}: max|d| = {err:.3e} > 1e-4 * {scale:.3e}"
+
+
+def _attn(*a, **kw):
+    from kore_amd import KoreAttn
+    return KoreAttn(*a, **kw)
+
+
+def _rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+# ---------------------------------------------------------------- golden
+
+GPU_CASES = [c["name"] for c in C.CASES if c["head_dim"] in (64, 128)]
+
+
+@pytest.mark.parametrize("name", GPU_CASES)
+def test_golden_replay(name):
+    """Replay a golden case through kore_attn_decode / kore_attn_prefill: the
+    K/V caches must hash to kore's, the sampled outputs must match kore's to
+    1e-4, and every step's output must match the oracle's to 1e-4."""
+    man, data = C.load(name)
+    case = C.case_by_name(name)
+    nl, nh, nkv, hd, ctx = (case[k] for k in ("n_layer", "n_head", "n_head_kv", "head_dim", "ctx"))
+    _say(f"golden {name} geometry {nh}/{nkv}/{hd} ctx {ctx} layers {nl}")
+    kv = oracle.KV(nl, ctx, nh, nkv, hd, case["rope_base"])
+    with _attn(nl, ctx, nh, nkv, hd, case["rope_base"]) as attn:
+        for st, (pos, nb) in enumerate(case["steps"]):
+            for layer in range(nl):
+                q, k, v = C.step_inputs(case, st, layer)
+                if case["mode"] == "decode":
+                    out = attn.decode(layer, pos, q, k, v)[None, :]
+                    ref = kv.decode(layer, pos, q, k, v)[None, :]
+                else:
+                    Q, K, V = np.tile(q, (nb, 1)), np.tile(k, (nb, 1)), np.tile(v, (nb, 1))
+                    out = attn.prefill(layer, pos, Q, K, V)
+                    ref = kv.prefill(layer, pos, Q, K, V, avx2=bool(case["avx2"]))
+                _close(out, ref, f"{name} step {st} layer {layer}")
+            if st in case["sample_steps"]:
+                rows = man["sample_rows"][str(st)]
+                _close(out[rows], data[f"att_{st}"], f"{name} step {st} vs kore")
+        filled = man["filled"]
+        kc = np.stack([attn.read_kv(layer, 0, filled)[0] for layer in range(nl)])
+        vc = np.stack([attn.read_kv(layer, 0, filled)[1] for layer in range(nl)])
+    assert filled == ctx
+    assert C.sha(kc) == man["sha256"]["kcache"], "K cache differs from kore's bits"
+    assert C.sha(vc) == man["sha256"]["vcache"], "V cache differs from kore's bits"
+
+
+def test_unsupported_head_dim_is_refused():
+    import kore_amd
+    _say("create with head_dim 40")
+    with pytest.raises(kore_amd.KoreAttnError) as ei:
+        _attn(1, 80, 32, 8, 40)
+    assert ei.value.code == kore_amd.KORE_ATTN_E_UNSUPPORTED
+
+
+# -------------------------------------------------------------- decode
+
+DECODE_GEOMS = [(14, 2, 64), (28, 4, 128), (16, 2, 128), (12, 2, 128), (8, 8, 128), (40, 8, 128),
+                (20, 4, 64), (24, 8, 64)]
+
+
+@pytest.mark.parametrize("nh,nkv,hd", DECODE_GEOMS)
+def test_decode_lengths(nh, nkv, hd):
+    """Attended lengths across split boundaries (1 row up to 4 splits of
+    every tile size), against kore's scalar decode."""
+    lengths = [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 300]
+    ctx = max(lengths) + 1
+    _say(f"decode lengths {nh}/{nkv}/{hd}")
+    kv = oracle.KV(1, ctx, nh, nkv, hd, 1e6)
+    rng = np.random.default_rng(nh * 1000 + hd)
+    with _attn(1, ctx, nh, nkv, hd, 1e6) as attn:
+        for p in range(max(lengths)):
+            q = rng.standard_normal(nh * hd).astype(np.float32) * 2
+            k = rng.standard_normal(nkv * hd).astype(np.float32)
+            v = rng.standard_normal(nkv * hd).astype(np.float32)
+            out = attn.decode(0, p, q, k, v)
+            ref = kv.decode(0, p, q, k, v)
+            if p + 1 in lengths:
+                _close(out, ref, f"L={p + 1}")
+        kg, vg = attn.read_kv(0, 0, max(lengths))
+    np.testing.assert_array_equal(kg, kv.kcache()[0, :max(lengths)])
+    np.testing.assert_array_equal(vg, kv.vcache()[0, :max(lengths)])
+
+
+def test_decode_7b_ctx4096_outliers():
+    """Qwen2.5-7B decode shape at ctx 4096 with 1 % outlier channels x20:
+    cache filled through the prefill append path, then decode steps."""
+    nh, nkv, hd, ctx, n0 = 28, 4, 128, 8192, 4096
+    _say("decode 7b ctx4096 outliers")
+    seed = 7
+    q0 = oracle.synth(n0, nh * hd, seed, 1 << 32, tensor=1, per_mille=10)
+    k0 = oracle.synth(n0, nkv * hd, seed, 2 << 32, tensor=2, per_mille=10)
+    v0 = oracle.synth(n0, nkv * hd, seed, 3 << 32, tensor=3, per_mille=10)
+    inv_f = oracle.inv_freq(hd, 1e6)
+    kexp = oracle.rope_rows(k0, np.arange(n0), nkv, hd, inv_f)
+    with _attn(2, ctx, nh, nkv, hd, 1e6) as attn:
+        attn.prefill(1, 0, q0, k0, v0)
+        kg, vg = attn.read_kv(1, 0, n0)
+        np.testing.assert_array_equal(kg, kexp)
+        np.testing.assert_array_equal(vg, v0)
+        K = np.zeros((ctx, nkv * hd), np.float32)
+        V = np.zeros((ctx, nkv * hd), np.float32)
+        K[:n0], V[:n0] = kexp, v0
+        for step in range(3):
+            pos = n0 + step
+            q = oracle.synth(1, nh * hd, seed, 1 << 32, row0=pos, tensor=1, per_mille=10)[0]
+            k = oracle.synth(1, nkv * hd, seed, 2 << 32, row0=pos, tensor=2, per_mille=10)[0]
+            v = oracle.synth(1, nkv * hd, seed, 3 << 32, row0=pos, tensor=3, per_mille=10)[0]
+            out = attn.decode(1, pos, q, k, v)
+            K[pos] = oracle.rope_rows(k[None], [pos], nkv, hd, inv_f)[0]
+            V[pos] = v
+            qr = oracle.rope_rows(q[None], [pos], nh, hd, inv_f)[0]
+            ref = oracle.attn_decode(qr, K, V, pos, nh, nkv, hd)
+            _close(out, ref, f"7b decode pos {pos}")
+        kg, vg = attn.read_kv(1, n0, 3)
+        np.testing.assert_array_equal(kg, K[n0:n0 + 3])
+        np.testing.assert_array_equal(vg, V[n0:n0 + 3])
+        # layer 0 untouched (zero-initialised like kore.cpp:1344)
+        k_l0, v_l0 = attn.read_kv(0, 0, 16)
+        assert not k_l0.any() and not v_l0.any()
+
+
+def test_decode_3b_long_context():
+    """Qwen2.5-3B shape, single decode at position 32767 over a full cache."""
+    nh, nkv, hd, ctx = 16, 2, 128, 32768
+    n0 = ctx - 1
+    _say("decode 3b pos 32767")
+    seed = 9
+    q0 = oracle.synth(n0, nh * hd, seed, 1 << 32)
+    k0 = oracle.synth(n0, nkv * hd, seed, 2 << 32)
+    v0 = oracle.synth(n0, nkv * hd, seed, 3 << 32)
+    inv_f = oracle.inv_freq(hd, 1e6)
+    with _attn(1, ctx, nh, nkv, hd, 1e6) as attn:
+        for p0 in range(0, n0, 8192):       # chunked prefill fills the cache
+            n = min(8192, n0 - p0)
+            attn.prefill(0, p0, q0[p0:p0 + n], k0[p0:p0 + n], v0[p0:p0 + n])
+        q = oracle.synth(1, nh * hd, seed, 1 << 32, row0=n0)[0]
+        k = oracle.synth(1, nkv * hd, seed, 2 << 32, row0=n0)[0]
+        v = oracle.synth(1, nkv * hd, seed, 3 << 32, row0=n0)[0]
+        out = attn.decode(0, n0, q, k, v)
+        kg, vg = attn.read_kv(0, 0, ctx)
+    K = oracle.rope_rows(np.concatenate([k0, k[None]]), np.arange(ctx), nkv, hd, inv_f)
+    V = np.concatenate([v0, v[None]])
+    np.testing.assert_array_equal(kg, K)
+    np.testing.assert_array_equal(vg, V)
+    qr = oracle.rope_rows(q[None], [n0], nh, hd, inv_f)[0]
+    _close(out, oracle.attn_decode(qr, K, V, n0, nh, nkv, hd), "3b decode pos 32767")
+
+
+def test_decode_deterministic():
+    nh, nkv, hd, ctx = 28, 4, 128, 2048
+    _say("decode determinism")
+    outs = []
+    for _ in range(2):
+        with _attn(1, ctx, nh, nkv, hd, 1e6) as attn:
+            rng = np.random.default_rng(5)
+            attn.prefill(0, 0, rng.standard_normal((1500, nh * hd), np.float32),
+                         rng.standard_normal((1500, nkv * hd), np.float32),
+                         rng.standard_normal((1500, nkv * hd), np.float32))
+            o = attn.decode(0, 1500, rng.standard_normal(nh * hd, np.float32),
+                            rng.standard_normal(nkv * hd, np.float32),
+                            rng.standard_normal(nkv * hd, np.float32))
+            outs.append(o)
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_window_decode():
+    """Sliding-window extension: ring of W slots, decode past W attends the
+    last W positions."""
+    nh, nkv, hd, W = 12, 2, 128, 256
+    _say("window decode")
+    kv = oracle.KV(1, W, nh, nkv, hd, 1e6, window=W)
+    rng = np.random.default_rng(11)
+    with _attn(1, W, nh, nkv, hd, 1e6, window=W) as attn:
+        q = rng.standard_normal((200, nh * hd)).astype(np.float32)
+        k = rng.standard_normal((200, nkv * hd)).astype(np.float32)
+        v = rng.standard_normal((200, nkv * hd)).astype(np.float32)
+        _close(attn.prefill(0, 0, q, k, v), kv.prefill(0, 0, q, k, v), "window prefill")
+        for p in range(200, 700):
+            q = rng.standard_normal(nh * hd).astype(np.float32)
+            k = rng.standard_normal(nkv * hd).astype(np.float32)
+            v = rng.standard_normal(nkv * hd).astype(np.float32)
+            out = attn.decode(0, p, q, k, v)
+            ref = kv.decode(0, p, q, k, v)
+            if p % 50 == 0 or p in (255, 256, 257, 511, 512, 699):
+                _close(out, ref, f"window pos {p}")
+        kg, vg = attn.read_kv(0, 699 - W + 1, W)
+    slots = np.arange(699 - W + 1, 700) % W
+    np.testing.assert_array_equal(kg, kv.kcache()[0, slots])
+    np.testing.assert_array_equal(vg, kv.vcache()[0, slots])
+
+
+# ------------------------------------------------------------- prefill
+
+PREFILL_CASES = [
+    # nh, nkv, hd, [(pos0, n), ...]
+    (28, 4, 128, [(0, 1), (1, 31), (32, 33), (65, 100), (165, 300)]),
+    (14, 2, 64, [(0, 64), (64, 1), (65, 257)]),
+    (12, 2, 128, [(0, 7), (7, 512)]),
+    (16, 2, 128, [(0, 96), (96, 5)]),
+    (8, 8, 128, [(0, 40), (40, 90)]),
+    (40, 8, 128, [(0, 70)]),
+]
+
+
+@pytest.mark.parametrize("nh,nkv,hd,chunks", PREFILL_CASES)
+def test_prefill_chunks(nh, nkv, hd, chunks):
+    """Causal prefill chunks of ragged sizes and offsets against kore's AVX2
+    batched attention; K/V rows bitwise."""
+    ctx = sum(n for _, n in chunks)
+    _say(f"prefill {nh}/{nkv}/{hd} chunks {chunks}")
+    kv = oracle.KV(1, ctx, nh, nkv, hd, 1e6)
+    rng = np.random.default_rng(nh + 7 * hd)
+    with _attn(1, ctx, nh, nkv, hd, 1e6) as attn:
+        for pos0, n in chunks:
+            q = rng.standard_normal((n, nh * hd)).astype(np.float32)
+            k = rng.standard_normal((n, nkv * hd)).astype(np.float32)
+            v = rng.standard_normal((n, nkv * hd)).astype(np.float32)
+            _close(attn.prefill(0, pos0, q, k, v), kv.prefill(0, pos0, q, k, v),
+                   f"chunk {pos0}+{n}")
+        kg, vg = attn.read_kv(0, 0, ctx)
+    np.testing.assert_array_equal(kg, kv.kcache()[0])
+    np.testing.assert_array_equal(vg, kv.vcache()[0])
+
+
+def test_prefill_7b_2048_rows_vs_brute_force():
+    """The 2048-token 7B prefill: sampled rows against the double brute force
+    (the full CPU restatement takes too long for a test)."""
+    nh, nkv, hd, n = 28, 4, 128, 2048
+    _say("prefill 7b 2048")
+    seed = 3
+    q = oracle.synth(n, nh * hd, seed, 1 << 32)
+    k = oracle.synth(n, nkv * hd, seed, 2 << 32)
+    v = oracle.synth(n, nkv * hd, seed, 3 << 32)
+    inv_f = oracle.inv_freq(hd, 1e6)
+    with _attn(1, n, nh, nkv, hd, 1e6) as attn:
+        out = attn.prefill(0, 0, q, k, v)
+        kg, vg = attn.read_kv(0, 0, n)
+    K = oracle.rope_rows(k, np.arange(n), nkv, hd, inv_f)
+    np.testing.assert_array_equal(kg, K)
+    np.testing.assert_array_equal(vg, v)
+    qr = oracle.rope_rows(q, np.arange(n), nh, hd, inv_f)
+    for z in (0, 1, 31, 32, 500, 1023, 1024, 2047):
+        ref = oracle.attn_ref64(qr[z], K, v, np.arange(z + 1), nh, nkv, hd)
+        _close(out[z], ref, f"row {z}")
+
+
+def test_prefill_chunk_then_window_decode_1p5b():
+    """Qwen2.5-1.5B shape: 1024-row chunk at 7168 onto a cache holding 7168
+    positions, then decode steps sliding the window at 8192."""
+    nh, nkv, hd, W = 12, 2, 128, 8192
+    _say("1.5b chunk at 7168 then sliding decode")
+    seed = 5
+    kv = oracle.KV(1, W, nh, nkv, hd, 1e6, window=W)
+    with _attn(1, W, nh, nkv, hd, 1e6, window=W) as attn:
+        q = oracle.synth(8192, nh * hd, seed, 1 << 32)
+        k = oracle.synth(8192, nkv * hd, seed, 2 << 32)
+        v = oracle.synth(8192, nkv * hd, seed, 3 << 32)
+        attn.prefill(0, 0, q[:7168], k[:7168], v[:7168])
+        kv_k, kv_v = kv.kcache(), kv.vcache()
+        inv_f = oracle.inv_freq(hd, 1e6)
+        kv_k[0, :7168] = oracle.rope_rows(k[:7168], np.arange(7168), nkv, hd, inv_f)
+        kv_v[0, :7168] = v[:7168]
+        out = attn.prefill(0, 7168, q[7168:], k[7168:], v[7168:])
+        K = oracle.rope_rows(k, np.arange(8192), nkv, hd, inv_f)
+        kv_k[0] = K
+        kv_v[0] = v
+        qr = oracle.rope_rows(q[7168:], np.arange(7168, 8192), nh, hd, inv_f)
+        for z in (0, 511, 1023):
+            ref = oracle.attn_ref64(qr[z], K, v, np.arange(7168 + z + 1), nh, nkv, hd)
+            _close(out[z], ref, f"chunk row {z}")
+        for p in range(8192, 8192 + 20):
+            qd = oracle.synth(1, nh * hd, seed, 1 << 32, row0=p)[0]
+            kd = oracle.synth(1, nkv * hd, seed, 2 << 32, row0=p)[0]
+            vd = oracle.synth(1, nkv * hd, seed, 3 << 32, row0=p)[0]
+            _close(attn.decode(0, p, qd, kd, vd), kv.decode(0, p, qd, kd, vd), f"decode {p}")
+
+
+# --------------------------------------------------------- errors, misc
+
+def test_error_codes():
+    import kore_amd as ka
+    _say("error codes")
+    z = np.zeros(28 * 128, np.float32)
+    zk = np.zeros(4 * 128, np.float32)
+    with _attn(2, 64, 28, 4, 128) as attn:
+        with pytest.raises(ka.KoreAttnError) as e:
+            attn.decode(0, 64, z, zk, zk)                       # kore.cpp:1400
+        assert e.value.code == ka.KORE_ATTN_E_RANGE
+        with pytest.raises(ka.KoreAttnError) as e:
+            attn.decode(0, -1, z, zk, zk)
+        assert e.value.code == ka.KORE_ATTN_E_RANGE
+        with pytest.raises(ka.KoreAttnError) as e:
+            attn.decode(2, 0, z, zk, zk)
+        assert e.value.code == ka.KORE_ATTN_E_INVALID
+        with pytest.raises(ka.KoreAttnError) as e:
+            attn.prefill(0, 60, np.zeros((5, 28 * 128), np.float32), np.zeros((5, 512), np.float32),
+                         np.zeros((5, 512), np.float32))        # kore.cpp:1490
+        assert e.value.code == ka.KORE_ATTN_E_RANGE
+        rc = ka._lib.lib().kore_attn_decode(attn.handle, 0, 0, 28, 2, 128, z.ctypes.data,
+                                            zk.ctypes.data, zk.ctypes.data, z.ctypes.data)
+        assert rc == ka.KORE_ATTN_E_INVALID                     # geometry mismatch
+        # a failed call leaves the handle usable
+        out = attn.decode(0, 0, np.ones(28 * 128, np.float32), np.ones(512, np.float32),
+                          np.full(512, 2.0, np.float32))
+        np.testing.assert_array_equal(out, np.full(28 * 128, 2.0, np.float32))
+
+
+def test_synth_kernel_matches_cpu_generator():
+    from kore_amd import hip, synth_dev
+    _say("synth kernel")
+    rows, dim = 37, 3584
+    buf = hip.DeviceBuffer(rows * dim)
+    synth_dev(buf.ptr, rows, dim, 1234, (1 << 32) | 3, row0=11, tensor=1, per_mille=10)
+    hip.synchronize()
+    got = buf.download().reshape(rows, dim)
+    np.testing.assert_array_equal(got, oracle.synth(rows, dim, 1234, (1 << 32) | 3, row0=11,
+                                                    tensor=1, per_mille=10))
+
+
+def test_device_api_matches_host_api():
+    from kore_amd import hip
+    nh, nkv, hd, ctx = 28, 4, 128, 512
+    _say("device api")
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((300, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((300, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((300, nkv * hd)).astype(np.float32)
+    with _attn(1, ctx, nh, nkv, hd) as a, _attn(1, ctx, nh, nkv, hd) as b:
+        ref_p = a.prefill(0, 0, q[:299], k[:299], v[:299])
+        ref_d = a.decode(0, 299, q[299], k[299], v[299])
+        dq, dk, dv = (hip.DeviceBuffer.from_array(x) for x in (q, k, v))
+        dout = hip.DeviceBuffer(300 * nh * hd)
+        b.prefill_dev(0, 0, 299, dq.ptr, dk.ptr, dv.ptr, dout.ptr)
+        b.decode_dev(0, 299, dq.at(299 * nh * hd), dk.at(299 * nkv * hd), dv.at(299 * nkv * hd),
+                     dout.at(299 * nh * hd))
+        b.sync()
+        got = dout.download().reshape(300, nh * hd)
+        np.testing.assert_array_equal(got[:299], ref_p)
+        np.testing.assert_array_equal(got[299], ref_d)
+        np.testing.assert_array_equal(a.read_kv(0, 0, 300)[0], b.read_kv(0, 0, 300)[0])
