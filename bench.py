@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path of kore (libkore_attn.so).
+
+Headline workload: Qwen2.5-7B-shape single-token decode attention, batch 1,
+28 layers (28 q-heads / 4 kv-heads, head_dim 128), fp32 KV cache sized for
+ctx 8192 and filled to 4096 positions, one new token per step at positions
+4096, 4097, ...; q/k/v are seeded counter-based N(0,1) values with 1 % of
+channels scaled x20.  One step = one token through all 28 layers, each layer
+one kore_attn_decode_dev call (kore's per-layer attention block,
+kore.cpp:1405-1455), driven from C++ (libkore_attn_bench.so) so no Python
+runs between launches.
+
+Reported next to it: Qwen2.5-7B-shape causal prefill attention of a
+2048-token prompt at position 0 over 28 layers (kore.cpp:1503-1563), and the
+CPU restatement of kore's attention (bit-identical to kore's own code) timed
+on this host on a bounded sample of the same inputs, single-threaded as
+kore's attention is (its loops at kore.cpp:1432 and 1542 sit outside
+parallel_rows).  The CPU leg doubles as a parity check: its outputs for the
+same (layer, position) are compared with the GPU's.
+
+    python bench.py [--steps 128] [--warmup 8] [--prefill-steps 3] [--no-cpu]
+
+Prints one JSON line.  One GPU only: --gpus N with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "7B decode attn µs/layer + HBM GB/s @ctx4096; prefill attn TFLOP/s"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
+
+# Qwen2.5-7B attention geometry
+NL, NH, NKV, HD = 28, 28, 4, 128
+E, KVD = NH * HD, NKV * HD
+ROPE_BASE = 1e6
+DEC_CTX, DEC_POS0 = 8192, 4096
+DEC_SEED, DEC_PER_MILLE, DEC_OUTLIER = 7, 10, 20.0
+PF_N, PF_SEED = 2048, 3
+
+
+def q_stream(layer): return (1 << 32) | layer
+def k_stream(layer): return (2 << 32) | layer
+def v_stream(layer): return (3 << 32) | layer
+
+
+def decode_bytes(L: int) -> int:
+    """Algorithmic HBM bytes of one decode layer attending L positions: K and
+    V rows read once per kv-head, q in and out, the new k/v row in and its
+    append."""
+    return 2 * L * KVD * 4 + 2 * E * 4 + 4 * KVD * 4
+
+
+def prefill_flops(pos0: int, n: int) -> int:
+    """QK^T and PV flops over the causal (unmasked) pairs of one layer."""
+    pairs = n * pos0 + n * (n + 1) // 2
+    return NH * 4 * HD * pairs
+
+
+def _stats(ms):
+    a = np.asarray(ms, np.float64)
+    return dict(mean=float(a.mean()), median=float(np.median(a)), p90=float(np.percentile(a, 90)),
+                min=float(a.min()), max=float(a.max()))
+
+
+def _bench_lib():
+    from kore_amd import _lib
+    _lib.lib()
+    path = os.path.join(ROOT, "kore_amd", "libkore_attn_bench.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run `make -C kore_amd/csrc`")
+    L = C.CDLL(path)
+    vp, i = C.c_void_p, C.c_int
+    L.kab_decode_run.argtypes = [vp, i, i, i, vp, vp, vp, i, vp, i, vp, C.POINTER(C.c_double)]
+    L.kab_prefill_run.argtypes = [vp, i, i, i, i, vp, vp, vp, vp, vp, C.POINTER(C.c_double)]
+    return L
+
+
+def _check(rc, what):
+    if rc != 0:
+        from kore_amd import _lib
+        raise RuntimeError(f"{what} failed ({rc}): {_lib.lib().kore_attn_last_error(None).decode()}")
+
+
+# ------------------------------------------------------------------ GPU legs
+
+def gpu_decode(steps: int, warmup: int):
+    from kore_amd import KoreAttn, hip, synth_dev
+    B = _bench_lib()
+    attn = KoreAttn(NL, DEC_CTX, NH, NKV, HD, ROPE_BASE)
+    st = attn.stream
+    # cache positions 0..4095 of every layer through the append path
+    qb, kb, vb = hip.DeviceBuffer(DEC_POS0 * E), hip.DeviceBuffer(DEC_POS0 * KVD), hip.DeviceBuffer(DEC_POS0 * KVD)
+    ob = hip.DeviceBuffer(DEC_POS0 * E)
+    for l in range(NL):
+        synth_dev(qb.ptr, DEC_POS0, E, DEC_SEED, q_stream(l), 0, 1, DEC_PER_MILLE, DEC_OUTLIER, st)
+        synth_dev(kb.ptr, DEC_POS0, KVD, DEC_SEED, k_stream(l), 0, 2, DEC_PER_MILLE, DEC_OUTLIER, st)
+        synth_dev(vb.ptr, DEC_POS0, KVD, DEC_SEED, v_stream(l), 0, 3, DEC_PER_MILLE, DEC_OUTLIER, st)
+        attn.prefill_dev(l, 0, DEC_POS0, qb.ptr, kb.ptr, vb.ptr, ob.ptr)
+    attn.sync()
+    for b in (qb, kb, vb, ob):
+        b.free()
+    n_in = max(steps, warmup)
+    dq, dk, dv = hip.DeviceBuffer(NL * n_in * E), hip.DeviceBuffer(NL * n_in * KVD), hip.DeviceBuffer(NL * n_in * KVD)
+    for l in range(NL):
+        synth_dev(dq.at(l * n_in * E), n_in, E, DEC_SEED, q_stream(l), DEC_POS0, 1, DEC_PER_MILLE, DEC_OUTLIER, st)
+        synth_dev(dk.at(l * n_in * KVD), n_in, KVD, DEC_SEED, k_stream(l), DEC_POS0, 2, DEC_PER_MILLE, DEC_OUTLIER, st)
+        synth_dev(dv.at(l * n_in * KVD), n_in, KVD, DEC_SEED, v_stream(l), DEC_POS0, 3, DEC_PER_MILLE, DEC_OUTLIER, st)
+    attn.sync()
+    out = hip.DeviceBuffer(steps * NL * E)
+    wall = C.c_double(0)
+    if warmup:
+        _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, warmup, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr,
+                                steps, None, C.byref(wall)), "decode warmup")
+    launch_ms = np.zeros(steps * NL, np.float32)
+    print(f"[bench] decode: {steps} timed steps x {NL} layers at positions {DEC_POS0}..", file=sys.stderr,
+          flush=True)
+    _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
+                            launch_ms.ctypes.data, C.byref(wall)), "decode timed")
+    outs = out.download().reshape(steps, NL, E)
+    info = attn.info()
+    return dict(attn=attn, outs=outs, launch_ms=launch_ms, wall_ms=wall.value, num_cu=info.num_cu,
+                buffers=(dq, dk, dv, out))
+
+
+def gpu_prefill(steps: int, warmup: int):
+    from kore_amd import KoreAttn, hip, synth_dev
+    B = _bench_lib()
+    attn = KoreAttn(NL, PF_N, NH, NKV, HD, ROPE_BASE)
+    st = attn.stream
+    dq, dk, dv = hip.DeviceBuffer(NL * PF_N * E), hip.DeviceBuffer(NL * PF_N * KVD), hip.DeviceBuffer(NL * PF_N * KVD)
+    for l in range(NL):
+        synth_dev(dq.at(l * PF_N * E), PF_N, E, PF_SEED, q_stream(l), 0, 1, 0, 1.0, st)
+        synth_dev(dk.at(l * PF_N * KVD), PF_N, KVD, PF_SEED, k_stream(l), 0, 2, 0, 1.0, st)
+        synth_dev(dv.at(l * PF_N * KVD), PF_N, KVD, PF_SEED, v_stream(l), 0, 3, 0, 1.0, st)
+    attn.sync()
+    out = hip.DeviceBuffer(NL * PF_N * E)
+    wall = C.c_double(0)
+    if warmup:
+        _check(B.kab_prefill_run(attn.handle, NL, 0, PF_N, warmup, dq.ptr, dk.ptr, dv.ptr, out.ptr, None,
+                                 C.byref(wall)), "prefill warmup")
+    launch_ms = np.zeros(steps * NL, np.float32)
+    print(f"[bench] prefill: {steps} timed passes x {NL} layers of {PF_N} rows", file=sys.stderr, flush=True)
+    _check(B.kab_prefill_run(attn.handle, NL, 0, PF_N, steps, dq.ptr, dk.ptr, dv.ptr, out.ptr,
+                             launch_ms.ctypes.data, C.byref(wall)), "prefill timed")
+    outs = out.download(2 * PF_N * E).reshape(2, PF_N, E)   # layers 0 and 1 for the parity check
+    attn.close()
+    for b in (dq, dk, dv, out):
+        b.free()
+    return dict(outs=outs, launch_ms=launch_ms, wall_ms=wall.value)
+
+
+# ------------------------------------------------------------------ CPU legs
+
+def _rel_err(out, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(out, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def cpu_decode(budget_s: float, max_steps: int, gpu_outs=None, gpu_attn=None):
+    """The oracle's decode (kore.cpp:1405-1455, scalar, single thread) on the
+    same inputs: cache positions 0..4095 filled as the GPU's were, then steps
+    at 4096.. over all 28 layers until `budget_s` of decode time is spent."""
+    import oracle
+    kv = oracle.KV(NL, DEC_POS0 + max_steps, NH, NKV, HD, ROPE_BASE)
+    inv_f = oracle.inv_freq(HD, ROPE_BASE)
+    kc, vc = kv.kcache(), kv.vcache()
+    for l in range(NL):
+        k0 = oracle.synth(DEC_POS0, KVD, DEC_SEED, k_stream(l), 0, 2, DEC_PER_MILLE, DEC_OUTLIER)
+        kc[l, :DEC_POS0] = oracle.rope_rows(k0, np.arange(DEC_POS0), NKV, HD, inv_f)
+        vc[l, :DEC_POS0] = oracle.synth(DEC_POS0, KVD, DEC_SEED, v_stream(l), 0, 3, DEC_PER_MILLE, DEC_OUTLIER)
+    spent, nbytes, done, err = 0.0, 0, 0, 0.0
+    while done < max_steps and (done == 0 or spent < budget_s):
+        pos = DEC_POS0 + done
+        for l in range(NL):
+            q = oracle.synth(1, E, DEC_SEED, q_stream(l), pos, 1, DEC_PER_MILLE, DEC_OUTLIER)[0]
+            k = oracle.synth(1, KVD, DEC_SEED, k_stream(l), pos, 2, DEC_PER_MILLE, DEC_OUTLIER)[0]
+            v = oracle.synth(1, KVD, DEC_SEED, v_stream(l), pos, 3, DEC_PER_MILLE, DEC_OUTLIER)[0]
+            t0 = time.perf_counter()
+            ref = kv.decode(l, pos, q, k, v)
+            spent += time.perf_counter() - t0
+            nbytes += decode_bytes(pos + 1)
+            if gpu_outs is not None and done < gpu_outs.shape[0]:
+                err = max(err, _rel_err(gpu_outs[done, l], ref))
+        done += 1
+    kv_equal = None
+    if gpu_attn is not None:
+        n = min(done, gpu_outs.shape[0])
+        kv_equal = True
+        for l in range(NL):
+            rows = (0, DEC_POS0 + n) if l in (0, NL - 1) else (DEC_POS0, DEC_POS0 + n)
+            kg, vg = gpu_attn.read_kv(l, rows[0], rows[1] - rows[0])
+            kv_equal &= bool(np.array_equal(kg, kc[l, rows[0]:rows[1]]) and
+                             np.array_equal(vg, vc[l, rows[0]:rows[1]]))
+    kv.close()
+    return dict(gbs=nbytes / spent / 1e9, seconds=spent, steps=done, us_per_layer=spent / (done * NL) * 1e6,
+                max_rel_err=err, kv_bitwise=kv_equal)
+
+
+def cpu_prefill(n_layers: int, gpu_outs=None):
+    """The oracle's batched causal attention (kore.cpp:1503-1563 with the AVX2
+    hd_dot/hd_fma arithmetic, single thread) for the first `n_layers` layers."""
+    import oracle
+    kv = oracle.KV(n_layers, PF_N, NH, NKV, HD, ROPE_BASE)
+    spent, err = 0.0, 0.0
+    for l in range(n_layers):
+        q = oracle.synth(PF_N, E, PF_SEED, q_stream(l), 0, 1)
+        k = oracle.synth(PF_N, KVD, PF_SEED, k_stream(l), 0, 2)
+        v = oracle.synth(PF_N, KVD, PF_SEED, v_stream(l), 0, 3)
+        t0 = time.perf_counter()
+        ref = kv.prefill(l, 0, q, k, v, avx2=True)
+        spent += time.perf_counter() - t0
+        if gpu_outs is not None and l < gpu_outs.shape[0]:
+            err = max(err, _rel_err(gpu_outs[l], ref))
+    kv.close()
+    return dict(tflops=prefill_flops(0, PF_N) * n_layers / spent / 1e12, seconds=spent, layers=n_layers,
+                max_rel_err=err)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------- main
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128, help="timed decode steps (tokens), 28 layers each")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prefill-steps", type=int, default=3, help="timed 28-layer prefill passes")
+    ap.add_argument("--prefill-warmup", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="decode time budget of the CPU sample")
+    ap.add_argument("--cpu-prefill-layers", type=int, default=2)
+    args = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): the "
+              "attention path runs on a single MI355X and has no multi-GPU leg.", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.steps + DEC_POS0 > DEC_CTX or args.warmup > args.steps:
+        print("--steps must be in 1..4096 and --warmup <= --steps", file=sys.stderr)
+        return 2
+
+    from kore_amd import hip
+    dev_name = hip.device_name(0)
+    clk = C.c_int(0)
+    hip.lib().hipDeviceGetAttribute(C.byref(clk), 5, 0)   # hipDeviceAttributeClockRate (kHz)
+
+    pf = None
+    if not args.no_prefill:
+        pf = gpu_prefill(args.prefill_steps, args.prefill_warmup)
+    dec = gpu_decode(args.steps, args.warmup)
+
+    K, W = args.steps, args.warmup
+    total_bytes = sum(decode_bytes(DEC_POS0 + s + 1) for s in range(K)) * NL
+    wall_s = dec["wall_ms"] / 1e3
+    value = total_bytes / wall_s / 1e9
+    lm = dec["launch_ms"].astype(np.float64)
+    mean_launch_s = float(lm.mean()) / 1e3
+    bytes_per_launch = total_bytes / (K * NL)
+    achieved = bytes_per_launch / mean_launch_s / 1e9
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(dec["wall_ms"] / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2.5-7B-shape decode attention, batch 1, 28 layers, fp32 KV cache ctx 8192 "
+                        f"filled to {DEC_POS0}, {K} steps at positions {DEC_POS0}..{DEC_POS0 + K - 1}, "
+                        "inputs N(0,1) with 1% of channels x20",
+            "n_layer": NL, "n_head": NH, "n_head_kv": NKV, "head_dim": HD, "ctx": DEC_CTX,
+            "pos_first": DEC_POS0, "rope_base": ROPE_BASE,
+        },
+        "decode": {
+            "us_per_layer_kernel": round(float(lm.mean()) * 1e3, 3),
+            "us_per_layer_wall": round(dec["wall_ms"] / (K * NL) * 1e3, 3),
+            "launch_us": {k: round(v * 1e3, 3) for k, v in _stats(lm).items()},
+            "bytes_per_launch_mean": int(bytes_per_launch),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "device": {"name": dev_name, "num_cu": dec["num_cu"], "clock_mhz": clk.value // 1000},
+    }
+    if pf is not None:
+        P = args.prefill_steps
+        plm = pf["launch_ms"].astype(np.float64)
+        F = prefill_flops(0, PF_N)
+        p_ach = F / (float(plm.mean()) / 1e3) / 1e12
+        res["prefill"] = {
+            "workload": f"Qwen2.5-7B-shape causal prefill attention, {PF_N} rows at position 0, 28 layers, "
+                        "inputs N(0,1)",
+            "tflops": round(F * NL * P / (pf["wall_ms"] / 1e3) / 1e12, 3),
+            "us_per_layer_kernel": round(float(plm.mean()) * 1e3, 2),
+            "launch_us": {k: round(v * 1e3, 2) for k, v in _stats(plm).items()},
+            "flop_per_layer": F,
+            "steps": P,
+            "roofline": {"bound": "mfma", "achieved": round(p_ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(p_ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        }
+    if not args.no_cpu:
+        print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
+              flush=True)
+        cd = cpu_decode(args.cpu_seconds, K, dec["outs"], dec["attn"])
+        res["cpu_baseline"] = {
+            "value": round(cd["gbs"], 4),
+            "unit": "GB/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{cd['steps']} decode steps x {NL} layers at positions {DEC_POS0}..{DEC_POS0 + cd['steps'] - 1} "
+                      f"of the same workload, {cd['seconds']:.1f} s, {cd['us_per_layer']:.0f} us/layer; "
+                      f"C restatement of kore.cpp:1405-1455 (bit-identical to kore), gcc -O3, one thread "
+                      f"as kore's attention; host {_cpu_model()}, {os.cpu_count()} cpus",
+        }
+        res["parity"] = {"decode_max_rel_err": cd["max_rel_err"], "decode_kv_bitwise": cd["kv_bitwise"],
+                         "tolerance": 1e-4}
+        if pf is not None:
+            print(f"[bench] cpu baseline: prefill sample ({args.cpu_prefill_layers} layers)", file=sys.stderr,
+                  flush=True)
+            cp = cpu_prefill(args.cpu_prefill_layers, pf["outs"])
+            res["prefill"]["cpu_baseline"] = {
+                "value": round(cp["tflops"], 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                "sample": f"{cp['layers']} layers x {PF_N}-row causal prefill, {cp['seconds']:.1f} s; C restatement "
+                          "of kore.cpp:1503-1563 with kore's AVX2 hd_dot/hd_fma arithmetic, one thread",
+            }
+            res["parity"]["prefill_max_rel_err"] = cp["max_rel_err"]
+    dec["attn"].close()
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,106 @@
+// kore_attn_bench.cpp - benchmark driver of libkore_attn.so (libkore_attn_bench.so).
+//
+// Not part of the kore drop-in boundary.  It plays the part of kore's C++
+// layer loop - forward() calls the attention block once per layer per token
+// (kore.cpp:1413-1455), forward_batch() once per layer per chunk
+// (kore.cpp:1516-1563) - so that a timed region contains no Python between
+// launches.  Every launch goes through the public device-pointer entry points
+// kore_attn_decode_dev / kore_attn_prefill_dev on the handle's own stream.
+//
+// Timing: std::chrono::steady_clock around the whole region (kore times
+// with steady_clock, kore.cpp:1886-1889), bracketed by a stream
+// synchronisation on both sides; when `launch_ms` is given, a pair of HIP
+// events on the same stream brackets each launch and its elapsed time is
+// returned per launch.
+#include "kore_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <vector>
+
+#define KAB_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+struct Events {
+    std::vector<hipEvent_t> ev;
+    explicit Events(size_t n) : ev(n, nullptr) {}
+    ~Events() {
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+    }
+    bool create() {
+        for (hipEvent_t &e : ev)
+            if (hipEventCreate(&e) != hipSuccess) return false;
+        return true;
+    }
+};
+
+// Runs `body(i)` for i < n launches on `stream`, timing the region and (when
+// launch_ms is non-null) each launch.
+template <class Body>
+int timed_region(hipStream_t stream, int n, float *launch_ms, double *wall_ms, Body body) {
+    Events evs(launch_ms ? 2 * (size_t)n : 0);
+    if (launch_ms && !evs.create()) return KORE_ATTN_E_HIP;
+    if (hipStreamSynchronize(stream) != hipSuccess) return KORE_ATTN_E_HIP;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < n; ++i) {
+        if (launch_ms && hipEventRecord(evs.ev[2 * i], stream) != hipSuccess) return KORE_ATTN_E_HIP;
+        if (int rc = body(i)) return rc;
+        if (launch_ms && hipEventRecord(evs.ev[2 * i + 1], stream) != hipSuccess) return KORE_ATTN_E_HIP;
+    }
+    if (hipStreamSynchronize(stream) != hipSuccess) return KORE_ATTN_E_HIP;
+    const auto t1 = std::chrono::steady_clock::now();
+    if (wall_ms) *wall_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (launch_ms)
+        for (int i = 0; i < n; ++i)
+            if (hipEventElapsedTime(&launch_ms[i], evs.ev[2 * i], evs.ev[2 * i + 1]) != hipSuccess)
+                return KORE_ATTN_E_HIP;
+    return KORE_ATTN_OK;
+}
+
+}  // namespace
+
+// n_steps single-token decode steps at positions pos_first.. over layers
+// 0..n_layer-1 (layer inner, like forward()).  Device inputs are laid out
+// [layer][in_steps][dim] (step s of layer l at (l*in_steps + s)*dim);
+// outputs [out_steps][layer][n_head*head_dim] with step s written to row
+// s % out_steps.  launch_ms (optional) receives n_steps*n_layer durations.
+KAB_API int kab_decode_run(kore_attn_t h, int n_layer, int pos_first, int n_steps, const float *q,
+                           const float *k, const float *v, int in_steps, float *out, int out_steps,
+                           float *launch_ms, double *wall_ms) {
+    kore_attn_info inf;
+    if (int rc = kore_attn_get_info(h, &inf)) return rc;
+    if (n_layer <= 0 || n_layer > inf.n_layer || n_steps <= 0 || in_steps < n_steps || out_steps <= 0)
+        return KORE_ATTN_E_INVALID;
+    const size_t E = (size_t)inf.n_head * inf.head_dim, kvd = (size_t)inf.n_head_kv * inf.head_dim;
+    hipStream_t stream = (hipStream_t)inf.stream;
+    return timed_region(stream, n_steps * n_layer, launch_ms, wall_ms, [&](int i) {
+        const int s = i / n_layer, l = i % n_layer;
+        const size_t row = (size_t)l * in_steps + s;
+        return kore_attn_decode_dev(h, l, pos_first + s, inf.n_head, inf.n_head_kv, inf.head_dim,
+                                    q + row * E, k + row * kvd, v + row * kvd,
+                                    out + ((size_t)(s % out_steps) * n_layer + l) * E, nullptr);
+    });
+}
+
+// n_steps passes of a causal prefill of n_tok rows at pos0 over layers
+// 0..n_layer-1 (one forward_batch() chunk per layer).  Inputs [layer][n_tok][dim],
+// outputs [layer][n_tok][n_head*head_dim].
+KAB_API int kab_prefill_run(kore_attn_t h, int n_layer, int pos0, int n_tok, int n_steps,
+                            const float *q, const float *k, const float *v, float *out,
+                            float *launch_ms, double *wall_ms) {
+    kore_attn_info inf;
+    if (int rc = kore_attn_get_info(h, &inf)) return rc;
+    if (n_layer <= 0 || n_layer > inf.n_layer || n_steps <= 0 || n_tok <= 0) return KORE_ATTN_E_INVALID;
+    const size_t E = (size_t)inf.n_head * inf.head_dim, kvd = (size_t)inf.n_head_kv * inf.head_dim;
+    hipStream_t stream = (hipStream_t)inf.stream;
+    return timed_region(stream, n_steps * n_layer, launch_ms, wall_ms, [&](int i) {
+        const int l = i % n_layer;
+        const size_t row = (size_t)l * n_tok;
+        return kore_attn_prefill_dev(h, l, pos0, n_tok, inf.n_head, inf.n_head_kv, inf.head_dim,
+                                     q + row * E, k + row * kvd, v + row * kvd, out + row * E,
+                                     nullptr);
+    });
+}
