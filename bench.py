@@ -252,6 +252,9 @@ def main(argv=None):
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="decode time budget of the CPU sample")
     ap.add_argument("--cpu-prefill-layers", type=int, default=2)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 8 device-to-device copies of 256 MiB (the runtime's copy kernel), "
+                         "the known-size reference for HBM byte counters")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -263,6 +266,14 @@ def main(argv=None):
         return 2
 
     from kore_amd import hip
+    if args.copy_calibration:
+        n = 64 << 20   # floats: 256 MiB
+        src, dst = hip.DeviceBuffer(n), hip.DeviceBuffer(n)
+        for _ in range(8):
+            hip.check(hip.lib().hipMemcpy(dst.ptr, src.ptr, n * 4, hip.D2D), "hipMemcpy D2D")
+        hip.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 8}), flush=True)
+        return 0
     dev_name = hip.device_name(0)
     clk = C.c_int(0)
     hip.lib().hipDeviceGetAttribute(C.byref(clk), 5, 0)   # hipDeviceAttributeClockRate (kHz)

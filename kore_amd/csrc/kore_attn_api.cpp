@@ -28,7 +28,6 @@ struct kore_attn {
     int cs_len = 0;
     std::vector<float> inv_freq;
     float *d_part_o = nullptr, *d_part_ml = nullptr;
-    unsigned *d_counters = nullptr;
     int max_split = 0;
     float *h_stage = nullptr;                // pinned staging of the host entry points
     size_t h_stage_floats = 0;
@@ -122,12 +121,12 @@ int ensure_io(kore_attn *h, size_t floats) {
     return KORE_ATTN_OK;
 }
 
-// Largest number of decode splits any attended length can need.
-int decode_max_split(int head_dim, int ctx, int n_head_kv, int num_cu) {
+// Largest number of decode splits any number of cache rows can need.
+int decode_max_split(int head_dim, int max_rows, int n_head_kv, int num_cu) {
     int m = 1;
-    for (int L = 1; L <= ctx; ++L) {
-        const int t = decode_rows_per_split(head_dim, L, n_head_kv, num_cu);
-        m = std::max(m, (L + t - 1) / t);
+    for (int n = 1; n <= max_rows; ++n) {
+        const int t = decode_rows_per_split(head_dim, n, n_head_kv, num_cu);
+        m = std::max(m, (n + t - 1) / t);
     }
     return m;
 }
@@ -141,7 +140,6 @@ void release(kore_attn *h) {
     if (h->d_cs) (void)hipFree(h->d_cs);
     if (h->d_part_o) (void)hipFree(h->d_part_o);
     if (h->d_part_ml) (void)hipFree(h->d_part_ml);
-    if (h->d_counters) (void)hipFree(h->d_counters);
     if (h->d_io) (void)hipFree(h->d_io);
     if (h->h_stage) (void)hipHostFree(h->h_stage);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -154,7 +152,11 @@ hipStream_t pick_stream(kore_attn *h, void *stream) {
 
 int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float *k, const float *v,
                    float *out, hipStream_t s) {
-    const int L = h->window ? std::min(pos + 1, h->window) : pos + 1;
+    // Cache rows read besides the new one: positions 0..pos-1 (kore.cpp:1437),
+    // or every slot of a ring that has wrapped (the new slot's stale copy is
+    // masked by the kernel).
+    const bool wrapped = h->window && pos >= h->window;
+    const int n_rows = wrapped ? h->window : pos;
     const int slot = h->window ? pos % h->window : pos;
     if (int rc = ensure_rope(h, pos + 1)) return rc;
     DecodeArgs a{};
@@ -167,12 +169,11 @@ int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float
     a.out = out;
     a.part_o = h->d_part_o;
     a.part_ml = h->d_part_ml;
-    a.counters = h->d_counters;
     a.slots = h->ctx;
-    a.n_attend = L;
+    a.n_rows = n_rows;
     a.new_slot = slot;
-    a.rows_per_split = decode_rows_per_split(h->head_dim, L, h->n_head_kv, h->num_cu);
-    a.n_split = (L + a.rows_per_split - 1) / a.rows_per_split;
+    a.rows_per_split = decode_rows_per_split(h->head_dim, n_rows, h->n_head_kv, h->num_cu);
+    a.n_split = std::max(1, (n_rows + a.rows_per_split - 1) / a.rows_per_split);
     a.n_head_kv = h->n_head_kv;
     a.n_rep = h->n_head / h->n_head_kv;
     a.scale = 1.0f / std::sqrt((float)h->head_dim);   // kore.cpp:1411
@@ -305,10 +306,6 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
     const size_t np = (size_t)n_head * h->max_split;
     if ((e = hipMalloc(&h->d_part_o, np * head_dim * sizeof(float))) != hipSuccess) return bail(e, "hipMalloc");
     if ((e = hipMalloc(&h->d_part_ml, np * 2 * sizeof(float))) != hipSuccess) return bail(e, "hipMalloc");
-    if ((e = hipMalloc(&h->d_counters, sizeof(unsigned) * (size_t)n_head_kv)) != hipSuccess)
-        return bail(e, "hipMalloc");
-    if ((e = hipMemsetAsync(h->d_counters, 0, sizeof(unsigned) * (size_t)n_head_kv, h->stream)) != hipSuccess)
-        return bail(e, "hipMemset");
     if ((e = hipStreamSynchronize(h->stream)) != hipSuccess) return bail(e, "hipStreamSynchronize");
     *out = h;
     return KORE_ATTN_OK;

@@ -14,9 +14,14 @@
 
 namespace kore_attn_gpu {
 
-// Single-token decode: RoPE of q and of the new k row, append of the new k/v
-// row, split-K attention over slots [0, n_attend) and the split combine, in
-// one launch.
+// Single-token decode, two launches.  The split kernel does RoPE of q and of
+// the new k row, the append of the new k/v row, and flash-decoding attention
+// of every (kv-head, split) over the cache slots [0, n_rows) in tiles of
+// kDecodeTile rows plus the new row itself; with one split it writes `out`,
+// otherwise unnormalised split partials that the combine kernel merges.
+constexpr int kDecodeTile = 64;
+constexpr int kMaxDecodeSplits = 128;   // splits per kv-head the combine merges in one round
+
 struct DecodeArgs {
     const float *q;       // [n_head][hd]        post-bias, pre-RoPE
     const float *k;       // [n_head_kv][hd]     post-bias, pre-RoPE
@@ -26,11 +31,11 @@ struct DecodeArgs {
     float *out;           // [n_head][hd]
     float *part_o;        // [n_head][n_split][hd]   split partial outputs
     float *part_ml;       // [n_head][n_split][2]    split max / sum
-    unsigned *counters;   // [n_groups] zero between launches
     int slots;            // rows per kv-head in the cache (ctx)
-    int n_attend;         // attended slots [0, n_attend)
+    int n_rows;           // cache slots read: [0, n_rows), the new row excluded
+                          // (a wrapped ring reads all slots and masks new_slot)
     int new_slot;         // slot receiving the new row
-    int rows_per_split;   // rows of one workgroup
+    int rows_per_split;   // multiple of kDecodeTile
     int n_split;
     int n_head_kv;
     int n_rep;            // q heads per kv head
@@ -76,9 +81,9 @@ struct SynthArgs {
     float outlier_scale;
 };
 
-// Number of splits / rows per split the decode launch uses for a given
-// attended length (the host sizes the partial buffers from the maximum).
-int decode_rows_per_split(int head_dim, int n_attend, int n_head_kv, int num_cu);
+// Rows per split the decode uses for n_rows cache rows (the host sizes the
+// partial buffers from the maximum split count over all lengths).
+int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu);
 bool decode_supported(int head_dim, int n_rep);
 bool prefill_supported(int head_dim, int n_rep);
 

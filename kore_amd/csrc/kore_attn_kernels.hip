@@ -1,12 +1,19 @@
 // kore_attn_kernels.hip - gfx950 (CDNA4) kernels of kore's attention path.
 //
-//   decode_kernel   single-token decode of one layer: RoPE of q and k
-//                   (kore.cpp:1424-1425), append of the new k/v row
-//                   (kore.cpp:1427-1430), split-K attention over the cache
-//                   (kore.cpp:1432-1455) and the combine of the splits, all in
-//                   one launch.  HBM-bound: every K/V byte is read once per
-//                   kv-head (not once per q-head as kore's head-outer loop
-//                   does) with 16-byte loads issued before any arithmetic.
+//   decode_split_kernel    single-token decode of one layer: RoPE of q and k
+//                          (kore.cpp:1424-1425), append of the new k/v row
+//                          (kore.cpp:1427-1430) and flash-decoding attention
+//                          (kore.cpp:1432-1455) of each (kv-head, split) of
+//                          the cache.  HBM-bound: every K/V byte is read once
+//                          per kv-head (not once per q-head as kore's
+//                          head-outer loop does) with 16-byte loads issued
+//                          before any arithmetic.
+//   decode_combine_kernel  log-sum-exp merge of the split partials, one
+//                          workgroup per (q-head, 16 dims): a second launch
+//                          instead of a last-workgroup merge, because a
+//                          device-scope fence costs an L2 write-back on every
+//                          workgroup and one workgroup reading every partial
+//                          serialises the merge.
 //   append_kernel   RoPE + append of a prefill chunk (kore.cpp:1535-1538).
 //   prefill_kernel  causal attention of a prefill chunk (kore.cpp:1542-1563)
 //                   on fp32 MFMA (v_mfma_f32_32x32x2_f32) with LDS-staged K and
@@ -22,6 +29,7 @@
 // fmaf() calls or MFMA instructions.
 #include "kore_attn_kernels.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace kore_attn_gpu {
@@ -39,16 +47,70 @@ __device__ __forceinline__ float comp(const float4 &v, int e) {
     return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+
+// Cross-lane moves inside a 16-lane DPP row (no LDS traffic).  CTRL is a
+// DPP control word: 0x121..0x12F rotate the row right by 1..15 lanes,
+// 0x141 mirrors each half-row of 8 lanes, 0x00..0xFF permute within quads.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// Sum over the aligned group of N lanes (N = 4, 8 or 16) that contains this
+// lane; every lane of the group receives it.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(N == 4 || N == 8 || N == 16, "DPP group of 4, 8 or 16 lanes");
+    if constexpr (N == 16) {
+        x += dpp<0x128>(x);   // row_ror:8
+        x += dpp<0x124>(x);   // row_ror:4
+    } else if constexpr (N == 8) {
+        x += dpp<0x141>(x);   // row_half_mirror: lane i + lane 7-i of each half-row
+    }
+    if constexpr (N == 16) {
+        x += dpp<0x122>(x);   // row_ror:2
+        x += dpp<0x121>(x);   // row_ror:1
+    } else {
+        x += dpp<0xB1>(x);    // quad_perm [1,0,3,2]
+        x += dpp<0x4E>(x);    // quad_perm [2,3,0,1]
+    }
     return x;
 }
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-    return x;
+
+// Max / sum over the 64 lanes of a value that is uniform within each aligned
+// group of N lanes (N = 8 or 16); every lane receives the result.  The
+// groups of a 16-lane row are folded with DPP, the four rows with v_readlane
+// (no LDS traffic).
+template <int N>
+__device__ __forceinline__ float wave_max_groups(float x) {
+    static_assert(N == 8 || N == 16, "groups of 8 or 16 lanes");
+    if constexpr (N == 8) x = fmaxf(x, dpp<0x128>(x));   // row_ror:8 pairs the two half-rows
+    const int i = __builtin_bit_cast(int, x);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
+template <int N>
+__device__ __forceinline__ float wave_sum_groups(float x) {
+    static_assert(N == 8 || N == 16, "groups of 8 or 16 lanes");
+    if constexpr (N == 8) x += dpp<0x128>(x);
+    const int i = __builtin_bit_cast(int, x);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+// Max over each 16-lane row; every lane of the row receives it.
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp<0x128>(x));
+    x = fmaxf(x, dpp<0x124>(x));
+    x = fmaxf(x, dpp<0x122>(x));
+    return fmaxf(x, dpp<0x121>(x));
+}
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+constexpr float kLog2e = 1.4426950408889634f;
 
 // NEOX rotation of the pair (x0, x1) = (x[i], x[i + hd/2]) by (c, s)
 // (kore.cpp:1379-1382): products rounded, then difference / sum rounded.
@@ -64,204 +126,271 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float2 cs, float &
 
 template <int HD>
 struct DecodeGeom {
-    static constexpr int LPR = HD / 16;       // lanes sharing one K row in the score pass
-    static constexpr int RPW = 64 / LPR;      // K rows per wave per pass
-    static constexpr int RPP = RPW * kWaves;  // K rows per workgroup per pass
-    static constexpr int VL = HD / 4;         // lanes sharing one V row in the PV pass
-    static constexpr int VRW = 64 / VL;       // V rows per wave per load
-    static constexpr int SMAX = kWaves * HD;  // splits the combine can hold (LDS reuse)
+    static constexpr int RW = kDecodeTile / kWaves;               // rows of a full tile per wave
+    static constexpr int LPR = HD / 8;                            // lanes per K row (8 floats each)
+    static constexpr int RPW = 64 / LPR;                          // K rows per wave per pass
+    static constexpr int KPASS = RW / RPW;                        // K passes of a full tile
+    static constexpr int VL = HD / 4;                             // lanes per V row (one float4 each)
+    static constexpr int VRW = 64 / VL;                           // V rows per wave per load
+    static constexpr int VLD = RW / VRW;                          // V loads per thread of a full tile
+    static_assert(KPASS >= 1 && VLD >= 1 && (LPR == 8 || LPR == 16), "unsupported head_dim");
 };
 
-// Workgroup (split, kv-head g): rows [split*T, split*T + T) of kv-head g for
-// the NR q-heads of g.  Score pass: LPR lanes per K row, each lane holds 16
-// of the row's floats (4 x 16 B loads, dims j*4*LPR + 4c + e) and the same
-// dims of the NR roped queries; partial dots are reduced over the LPR lanes.
-// The split's softmax is exact (two passes over LDS-resident scores, no
-// rescaling); the PV pass puts VL lanes on a V row (one float4 each).  Split
-// partials (o, max, sum) go to HBM; the last workgroup of kv-head g to
-// finish (device-scope counter) merges them.
-template <int HD, int NR, int NPASS>
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
+// Workgroup (split, kv-head g): cache slots [r0, r_end) of kv-head g for the
+// NR q-heads of g, so every K/V byte is read once per kv-head (kore's
+// head-outer loop, kore.cpp:1432, reads it once per q-head).  The slots are
+// processed in tiles of kDecodeTile rows, the last of which may carry up to
+// kWaves extra rows (row 64 + w goes to wave w as one more, mostly masked
+// pass); that lets the host give every CU exactly one workgroup when the row
+// count is a little above a multiple of 64 per CU.  Wave w owns rows
+// [16w, 16w + 16) of a tile and keeps its own online softmax (max, sum,
+// output) over them, so the tile loop has no workgroup barrier.  A tile's K
+// and V rows are loaded into registers by unconditional 16-byte loads (rows
+// past the end are clamped to the last row and masked afterwards), issued
+// before any arithmetic and consumed in issue order.
+//   score pass: LPR lanes per K row, each lane 8 of the row's floats (2 x
+//               16 B loads at dims 4c + j*4*LPR) and the same dims of the NR
+//               roped queries, pre-multiplied by 1/sqrt(hd) * log2(e) so the
+//               softmax runs in base 2 on v_exp_f32; the partial dots are
+//               summed over the LPR lanes with DPP, which leaves every lane
+//               of a row group with the scores of its row.
+//   softmax:    the running max of each head is wave-uniform (a max over the
+//               row groups by v_readlane); the running sums stay per row
+//               group until the end.
+//   PV pass:    VL lanes per V row (one float4 each), VRW rows per wave per
+//               load; the weights go through a wave-private LDS slice.
+// The new token's row is not read from the cache: the owner workgroup ropes
+// it, appends it, and adds it as one more softmax state (its own score, sum
+// 1, output v) when the four wave states are merged.  Slots [0, n_rows) never
+// include it except in a wrapped ring, where its stale slot is masked.
+template <int HD, int NR>
+__global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     using G = DecodeGeom<HD>;
-    constexpr int T = G::RPP * NPASS;
+    constexpr int TILE = kDecodeTile;
     constexpr int HALF = HD / 2;
-    constexpr int NV = T / (kWaves * G::VRW);
-    static_assert(T <= kThreads, "one thread per row in the softmax pass");
+    constexpr int NPAIR = (NR * HALF + kThreads - 1) / kThreads;   // q RoPE pairs per thread
+    constexpr int NST = kWaves + 1;                                // softmax states merged at the end
+    constexpr int KP = G::KPASS + 1;                               // passes incl. the extra-row pass
+    constexpr int VP = G::VLD + 1;
     static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
 
-    __shared__ __align__(16) float s_q[NR * HD];
+    __shared__ __align__(16) float s_q[NR * HD];           // roped q * scale * log2(e)
     __shared__ __align__(16) float s_knew[HD];
-    __shared__ __align__(16) float s_vnew[HD];
-    __shared__ __align__(16) float s_p[T * 8];
-    __shared__ __align__(16) float s_red[kWaves * NR * HD > G::SMAX * NR ? kWaves * NR * HD : G::SMAX * NR];
-    __shared__ float s_stat[2 * kWaves * 8];
-    __shared__ float s_m[8], s_l[8];
-    __shared__ unsigned s_ticket;
+    __shared__ __align__(16) float s_p[(TILE + kWaves) * 8];   // [row][head] weights, wave-private rows
+    __shared__ __align__(16) float s_red[NST * NR * HD];   // per state: unnormalised output
+    __shared__ float s_wm[NST * 8], s_wl[NST * 8], s_we[NST * 8], s_hm[8], s_hl[8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int split = blockIdx.x, g = blockIdx.y;
     const int r0 = split * a.rows_per_split;
-    const int nrows = min(T, a.n_attend - r0);
+    const int r_end = min(r0 + a.rows_per_split, a.n_rows);
+    const int n_own = max(r_end - r0, 0);
+    const int n_tiles = n_own == 0 ? 0 : max(1, (n_own - kWaves + TILE - 1) / TILE);
+    const int last_row = max(r_end - 1, 0);
+    const int owner = a.n_rows == 0 ? 0 : min(a.new_slot, a.n_rows - 1) / a.rows_per_split;
+    const bool is_owner = split == owner;
     const size_t head_base = (size_t)g * a.slots * HD;
-    const float *kbase = a.kc + head_base + (size_t)r0 * HD;
-    const float *vbase = a.vc + head_base + (size_t)r0 * HD;
-    const int new_local = a.new_slot - r0;
-    const bool has_new = new_local >= 0 && new_local < nrows;
-
-    // ---- all K and V loads of the split first: the HBM latency overlaps
-    // the RoPE work below.
+    const float *kg = a.kc + head_base;
+    const float *vg = a.vc + head_base;
     const int c = lane % G::LPR, rw = lane / G::LPR;
-    float4 kreg[NPASS][4];
-#pragma unroll
-    for (int ps = 0; ps < NPASS; ++ps) {
-        const int row = ps * G::RPP + wave * G::RPW + rw;
-        const bool ok = row < nrows;
-        const float *kp = kbase + (size_t)(ok ? row : 0) * HD + c * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kreg[ps][j] = ok ? ld4(kp + j * (G::LPR * 4)) : zero4();
-    }
     const int vc4 = lane % G::VL, vr = lane / G::VL;
-    float4 vreg[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int row = wave * (T / kWaves) + i * G::VRW + vr;
-        const bool ok = row < nrows;
-        vreg[i] = ok ? ld4(vbase + (size_t)(ok ? row : 0) * HD + vc4 * 4) : zero4();
-    }
+    const float qscale = a.scale * kLog2e;
 
-    // ---- RoPE of this group's q heads; RoPE + append of the new k/v row.
-    for (int idx = tid; idx < NR * HALF; idx += kThreads) {
+    // ---- loads: q pairs and their cos/sin first (needed first), then the
+    // first tile of K and V (every load in bounds, consumed in issue order).
+    float qx0[NPAIR], qx1[NPAIR];
+    float2 qcs[NPAIR];
+#pragma unroll
+    for (int it = 0; it < NPAIR; ++it) {
+        const int idx = min(tid + it * kThreads, NR * HALF - 1);
         const int h = idx / HALF, i = idx - h * HALF;
         const float *qh = a.q + (size_t)(g * a.n_rep + h) * HD;
-        float y0, y1;
-        rope_pair(qh[i], qh[i + HALF], a.cs[i], y0, y1);
-        s_q[h * HD + i] = y0;
-        s_q[h * HD + i + HALF] = y1;
+        qx0[it] = qh[i];
+        qx1[it] = qh[i + HALF];
+        qcs[it] = a.cs[i];
     }
-    if (has_new) {
-        const float *kh = a.k + (size_t)g * HD;
-        float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
-        for (int i = tid; i < HALF; i += kThreads) {
+    // the new k/v row (used by the owner workgroup only; loaded by all so
+    // that no load is conditional): thread i < HALF takes pair i of k and
+    // elements i, i + HALF of v
+    const int ni = tid % HALF;
+    const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
+    const float2 ncs = a.cs[ni];
+    const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
+    __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the K/V tile
+    float4 kreg[KP][2];
+    float4 vreg[VP];
+    // tile row of K pass ps (the last pass is row TILE + wave) / of V load i
+    auto krow = [&](int ps) { return ps < G::KPASS ? wave * G::RW + ps * G::RPW + rw : TILE + wave; };
+    auto vrow = [&](int i) { return i < G::VLD ? wave * G::RW + i * G::VRW + vr : TILE + wave; };
+    // The extra-row loads are issued even when the tile has no extra rows:
+    // they are then clamped to the tile's last row, which the tile loads
+    // anyway, so they cost cache hits only, and the loads stay unconditional
+    // (exact in-order wait counts).
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int ps = 0; ps < KP; ++ps) {
+            const int r = min(t0 + krow(ps), last_row);
+            const float *p = kg + (size_t)r * HD + c * 4;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) kreg[ps][j] = ld4(p + j * (G::LPR * 4));
+        }
+#pragma unroll
+        for (int i = 0; i < VP; ++i) {
+            const int r = min(t0 + vrow(i), last_row);
+            vreg[i] = ld4(vg + (size_t)r * HD + vc4 * 4);
+        }
+    };
+    load_tile(r0);
+
+    // ---- RoPE of this group's q heads (stored pre-scaled for the scores);
+    // RoPE + append of the new k/v row.
+#pragma unroll
+    for (int it = 0; it < NPAIR; ++it) {
+        const int idx = tid + it * kThreads;
+        if (idx < NR * HALF) {
+            const int h = idx / HALF, i = idx - h * HALF;
             float y0, y1;
-            rope_pair(kh[i], kh[i + HALF], a.cs[i], y0, y1);
-            s_knew[i] = y0;
-            s_knew[i + HALF] = y1;
-            kd[i] = y0;
-            kd[i + HALF] = y1;
+            rope_pair(qx0[it], qx1[it], qcs[it], y0, y1);
+            s_q[h * HD + i] = y0 * qscale;
+            s_q[h * HD + i + HALF] = y1 * qscale;
         }
+    }
+    if (is_owner && tid < HALF) {
+        float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
         float *vd = a.vc + head_base + (size_t)a.new_slot * HD;
-        for (int i = tid; i < HD; i += kThreads) {
-            const float x = a.v[(size_t)g * HD + i];
-            s_vnew[i] = x;
-            vd[i] = x;
-        }
+        float y0, y1;
+        rope_pair(nk0, nk1, ncs, y0, y1);
+        s_knew[ni] = y0;
+        s_knew[ni + HALF] = y1;
+        kd[ni] = y0;
+        kd[ni + HALF] = y1;
+        s_red[(kWaves * NR) * HD + ni] = nv0;          // state kWaves: v of the new row
+        s_red[(kWaves * NR) * HD + ni + HALF] = nv1;
+        vd[ni] = nv0;
+        vd[ni + HALF] = nv1;
     }
     __syncthreads();
 
-    // ---- scores s = (q . k) * scale, as kore (kore.cpp:1438-1440)
-    float qv[NR][16];
+    float qv[NR][8];
 #pragma unroll
     for (int h = 0; h < NR; ++h)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 2; ++j) {
             const float4 t = ld4(&s_q[h * HD + j * (G::LPR * 4) + c * 4]);
             qv[h][4 * j + 0] = t.x;
             qv[h][4 * j + 1] = t.y;
             qv[h][4 * j + 2] = t.z;
             qv[h][4 * j + 3] = t.w;
         }
-#pragma unroll
-    for (int ps = 0; ps < NPASS; ++ps) {
-        const int row = ps * G::RPP + wave * G::RPW + rw;
-        float4 kk[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kk[j] = kreg[ps][j];
-        if (row == new_local) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) kk[j] = ld4(&s_knew[j * (G::LPR * 4) + c * 4]);
-        }
-        float acc[NR];
-#pragma unroll
-        for (int h = 0; h < NR; ++h) {
-            float s = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                s = fmaf(qv[h][4 * j + 0], kk[j].x, s);
-                s = fmaf(qv[h][4 * j + 1], kk[j].y, s);
-                s = fmaf(qv[h][4 * j + 2], kk[j].z, s);
-                s = fmaf(qv[h][4 * j + 3], kk[j].w, s);
-            }
-            acc[h] = s;
-        }
-#pragma unroll
-        for (int off = 1; off < G::LPR; off <<= 1)
-#pragma unroll
-            for (int h = 0; h < NR; ++h) acc[h] += __shfl_xor(acc[h], off);
-        if (row < nrows) {
-#pragma unroll
-            for (int h = 0; h < NR; ++h)
-                if (h % G::LPR == c) s_p[row * 8 + h] = acc[h] * a.scale;
-        }
-    }
-    __syncthreads();
-
-    // ---- split softmax: exact max, then exp and sum (one thread per row)
-    {
-        const bool ok = tid < nrows;
-#pragma unroll
-        for (int h = 0; h < NR; ++h) {
-            const float m = wave_max(ok ? s_p[tid * 8 + h] : -INFINITY);
-            if (lane == 0) s_stat[wave * 8 + h] = m;
-        }
-        __syncthreads();
-        if (tid < NR) {
-            float m = s_stat[tid];
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) m = fmaxf(m, s_stat[w * 8 + tid]);
-            s_m[tid] = m;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < NR; ++h) {
-            float p = 0.f;
-            if (ok) {
-                p = __expf(s_p[tid * 8 + h] - s_m[h]);
-                s_p[tid * 8 + h] = p;
-            }
-            p = wave_sum(p);
-            if (lane == 0) s_stat[kWaves * 8 + wave * 8 + h] = p;
-        }
-        __syncthreads();
-        if (tid < NR) {
-            float l = 0.f;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) l += s_stat[kWaves * 8 + w * 8 + tid];
-            s_l[tid] = l;
-        }
-    }
-
-    // ---- o = sum_t p_t v_t over the split's rows (PV pass)
     float o[NR][4];
+    float m_run[NR], l_run[NR];
 #pragma unroll
-    for (int h = 0; h < NR; ++h) o[h][0] = o[h][1] = o[h][2] = o[h][3] = 0.f;
+    for (int h = 0; h < NR; ++h) {
+        o[h][0] = o[h][1] = o[h][2] = o[h][3] = 0.f;
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.f;
+    }
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const int t0 = r0 + t * TILE;
+        const bool last = t + 1 == n_tiles;
+        const bool extra = last && n_own - t * TILE > TILE;
+        if (t > 0) load_tile(t0);
+        const int nrows = last ? r_end - t0 : TILE;
+        const int skip = a.new_slot - t0;   // a wrapped ring's stale copy of the new slot
+        const int npass = extra ? KP : G::KPASS;
+
+        // ---- scores (log2 domain): s = (q . k) / sqrt(hd) * log2(e)
+        float sc[KP][NR];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int row = wave * (T / kWaves) + i * G::VRW + vr;
-        if (row < nrows) {
-            float4 vv = vreg[i];
-            if (row == new_local) vv = ld4(&s_vnew[vc4 * 4]);
-            const float4 p0 = ld4(&s_p[row * 8]);
-            const float4 p1 = ld4(&s_p[row * 8 + 4]);
-            const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        for (int ps = 0; ps < KP; ++ps) {
+            if (ps >= npass) {
+#pragma unroll
+                for (int h = 0; h < NR; ++h) sc[ps][h] = -INFINITY;
+                continue;
+            }
+            const int row = krow(ps);
+            const bool ok = row < nrows && row != skip && (ps < G::KPASS || rw == 0);
 #pragma unroll
             for (int h = 0; h < NR; ++h) {
-                o[h][0] = fmaf(pp[h], vv.x, o[h][0]);
-                o[h][1] = fmaf(pp[h], vv.y, o[h][1]);
-                o[h][2] = fmaf(pp[h], vv.z, o[h][2]);
-                o[h][3] = fmaf(pp[h], vv.w, o[h][3]);
+                float s = 0.f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    s = fmaf(qv[h][4 * j + 0], kreg[ps][j].x, s);
+                    s = fmaf(qv[h][4 * j + 1], kreg[ps][j].y, s);
+                    s = fmaf(qv[h][4 * j + 2], kreg[ps][j].z, s);
+                    s = fmaf(qv[h][4 * j + 3], kreg[ps][j].w, s);
+                }
+                s = group_sum<G::LPR>(s);
+                sc[ps][h] = ok ? s : -INFINITY;
+            }
+        }
+
+        // ---- online softmax: wave-uniform running max, per-group sums
+        float alpha[NR];
+#pragma unroll
+        for (int h = 0; h < NR; ++h) {
+            float mt = sc[0][h];
+#pragma unroll
+            for (int ps = 1; ps < KP; ++ps) mt = fmaxf(mt, sc[ps][h]);
+            const float m_new = fmaxf(m_run[h], wave_max_groups<G::LPR>(mt));
+            float lt = 0.f;
+#pragma unroll
+            for (int ps = 0; ps < KP; ++ps) {
+                const float p = sc[ps][h] == -INFINITY ? 0.f : fast_exp2(sc[ps][h] - m_new);
+                sc[ps][h] = p;
+                lt += p;
+            }
+            alpha[h] = m_run[h] == -INFINITY ? 0.f : fast_exp2(m_run[h] - m_new);
+            l_run[h] = fmaf(l_run[h], alpha[h], lt);
+            m_run[h] = m_new;
+        }
+        // weights of the wave's rows to its LDS slice: lane c == 0 of each row
+        if (c == 0) {
+#pragma unroll
+            for (int ps = 0; ps < KP; ++ps) {
+                if (ps < npass && (ps < G::KPASS || rw == 0)) {
+                    float pw[8];
+#pragma unroll
+                    for (int h = 0; h < 8; ++h) pw[h] = h < NR ? sc[ps][h] : 0.f;
+                    float *dst = &s_p[krow(ps) * 8];
+                    st4(dst, make_float4(pw[0], pw[1], pw[2], pw[3]));
+                    st4(dst + 4, make_float4(pw[4], pw[5], pw[6], pw[7]));
+                }
+            }
+        }
+
+        // ---- o = alpha * o + sum_t p_t v_t over the wave's rows
+        if (t > 0) {
+#pragma unroll
+            for (int h = 0; h < NR; ++h) {
+                o[h][0] *= alpha[h];
+                o[h][1] *= alpha[h];
+                o[h][2] *= alpha[h];
+                o[h][3] *= alpha[h];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VP; ++i) {
+            if (i < G::VLD || (extra && vr == 0)) {
+                const int row = vrow(i);
+                const float4 vv = vreg[i];
+                const float4 p0 = ld4(&s_p[row * 8]);
+                const float4 p1 = ld4(&s_p[row * 8 + 4]);
+                const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                for (int h = 0; h < NR; ++h) {
+                    o[h][0] = fmaf(pp[h], vv.x, o[h][0]);
+                    o[h][1] = fmaf(pp[h], vv.y, o[h][1]);
+                    o[h][2] = fmaf(pp[h], vv.z, o[h][2]);
+                    o[h][3] = fmaf(pp[h], vv.w, o[h][3]);
+                }
             }
         }
     }
+
+    // ---- the wave's state: o summed over the lanes sharing dims, l over
+    // the row groups; then the four wave states and the new row's are merged
 #pragma unroll
     for (int off = G::VL; off < 64; off <<= 1)
 #pragma unroll
@@ -273,68 +402,129 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
         for (int h = 0; h < NR; ++h)
             st4(&s_red[(wave * NR + h) * HD + vc4 * 4], make_float4(o[h][0], o[h][1], o[h][2], o[h][3]));
     }
-    __syncthreads();
-
-    const bool single = a.n_split == 1;
-    for (int idx = tid; idx < NR * HD; idx += kThreads) {
-        float sum = s_red[idx];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) sum += s_red[w * NR * HD + idx];
-        const int h = idx / HD, d = idx - h * HD;
-        const size_t hg = (size_t)g * a.n_rep + h;
-        if (single) a.out[hg * HD + d] = sum / s_l[h];
-        else a.part_o[(hg * a.n_split + split) * HD + d] = sum;
-    }
-    if (single) return;
-    if (tid < NR) {
-        const size_t hg = (size_t)g * a.n_rep + tid;
-        a.part_ml[(hg * a.n_split + split) * 2 + 0] = s_m[tid];
-        a.part_ml[(hg * a.n_split + split) * 2 + 1] = s_l[tid];
-    }
-
-    // ---- last workgroup of this kv-head merges the splits
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_ticket = atomicAdd(&a.counters[g], 1u);
-    __syncthreads();
-    if (s_ticket != (unsigned)(a.n_split - 1)) return;
-    __threadfence();
-
-    const int S = a.n_split;
-    float *s_w = s_red;  // [NR][SMAX] normalised split weights
-    for (int h = wave; h < NR; h += kWaves) {
-        const float *ml = a.part_ml + ((size_t)g * a.n_rep + h) * S * 2;
-        float m = -INFINITY;
-        for (int s = lane; s < S; s += 64) m = fmaxf(m, ml[2 * s]);
-        m = wave_max(m);
-        float den = 0.f;
-        for (int s = lane; s < S; s += 64) {
-            const float w = __expf(ml[2 * s] - m);
-            s_w[h * G::SMAX + s] = w;
-            den = fmaf(w, ml[2 * s + 1], den);
+    for (int h = 0; h < NR; ++h) {
+        const float lw = wave_sum_groups<G::LPR>(l_run[h]);
+        if (lane == 0) {
+            s_wm[wave * 8 + h] = m_run[h];
+            s_wl[wave * 8 + h] = lw;
         }
-        den = wave_sum(den);
-        const float inv = 1.f / den;
-        for (int s = lane; s < S; s += 64) s_w[h * G::SMAX + s] *= inv;
+    }
+    if (is_owner) {
+        // score of the new row for head h (wave w takes heads w, w + 4):
+        // lane-strided dot over the scaled roped q and the roped k, then a
+        // wave sum
+        for (int h = wave; h < NR; h += kWaves) {
+            float s = 0.f;
+            for (int d = lane; d < HD; d += 64) s = fmaf(s_q[h * HD + d], s_knew[d], s);
+            s = wave_sum_groups<16>(group_sum<16>(s));
+            if (lane == 0) {
+                s_wm[kWaves * 8 + h] = s;
+                s_wl[kWaves * 8 + h] = 1.f;
+            }
+        }
+    }
+    __syncthreads();
+    const bool single = a.n_split == 1;
+    if (tid < NR) {
+        const int h = tid, nst = is_owner ? NST : kWaves;
+        float m = -INFINITY;
+        for (int w = 0; w < nst; ++w) m = fmaxf(m, s_wm[w * 8 + h]);
+        float l = 0.f;
+        for (int w = 0; w < NST; ++w) {
+            const float mw = s_wm[w * 8 + h];
+            const float e = (w >= nst || mw == -INFINITY) ? 0.f : fast_exp2(mw - m);
+            s_we[w * 8 + h] = e;
+            l = fmaf(e, s_wl[w * 8 + h], l);
+        }
+        if (single) {
+            const float inv = 1.f / l;
+            for (int w = 0; w < NST; ++w) s_we[w * 8 + h] *= inv;
+        }
+        s_hm[h] = m;
+        s_hl[h] = l;
     }
     __syncthreads();
     for (int idx = tid; idx < NR * (HD / 4); idx += kThreads) {
         const int h = idx / (HD / 4), d4 = idx - h * (HD / 4);
-        const size_t hg = (size_t)g * a.n_rep + h;
-        const float *po = a.part_o + hg * S * HD + d4 * 4;
         float4 acc = zero4();
-#pragma unroll 8
-        for (int s = 0; s < S; ++s) {
-            const float w = s_w[h * G::SMAX + s];
-            const float4 x = ld4(po + (size_t)s * HD);
-            acc.x = fmaf(w, x.x, acc.x);
-            acc.y = fmaf(w, x.y, acc.y);
-            acc.z = fmaf(w, x.z, acc.z);
-            acc.w = fmaf(w, x.w, acc.w);
+#pragma unroll
+        for (int w = 0; w < NST; ++w) {
+            const float e = s_we[w * 8 + h];
+            const float4 x = ld4(&s_red[(w < kWaves ? (w * NR + h) * HD : (kWaves * NR) * HD) + d4 * 4]);
+            acc.x = fmaf(e, x.x, acc.x);
+            acc.y = fmaf(e, x.y, acc.y);
+            acc.z = fmaf(e, x.z, acc.z);
+            acc.w = fmaf(e, x.w, acc.w);
         }
-        st4(a.out + hg * HD + d4 * 4, acc);
+        const size_t hg = (size_t)g * a.n_rep + h;
+        if (single) {
+            st4(a.out + hg * HD + d4 * 4, acc);
+        } else {
+            st4(a.part_o + (hg * a.n_split + split) * HD + d4 * 4, acc);
+            if (d4 == 0) {
+                a.part_ml[(hg * a.n_split + split) * 2 + 0] = s_hm[h];
+                a.part_ml[(hg * a.n_split + split) * 2 + 1] = s_hl[h];
+            }
+        }
     }
-    if (tid == 0) atomicExch(&a.counters[g], 0u);
+}
+
+// Block (q-head h, 16-dim chunk): out[h][chunk] = sum_s w_s o_s / sum_s w_s l_s
+// with w_s = 2^(m_s - max_s m_s) (split maxima are in the log2 domain), the
+// log-sum-exp merge of the splits.  Lane (sub, c) takes splits sub + 16 i
+// (i < 8, so n_split <= 128) and float4 c of the chunk; every load is issued
+// before the first use.
+template <int HD>
+__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
+    constexpr int PER = kMaxDecodeSplits / 16;
+    const int h = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
+    const int S = a.n_split;
+    const int sub = lane >> 2, c = lane & 3;
+    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + (size_t)h * S;
+    const float *po = a.part_o + (size_t)h * S * HD + chunk * 16 + c * 4;
+    float4 x[PER];
+    float2 st[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int s = min(sub + 16 * i, S - 1);
+        x[i] = ld4(po + (size_t)s * HD);
+        st[i] = ml[s];
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) m = fmaxf(m, st[i].x);
+    m = wave_max_groups<16>(row16_max(m));
+    float4 acc = zero4();
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const float w = (sub + 16 * i < S) ? fast_exp2(st[i].x - m) : 0.f;
+        den = fmaf(w, st[i].y, den);
+        acc.x = fmaf(w, x[i].x, acc.x);
+        acc.y = fmaf(w, x[i].y, acc.y);
+        acc.z = fmaf(w, x[i].z, acc.z);
+        acc.w = fmaf(w, x[i].w, acc.w);
+    }
+    // sum over sub (lane bits 2..5): the four subs of a row by DPP (rotations
+    // by 8 and 4 keep c), the four rows by shuffles
+    acc.x += dpp<0x128>(acc.x); acc.y += dpp<0x128>(acc.y); acc.z += dpp<0x128>(acc.z); acc.w += dpp<0x128>(acc.w);
+    den += dpp<0x128>(den);
+    acc.x += dpp<0x124>(acc.x); acc.y += dpp<0x124>(acc.y); acc.z += dpp<0x124>(acc.z); acc.w += dpp<0x124>(acc.w);
+    den += dpp<0x124>(den);
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+        acc.x += __shfl_xor(acc.x, off);
+        acc.y += __shfl_xor(acc.y, off);
+        acc.z += __shfl_xor(acc.z, off);
+        acc.w += __shfl_xor(acc.w, off);
+        den += __shfl_xor(den, off);
+    }
+    if (sub == 0) {
+        const float inv = 1.f / den;
+        st4(a.out + (size_t)h * HD + chunk * 16 + c * 4,
+            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
+    }
 }
 
 // ------------------------------------------------------------------ append
@@ -555,20 +745,9 @@ __global__ void synth_kernel(SynthArgs a, uint64_t key, uint64_t okey) {
 
 template <int HD, int NR>
 hipError_t launch_decode_nr(const DecodeArgs &a, hipStream_t s) {
-    using G = DecodeGeom<HD>;
-    const dim3 grid(a.n_split, a.n_head_kv);
-    const int npass = a.rows_per_split / G::RPP;
-    switch (npass) {
-        case 1: hipLaunchKernelGGL((decode_kernel<HD, NR, 1>), grid, dim3(kThreads), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((decode_kernel<HD, NR, 2>), grid, dim3(kThreads), 0, s, a); break;
-        case 4:
-            if constexpr (G::RPP * 4 <= kThreads) {
-                hipLaunchKernelGGL((decode_kernel<HD, NR, 4>), grid, dim3(kThreads), 0, s, a);
-                break;
-            }
-            return hipErrorInvalidValue;
-        default: return hipErrorInvalidValue;
-    }
+    hipLaunchKernelGGL((decode_split_kernel<HD, NR>), dim3(a.n_split, a.n_head_kv), dim3(kThreads), 0, s, a);
+    if (a.n_split > 1)
+        hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(a.n_head_kv * a.n_rep, HD / 16), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -597,22 +776,18 @@ bool prefill_supported(int head_dim, int n_rep) {
     return (head_dim == 64 || head_dim == 128) && n_rep >= 1;
 }
 
-int decode_rows_per_split(int head_dim, int n_attend, int n_head_kv, int num_cu) {
-    // Candidates (rows per workgroup) in decreasing order; take the largest
-    // that still gives at least one workgroup per CU, and never more splits
-    // than the merge can hold.
-    const int rpp = head_dim == 128 ? DecodeGeom<128>::RPP : DecodeGeom<64>::RPP;
-    const int smax = head_dim == 128 ? DecodeGeom<128>::SMAX : DecodeGeom<64>::SMAX;
-    const int maxpass = (rpp * 4 <= kThreads) ? 4 : 2;
-    int best = rpp;
-    for (int np = maxpass; np >= 1; np >>= 1) {
-        const int t = rpp * np;
-        const int splits = (n_attend + t - 1) / t;
-        if ((long)splits * n_head_kv >= num_cu) { best = t; break; }
-        best = t;
-    }
-    while ((n_attend + best - 1) / best > smax && best < rpp * maxpass) best *= 2;
-    return best;
+int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu) {
+    // One workgroup per CU where the rows allow it: S splits per kv-head with
+    // S = min(num_cu / n_head_kv, kMaxDecodeSplits).  Up to 64 * S rows use
+    // 64-row splits; a little more gives S splits of 65..68 rows (one tile
+    // plus an extra row per wave); beyond that the split grows to the next
+    // size whose remainder over whole tiles is at most kWaves rows.
+    (void)head_dim;
+    const int S = std::max(1, std::min(num_cu / std::max(n_head_kv, 1), kMaxDecodeSplits));
+    if (n_rows <= kDecodeTile * S) return kDecodeTile;
+    int rps = (n_rows + S - 1) / S;
+    if (rps % kDecodeTile > kWaves) rps = (rps + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
+    return rps;
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, hipStream_t s) {
