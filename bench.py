@@ -49,6 +49,13 @@ DEC_CTX, DEC_POS0 = 8192, 4096
 DEC_SEED, DEC_PER_MILLE, DEC_OUTLIER = 7, 10, 20.0
 PF_N, PF_SEED = 2048, 3
 
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on these
+# kernels and workloads, each counter scaled by what it reads for a 256 MiB device copy
+# (fetch x 2.0, write x 1.0): decode layer = split + combine kernel, prefill layer =
+# append + prefill kernel.  Re-measure when a kernel changes.
+TRAFFIC_DECODE_BYTES = 20_053_000
+TRAFFIC_PREFILL_BYTES = 102_958_000
+
 
 def q_stream(layer): return (1 << 32) | layer
 def k_stream(layer): return (2 << 32) | layer
@@ -323,7 +330,7 @@ def main(argv=None):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_DECODE_BYTES,
         },
         "device": {"name": dev_name, "num_cu": dec["num_cu"], "clock_mhz": clk.value // 1000},
     }
@@ -341,7 +348,8 @@ def main(argv=None):
             "flop_per_layer": F,
             "steps": P,
             "roofline": {"bound": "mfma", "achieved": round(p_ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(p_ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+                         "unit": "TFLOP/s", "frac": round(p_ach / FP32_MFMA_PEAK_TFLOPS, 4),
+                         "traffic": TRAFFIC_PREFILL_BYTES},
         }
     if not args.no_cpu:
         print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
