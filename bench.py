@@ -89,7 +89,7 @@ def _bench_lib():
         raise RuntimeError(f"{path} is not built; run `make -C kore_amd/csrc`")
     L = C.CDLL(path)
     vp, i = C.c_void_p, C.c_int
-    L.kab_decode_run.argtypes = [vp, i, i, i, vp, vp, vp, i, vp, i, vp, C.POINTER(C.c_double)]
+    L.kab_decode_run.argtypes = [vp, i, i, i, i, vp, vp, vp, i, vp, i, vp, C.POINTER(C.c_double)]
     L.kab_prefill_run.argtypes = [vp, i, i, i, i, vp, vp, vp, vp, vp, C.POINTER(C.c_double)]
     return L
 
@@ -128,12 +128,12 @@ def gpu_decode(steps: int, warmup: int):
     out = hip.DeviceBuffer(steps * NL * E)
     wall = C.c_double(0)
     if warmup:
-        _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, warmup, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr,
+        _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, warmup, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr,
                                 steps, None, C.byref(wall)), "decode warmup")
     launch_ms = np.zeros(steps * NL, np.float32)
     print(f"[bench] decode: {steps} timed steps x {NL} layers at positions {DEC_POS0}..", file=sys.stderr,
           flush=True)
-    _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
+    _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
                             launch_ms.ctypes.data, C.byref(wall)), "decode timed")
     outs = out.download().reshape(steps, NL, E)
     info = attn.info()
@@ -166,6 +166,119 @@ def gpu_prefill(steps: int, warmup: int):
     for b in (dq, dk, dv, out):
         b.free()
     return dict(outs=outs, launch_ms=launch_ms, wall_ms=wall.value)
+
+
+def _decode_bytes_geom(L: int, nh: int, nkv: int, hd: int) -> int:
+    return 2 * L * nkv * hd * 4 + 2 * nh * hd * 4 + 4 * nkv * hd * 4
+
+
+def _prefill_flops_geom(pos0: int, n: int, nh: int, hd: int) -> int:
+    return nh * 4 * hd * (n * pos0 + n * (n + 1) // 2)
+
+
+def _fill_cache(attn, n_layer, rows, kvd, seed, stream):
+    """Cache rows 0..rows-1 of every layer through the append path."""
+    from kore_amd import hip, synth_dev
+    kb, vb = hip.DeviceBuffer(rows * kvd), hip.DeviceBuffer(rows * kvd)
+    for l in range(n_layer):
+        synth_dev(kb.ptr, rows, kvd, seed, k_stream(l), 0, 2, 0, 1.0, stream)
+        synth_dev(vb.ptr, rows, kvd, seed, v_stream(l), 0, 3, 0, 1.0, stream)
+        attn.append_dev(l, 0, rows, kb.ptr, vb.ptr)
+    attn.sync()
+    kb.free()
+    vb.free()
+
+
+def _decode_leg(attn, n_layer, pos_first, pos_step, steps, warmup, nh, nkv, hd, seed, attended):
+    """Timed decode steps (one kore_attn_decode_dev per layer and step);
+    `attended(s)` is the number of positions step s attends."""
+    from kore_amd import hip, synth_dev
+    B = _bench_lib()
+    st = attn.stream
+    E_, kvd = nh * hd, nkv * hd
+    n_in = max(steps, warmup) if pos_step else 1
+    dq, dk, dv = hip.DeviceBuffer(n_layer * n_in * E_), hip.DeviceBuffer(n_layer * n_in * kvd), \
+        hip.DeviceBuffer(n_layer * n_in * kvd)
+    for l in range(n_layer):
+        synth_dev(dq.at(l * n_in * E_), n_in, E_, seed, q_stream(l), pos_first, 1, 0, 1.0, st)
+        synth_dev(dk.at(l * n_in * kvd), n_in, kvd, seed, k_stream(l), pos_first, 2, 0, 1.0, st)
+        synth_dev(dv.at(l * n_in * kvd), n_in, kvd, seed, v_stream(l), pos_first, 3, 0, 1.0, st)
+    attn.sync()
+    out = hip.DeviceBuffer(n_layer * E_)
+    wall = C.c_double(0)
+    if warmup:
+        _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, warmup, dq.ptr, dk.ptr, dv.ptr, n_in,
+                                out.ptr, 1, None, C.byref(wall)), "decode warmup")
+    lm = np.zeros(steps * n_layer, np.float32)
+    _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, steps, dq.ptr, dk.ptr, dv.ptr, n_in,
+                            out.ptr, 1, lm.ctypes.data, C.byref(wall)), "decode timed")
+    for b in (dq, dk, dv, out):
+        b.free()
+    nbytes = sum(_decode_bytes_geom(attended(s), nh, nkv, hd) for s in range(steps)) * n_layer
+    mean_s = float(lm.astype(np.float64).mean()) / 1e3
+    ach = nbytes / (steps * n_layer) / mean_s / 1e9
+    return {"us_per_layer_kernel": round(mean_s * 1e6, 3), "launch_us_median": round(float(np.median(lm)) * 1e3, 3),
+            "gbs_wall": round(nbytes / (wall.value / 1e3) / 1e9, 2),
+            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4)}}
+
+
+def gpu_other_workloads(quick: bool):
+    """The other attention workloads of the path, each on its own handle:
+    0.5B single-layer decode at 511, 3B decode at 32767 over 36 layers, 1.5B
+    1024-row chunk at 7168 then sliding-window decode at ctx 8192."""
+    from kore_amd import KoreAttn, hip, synth_dev
+    B = _bench_lib()
+    res = {}
+    reps = 20 if quick else 50
+    # 0.5B: 14/2/64, one layer, cache 0..510, decode at 511
+    with KoreAttn(1, 512, 14, 2, 64, ROPE_BASE) as a:
+        _fill_cache(a, 1, 511, 128, 11, a.stream)
+        r = _decode_leg(a, 1, 511, 0, reps * 10, 10, 14, 2, 64, 11, lambda s: 512)
+        r["workload"] = "Qwen2.5-0.5B-shape decode, 1 layer, 14/2/64, position 511 (cache 0..510)"
+        res["decode_0p5b_pos511"] = r
+    print("[bench] 0.5B decode done", file=sys.stderr, flush=True)
+    # 3B: 16/2/128, 36 layers, ctx 32768, decode at 32767
+    with KoreAttn(36, 32768, 16, 2, 128, ROPE_BASE) as a:
+        _fill_cache(a, 36, 32767, 256, 9, a.stream)
+        r = _decode_leg(a, 36, 32767, 0, reps, 2, 16, 2, 128, 9, lambda s: 32768)
+        r["workload"] = "Qwen2.5-3B-shape decode, 36 layers, 16/2/128, position 32767 (cache 0..32766)"
+        res["decode_3b_pos32767"] = r
+    print("[bench] 3B decode done", file=sys.stderr, flush=True)
+    # 1.5B: 12/2/128, 28 layers, ring of 8192 slots
+    nl, nh, nkv, hd, W, c0, cn = 28, 12, 2, 128, 8192, 7168, 1024
+    with KoreAttn(nl, W, nh, nkv, hd, ROPE_BASE, window=W) as a:
+        st = a.stream
+        _fill_cache(a, nl, c0, nkv * hd, 5, st)
+        E_, kvd = nh * hd, nkv * hd
+        dq, dk, dv = hip.DeviceBuffer(nl * cn * E_), hip.DeviceBuffer(nl * cn * kvd), hip.DeviceBuffer(nl * cn * kvd)
+        for l in range(nl):
+            synth_dev(dq.at(l * cn * E_), cn, E_, 5, q_stream(l), c0, 1, 0, 1.0, st)
+            synth_dev(dk.at(l * cn * kvd), cn, kvd, 5, k_stream(l), c0, 2, 0, 1.0, st)
+            synth_dev(dv.at(l * cn * kvd), cn, kvd, 5, v_stream(l), c0, 3, 0, 1.0, st)
+        a.sync()
+        out = hip.DeviceBuffer(nl * cn * E_)
+        wall = C.c_double(0)
+        _check(B.kab_prefill_run(a.handle, nl, c0, cn, 1, dq.ptr, dk.ptr, dv.ptr, out.ptr, None, C.byref(wall)),
+               "chunk warmup")
+        P = 2
+        lm = np.zeros(P * nl, np.float32)
+        _check(B.kab_prefill_run(a.handle, nl, c0, cn, P, dq.ptr, dk.ptr, dv.ptr, out.ptr, lm.ctypes.data,
+                                 C.byref(wall)), "chunk timed")
+        for b in (dq, dk, dv, out):
+            b.free()
+        F = _prefill_flops_geom(c0, cn, nh, hd)
+        ach = F / (float(lm.astype(np.float64).mean()) / 1e3) / 1e12
+        chunk = {"us_per_layer_kernel": round(float(lm.mean()) * 1e3, 2), "flop_per_layer": F,
+                 "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                              "unit": "TFLOP/s", "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4)}}
+        dec = _decode_leg(a, nl, W, 1, 256, 0, nh, nkv, hd, 5, lambda s: W)
+        res["chunk_1p5b_1024_at_7168"] = dict(chunk, workload="Qwen2.5-1.5B-shape causal prefill chunk, 28 layers, "
+                                                              "12/2/128, 1024 rows at 7168 onto 7168 cached rows")
+        res["decode_1p5b_sliding_8192"] = dict(dec, workload="Qwen2.5-1.5B-shape decode, 28 layers, ring of 8192 "
+                                                             "slots, 256 steps at positions 8192..8447")
+    print("[bench] 1.5B chunk + sliding decode done", file=sys.stderr, flush=True)
+    return res
 
 
 # ------------------------------------------------------------------ CPU legs
@@ -257,6 +370,7 @@ def main(argv=None):
     ap.add_argument("--prefill-warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-other", action="store_true", help="skip the 0.5B / 3B / 1.5B workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="decode time budget of the CPU sample")
     ap.add_argument("--cpu-prefill-layers", type=int, default=2)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -289,6 +403,7 @@ def main(argv=None):
     if not args.no_prefill:
         pf = gpu_prefill(args.prefill_steps, args.prefill_warmup)
     dec = gpu_decode(args.steps, args.warmup)
+    other = None if args.no_other else gpu_other_workloads(quick=args.steps < 64)
 
     K, W = args.steps, args.warmup
     total_bytes = sum(decode_bytes(DEC_POS0 + s + 1) for s in range(K)) * NL
@@ -351,6 +466,8 @@ def main(argv=None):
                          "unit": "TFLOP/s", "frac": round(p_ach / FP32_MFMA_PEAK_TFLOPS, 4),
                          "traffic": TRAFFIC_PREFILL_BYTES},
         }
+    if other is not None:
+        res["other_workloads"] = other
     if not args.no_cpu:
         print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
               flush=True)

@@ -115,6 +115,15 @@ KORE_ATTN_API int kore_attn_prefill_dev(kore_attn_t h, int layer, int pos0, int 
                           int n_head_kv, int head_dim, const float *q, const float *k,
                           const float *v, float *out, void *stream);
 
+/* RoPE + append of n_tok rows at positions pos0.. of one layer, without
+ * attention: the cache-row half of kore_attn_prefill_dev (kore.cpp:1535-1538).
+ * kore has no counterpart (its forward_batch() always attends); it is for
+ * restoring a cache from saved pre-RoPE k/v rows or filling one for a long
+ * context.  k/v: device [n_tok][n_head_kv*head_dim].  Same range rules as
+ * kore_attn_prefill. */
+KORE_ATTN_API int kore_attn_append_dev(kore_attn_t h, int layer, int pos0, int n_tok, const float *k,
+                         const float *v, void *stream);
+
 /* Wait for all work enqueued on the handle's own stream. */
 KORE_ATTN_API int kore_attn_sync(kore_attn_t h);
 

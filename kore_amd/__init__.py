@@ -140,6 +140,10 @@ class KoreAttn:
                                                      self.n_head_kv, self.head_dim, q, k, v, out,
                                                      stream))
 
+    def append_dev(self, layer: int, pos0: int, n_tok: int, k: int, v: int, stream=None) -> None:
+        """RoPE + append of n_tok device rows without attention (cache fill)."""
+        self._check(_lib.lib().kore_attn_append_dev(self._h, layer, pos0, n_tok, k, v, stream))
+
     def sync(self) -> None:
         self._check(_lib.lib().kore_attn_sync(self._h))
 

@@ -32,6 +32,7 @@ SYMBOLS = [
     ("kore_attn_last_error", C.c_char_p, [_vp]),
     ("kore_attn_decode_dev", _i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     ("kore_attn_prefill_dev", _i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    ("kore_attn_append_dev", _i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     ("kore_attn_sync", _i, [_vp]),
     ("kore_attn_get_info", _i, [_vp, C.POINTER(AttnInfo)]),
     ("kore_attn_synth_dev", _i, [_vp, _i, _i, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,

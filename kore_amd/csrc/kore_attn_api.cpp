@@ -351,6 +351,31 @@ int kore_attn_prefill_dev(kore_attn_t h, int layer, int pos0, int n_tok, int n_h
     return prefill_enqueue(h, layer, pos0, n_tok, q, k, v, out, pick_stream(h, stream));
 }
 
+int kore_attn_append_dev(kore_attn_t h, int layer, int pos0, int n_tok, const float *k, const float *v,
+                         void *stream) {
+    if (!h) return fail(nullptr, KORE_ATTN_E_INVALID, "null handle");
+    if (!k || !v) return fail(h, KORE_ATTN_E_INVALID, "null buffer");
+    if (layer < 0 || layer >= h->n_layer)
+        return fail(h, KORE_ATTN_E_INVALID, "layer %d outside [0, %d)", layer, h->n_layer);
+    if (n_tok <= 0 || pos0 < 0 || (long)pos0 + n_tok > (long)h->ctx)
+        return fail(h, KORE_ATTN_E_RANGE, "rows [%d, %d + %d) outside the cache (ctx %d)", pos0, pos0,
+                    n_tok, h->ctx);
+    HIP_TRY(h, hipSetDevice(h->device));
+    if (int rc = ensure_rope(h, pos0 + n_tok)) return rc;
+    AppendArgs ap{};
+    ap.k = k;
+    ap.v = v;
+    ap.cs = h->d_cs;
+    ap.kc = h->d_k + (size_t)layer * h->layer_floats();
+    ap.vc = h->d_v + (size_t)layer * h->layer_floats();
+    ap.slots = h->ctx;
+    ap.pos0 = pos0;
+    ap.n_tok = n_tok;
+    ap.n_head_kv = h->n_head_kv;
+    HIP_TRY(h, launch_append(ap, h->head_dim, pick_stream(h, stream)));
+    return KORE_ATTN_OK;
+}
+
 int kore_attn_prefill(kore_attn_t h, int layer, int pos0, int n_tok, int n_head, int n_head_kv,
                       int head_dim, const float *q, const float *k, const float *v, float *out) {
     if (!h) return fail(nullptr, KORE_ATTN_E_INVALID, "null handle");

@@ -62,24 +62,26 @@ int timed_region(hipStream_t stream, int n, float *launch_ms, double *wall_ms, B
 
 }  // namespace
 
-// n_steps single-token decode steps at positions pos_first.. over layers
-// 0..n_layer-1 (layer inner, like forward()).  Device inputs are laid out
-// [layer][in_steps][dim] (step s of layer l at (l*in_steps + s)*dim);
+// n_steps single-token decode steps at positions pos_first + s * pos_step
+// (pos_step 1: one new token per step; 0: the same position again) over
+// layers 0..n_layer-1 (layer inner, like forward()).  Device inputs are laid
+// out [layer][in_steps][dim] (step s of layer l at (l*in_steps + s)*dim);
 // outputs [out_steps][layer][n_head*head_dim] with step s written to row
 // s % out_steps.  launch_ms (optional) receives n_steps*n_layer durations.
-KAB_API int kab_decode_run(kore_attn_t h, int n_layer, int pos_first, int n_steps, const float *q,
-                           const float *k, const float *v, int in_steps, float *out, int out_steps,
-                           float *launch_ms, double *wall_ms) {
+KAB_API int kab_decode_run(kore_attn_t h, int n_layer, int pos_first, int pos_step, int n_steps,
+                           const float *q, const float *k, const float *v, int in_steps, float *out,
+                           int out_steps, float *launch_ms, double *wall_ms) {
     kore_attn_info inf;
     if (int rc = kore_attn_get_info(h, &inf)) return rc;
-    if (n_layer <= 0 || n_layer > inf.n_layer || n_steps <= 0 || in_steps < n_steps || out_steps <= 0)
+    if (n_layer <= 0 || n_layer > inf.n_layer || n_steps <= 0 || out_steps <= 0 || pos_step < 0 ||
+        in_steps < (pos_step ? n_steps : 1))
         return KORE_ATTN_E_INVALID;
     const size_t E = (size_t)inf.n_head * inf.head_dim, kvd = (size_t)inf.n_head_kv * inf.head_dim;
     hipStream_t stream = (hipStream_t)inf.stream;
     return timed_region(stream, n_steps * n_layer, launch_ms, wall_ms, [&](int i) {
         const int s = i / n_layer, l = i % n_layer;
-        const size_t row = (size_t)l * in_steps + s;
-        return kore_attn_decode_dev(h, l, pos_first + s, inf.n_head, inf.n_head_kv, inf.head_dim,
+        const size_t row = (size_t)l * in_steps + (pos_step ? s : 0);
+        return kore_attn_decode_dev(h, l, pos_first + s * pos_step, inf.n_head, inf.n_head_kv, inf.head_dim,
                                     q + row * E, k + row * kvd, v + row * kvd,
                                     out + ((size_t)(s % out_steps) * n_layer + l) * E, nullptr);
     });

@@ -26,7 +26,7 @@ def test_headers_declare_the_abi():
     names = _declared()
     for fn in ("kore_attn_create", "kore_attn_destroy", "kore_attn_decode", "kore_attn_prefill",
                "kore_attn_read_kv", "kore_attn_last_error", "kore_attn_decode_dev",
-               "kore_attn_prefill_dev", "kore_attn_sync", "kore_attn_get_info",
+               "kore_attn_prefill_dev", "kore_attn_append_dev", "kore_attn_sync", "kore_attn_get_info",
                "kore_attn_synth_dev"):
         assert fn in names
 
@@ -90,6 +90,7 @@ def test_null_handle_calls_fail_cleanly():
     assert L.kore_attn_prefill(None, 0, 0, 1, 4, 2, 64, None, None, None, None) == kore_amd.KORE_ATTN_E_INVALID
     assert L.kore_attn_read_kv(None, 0, 0, 1, None, None) == kore_amd.KORE_ATTN_E_INVALID
     assert L.kore_attn_sync(None) == kore_amd.KORE_ATTN_E_INVALID
+    assert L.kore_attn_append_dev(None, 0, 0, 1, None, None, None) == kore_amd.KORE_ATTN_E_INVALID
     assert L.kore_attn_last_error(None) is not None
     L.kore_attn_destroy(None)
 

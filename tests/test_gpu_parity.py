@@ -371,3 +371,31 @@ def test_device_api_matches_host_api():
         np.testing.assert_array_equal(got[:299], ref_p)
         np.testing.assert_array_equal(got[299], ref_d)
         np.testing.assert_array_equal(a.read_kv(0, 0, 300)[0], b.read_kv(0, 0, 300)[0])
+
+
+def test_append_dev_matches_prefill_cache_rows():
+    """kore_attn_append_dev writes the same cache rows as kore_attn_prefill
+    (kore.cpp:1535-1538), and keeps kore's range rule (kore.cpp:1490)."""
+    import kore_amd as ka
+    from kore_amd import hip
+    nh, nkv, hd, ctx = 12, 2, 128, 300
+    _say("append_dev")
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((ctx, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((ctx, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((ctx, nkv * hd)).astype(np.float32)
+    with _attn(2, ctx, nh, nkv, hd) as a, _attn(2, ctx, nh, nkv, hd) as b:
+        a.prefill(1, 0, q[:170], k[:170], v[:170])
+        a.prefill(1, 170, q[170:], k[170:], v[170:])
+        dk, dv = hip.DeviceBuffer.from_array(k), hip.DeviceBuffer.from_array(v)
+        b.append_dev(1, 0, 170, dk.ptr, dv.ptr)
+        b.append_dev(1, 170, ctx - 170, dk.at(170 * nkv * hd), dv.at(170 * nkv * hd))
+        b.sync()
+        for x, y in zip(a.read_kv(1, 0, ctx), b.read_kv(1, 0, ctx)):
+            np.testing.assert_array_equal(x, y)
+        with pytest.raises(ka.KoreAttnError) as e:
+            b.append_dev(1, ctx - 5, 6, dk.ptr, dv.ptr)
+        assert e.value.code == ka.KORE_ATTN_E_RANGE
+        # a decode over appended rows equals a decode over prefilled rows
+        np.testing.assert_array_equal(a.decode(1, ctx - 1, q[-1], k[-1], v[-1]),
+                                      b.decode(1, ctx - 1, q[-1], k[-1], v[-1]))
