@@ -567,7 +567,7 @@ __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
 // K tile rows are padded to HD+4 floats and V^T rows to 36 floats so the
 // 16-byte LDS reads of 32 different rows fall in different banks.
 template <int HD>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int BK = 32;
     constexpr int KSTR = HD + 4;
     constexpr int VSTR = BK + 4;
