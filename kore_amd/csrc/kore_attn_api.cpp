@@ -29,6 +29,8 @@ struct kore_attn {
     std::vector<float> inv_freq;
     float *d_part_o = nullptr, *d_part_ml = nullptr;
     int max_split = 0;
+    float *d_pf_part = nullptr;              // prefill key-segment partials
+    size_t pf_part_floats = 0;
     float *h_stage = nullptr;                // pinned staging of the host entry points
     size_t h_stage_floats = 0;
     float *d_io = nullptr;                   // device copies of q/k/v/out
@@ -140,6 +142,7 @@ void release(kore_attn *h) {
     if (h->d_cs) (void)hipFree(h->d_cs);
     if (h->d_part_o) (void)hipFree(h->d_part_o);
     if (h->d_part_ml) (void)hipFree(h->d_part_ml);
+    if (h->d_pf_part) (void)hipFree(h->d_pf_part);
     if (h->d_io) (void)hipFree(h->d_io);
     if (h->h_stage) (void)hipHostFree(h->h_stage);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -211,6 +214,23 @@ int prefill_enqueue(kore_attn *h, int layer, int pos0, int n_tok, const float *q
     pa.n_rep = h->n_head / h->n_head_kv;
     pa.n_strips = (n_tok + 31) / 32;
     pa.scale_log2 = (1.0f / std::sqrt((float)h->head_dim)) * 1.4426950408889634f;
+    pa.n_kseg = prefill_key_segments(n_tok, pos0, h->n_head_kv, pa.n_rep, h->num_cu, &pa.seg_tiles);
+    if (pa.n_kseg > 1) {
+        const size_t entries = (size_t)h->n_head_kv * pa.n_rep * pa.n_strips * pa.n_kseg * 32;
+        const size_t need = entries * ((size_t)h->head_dim + 2);
+        if (need > h->pf_part_floats) {
+            if (h->d_pf_part) {
+                HIP_TRY(h, hipDeviceSynchronize());   // earlier launches may still read it
+                (void)hipFree(h->d_pf_part);
+                h->d_pf_part = nullptr;
+                h->pf_part_floats = 0;
+            }
+            HIP_TRY(h, hipMalloc(&h->d_pf_part, need * sizeof(float)));
+            h->pf_part_floats = need;
+        }
+        pa.part_o = h->d_pf_part;
+        pa.part_ml = h->d_pf_part + entries * h->head_dim;
+    }
     HIP_TRY(h, launch_prefill(pa, h->head_dim, s));
     return KORE_ATTN_OK;
 }

@@ -69,6 +69,13 @@ struct PrefillArgs {
     int n_rep;
     int n_strips;         // ceil(n_tok / 32)
     float scale_log2;     // kore's 1/sqrt(hd) times log2(e)
+    // Key segments: with n_kseg > 1 every workgroup item is split into
+    // n_kseg launches over key tiles [seg * seg_tiles, (seg + 1) * seg_tiles)
+    // that write unnormalised partials, merged by the prefill combine kernel.
+    int n_kseg;
+    int seg_tiles;
+    float *part_o;        // [n_head_kv * n_rep * n_strips][n_kseg][32][hd]
+    float *part_ml;       // [n_head_kv * n_rep * n_strips][n_kseg][32][2]
 };
 
 // Counter-based synthetic inputs (identical bits to the CPU oracle's
@@ -90,6 +97,8 @@ bool prefill_supported(int head_dim, int n_rep);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, int head_dim, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
+// Key segments the prefill uses for n_tok rows at pos0 (1 = none).
+int prefill_key_segments(int n_tok, int pos0, int n_head_kv, int n_rep, int num_cu, int *seg_tiles);
 hipError_t launch_synth(const SynthArgs &a, hipStream_t s);
 
 }  // namespace kore_attn_gpu

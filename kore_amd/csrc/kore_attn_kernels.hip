@@ -565,7 +565,10 @@ __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
 // them, and accumulates O^T += V^T P^T (64 MFMAs), whose D layout again gives
 // each lane one query; the softmax statistics need one cross-lane exchange.
 // K tile rows are padded to HD+4 floats and V^T rows to 36 floats so the
-// 16-byte LDS reads of 32 different rows fall in different banks.
+// 16-byte LDS reads of 32 different rows fall in different banks.  With key
+// segments (a short chunk over a long cache has too few workgroups to fill the
+// GPU) a workgroup covers one range of key tiles and writes its rows'
+// unnormalised output with their max and sum instead.
 template <int HD>
 __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int BK = 32;
@@ -579,7 +582,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nkv = a.n_head_kv;
     const int g = blockIdx.x % nkv;
-    const int item = blockIdx.x / nkv;
+    const int seg = (blockIdx.x / nkv) % a.n_kseg;
+    const int item = blockIdx.x / nkv / a.n_kseg;
     const int total = a.n_rep * a.n_strips;
     const int e = item * 4 + wave;
     const bool active = e < total;
@@ -626,7 +630,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    for (int t = 0; t < n_tiles; ++t) {
+    const int t_begin = seg * a.seg_tiles;
+    const int t_end = a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles);
+    for (int t = t_begin; t < t_end; ++t) {
         const int k0 = t * BK;
         __syncthreads();
         for (int idx = tid; idx < BK * HD / 4; idx += kThreads) {
@@ -669,11 +675,13 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         }
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float m_new = fmaxf(m_run, mt);
-        const float alpha = exp2f(m_run - m_new);
+        // a segment may start with a tile that is all masked for a row
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(m_run - m_use);
         float psum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s[r] = exp2f(s[r] - m_new);
+            s[r] = exp2f(s[r] - m_use);
             psum += s[r];
         }
         psum += __shfl_xor(psum, 32);
@@ -694,6 +702,22 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         }
     }
 
+    if (a.n_kseg > 1) {
+        if (!active) return;
+        const size_t pe = ((size_t)g * total + ee) * a.n_kseg + seg;
+        float *po = a.part_o + (pe * 32 + qi) * HD;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+                st4(po + 32 * tt + 8 * rb + 4 * qg,
+                    make_float4(acc[tt][4 * rb + 0], acc[tt][4 * rb + 1], acc[tt][4 * rb + 2], acc[tt][4 * rb + 3]));
+        if (qg == 0) {
+            a.part_ml[(pe * 32 + qi) * 2 + 0] = m_run;
+            a.part_ml[(pe * 32 + qi) * 2 + 1] = l_run;
+        }
+        return;
+    }
     if (qvalid) {
         const float inv = 1.f / l_run;
         float *op = a.out + ((size_t)qrow * n_head + h) * HD;
@@ -705,6 +729,49 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
                     make_float4(acc[tt][4 * rb + 0] * inv, acc[tt][4 * rb + 1] * inv,
                                 acc[tt][4 * rb + 2] * inv, acc[tt][4 * rb + 3] * inv));
     }
+}
+
+// Block = one (kv-head, strip, q-head) entry of the prefill: the log-sum-exp
+// merge of its key segments for 32 query rows; thread (row r, chunk c) owns
+// 16 dims of one row.
+template <int HD>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
+    constexpr int CH = HD / 8;                          // dims per thread
+    const int entry = blockIdx.x;
+    const int total = a.n_rep * a.n_strips;
+    const int g = entry / total, e = entry - g * total;
+    const int strip = a.n_strips - 1 - e / a.n_rep;
+    const int h = g * a.n_rep + e % a.n_rep;
+    const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
+    const int qrow = 32 * strip + r;
+    if (qrow >= a.n_tok) return;
+    const int S = a.n_kseg;
+    const size_t base = (size_t)entry * S;
+    float m = -INFINITY;
+    for (int s = 0; s < S; ++s) m = fmaxf(m, a.part_ml[((base + s) * 32 + r) * 2]);
+    float den = 0.f;
+    float4 acc[CH / 4];
+#pragma unroll
+    for (int j = 0; j < CH / 4; ++j) acc[j] = zero4();
+    for (int s = 0; s < S; ++s) {
+        const float ms = a.part_ml[((base + s) * 32 + r) * 2];
+        const float w = ms == -INFINITY ? 0.f : exp2f(ms - m);
+        den = fmaf(w, a.part_ml[((base + s) * 32 + r) * 2 + 1], den);
+        const float *po = a.part_o + ((base + s) * 32 + r) * HD + c * CH;
+#pragma unroll
+        for (int j = 0; j < CH / 4; ++j) {
+            const float4 x = ld4(po + 4 * j);
+            acc[j].x = fmaf(w, x.x, acc[j].x);
+            acc[j].y = fmaf(w, x.y, acc[j].y);
+            acc[j].z = fmaf(w, x.z, acc[j].z);
+            acc[j].w = fmaf(w, x.w, acc[j].w);
+        }
+    }
+    const float inv = 1.f / den;
+    float *op = a.out + ((size_t)qrow * a.n_head_kv * a.n_rep + h) * HD + c * CH;
+#pragma unroll
+    for (int j = 0; j < CH / 4; ++j)
+        st4(op + 4 * j, make_float4(acc[j].x * inv, acc[j].y * inv, acc[j].z * inv, acc[j].w * inv));
 }
 
 // ------------------------------------------------------------------- synth
@@ -803,12 +870,31 @@ hipError_t launch_append(const AppendArgs &a, int head_dim, hipStream_t s) {
     return hipGetLastError();
 }
 
+int prefill_key_segments(int n_tok, int pos0, int n_head_kv, int n_rep, int num_cu, int *seg_tiles) {
+    // Split the key range when the workgroups of a chunk do not fill every
+    // CU (two fit per CU): as many segments as keep all of them in one wave
+    // of two per CU, each of at least 8 key tiles.
+    const int n_strips = (n_tok + 31) / 32;
+    const int n_wg = (n_rep * n_strips + 3) / 4 * n_head_kv;
+    const int n_tiles = (pos0 + n_tok - 1) / 32 + 1;
+    int n_kseg = 1;
+    if (n_wg < num_cu)
+        n_kseg = std::max(1, std::min(2 * num_cu / n_wg, n_tiles / 8));
+    *seg_tiles = (n_tiles + n_kseg - 1) / n_kseg;
+    return n_kseg;
+}
+
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     const int items = (a.n_rep * a.n_strips + 3) / 4;
-    const dim3 grid(items * a.n_head_kv);
+    const dim3 grid(items * a.n_head_kv * a.n_kseg);
     if (head_dim == 128) hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, s, a);
     else if (head_dim == 64) hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kThreads), 0, s, a);
     else return hipErrorInvalidValue;
+    if (a.n_kseg > 1) {
+        const dim3 cgrid(a.n_head_kv * a.n_rep * a.n_strips);
+        if (head_dim == 128) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL(prefill_combine_kernel<64>, cgrid, dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -232,6 +232,9 @@ PREFILL_CASES = [
     (16, 2, 128, [(0, 96), (96, 5)]),
     (8, 8, 128, [(0, 40), (40, 90)]),
     (40, 8, 128, [(0, 70)]),
+    # short chunks over a longer cache: the key range is split into segments
+    (28, 4, 128, [(0, 700), (700, 45)]),
+    (14, 2, 64, [(0, 900), (900, 40)]),
 ]
 
 
