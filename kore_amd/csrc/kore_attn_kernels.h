@@ -16,10 +16,10 @@ namespace kore_attn_gpu {
 
 // Single-token decode, two launches.  The split kernel does RoPE of q and of
 // the new k row, the append of the new k/v row, and flash-decoding attention
-// of every (kv-head, split) over the cache slots [0, n_rows) in tiles of
-// kDecodeTile rows plus the new row itself; with one split it writes `out`,
+// of every (kv-head, split) over the cache slots [0, n_rows) in blocks of
+// kDecodeBlock rows plus the new row itself; with one split it writes `out`,
 // otherwise unnormalised split partials that the combine kernel merges.
-constexpr int kDecodeTile = 64;
+constexpr int kDecodeBlock = 16;
 constexpr int kMaxDecodeSplits = 128;   // splits per kv-head the combine merges in one round
 
 struct DecodeArgs {
@@ -35,7 +35,7 @@ struct DecodeArgs {
     int n_rows;           // cache slots read: [0, n_rows), the new row excluded
                           // (a wrapped ring reads all slots and masks new_slot)
     int new_slot;         // slot receiving the new row
-    int rows_per_split;   // multiple of kDecodeTile
+    int rows_per_split;   // multiple of kDecodeBlock
     int n_split;
     int n_head_kv;
     int n_rep;            // q heads per kv head

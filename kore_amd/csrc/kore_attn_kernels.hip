@@ -4,10 +4,11 @@
 //                          (kore.cpp:1424-1425), append of the new k/v row
 //                          (kore.cpp:1427-1430) and flash-decoding attention
 //                          (kore.cpp:1432-1455) of each (kv-head, split) of
-//                          the cache.  HBM-bound: every K/V byte is read once
-//                          per kv-head (not once per q-head as kore's
-//                          head-outer loop does) with 16-byte loads issued
-//                          before any arithmetic.
+//                          the cache on fp32 MFMA (v_mfma_f32_16x16x4f32),
+//                          16 rows per wave and block.  HBM-bound: every K/V
+//                          byte is read once per kv-head (not once per q-head
+//                          as kore's head-outer loop does) with 16-byte loads
+//                          straight into the MFMA operands.
 //   decode_combine_kernel  log-sum-exp merge of the split partials, one
 //                          workgroup per (q-head, 16 dims): a second launch
 //                          instead of a last-workgroup merge, because a
@@ -39,6 +40,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
@@ -124,347 +126,309 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float2 cs, float &
 
 // ------------------------------------------------------------------ decode
 
-template <int HD>
-struct DecodeGeom {
-    static constexpr int RW = kDecodeTile / kWaves;               // rows of a full tile per wave
-    static constexpr int LPR = HD / 8;                            // lanes per K row (8 floats each)
-    static constexpr int RPW = 64 / LPR;                          // K rows per wave per pass
-    static constexpr int KPASS = RW / RPW;                        // K passes of a full tile
-    static constexpr int VL = HD / 4;                             // lanes per V row (one float4 each)
-    static constexpr int VRW = 64 / VL;                           // V rows per wave per load
-    static constexpr int VLD = RW / VRW;                          // V loads per thread of a full tile
-    static_assert(KPASS >= 1 && VLD >= 1 && (LPR == 8 || LPR == 16), "unsupported head_dim");
-};
+// v_mfma_f32_16x16x4f32, one block: lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; D register v of lane l is D[4(l/16) + v][l%16].
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// x of lane l and of lane l ^ 16 (v_permlane16_swap with x as both operands
+// returns the even 16-lane rows in one result and the odd rows in the other),
+// and likewise of lane l ^ 32 (v_permlane32_swap).  The results are copied
+// to integers before the bit casts: a bit cast applied to an element of the
+// returned vector directly is compiled as the first element by this hipcc
+// (ROCm 7.2) for either index.
+__device__ __forceinline__ void pair16(float x, float &a, float &b) {
+    const unsigned xb = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(xb, xb, false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    a = __builtin_bit_cast(float, r0);
+    b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void pair32(float x, float &a, float &b) {
+    const unsigned xb = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(xb, xb, false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    a = __builtin_bit_cast(float, r0);
+    b = __builtin_bit_cast(float, r1);
+}
+// Max / sum over the four lanes l % 16 + 16 k (k = 0..3); every one of them
+// receives the same value (the operands are the same in all four lanes).
+__device__ __forceinline__ float max4rows(float x) {
+    float a, b;
+    pair16(x, a, b);
+    x = fmaxf(a, b);
+    pair32(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum4rows(float x) {
+    float a, b;
+    pair16(x, a, b);
+    x = a + b;
+    pair32(x, a, b);
+    return a + b;
+}
 
 // Workgroup (split, kv-head g): cache slots [r0, r_end) of kv-head g for the
 // NR q-heads of g, so every K/V byte is read once per kv-head (kore's
 // head-outer loop, kore.cpp:1432, reads it once per q-head).  The slots are
-// processed in tiles of kDecodeTile rows, the last of which may carry up to
-// kWaves extra rows (row 64 + w goes to wave w as one more, mostly masked
-// pass); that lets the host give every CU exactly one workgroup when the row
-// count is a little above a multiple of 64 per CU.  Wave w owns rows
-// [16w, 16w + 16) of a tile and keeps its own online softmax (max, sum,
-// output) over them, so the tile loop has no workgroup barrier.  A tile's K
-// and V rows are loaded into registers by unconditional 16-byte loads (rows
-// past the end are clamped to the last row and masked afterwards), issued
-// before any arithmetic and consumed in issue order.
-//   score pass: LPR lanes per K row, each lane 8 of the row's floats (2 x
-//               16 B loads at dims 4c + j*4*LPR) and the same dims of the NR
-//               roped queries, pre-multiplied by 1/sqrt(hd) * log2(e) so the
-//               softmax runs in base 2 on v_exp_f32; the partial dots are
-//               summed over the LPR lanes with DPP, which leaves every lane
-//               of a row group with the scores of its row.
-//   softmax:    the running max of each head is wave-uniform (a max over the
-//               row groups by v_readlane); the running sums stay per row
-//               group until the end.
-//   PV pass:    VL lanes per V row (one float4 each), VRW rows per wave per
-//               load; the weights go through a wave-private LDS slice.
+// cut into blocks of 16 rows; wave w takes blocks w, w + 4, ... and keeps its
+// own online softmax (max, sum, output) for all NR heads, so the block loop
+// has no workgroup barrier.  Per block, on fp32 MFMA (v_mfma_f32_16x16x4f32):
+//   scores  S[row][head] = K[16 rows][hd] . q^T: lane (m, k) = (l % 16, l / 16)
+//           gives K[row m][16t + 4k + e] and the roped, pre-scaled q of head m
+//           at the same dim for MFMA k-step (t, e), so both operands come
+//           straight from 16-byte loads (the dims are summed in a different
+//           order, which the dot product allows).  The scores are already
+//           multiplied by 1/sqrt(hd) * log2(e): the softmax runs in base 2
+//           on v_exp_f32.  Lane (m, k) ends up with rows 4k..4k+3 of head m.
+//   softmax the head's running max over the 16 rows is a max over the lane's
+//           four registers and lanes m, m+16, m+32, m+48 (permlane swaps);
+//           the exponentials stay in the score registers.
+//   values  O^T[dim][head] += V^T[dim][16 rows] . P: k-step s takes rows
+//           4k + s, which is exactly score register s of lane (m, k), so P
+//           is fed back as the B operand without any data movement; lane
+//           (m, k) gives V[row 4k + s][64j + 4m + e] (16-byte loads) for the
+//           output block 4j + e.
+// Every load is in bounds: rows past the split's end are clamped to its last
+// row and masked.  A wave with more than one block prefetches its next block
+// into a second register set while it works on the current one.
 // The new token's row is not read from the cache: the owner workgroup ropes
 // it, appends it, and adds it as one more softmax state (its own score, sum
-// 1, output v) when the four wave states are merged.  Slots [0, n_rows) never
-// include it except in a wrapped ring, where its stale slot is masked.
+// 1, output v).  Slots [0, n_rows) never include it except in a wrapped ring,
+// where its stale slot is masked.  The four wave states (and the new row's)
+// are merged in LDS into one partial per q-head, or into `out` when the
+// kv-head has a single split.
 template <int HD, int NR>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
-    using G = DecodeGeom<HD>;
-    constexpr int TILE = kDecodeTile;
+    constexpr int NT = HD / 16;    // K float4 per lane per block (MFMA k-steps / 4)
+    constexpr int NJ = HD / 64;    // V float4 per lane per row
+    constexpr int NMB = HD / 16;   // 16-dim output blocks
     constexpr int HALF = HD / 2;
-    constexpr int NPAIR = (NR * HALF + kThreads - 1) / kThreads;   // q RoPE pairs per thread
-    constexpr int NST = kWaves + 1;                                // softmax states merged at the end
-    constexpr int KP = G::KPASS + 1;                               // passes incl. the extra-row pass
-    constexpr int VP = G::VLD + 1;
+    constexpr int NST = kWaves + 1;
     static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
 
-    __shared__ __align__(16) float s_q[NR * HD];           // roped q * scale * log2(e)
-    __shared__ __align__(16) float s_knew[HD];
-    __shared__ __align__(16) float s_p[(TILE + kWaves) * 8];   // [row][head] weights, wave-private rows
-    __shared__ __align__(16) float s_red[NST * NR * HD];   // per state: unnormalised output
-    __shared__ float s_wm[NST * 8], s_wl[NST * 8], s_we[NST * 8], s_hm[8], s_hl[8];
+    __shared__ __align__(16) float s_o[kWaves * NR * HD];   // unnormalised wave outputs
+    __shared__ __align__(16) float s_knew[HD];              // the new row: roped k
+    __shared__ __align__(16) float s_vnew[HD];              // ... and v
+    __shared__ float s_m[NST * 8], s_l[NST * 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m16 = lane & 15, kq = lane >> 4;
     const int split = blockIdx.x, g = blockIdx.y;
     const int r0 = split * a.rows_per_split;
     const int r_end = min(r0 + a.rows_per_split, a.n_rows);
-    const int n_own = max(r_end - r0, 0);
-    const int n_tiles = n_own == 0 ? 0 : max(1, (n_own - kWaves + TILE - 1) / TILE);
+    const int n_blk = (max(r_end - r0, 0) + kDecodeBlock - 1) / kDecodeBlock;
     const int last_row = max(r_end - 1, 0);
     const int owner = a.n_rows == 0 ? 0 : min(a.new_slot, a.n_rows - 1) / a.rows_per_split;
     const bool is_owner = split == owner;
     const size_t head_base = (size_t)g * a.slots * HD;
     const float *kg = a.kc + head_base;
     const float *vg = a.vc + head_base;
-    const int c = lane % G::LPR, rw = lane / G::LPR;
-    const int vc4 = lane % G::VL, vr = lane / G::VL;
-    const float qscale = a.scale * kLog2e;
 
-    // ---- loads: q pairs and their cos/sin first (needed first), then the
-    // first tile of K and V (every load in bounds, consumed in issue order).
-    float qx0[NPAIR], qx1[NPAIR];
-    float2 qcs[NPAIR];
+    // ---- loads: q of head m16 at dims 16t + 4kq (+0..3) and their cos/sin,
+    // the new k/v row (pair i, i + hd/2 in lane i), then the first block
+    const int hq = min(m16, NR - 1);
+    const float *qp = a.q + (size_t)(g * a.n_rep + hq) * HD + 4 * kq;
+    const float *csp = reinterpret_cast<const float *>(a.cs) + 8 * kq;
+    float4 qf[NT], csf[NT];
 #pragma unroll
-    for (int it = 0; it < NPAIR; ++it) {
-        const int idx = min(tid + it * kThreads, NR * HALF - 1);
-        const int h = idx / HALF, i = idx - h * HALF;
-        const float *qh = a.q + (size_t)(g * a.n_rep + h) * HD;
-        qx0[it] = qh[i];
-        qx1[it] = qh[i + HALF];
-        qcs[it] = a.cs[i];
+    for (int t = 0; t < NT; ++t) qf[t] = ld4(qp + 16 * t);
+#pragma unroll
+    for (int t = 0; t < NT / 2; ++t) {
+        csf[2 * t] = ld4(csp + 32 * t);         // (c, s) of dims 16t + 4kq, +1
+        csf[2 * t + 1] = ld4(csp + 32 * t + 4); // ... +2, +3
     }
-    // the new k/v row (used by the owner workgroup only; loaded by all so
-    // that no load is conditional): thread i < HALF takes pair i of k and
-    // elements i, i + HALF of v
-    const int ni = tid % HALF;
+    const int ni = min(lane, HALF - 1);
     const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
-    const float2 ncs = a.cs[ni];
     const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
-    __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the K/V tile
-    float4 kreg[KP][2];
-    float4 vreg[VP];
-    // tile row of K pass ps (the last pass is row TILE + wave) / of V load i
-    auto krow = [&](int ps) { return ps < G::KPASS ? wave * G::RW + ps * G::RPW + rw : TILE + wave; };
-    auto vrow = [&](int i) { return i < G::VLD ? wave * G::RW + i * G::VRW + vr : TILE + wave; };
-    // The extra-row loads are issued even when the tile has no extra rows:
-    // they are then clamped to the tile's last row, which the tile loads
-    // anyway, so they cost cache hits only, and the loads stay unconditional
-    // (exact in-order wait counts).
-    auto load_tile = [&](int t0) {
+    const float2 ncs = a.cs[ni];
+    // q is roped before any K/V load is issued.  Once every CU streams its
+    // K/V rows, a q load that misses the caches waits behind them in the
+    // memory controllers and arrives with the bulk of the data (measured
+    // ~3.5 us into the kernel instead of ~1 us), and the score MFMAs need q.
+    // ---- RoPE of q into the B operand, pre-scaled by 1/sqrt(hd) * log2(e)
+    const float qscale = a.scale * kLog2e;
+    float qb[NT][4];
 #pragma unroll
-        for (int ps = 0; ps < KP; ++ps) {
-            const int r = min(t0 + krow(ps), last_row);
-            const float *p = kg + (size_t)r * HD + c * 4;
+    for (int t = 0; t < NT / 2; ++t)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) kreg[ps][j] = ld4(p + j * (G::LPR * 4));
+        for (int e = 0; e < 4; ++e) {
+            const float4 c4 = csf[2 * t + e / 2];
+            const float2 cs = (e & 1) ? make_float2(c4.z, c4.w) : make_float2(c4.x, c4.y);
+            float y0, y1;
+            rope_pair(comp(qf[t], e), comp(qf[t + NT / 2], e), cs, y0, y1);
+            qb[t][e] = m16 < NR ? y0 * qscale : 0.f;
+            qb[t + NT / 2][e] = m16 < NR ? y1 * qscale : 0.f;
         }
+
+    __builtin_amdgcn_sched_barrier(0);   // the K/V loads come after
+
+    float4 kA[NT], vA[4][NJ], kB[NT], vB[4][NJ];
+    auto load_blk = [&](float4 (&kf)[NT], float4 (&vf)[4][NJ], int b) {
+        const int rb = r0 + 16 * b;
+        const float *kr = kg + (size_t)min(rb + m16, last_row) * HD + 4 * kq;
 #pragma unroll
-        for (int i = 0; i < VP; ++i) {
-            const int r = min(t0 + vrow(i), last_row);
-            vreg[i] = ld4(vg + (size_t)r * HD + vc4 * 4);
+        for (int t = 0; t < NT; ++t) kf[t] = ld4(kr + 16 * t);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float *vr = vg + (size_t)min(rb + 4 * kq + s, last_row) * HD + 4 * m16;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) vf[s][j] = ld4(vr + 64 * j);
         }
     };
-    load_tile(r0);
+    // The first block is loaded unconditionally (a wave without one loads the
+    // split's last rows again and ignores them): a load under a branch makes
+    // the compiler's wait counts for everything after it conservative, so
+    // the score MFMAs would wait for the whole block instead of its first K
+    // registers.
+    load_blk(kA, vA, wave);
+    if (wave + kWaves < n_blk) load_blk(kB, vB, wave + kWaves);
 
-    // ---- RoPE of this group's q heads (stored pre-scaled for the scores);
-    // RoPE + append of the new k/v row.
+    floatx4 o[NMB];
 #pragma unroll
-    for (int it = 0; it < NPAIR; ++it) {
-        const int idx = tid + it * kThreads;
-        if (idx < NR * HALF) {
-            const int h = idx / HALF, i = idx - h * HALF;
-            float y0, y1;
-            rope_pair(qx0[it], qx1[it], qcs[it], y0, y1);
-            s_q[h * HD + i] = y0 * qscale;
-            s_q[h * HD + i + HALF] = y1 * qscale;
+    for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    auto process = [&](const float4 (&kf)[NT], const float4 (&vf)[4][NJ], int b, bool first) {
+        const int rb = r0 + 16 * b;
+        floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s = mfma16(comp(kf[t], e), qb[t][e], s);
+        float x[4], mt = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = rb + 4 * kq + v;
+            x[v] = (row < r_end && row != a.new_slot) ? s[v] : -INFINITY;
+            mt = fmaxf(mt, x[v]);
+        }
+        const float m_new = fmaxf(m_run, max4rows(mt));
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;   // a block with every row masked
+        const float alpha = fast_exp2(m_run - m_use);
+        float p[4], ps = 0.f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            p[v] = fast_exp2(x[v] - m_use);
+            ps += p[v];
+        }
+        l_part = fmaf(l_part, alpha, ps);
+        m_run = m_new;
+        if (!first) {
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) o[mb] *= alpha;
+        }
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+            for (int sk = 0; sk < 4; ++sk) o[mb] = mfma16(comp(vf[sk][mb / 4], mb % 4), p[sk], o[mb]);
+    };
+    for (int b = wave; b < n_blk;) {
+        process(kA, vA, b, b == wave);
+        b += kWaves;
+        if (b >= n_blk) break;
+        if (b + kWaves < n_blk) load_blk(kA, vA, b + kWaves);
+        process(kB, vB, b, false);
+        b += kWaves;
+        if (b + kWaves < n_blk) load_blk(kB, vB, b + kWaves);
+    }
+
+    // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
+    // 64(mb / 4) + 16kq + 4v + mb % 4
+    const float l_w = sum4rows(l_part);
+    if (m16 < NR) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                st4(&s_o[(wave * NR + m16) * HD + 64 * j + 16 * kq + 4 * v],
+                    make_float4(o[4 * j][v], o[4 * j + 1][v], o[4 * j + 2][v], o[4 * j + 3][v]));
+        if (kq == 0) {
+            s_m[wave * 8 + m16] = m_run;
+            s_l[wave * 8 + m16] = l_w;
         }
     }
-    if (is_owner && tid < HALF) {
-        float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
-        float *vd = a.vc + head_base + (size_t)a.new_slot * HD;
+    // ---- the new row (owner workgroup, wave 0): RoPE, append, and its score
+    // for every head (state kWaves: score, sum 1, output v)
+    if (is_owner && wave == 0) {
         float y0, y1;
         rope_pair(nk0, nk1, ncs, y0, y1);
-        s_knew[ni] = y0;
-        s_knew[ni + HALF] = y1;
-        kd[ni] = y0;
-        kd[ni + HALF] = y1;
-        s_red[(kWaves * NR) * HD + ni] = nv0;          // state kWaves: v of the new row
-        s_red[(kWaves * NR) * HD + ni + HALF] = nv1;
-        vd[ni] = nv0;
-        vd[ni + HALF] = nv1;
-    }
-    __syncthreads();
-
-    float qv[NR][8];
-#pragma unroll
-    for (int h = 0; h < NR; ++h)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float4 t = ld4(&s_q[h * HD + j * (G::LPR * 4) + c * 4]);
-            qv[h][4 * j + 0] = t.x;
-            qv[h][4 * j + 1] = t.y;
-            qv[h][4 * j + 2] = t.z;
-            qv[h][4 * j + 3] = t.w;
+        if (lane < HALF) {
+            float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
+            float *vd = a.vc + head_base + (size_t)a.new_slot * HD;
+            kd[lane] = y0;
+            kd[lane + HALF] = y1;
+            vd[lane] = nv0;
+            vd[lane + HALF] = nv1;
+            s_knew[lane] = y0;
+            s_knew[lane + HALF] = y1;
+            s_vnew[lane] = nv0;
+            s_vnew[lane + HALF] = nv1;
         }
-    float o[NR][4];
-    float m_run[NR], l_run[NR];
+        __builtin_amdgcn_wave_barrier();
+        float sn = 0.f;
 #pragma unroll
-    for (int h = 0; h < NR; ++h) {
-        o[h][0] = o[h][1] = o[h][2] = o[h][3] = 0.f;
-        m_run[h] = -INFINITY;
-        l_run[h] = 0.f;
-    }
-
-    for (int t = 0; t < n_tiles; ++t) {
-        const int t0 = r0 + t * TILE;
-        const bool last = t + 1 == n_tiles;
-        const bool extra = last && n_own - t * TILE > TILE;
-        if (t > 0) load_tile(t0);
-        const int nrows = last ? r_end - t0 : TILE;
-        const int skip = a.new_slot - t0;   // a wrapped ring's stale copy of the new slot
-        const int npass = extra ? KP : G::KPASS;
-
-        // ---- scores (log2 domain): s = (q . k) / sqrt(hd) * log2(e)
-        float sc[KP][NR];
-#pragma unroll
-        for (int ps = 0; ps < KP; ++ps) {
-            if (ps >= npass) {
-#pragma unroll
-                for (int h = 0; h < NR; ++h) sc[ps][h] = -INFINITY;
-                continue;
-            }
-            const int row = krow(ps);
-            const bool ok = row < nrows && row != skip && (ps < G::KPASS || rw == 0);
-#pragma unroll
-            for (int h = 0; h < NR; ++h) {
-                float s = 0.f;
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    s = fmaf(qv[h][4 * j + 0], kreg[ps][j].x, s);
-                    s = fmaf(qv[h][4 * j + 1], kreg[ps][j].y, s);
-                    s = fmaf(qv[h][4 * j + 2], kreg[ps][j].z, s);
-                    s = fmaf(qv[h][4 * j + 3], kreg[ps][j].w, s);
-                }
-                s = group_sum<G::LPR>(s);
-                sc[ps][h] = ok ? s : -INFINITY;
-            }
+        for (int t = 0; t < NT; ++t) {
+            const float4 kn = ld4(&s_knew[16 * t + 4 * kq]);
+            sn = fmaf(qb[t][0], kn.x, sn);
+            sn = fmaf(qb[t][1], kn.y, sn);
+            sn = fmaf(qb[t][2], kn.z, sn);
+            sn = fmaf(qb[t][3], kn.w, sn);
         }
-
-        // ---- online softmax: wave-uniform running max, per-group sums
-        float alpha[NR];
-#pragma unroll
-        for (int h = 0; h < NR; ++h) {
-            float mt = sc[0][h];
-#pragma unroll
-            for (int ps = 1; ps < KP; ++ps) mt = fmaxf(mt, sc[ps][h]);
-            const float m_new = fmaxf(m_run[h], wave_max_groups<G::LPR>(mt));
-            float lt = 0.f;
-#pragma unroll
-            for (int ps = 0; ps < KP; ++ps) {
-                const float p = sc[ps][h] == -INFINITY ? 0.f : fast_exp2(sc[ps][h] - m_new);
-                sc[ps][h] = p;
-                lt += p;
-            }
-            alpha[h] = m_run[h] == -INFINITY ? 0.f : fast_exp2(m_run[h] - m_new);
-            l_run[h] = fmaf(l_run[h], alpha[h], lt);
-            m_run[h] = m_new;
-        }
-        // weights of the wave's rows to its LDS slice: lane c == 0 of each row
-        if (c == 0) {
-#pragma unroll
-            for (int ps = 0; ps < KP; ++ps) {
-                if (ps < npass && (ps < G::KPASS || rw == 0)) {
-                    float pw[8];
-#pragma unroll
-                    for (int h = 0; h < 8; ++h) pw[h] = h < NR ? sc[ps][h] : 0.f;
-                    float *dst = &s_p[krow(ps) * 8];
-                    st4(dst, make_float4(pw[0], pw[1], pw[2], pw[3]));
-                    st4(dst + 4, make_float4(pw[4], pw[5], pw[6], pw[7]));
-                }
-            }
-        }
-
-        // ---- o = alpha * o + sum_t p_t v_t over the wave's rows
-        if (t > 0) {
-#pragma unroll
-            for (int h = 0; h < NR; ++h) {
-                o[h][0] *= alpha[h];
-                o[h][1] *= alpha[h];
-                o[h][2] *= alpha[h];
-                o[h][3] *= alpha[h];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < VP; ++i) {
-            if (i < G::VLD || (extra && vr == 0)) {
-                const int row = vrow(i);
-                const float4 vv = vreg[i];
-                const float4 p0 = ld4(&s_p[row * 8]);
-                const float4 p1 = ld4(&s_p[row * 8 + 4]);
-                const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-                for (int h = 0; h < NR; ++h) {
-                    o[h][0] = fmaf(pp[h], vv.x, o[h][0]);
-                    o[h][1] = fmaf(pp[h], vv.y, o[h][1]);
-                    o[h][2] = fmaf(pp[h], vv.z, o[h][2]);
-                    o[h][3] = fmaf(pp[h], vv.w, o[h][3]);
-                }
-            }
-        }
-    }
-
-    // ---- the wave's state: o summed over the lanes sharing dims, l over
-    // the row groups; then the four wave states and the new row's are merged
-#pragma unroll
-    for (int off = G::VL; off < 64; off <<= 1)
-#pragma unroll
-        for (int h = 0; h < NR; ++h)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[h][e] += __shfl_xor(o[h][e], off);
-    if (vr == 0) {
-#pragma unroll
-        for (int h = 0; h < NR; ++h)
-            st4(&s_red[(wave * NR + h) * HD + vc4 * 4], make_float4(o[h][0], o[h][1], o[h][2], o[h][3]));
-    }
-#pragma unroll
-    for (int h = 0; h < NR; ++h) {
-        const float lw = wave_sum_groups<G::LPR>(l_run[h]);
-        if (lane == 0) {
-            s_wm[wave * 8 + h] = m_run[h];
-            s_wl[wave * 8 + h] = lw;
-        }
-    }
-    if (is_owner) {
-        // score of the new row for head h (wave w takes heads w, w + 4):
-        // lane-strided dot over the scaled roped q and the roped k, then a
-        // wave sum
-        for (int h = wave; h < NR; h += kWaves) {
-            float s = 0.f;
-            for (int d = lane; d < HD; d += 64) s = fmaf(s_q[h * HD + d], s_knew[d], s);
-            s = wave_sum_groups<16>(group_sum<16>(s));
-            if (lane == 0) {
-                s_wm[kWaves * 8 + h] = s;
-                s_wl[kWaves * 8 + h] = 1.f;
-            }
+        sn = sum4rows(sn);
+        if (kq == 0 && m16 < NR) {
+            s_m[kWaves * 8 + m16] = sn;
+            s_l[kWaves * 8 + m16] = 1.f;
         }
     }
     __syncthreads();
-    const bool single = a.n_split == 1;
-    if (tid < NR) {
-        const int h = tid, nst = is_owner ? NST : kWaves;
-        float m = -INFINITY;
-        for (int w = 0; w < nst; ++w) m = fmaxf(m, s_wm[w * 8 + h]);
+
+    // ---- merge of the wave states (and the new row's) per (head, float4):
+    // thread (h, d4) for h < NR, d4 < hd/4 (NR * hd/4 <= kThreads)
+    static_assert(8 * (HD / 4) <= kThreads, "one merge thread per output float4");
+    if (tid < NR * (HD / 4)) {
+        const int h = tid / (HD / 4), d4 = tid - h * (HD / 4);
+        float mw[kWaves], lw[kWaves];
+        float4 xw[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            mw[w] = s_m[w * 8 + h];
+            lw[w] = s_l[w * 8 + h];
+            xw[w] = ld4(&s_o[(w * NR + h) * HD + 4 * d4]);
+        }
+        float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+        float mn = -INFINITY, ln = 0.f;
+        float4 xn = zero4();
+        if (is_owner) {   // the new row's state (only the owner wrote it)
+            mn = s_m[kWaves * 8 + h];
+            ln = s_l[kWaves * 8 + h];
+            xn = ld4(&s_vnew[4 * d4]);
+            m = fmaxf(m, mn);
+        }
         float l = 0.f;
-        for (int w = 0; w < NST; ++w) {
-            const float mw = s_wm[w * 8 + h];
-            const float e = (w >= nst || mw == -INFINITY) ? 0.f : fast_exp2(mw - m);
-            s_we[w * 8 + h] = e;
-            l = fmaf(e, s_wl[w * 8 + h], l);
-        }
-        if (single) {
-            const float inv = 1.f / l;
-            for (int w = 0; w < NST; ++w) s_we[w * 8 + h] *= inv;
-        }
-        s_hm[h] = m;
-        s_hl[h] = l;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < NR * (HD / 4); idx += kThreads) {
-        const int h = idx / (HD / 4), d4 = idx - h * (HD / 4);
         float4 acc = zero4();
 #pragma unroll
-        for (int w = 0; w < NST; ++w) {
-            const float e = s_we[w * 8 + h];
-            const float4 x = ld4(&s_red[(w < kWaves ? (w * NR + h) * HD : (kWaves * NR) * HD) + d4 * 4]);
+        for (int w = 0; w <= kWaves; ++w) {
+            const float mx = w < kWaves ? mw[w] : mn;
+            const float e = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
+            const float4 x = w < kWaves ? xw[w] : xn;
+            l = fmaf(e, w < kWaves ? lw[w] : ln, l);
             acc.x = fmaf(e, x.x, acc.x);
             acc.y = fmaf(e, x.y, acc.y);
             acc.z = fmaf(e, x.z, acc.z);
             acc.w = fmaf(e, x.w, acc.w);
         }
         const size_t hg = (size_t)g * a.n_rep + h;
-        if (single) {
-            st4(a.out + hg * HD + d4 * 4, acc);
+        if (a.n_split == 1) {
+            const float inv = 1.f / l;
+            st4(a.out + hg * HD + 4 * d4, make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
         } else {
-            st4(a.part_o + (hg * a.n_split + split) * HD + d4 * 4, acc);
+            st4(a.part_o + (hg * a.n_split + split) * HD + 4 * d4, acc);
             if (d4 == 0) {
-                a.part_ml[(hg * a.n_split + split) * 2 + 0] = s_hm[h];
-                a.part_ml[(hg * a.n_split + split) * 2 + 1] = s_hl[h];
+                a.part_ml[(hg * a.n_split + split) * 2 + 0] = m;
+                a.part_ml[(hg * a.n_split + split) * 2 + 1] = l;
             }
         }
     }
@@ -844,17 +808,13 @@ bool prefill_supported(int head_dim, int n_rep) {
 }
 
 int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu) {
-    // One workgroup per CU where the rows allow it: S splits per kv-head with
-    // S = min(num_cu / n_head_kv, kMaxDecodeSplits).  Up to 64 * S rows use
-    // 64-row splits; a little more gives S splits of 65..68 rows (one tile
-    // plus an extra row per wave); beyond that the split grows to the next
-    // size whose remainder over whole tiles is at most kWaves rows.
+    // Blocks of kDecodeBlock rows over S = num_cu / n_head_kv splits per
+    // kv-head (at most kMaxDecodeSplits): one workgroup per CU, since the
+    // split kernel's register use leaves room for only one per CU.
     (void)head_dim;
+    const int nb = std::max(1, (n_rows + kDecodeBlock - 1) / kDecodeBlock);
     const int S = std::max(1, std::min(num_cu / std::max(n_head_kv, 1), kMaxDecodeSplits));
-    if (n_rows <= kDecodeTile * S) return kDecodeTile;
-    int rps = (n_rows + S - 1) / S;
-    if (rps % kDecodeTile > kWaves) rps = (rps + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
-    return rps;
+    return kDecodeBlock * ((nb + S - 1) / S);
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, hipStream_t s) {
