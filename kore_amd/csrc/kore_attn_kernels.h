@@ -35,7 +35,7 @@ struct DecodeArgs {
     int n_rows;           // cache slots read: [0, n_rows), the new row excluded
                           // (a wrapped ring reads all slots and masks new_slot)
     int new_slot;         // slot receiving the new row
-    int rows_per_split;   // multiple of kDecodeBlock
+    int rows_per_split;   // whole blocks of kDecodeBlock rows plus at most 4 extra rows
     int n_split;
     int n_head_kv;
     int n_rep;            // q heads per kv head

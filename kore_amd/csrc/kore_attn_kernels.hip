@@ -57,53 +57,6 @@ template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
-// Sum over the aligned group of N lanes (N = 4, 8 or 16) that contains this
-// lane; every lane of the group receives it.
-template <int N>
-__device__ __forceinline__ float group_sum(float x) {
-    static_assert(N == 4 || N == 8 || N == 16, "DPP group of 4, 8 or 16 lanes");
-    if constexpr (N == 16) {
-        x += dpp<0x128>(x);   // row_ror:8
-        x += dpp<0x124>(x);   // row_ror:4
-    } else if constexpr (N == 8) {
-        x += dpp<0x141>(x);   // row_half_mirror: lane i + lane 7-i of each half-row
-    }
-    if constexpr (N == 16) {
-        x += dpp<0x122>(x);   // row_ror:2
-        x += dpp<0x121>(x);   // row_ror:1
-    } else {
-        x += dpp<0xB1>(x);    // quad_perm [1,0,3,2]
-        x += dpp<0x4E>(x);    // quad_perm [2,3,0,1]
-    }
-    return x;
-}
-
-// Max / sum over the 64 lanes of a value that is uniform within each aligned
-// group of N lanes (N = 8 or 16); every lane receives the result.  The
-// groups of a 16-lane row are folded with DPP, the four rows with v_readlane
-// (no LDS traffic).
-template <int N>
-__device__ __forceinline__ float wave_max_groups(float x) {
-    static_assert(N == 8 || N == 16, "groups of 8 or 16 lanes");
-    if constexpr (N == 8) x = fmaxf(x, dpp<0x128>(x));   // row_ror:8 pairs the two half-rows
-    const int i = __builtin_bit_cast(int, x);
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-template <int N>
-__device__ __forceinline__ float wave_sum_groups(float x) {
-    static_assert(N == 8 || N == 16, "groups of 8 or 16 lanes");
-    if constexpr (N == 8) x += dpp<0x128>(x);
-    const int i = __builtin_bit_cast(int, x);
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
-    return (r0 + r1) + (r2 + r3);
-}
 // Max over each 16-lane row; every lane of the row receives it.
 __device__ __forceinline__ float row16_max(float x) {
     x = fmaxf(x, dpp<0x128>(x));
@@ -205,13 +158,15 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     constexpr int NJ = HD / 64;    // V float4 per lane per row
     constexpr int NMB = HD / 16;   // 16-dim output blocks
     constexpr int HALF = HD / 2;
-    constexpr int NST = kWaves + 1;
+    constexpr int NST = 2 * kWaves + 1;   // wave states, extra-row states, new row
     static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
 
     __shared__ __align__(16) float s_o[kWaves * NR * HD];   // unnormalised wave outputs
     __shared__ __align__(16) float s_knew[HD];              // the new row: roped k
     __shared__ __align__(16) float s_vnew[HD];              // ... and v
+    __shared__ __align__(16) float s_kx[kWaves * HD];       // the extra rows: k
+    __shared__ __align__(16) float s_vx[kWaves * HD];       // ... and v
     __shared__ float s_m[NST * 8], s_l[NST * 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -219,7 +174,12 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const int split = blockIdx.x, g = blockIdx.y;
     const int r0 = split * a.rows_per_split;
     const int r_end = min(r0 + a.rows_per_split, a.n_rows);
-    const int n_blk = (max(r_end - r0, 0) + kDecodeBlock - 1) / kDecodeBlock;
+    const int n_own = max(r_end - r0, 0);
+    // whole blocks, plus a last partial block of more than kWaves rows; a
+    // remainder of at most kWaves rows is taken as extra rows, one per wave
+    const int rem = n_own % kDecodeBlock;
+    const int n_blk = n_own / kDecodeBlock + (rem > kWaves ? 1 : 0);
+    const int n_extra = rem > kWaves ? 0 : rem;
     const int last_row = max(r_end - 1, 0);
     const int owner = a.n_rows == 0 ? 0 : min(a.new_slot, a.n_rows - 1) / a.rows_per_split;
     const bool is_owner = split == owner;
@@ -284,6 +244,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     // the score MFMAs would wait for the whole block instead of its first K
     // registers.
     load_blk(kA, vA, wave);
+    // this wave's extra row (clamped: loaded by every wave, used by wave < n_extra)
+    const int xrow = min(r0 + (n_own - n_extra) + wave, last_row);
+    const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
+    const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
     if (wave + kWaves < n_blk) load_blk(kB, vB, wave + kWaves);
 
     floatx4 o[NMB];
@@ -335,6 +299,31 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
         if (b + kWaves < n_blk) load_blk(kB, vB, b + kWaves);
     }
 
+    // ---- the wave's extra row (state kWaves + wave): its score for every
+    // head by VALU (k staged through LDS into the q operand's dim order)
+    if (wave < n_extra) {
+        if (lane < HALF) {
+            s_kx[wave * HD + lane] = xk0;
+            s_kx[wave * HD + lane + HALF] = xk1;
+            s_vx[wave * HD + lane] = xv0;
+            s_vx[wave * HD + lane + HALF] = xv1;
+        }
+        __builtin_amdgcn_wave_barrier();
+        float sx = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 kx = ld4(&s_kx[wave * HD + 16 * t + 4 * kq]);
+            sx = fmaf(qb[t][0], kx.x, sx);
+            sx = fmaf(qb[t][1], kx.y, sx);
+            sx = fmaf(qb[t][2], kx.z, sx);
+            sx = fmaf(qb[t][3], kx.w, sx);
+        }
+        sx = sum4rows(sx);
+        if (kq == 0 && m16 < NR) {
+            s_m[(kWaves + wave) * 8 + m16] = xrow == a.new_slot ? -INFINITY : sx;
+            s_l[(kWaves + wave) * 8 + m16] = 1.f;
+        }
+    }
     // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
     // 64(mb / 4) + 16kq + 4v + mb % 4
     const float l_w = sum4rows(l_part);
@@ -351,7 +340,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
         }
     }
     // ---- the new row (owner workgroup, wave 0): RoPE, append, and its score
-    // for every head (state kWaves: score, sum 1, output v)
+    // for every head (state 2 kWaves: score, sum 1, output v)
     if (is_owner && wave == 0) {
         float y0, y1;
         rope_pair(nk0, nk1, ncs, y0, y1);
@@ -379,8 +368,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
         }
         sn = sum4rows(sn);
         if (kq == 0 && m16 < NR) {
-            s_m[kWaves * 8 + m16] = sn;
-            s_l[kWaves * 8 + m16] = 1.f;
+            s_m[2 * kWaves * 8 + m16] = sn;
+            s_l[2 * kWaves * 8 + m16] = 1.f;
         }
     }
     __syncthreads();
@@ -399,22 +388,26 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
             xw[w] = ld4(&s_o[(w * NR + h) * HD + 4 * d4]);
         }
         float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
-        float mn = -INFINITY, ln = 0.f;
-        float4 xn = zero4();
-        if (is_owner) {   // the new row's state (only the owner wrote it)
-            mn = s_m[kWaves * 8 + h];
-            ln = s_l[kWaves * 8 + h];
-            xn = ld4(&s_vnew[4 * d4]);
-            m = fmaxf(m, mn);
-        }
         float l = 0.f;
         float4 acc = zero4();
+        // the extra rows' and the new row's states exist only where written
+        float ms[kWaves + 1], ls[kWaves + 1];
+        float4 xs[kWaves + 1];
 #pragma unroll
         for (int w = 0; w <= kWaves; ++w) {
-            const float mx = w < kWaves ? mw[w] : mn;
+            const bool on = w < kWaves ? w < n_extra : is_owner;
+            const int st = kWaves + w;
+            ms[w] = on ? s_m[st * 8 + h] : -INFINITY;
+            ls[w] = on ? s_l[st * 8 + h] : 0.f;
+            xs[w] = on ? ld4(w < kWaves ? &s_vx[w * HD + 4 * d4] : &s_vnew[4 * d4]) : zero4();
+            m = fmaxf(m, ms[w]);
+        }
+#pragma unroll
+        for (int w = 0; w < 2 * kWaves + 1; ++w) {
+            const float mx = w < kWaves ? mw[w] : ms[w - kWaves];
             const float e = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
-            const float4 x = w < kWaves ? xw[w] : xn;
-            l = fmaf(e, w < kWaves ? lw[w] : ln, l);
+            const float4 x = w < kWaves ? xw[w] : xs[w - kWaves];
+            l = fmaf(e, w < kWaves ? lw[w] : ls[w - kWaves], l);
             acc.x = fmaf(e, x.x, acc.x);
             acc.y = fmaf(e, x.y, acc.y);
             acc.z = fmaf(e, x.z, acc.z);
@@ -437,11 +430,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
 // Block (q-head h, 16-dim chunk): out[h][chunk] = sum_s w_s o_s / sum_s w_s l_s
 // with w_s = 2^(m_s - max_s m_s) (split maxima are in the log2 domain), the
 // log-sum-exp merge of the splits.  Lane (sub, c) takes splits sub + 16 i
-// (i < 8, so n_split <= 128) and float4 c of the chunk; every load is issued
-// before the first use.
-template <int HD>
+// (i < PER, so n_split <= 16 PER) and float4 c of the chunk; every load is
+// issued before the first use (one memory round trip).
+template <int HD, int PER>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
-    constexpr int PER = kMaxDecodeSplits / 16;
     const int h = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
     const int S = a.n_split;
     const int sub = lane >> 2, c = lane & 3;
@@ -455,15 +447,16 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
         x[i] = ld4(po + (size_t)s * HD);
         st[i] = ml[s];
     }
+    __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; ++i) m = fmaxf(m, st[i].x);
-    m = wave_max_groups<16>(row16_max(m));
+    m = max4rows(row16_max(m));
     float4 acc = zero4();
     float den = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const float w = (sub + 16 * i < S) ? fast_exp2(st[i].x - m) : 0.f;
+        const float w = (sub + 16 * i < S && st[i].x != -INFINITY) ? fast_exp2(st[i].x - m) : 0.f;
         den = fmaf(w, st[i].y, den);
         acc.x = fmaf(w, x[i].x, acc.x);
         acc.y = fmaf(w, x[i].y, acc.y);
@@ -471,19 +464,16 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
         acc.w = fmaf(w, x[i].w, acc.w);
     }
     // sum over sub (lane bits 2..5): the four subs of a row by DPP (rotations
-    // by 8 and 4 keep c), the four rows by shuffles
+    // by 8 and 4 keep c), the four rows by permlane swaps
     acc.x += dpp<0x128>(acc.x); acc.y += dpp<0x128>(acc.y); acc.z += dpp<0x128>(acc.z); acc.w += dpp<0x128>(acc.w);
     den += dpp<0x128>(den);
     acc.x += dpp<0x124>(acc.x); acc.y += dpp<0x124>(acc.y); acc.z += dpp<0x124>(acc.z); acc.w += dpp<0x124>(acc.w);
     den += dpp<0x124>(den);
-#pragma unroll
-    for (int off = 16; off < 64; off <<= 1) {
-        acc.x += __shfl_xor(acc.x, off);
-        acc.y += __shfl_xor(acc.y, off);
-        acc.z += __shfl_xor(acc.z, off);
-        acc.w += __shfl_xor(acc.w, off);
-        den += __shfl_xor(den, off);
-    }
+    acc.x = sum4rows(acc.x);
+    acc.y = sum4rows(acc.y);
+    acc.z = sum4rows(acc.z);
+    acc.w = sum4rows(acc.w);
+    den = sum4rows(den);
     if (sub == 0) {
         const float inv = 1.f / den;
         st4(a.out + (size_t)h * HD + chunk * 16 + c * 4,
@@ -777,8 +767,11 @@ __global__ void synth_kernel(SynthArgs a, uint64_t key, uint64_t okey) {
 template <int HD, int NR>
 hipError_t launch_decode_nr(const DecodeArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((decode_split_kernel<HD, NR>), dim3(a.n_split, a.n_head_kv), dim3(kThreads), 0, s, a);
-    if (a.n_split > 1)
-        hipLaunchKernelGGL(decode_combine_kernel<HD>, dim3(a.n_head_kv * a.n_rep, HD / 16), dim3(64), 0, s, a);
+    static_assert(kMaxDecodeSplits <= 16 * 8, "the combine takes at most 8 splits per lane");
+    const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 16);
+    if (a.n_split > 64) hipLaunchKernelGGL((decode_combine_kernel<HD, 8>), cgrid, dim3(64), 0, s, a);
+    else if (a.n_split > 32) hipLaunchKernelGGL((decode_combine_kernel<HD, 4>), cgrid, dim3(64), 0, s, a);
+    else if (a.n_split > 1) hipLaunchKernelGGL((decode_combine_kernel<HD, 2>), cgrid, dim3(64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -808,13 +801,20 @@ bool prefill_supported(int head_dim, int n_rep) {
 }
 
 int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu) {
-    // Blocks of kDecodeBlock rows over S = num_cu / n_head_kv splits per
-    // kv-head (at most kMaxDecodeSplits): one workgroup per CU, since the
-    // split kernel's register use leaves room for only one per CU.
+    // S = num_cu / n_head_kv splits per kv-head (one workgroup per CU, since
+    // the split kernel's register use leaves room for only one per CU; at
+    // most kMaxDecodeSplits, and at least kDecodeBlock rows per split) of
+    // ceil(n_rows / S) rows.  A split is processed as whole blocks of
+    // kDecodeBlock rows (MFMA) plus up to kWaves extra rows (VALU, one per
+    // wave), so a row count a little over a multiple of the blocks does not
+    // cost a wave a second block; a larger remainder is rounded up to a
+    // whole block.
     (void)head_dim;
-    const int nb = std::max(1, (n_rows + kDecodeBlock - 1) / kDecodeBlock);
-    const int S = std::max(1, std::min(num_cu / std::max(n_head_kv, 1), kMaxDecodeSplits));
-    return kDecodeBlock * ((nb + S - 1) / S);
+    const int S = std::max(1, std::min({num_cu / std::max(n_head_kv, 1), kMaxDecodeSplits,
+                                        n_rows / kDecodeBlock}));
+    int rps = std::max(1, (n_rows + S - 1) / S);
+    if (rps % kDecodeBlock > kWaves) rps = (rps + kDecodeBlock - 1) / kDecodeBlock * kDecodeBlock;
+    return rps;
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, hipStream_t s) {
