@@ -89,8 +89,9 @@ def _bench_lib():
         raise RuntimeError(f"{path} is not built; run `make -C kore_amd/csrc`")
     L = C.CDLL(path)
     vp, i = C.c_void_p, C.c_int
-    L.kab_decode_run.argtypes = [vp, i, i, i, i, vp, vp, vp, i, vp, i, vp, C.POINTER(C.c_double)]
-    L.kab_prefill_run.argtypes = [vp, i, i, i, i, vp, vp, vp, vp, vp, C.POINTER(C.c_double)]
+    L.kab_decode_run.argtypes = [vp, i, i, i, i, vp, vp, vp, i, vp, i, vp, C.POINTER(C.c_float),
+                                 C.POINTER(C.c_double)]
+    L.kab_prefill_run.argtypes = [vp, i, i, i, i, vp, vp, vp, vp, vp, C.POINTER(C.c_float), C.POINTER(C.c_double)]
     return L
 
 
@@ -126,19 +127,24 @@ def gpu_decode(steps: int, warmup: int):
         synth_dev(dv.at(l * n_in * KVD), n_in, KVD, DEC_SEED, v_stream(l), DEC_POS0, 3, DEC_PER_MILLE, DEC_OUTLIER, st)
     attn.sync()
     out = hip.DeviceBuffer(steps * NL * E)
-    wall = C.c_double(0)
+    wall, wall2, region = C.c_double(0), C.c_double(0), C.c_float(0)
     if warmup:
         _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, warmup, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr,
-                                steps, None, C.byref(wall)), "decode warmup")
-    launch_ms = np.zeros(steps * NL, np.float32)
+                                steps, None, None, C.byref(wall)), "decode warmup")
     print(f"[bench] decode: {steps} timed steps x {NL} layers at positions {DEC_POS0}..", file=sys.stderr,
           flush=True)
+    # the timed steps: host clock and one HIP event pair around the region
     _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
-                            launch_ms.ctypes.data, C.byref(wall)), "decode timed")
+                            None, C.byref(region), C.byref(wall)), "decode timed")
     outs = out.download().reshape(steps, NL, E)
+    # the same steps again with an event pair around every launch (per-launch
+    # spread; re-running a step rewrites the same cache row with the same data)
+    launch_ms = np.zeros(steps * NL, np.float32)
+    _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
+                            launch_ms.ctypes.data, None, C.byref(wall2)), "decode per-launch events")
     info = attn.info()
-    return dict(attn=attn, outs=outs, launch_ms=launch_ms, wall_ms=wall.value, num_cu=info.num_cu,
-                buffers=(dq, dk, dv, out))
+    return dict(attn=attn, outs=outs, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value,
+                num_cu=info.num_cu, buffers=(dq, dk, dv, out))
 
 
 def gpu_prefill(steps: int, warmup: int):
@@ -153,19 +159,20 @@ def gpu_prefill(steps: int, warmup: int):
         synth_dev(dv.at(l * PF_N * KVD), PF_N, KVD, PF_SEED, v_stream(l), 0, 3, 0, 1.0, st)
     attn.sync()
     out = hip.DeviceBuffer(NL * PF_N * E)
-    wall = C.c_double(0)
+    wall, region = C.c_double(0), C.c_float(0)
     if warmup:
-        _check(B.kab_prefill_run(attn.handle, NL, 0, PF_N, warmup, dq.ptr, dk.ptr, dv.ptr, out.ptr, None,
+        _check(B.kab_prefill_run(attn.handle, NL, 0, PF_N, warmup, dq.ptr, dk.ptr, dv.ptr, out.ptr, None, None,
                                  C.byref(wall)), "prefill warmup")
     launch_ms = np.zeros(steps * NL, np.float32)
     print(f"[bench] prefill: {steps} timed passes x {NL} layers of {PF_N} rows", file=sys.stderr, flush=True)
+    # per-launch events cost ~1 us against ~450 us launches: one pass gives both
     _check(B.kab_prefill_run(attn.handle, NL, 0, PF_N, steps, dq.ptr, dk.ptr, dv.ptr, out.ptr,
-                             launch_ms.ctypes.data, C.byref(wall)), "prefill timed")
+                             launch_ms.ctypes.data, C.byref(region), C.byref(wall)), "prefill timed")
     outs = out.download(2 * PF_N * E).reshape(2, PF_N, E)   # layers 0 and 1 for the parity check
     attn.close()
     for b in (dq, dk, dv, out):
         b.free()
-    return dict(outs=outs, launch_ms=launch_ms, wall_ms=wall.value)
+    return dict(outs=outs, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value)
 
 
 def _decode_bytes_geom(L: int, nh: int, nkv: int, hd: int) -> int:
@@ -205,19 +212,21 @@ def _decode_leg(attn, n_layer, pos_first, pos_step, steps, warmup, nh, nkv, hd, 
         synth_dev(dv.at(l * n_in * kvd), n_in, kvd, seed, v_stream(l), pos_first, 3, 0, 1.0, st)
     attn.sync()
     out = hip.DeviceBuffer(n_layer * E_)
-    wall = C.c_double(0)
+    wall, wall2, region = C.c_double(0), C.c_double(0), C.c_float(0)
     if warmup:
         _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, warmup, dq.ptr, dk.ptr, dv.ptr, n_in,
-                                out.ptr, 1, None, C.byref(wall)), "decode warmup")
+                                out.ptr, 1, None, None, C.byref(wall)), "decode warmup")
+    _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, steps, dq.ptr, dk.ptr, dv.ptr, n_in,
+                            out.ptr, 1, None, C.byref(region), C.byref(wall)), "decode timed")
     lm = np.zeros(steps * n_layer, np.float32)
     _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, steps, dq.ptr, dk.ptr, dv.ptr, n_in,
-                            out.ptr, 1, lm.ctypes.data, C.byref(wall)), "decode timed")
+                            out.ptr, 1, lm.ctypes.data, None, C.byref(wall2)), "decode per-launch events")
     for b in (dq, dk, dv, out):
         b.free()
     nbytes = sum(_decode_bytes_geom(attended(s), nh, nkv, hd) for s in range(steps)) * n_layer
-    mean_s = float(lm.astype(np.float64).mean()) / 1e3
+    mean_s = region.value / 1e3 / (steps * n_layer)
     ach = nbytes / (steps * n_layer) / mean_s / 1e9
-    return {"us_per_layer_kernel": round(mean_s * 1e6, 3), "launch_us_median": round(float(np.median(lm)) * 1e3, 3),
+    return {"us_per_layer_gpu": round(mean_s * 1e6, 3), "launch_us_median": round(float(np.median(lm)) * 1e3, 3),
             "gbs_wall": round(nbytes / (wall.value / 1e3) / 1e9, 2),
             "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4)}}
@@ -258,18 +267,19 @@ def gpu_other_workloads(quick: bool):
             synth_dev(dv.at(l * cn * kvd), cn, kvd, 5, v_stream(l), c0, 3, 0, 1.0, st)
         a.sync()
         out = hip.DeviceBuffer(nl * cn * E_)
-        wall = C.c_double(0)
-        _check(B.kab_prefill_run(a.handle, nl, c0, cn, 1, dq.ptr, dk.ptr, dv.ptr, out.ptr, None, C.byref(wall)),
-               "chunk warmup")
+        wall, region = C.c_double(0), C.c_float(0)
+        _check(B.kab_prefill_run(a.handle, nl, c0, cn, 1, dq.ptr, dk.ptr, dv.ptr, out.ptr, None, None,
+                                 C.byref(wall)), "chunk warmup")
         P = 2
         lm = np.zeros(P * nl, np.float32)
         _check(B.kab_prefill_run(a.handle, nl, c0, cn, P, dq.ptr, dk.ptr, dv.ptr, out.ptr, lm.ctypes.data,
-                                 C.byref(wall)), "chunk timed")
+                                 C.byref(region), C.byref(wall)), "chunk timed")
         for b in (dq, dk, dv, out):
             b.free()
         F = _prefill_flops_geom(c0, cn, nh, hd)
-        ach = F / (float(lm.astype(np.float64).mean()) / 1e3) / 1e12
-        chunk = {"us_per_layer_kernel": round(float(lm.mean()) * 1e3, 2), "flop_per_layer": F,
+        per_s = region.value / 1e3 / (P * nl)
+        ach = F / per_s / 1e12
+        chunk = {"us_per_layer_gpu": round(per_s * 1e6, 2), "flop_per_layer": F,
                  "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
                               "unit": "TFLOP/s", "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4)}}
         dec = _decode_leg(a, nl, W, 1, 256, 0, nh, nkv, hd, 5, lambda s: W)
@@ -410,7 +420,9 @@ def main(argv=None):
     wall_s = dec["wall_ms"] / 1e3
     value = total_bytes / wall_s / 1e9
     lm = dec["launch_ms"].astype(np.float64)
-    mean_launch_s = float(lm.mean()) / 1e3
+    # GPU time per launch: the HIP event pair around the timed region over the
+    # K * NL launches (split + combine kernel of every layer, gaps included)
+    mean_launch_s = dec["region_ms"] / 1e3 / (K * NL)
     bytes_per_launch = total_bytes / (K * NL)
     achieved = bytes_per_launch / mean_launch_s / 1e9
     res = {
@@ -434,9 +446,9 @@ def main(argv=None):
             "pos_first": DEC_POS0, "rope_base": ROPE_BASE,
         },
         "decode": {
-            "us_per_layer_kernel": round(float(lm.mean()) * 1e3, 3),
+            "us_per_layer_gpu": round(mean_launch_s * 1e6, 3),
             "us_per_layer_wall": round(dec["wall_ms"] / (K * NL) * 1e3, 3),
-            "launch_us": {k: round(v * 1e3, 3) for k, v in _stats(lm).items()},
+            "launch_us_events": {k: round(v * 1e3, 3) for k, v in _stats(lm).items()},
             "bytes_per_launch_mean": int(bytes_per_launch),
         },
         "roofline": {
@@ -453,13 +465,14 @@ def main(argv=None):
         P = args.prefill_steps
         plm = pf["launch_ms"].astype(np.float64)
         F = prefill_flops(0, PF_N)
-        p_ach = F / (float(plm.mean()) / 1e3) / 1e12
+        p_per_s = pf["region_ms"] / 1e3 / (P * NL)
+        p_ach = F / p_per_s / 1e12
         res["prefill"] = {
             "workload": f"Qwen2.5-7B-shape causal prefill attention, {PF_N} rows at position 0, 28 layers, "
                         "inputs N(0,1)",
             "tflops": round(F * NL * P / (pf["wall_ms"] / 1e3) / 1e12, 3),
-            "us_per_layer_kernel": round(float(plm.mean()) * 1e3, 2),
-            "launch_us": {k: round(v * 1e3, 2) for k, v in _stats(plm).items()},
+            "us_per_layer_gpu": round(p_per_s * 1e6, 2),
+            "launch_us_events": {k: round(v * 1e3, 2) for k, v in _stats(plm).items()},
             "flop_per_layer": F,
             "steps": P,
             "roofline": {"bound": "mfma", "achieved": round(p_ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,

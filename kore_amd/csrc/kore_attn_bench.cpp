@@ -9,9 +9,12 @@
 //
 // Timing: std::chrono::steady_clock around the whole region (kore times
 // with steady_clock, kore.cpp:1886-1889), bracketed by a stream
-// synchronisation on both sides; when `launch_ms` is given, a pair of HIP
-// events on the same stream brackets each launch and its elapsed time is
-// returned per launch.
+// synchronisation on both sides; when `region_ms` is given, a pair of HIP
+// events on the same stream brackets the whole region (GPU time of all its
+// launches, gaps between them included); when `launch_ms` is given, a pair
+// of HIP events brackets each launch and its elapsed time is returned per
+// launch (the events themselves add to the region's time, so a pass that
+// measures the region should not ask for them).
 #include "kore_attn.h"
 
 #include <hip/hip_runtime.h>
@@ -37,22 +40,25 @@ struct Events {
     }
 };
 
-// Runs `body(i)` for i < n launches on `stream`, timing the region and (when
-// launch_ms is non-null) each launch.
+// Runs `body(i)` for i < n launches on `stream`, timing the region and
+// (when launch_ms is non-null) each launch.
 template <class Body>
-int timed_region(hipStream_t stream, int n, float *launch_ms, double *wall_ms, Body body) {
-    Events evs(launch_ms ? 2 * (size_t)n : 0);
-    if (launch_ms && !evs.create()) return KORE_ATTN_E_HIP;
+int timed_region(hipStream_t stream, int n, float *launch_ms, float *region_ms, double *wall_ms, Body body) {
+    Events evs(launch_ms ? 2 * (size_t)n : 0), reg(region_ms ? 2 : 0);
+    if ((launch_ms && !evs.create()) || (region_ms && !reg.create())) return KORE_ATTN_E_HIP;
     if (hipStreamSynchronize(stream) != hipSuccess) return KORE_ATTN_E_HIP;
     const auto t0 = std::chrono::steady_clock::now();
+    if (region_ms && hipEventRecord(reg.ev[0], stream) != hipSuccess) return KORE_ATTN_E_HIP;
     for (int i = 0; i < n; ++i) {
         if (launch_ms && hipEventRecord(evs.ev[2 * i], stream) != hipSuccess) return KORE_ATTN_E_HIP;
         if (int rc = body(i)) return rc;
         if (launch_ms && hipEventRecord(evs.ev[2 * i + 1], stream) != hipSuccess) return KORE_ATTN_E_HIP;
     }
+    if (region_ms && hipEventRecord(reg.ev[1], stream) != hipSuccess) return KORE_ATTN_E_HIP;
     if (hipStreamSynchronize(stream) != hipSuccess) return KORE_ATTN_E_HIP;
     const auto t1 = std::chrono::steady_clock::now();
     if (wall_ms) *wall_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (region_ms && hipEventElapsedTime(region_ms, reg.ev[0], reg.ev[1]) != hipSuccess) return KORE_ATTN_E_HIP;
     if (launch_ms)
         for (int i = 0; i < n; ++i)
             if (hipEventElapsedTime(&launch_ms[i], evs.ev[2 * i], evs.ev[2 * i + 1]) != hipSuccess)
@@ -67,10 +73,11 @@ int timed_region(hipStream_t stream, int n, float *launch_ms, double *wall_ms, B
 // layers 0..n_layer-1 (layer inner, like forward()).  Device inputs are laid
 // out [layer][in_steps][dim] (step s of layer l at (l*in_steps + s)*dim);
 // outputs [out_steps][layer][n_head*head_dim] with step s written to row
-// s % out_steps.  launch_ms (optional) receives n_steps*n_layer durations.
+// s % out_steps.  launch_ms (optional) receives n_steps*n_layer durations,
+// region_ms (optional) the GPU time of the whole region.
 KAB_API int kab_decode_run(kore_attn_t h, int n_layer, int pos_first, int pos_step, int n_steps,
                            const float *q, const float *k, const float *v, int in_steps, float *out,
-                           int out_steps, float *launch_ms, double *wall_ms) {
+                           int out_steps, float *launch_ms, float *region_ms, double *wall_ms) {
     kore_attn_info inf;
     if (int rc = kore_attn_get_info(h, &inf)) return rc;
     if (n_layer <= 0 || n_layer > inf.n_layer || n_steps <= 0 || out_steps <= 0 || pos_step < 0 ||
@@ -78,7 +85,7 @@ KAB_API int kab_decode_run(kore_attn_t h, int n_layer, int pos_first, int pos_st
         return KORE_ATTN_E_INVALID;
     const size_t E = (size_t)inf.n_head * inf.head_dim, kvd = (size_t)inf.n_head_kv * inf.head_dim;
     hipStream_t stream = (hipStream_t)inf.stream;
-    return timed_region(stream, n_steps * n_layer, launch_ms, wall_ms, [&](int i) {
+    return timed_region(stream, n_steps * n_layer, launch_ms, region_ms, wall_ms, [&](int i) {
         const int s = i / n_layer, l = i % n_layer;
         const size_t row = (size_t)l * in_steps + (pos_step ? s : 0);
         return kore_attn_decode_dev(h, l, pos_first + s * pos_step, inf.n_head, inf.n_head_kv, inf.head_dim,
@@ -92,13 +99,13 @@ KAB_API int kab_decode_run(kore_attn_t h, int n_layer, int pos_first, int pos_st
 // outputs [layer][n_tok][n_head*head_dim].
 KAB_API int kab_prefill_run(kore_attn_t h, int n_layer, int pos0, int n_tok, int n_steps,
                             const float *q, const float *k, const float *v, float *out,
-                            float *launch_ms, double *wall_ms) {
+                            float *launch_ms, float *region_ms, double *wall_ms) {
     kore_attn_info inf;
     if (int rc = kore_attn_get_info(h, &inf)) return rc;
     if (n_layer <= 0 || n_layer > inf.n_layer || n_steps <= 0 || n_tok <= 0) return KORE_ATTN_E_INVALID;
     const size_t E = (size_t)inf.n_head * inf.head_dim, kvd = (size_t)inf.n_head_kv * inf.head_dim;
     hipStream_t stream = (hipStream_t)inf.stream;
-    return timed_region(stream, n_steps * n_layer, launch_ms, wall_ms, [&](int i) {
+    return timed_region(stream, n_steps * n_layer, launch_ms, region_ms, wall_ms, [&](int i) {
         const int l = i % n_layer;
         const size_t row = (size_t)l * n_tok;
         return kore_attn_prefill_dev(h, l, pos0, n_tok, inf.n_head, inf.n_head_kv, inf.head_dim,
