@@ -179,6 +179,64 @@ def test_decode_3b_long_context():
     _close(out, oracle.attn_decode(qr, K, V, n0, nh, nkv, hd), "3b decode pos 32767")
 
 
+@pytest.mark.parametrize("nh,nkv,hd,n0", [(40, 8, 128, 2600), (40, 8, 128, 2700), (20, 4, 64, 5200)])
+def test_decode_extra_rows_and_multiblock_waves(nh, nkv, hd, n0):
+    """Row counts where a split has more 16-row blocks than waves (a wave
+    prefetches its second block) with and without extra rows past the last
+    block, on 256 CUs: kv-heads 8 give 32 splits (2600 rows -> 82-row splits
+    = 5 blocks + 2 extra rows, 2700 -> 96 = 6 blocks); kv-heads 4 give 64
+    (5200 -> 82 = 5 blocks + 2 extra rows)."""
+    _say(f"decode extra rows / multi-block {nh}/{nkv}/{hd} at {n0}")
+    seed = 13
+    q0 = oracle.synth(n0, nh * hd, seed, 1 << 32)
+    k0 = oracle.synth(n0, nkv * hd, seed, 2 << 32)
+    v0 = oracle.synth(n0, nkv * hd, seed, 3 << 32)
+    inv_f = oracle.inv_freq(hd, 1e6)
+    ctx = n0 + 4
+    K = np.zeros((ctx, nkv * hd), np.float32)
+    V = np.zeros((ctx, nkv * hd), np.float32)
+    K[:n0] = oracle.rope_rows(k0, np.arange(n0), nkv, hd, inv_f)
+    V[:n0] = v0
+    with _attn(1, ctx, nh, nkv, hd, 1e6) as attn:
+        attn.prefill(0, 0, q0, k0, v0)
+        for pos in range(n0, n0 + 3):
+            q = oracle.synth(1, nh * hd, seed, 1 << 32, row0=pos)[0]
+            k = oracle.synth(1, nkv * hd, seed, 2 << 32, row0=pos)[0]
+            v = oracle.synth(1, nkv * hd, seed, 3 << 32, row0=pos)[0]
+            out = attn.decode(0, pos, q, k, v)
+            K[pos] = oracle.rope_rows(k[None], [pos], nkv, hd, inv_f)[0]
+            V[pos] = v
+            qr = oracle.rope_rows(q[None], [pos], nh, hd, inv_f)[0]
+            _close(out, oracle.attn_decode(qr, K, V, pos, nh, nkv, hd), f"pos {pos}")
+        kg, vg = attn.read_kv(0, 0, n0 + 3)
+    np.testing.assert_array_equal(kg, K[:n0 + 3])
+    np.testing.assert_array_equal(vg, V[:n0 + 3])
+
+
+@pytest.mark.parametrize("nh,nkv,hd,W", [(12, 2, 128, 260), (14, 2, 64, 130)])
+def test_window_decode_stale_slot_on_extra_row(nh, nkv, hd, W):
+    """Wrapped ring whose splits end in an extra row (W = 260: 16 splits of
+    17 rows; W = 130: 8 of 17): over a full turn of the ring the stale copy of
+    the new slot falls on every slot, extra rows included, and is masked."""
+    _say(f"window {W} stale slot on extra rows {nh}/{nkv}/{hd}")
+    kv = oracle.KV(1, W, nh, nkv, hd, 1e6, window=W)
+    rng = np.random.default_rng(W + hd)
+    with _attn(1, W, nh, nkv, hd, 1e6, window=W) as attn:
+        q = rng.standard_normal((W, nh * hd)).astype(np.float32)
+        k = rng.standard_normal((W, nkv * hd)).astype(np.float32)
+        v = rng.standard_normal((W, nkv * hd)).astype(np.float32)
+        _close(attn.prefill(0, 0, q, k, v), kv.prefill(0, 0, q, k, v), "window prefill")
+        for p in range(W, 2 * W + 3):
+            q = rng.standard_normal(nh * hd).astype(np.float32)
+            k = rng.standard_normal(nkv * hd).astype(np.float32)
+            v = rng.standard_normal(nkv * hd).astype(np.float32)
+            _close(attn.decode(0, p, q, k, v), kv.decode(0, p, q, k, v), f"window pos {p}")
+        kg, vg = attn.read_kv(0, W + 3, W)
+    slots = np.arange(W + 3, 2 * W + 3) % W
+    np.testing.assert_array_equal(kg, kv.kcache()[0, slots])
+    np.testing.assert_array_equal(vg, kv.vcache()[0, slots])
+
+
 def test_decode_deterministic():
     nh, nkv, hd, ctx = 28, 4, 128, 2048
     _say("decode determinism")
