@@ -162,7 +162,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
 
-    __shared__ __align__(16) float s_o[kWaves * NR * HD];   // unnormalised wave outputs
+    constexpr int OST = HD + 4;    // LDS stride of a head's output (bank spread)
+    __shared__ __align__(16) float s_o[kWaves * NR * OST];  // unnormalised wave outputs
     __shared__ __align__(16) float s_knew[HD];              // the new row: roped k
     __shared__ __align__(16) float s_vnew[HD];              // ... and v
     __shared__ __align__(16) float s_kx[kWaves * HD];       // the extra rows: k
@@ -250,6 +251,40 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
     if (wave + kWaves < n_blk) load_blk(kB, vB, wave + kWaves);
 
+    // ---- the new row (owner workgroup, wave 0, while its K/V loads are in
+    // flight): RoPE, append, and its score for every head (state 2 kWaves:
+    // score, sum 1, output v)
+    if (is_owner && wave == 0) {
+        float y0, y1;
+        rope_pair(nk0, nk1, ncs, y0, y1);
+        if (lane < HALF) {
+            float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
+            float *vd = a.vc + head_base + (size_t)a.new_slot * HD;
+            kd[lane] = y0;
+            kd[lane + HALF] = y1;
+            vd[lane] = nv0;
+            vd[lane + HALF] = nv1;
+            s_knew[lane] = y0;
+            s_knew[lane + HALF] = y1;
+            s_vnew[lane] = nv0;
+            s_vnew[lane + HALF] = nv1;
+        }
+        __builtin_amdgcn_wave_barrier();
+        float sn = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 kn = ld4(&s_knew[16 * t + 4 * kq]);
+            sn = fmaf(qb[t][0], kn.x, sn);
+            sn = fmaf(qb[t][1], kn.y, sn);
+            sn = fmaf(qb[t][2], kn.z, sn);
+            sn = fmaf(qb[t][3], kn.w, sn);
+        }
+        sn = sum4rows(sn);
+        if (kq == 0 && m16 < NR) {
+            s_m[2 * kWaves * 8 + m16] = sn;
+            s_l[2 * kWaves * 8 + m16] = 1.f;
+        }
+    }
     floatx4 o[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -332,44 +367,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                st4(&s_o[(wave * NR + m16) * HD + 64 * j + 16 * kq + 4 * v],
+                st4(&s_o[(wave * NR + m16) * OST + 64 * j + 16 * kq + 4 * v],
                     make_float4(o[4 * j][v], o[4 * j + 1][v], o[4 * j + 2][v], o[4 * j + 3][v]));
         if (kq == 0) {
             s_m[wave * 8 + m16] = m_run;
             s_l[wave * 8 + m16] = l_w;
-        }
-    }
-    // ---- the new row (owner workgroup, wave 0): RoPE, append, and its score
-    // for every head (state 2 kWaves: score, sum 1, output v)
-    if (is_owner && wave == 0) {
-        float y0, y1;
-        rope_pair(nk0, nk1, ncs, y0, y1);
-        if (lane < HALF) {
-            float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
-            float *vd = a.vc + head_base + (size_t)a.new_slot * HD;
-            kd[lane] = y0;
-            kd[lane + HALF] = y1;
-            vd[lane] = nv0;
-            vd[lane + HALF] = nv1;
-            s_knew[lane] = y0;
-            s_knew[lane + HALF] = y1;
-            s_vnew[lane] = nv0;
-            s_vnew[lane + HALF] = nv1;
-        }
-        __builtin_amdgcn_wave_barrier();
-        float sn = 0.f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float4 kn = ld4(&s_knew[16 * t + 4 * kq]);
-            sn = fmaf(qb[t][0], kn.x, sn);
-            sn = fmaf(qb[t][1], kn.y, sn);
-            sn = fmaf(qb[t][2], kn.z, sn);
-            sn = fmaf(qb[t][3], kn.w, sn);
-        }
-        sn = sum4rows(sn);
-        if (kq == 0 && m16 < NR) {
-            s_m[2 * kWaves * 8 + m16] = sn;
-            s_l[2 * kWaves * 8 + m16] = 1.f;
         }
     }
     __syncthreads();
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
         for (int w = 0; w < kWaves; ++w) {
             mw[w] = s_m[w * 8 + h];
             lw[w] = s_l[w * 8 + h];
-            xw[w] = ld4(&s_o[(w * NR + h) * HD + 4 * d4]);
+            xw[w] = ld4(&s_o[(w * NR + h) * OST + 4 * d4]);
         }
         float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
         float l = 0.f;
