@@ -429,23 +429,24 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     }
 }
 
-// Block (q-head h, 16-dim chunk): out[h][chunk] = sum_s w_s o_s / sum_s w_s l_s
+// Block (q-head h, 32-dim chunk): out[h][chunk] = sum_s w_s o_s / sum_s w_s l_s
 // with w_s = 2^(m_s - max_s m_s) (split maxima are in the log2 domain), the
-// log-sum-exp merge of the splits.  Lane (sub, c) takes splits sub + 16 i
-// (i < PER, so n_split <= 16 PER) and float4 c of the chunk; every load is
-// issued before the first use (one memory round trip).
+// log-sum-exp merge of the splits.  Lane (sub, c) takes splits sub + 8 i
+// (i < PER, so n_split <= 8 PER) and float4 c of the chunk, so a split's
+// chunk is one whole 128-byte line; every load is issued before the first
+// use (one memory round trip).
 template <int HD, int PER>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
     const int h = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
     const int S = a.n_split;
-    const int sub = lane >> 2, c = lane & 3;
+    const int sub = lane >> 3, c = lane & 7;
     const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + (size_t)h * S;
-    const float *po = a.part_o + (size_t)h * S * HD + chunk * 16 + c * 4;
+    const float *po = a.part_o + (size_t)h * S * HD + chunk * 32 + c * 4;
     float4 x[PER];
     float2 st[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int s = min(sub + 16 * i, S - 1);
+        const int s = min(sub + 8 * i, S - 1);
         x[i] = ld4(po + (size_t)s * HD);
         st[i] = ml[s];
     }
@@ -458,19 +459,17 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
     float den = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const float w = (sub + 16 * i < S && st[i].x != -INFINITY) ? fast_exp2(st[i].x - m) : 0.f;
+        const float w = (sub + 8 * i < S && st[i].x != -INFINITY) ? fast_exp2(st[i].x - m) : 0.f;
         den = fmaf(w, st[i].y, den);
         acc.x = fmaf(w, x[i].x, acc.x);
         acc.y = fmaf(w, x[i].y, acc.y);
         acc.z = fmaf(w, x[i].z, acc.z);
         acc.w = fmaf(w, x[i].w, acc.w);
     }
-    // sum over sub (lane bits 2..5): the four subs of a row by DPP (rotations
-    // by 8 and 4 keep c), the four rows by permlane swaps
+    // sum over sub (lane bits 3..5): the two subs of a row by DPP (rotation
+    // by 8 keeps c), the four rows by permlane swaps
     acc.x += dpp<0x128>(acc.x); acc.y += dpp<0x128>(acc.y); acc.z += dpp<0x128>(acc.z); acc.w += dpp<0x128>(acc.w);
     den += dpp<0x128>(den);
-    acc.x += dpp<0x124>(acc.x); acc.y += dpp<0x124>(acc.y); acc.z += dpp<0x124>(acc.z); acc.w += dpp<0x124>(acc.w);
-    den += dpp<0x124>(den);
     acc.x = sum4rows(acc.x);
     acc.y = sum4rows(acc.y);
     acc.z = sum4rows(acc.z);
@@ -478,7 +477,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
     den = sum4rows(den);
     if (sub == 0) {
         const float inv = 1.f / den;
-        st4(a.out + (size_t)h * HD + chunk * 16 + c * 4,
+        st4(a.out + (size_t)h * HD + chunk * 32 + c * 4,
             make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
     }
 }
@@ -769,10 +768,11 @@ __global__ void synth_kernel(SynthArgs a, uint64_t key, uint64_t okey) {
 template <int HD, int NR>
 hipError_t launch_decode_nr(const DecodeArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((decode_split_kernel<HD, NR>), dim3(a.n_split, a.n_head_kv), dim3(kThreads), 0, s, a);
-    static_assert(kMaxDecodeSplits <= 16 * 8, "the combine takes at most 8 splits per lane");
-    const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 16);
-    if (a.n_split > 64) hipLaunchKernelGGL((decode_combine_kernel<HD, 8>), cgrid, dim3(64), 0, s, a);
-    else if (a.n_split > 32) hipLaunchKernelGGL((decode_combine_kernel<HD, 4>), cgrid, dim3(64), 0, s, a);
+    static_assert(kMaxDecodeSplits <= 8 * 16, "the combine takes at most 16 splits per lane");
+    const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 32);
+    if (a.n_split > 64) hipLaunchKernelGGL((decode_combine_kernel<HD, 16>), cgrid, dim3(64), 0, s, a);
+    else if (a.n_split > 32) hipLaunchKernelGGL((decode_combine_kernel<HD, 8>), cgrid, dim3(64), 0, s, a);
+    else if (a.n_split > 16) hipLaunchKernelGGL((decode_combine_kernel<HD, 4>), cgrid, dim3(64), 0, s, a);
     else if (a.n_split > 1) hipLaunchKernelGGL((decode_combine_kernel<HD, 2>), cgrid, dim3(64), 0, s, a);
     return hipGetLastError();
 }
