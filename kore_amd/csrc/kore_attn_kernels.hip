@@ -558,7 +558,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     const int qrow_c = min(qrow, a.n_tok - 1);
     const int qpos = a.pos0 + qrow_c;
 
-    // Q^T operand: qreg[4j+e] = roped q[qrow][8j + 4qg + e]
+    // Q^T operand: qreg[4j+e] = roped q[qrow][8j + 4qg + e] * 1/sqrt(hd) * log2(e)
     float qreg[HD / 2];
     {
         const float *qp = a.q + ((size_t)qrow_c * n_head + h) * HD;
@@ -572,8 +572,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
             for (int e2 = 0; e2 < 4; ++e2) {
                 float y0, y1;
                 rope_pair(comp(lo, e2), comp(hi, e2), cs[d + e2], y0, y1);
-                qreg[4 * j + e2] = y0;
-                qreg[4 * (j + HD / 16) + e2] = y1;
+                qreg[4 * j + e2] = y0 * a.scale_log2;
+                qreg[4 * (j + HD / 16) + e2] = y1 * a.scale_log2;
             }
         }
     }
@@ -585,27 +585,55 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    const int t_begin = seg * a.seg_tiles;
-    const int t_end = a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles);
-    for (int t = t_begin; t < t_end; ++t) {
-        const int k0 = t * BK;
-        __syncthreads();
-        for (int idx = tid; idx < BK * HD / 4; idx += kThreads) {
-            const int key = idx / (HD / 4), c4 = idx - key * (HD / 4);
-            const int kp = k0 + key;
-            float4 kv = zero4(), vv = zero4();
-            if (kp < n_keys) {
-                const size_t off = ((size_t)g * a.slots + kp) * HD + c4 * 4;
-                kv = ld4(a.kc + off);
-                vv = ld4(a.vc + off);
-            }
+    // K/V tiles go global -> registers -> LDS; the next tile's loads are
+    // issued before the current tile's arithmetic, so their latency hides
+    // behind it.  Every load is in bounds (keys past the cache end are
+    // clamped to its last row and zeroed; the causal mask excludes them).
+    // Copy i of wave w covers keys 16 kb + (lane % 16) and float4 columns
+    // 4 cb + lane / 16 with (kb, cb) from w * NLD + i: the transposed V
+    // stores of a wave then touch 64 different banks ((4 c4 + e) * VSTR + key
+    // = lane + const mod 64), and each global load reads 16 rows x 64 bytes.
+    constexpr int NLD = BK * HD / 4 / kThreads;   // float4 per thread per tensor
+    static_assert(BK == 32 && 4 * NLD == 2 * (HD / 16), "two 16-key halves x hd/16 column blocks");
+    float4 kpre[NLD], vpre[NLD];
+    auto tile_slot = [&](int i, int &key, int &c4) {
+        const int combo = wave * NLD + i;
+        key = 16 * (combo & 1) + (lane & 15);
+        c4 = 4 * (combo >> 1) + (lane >> 4);
+    };
+    auto load_tile = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            int key, c4;
+            tile_slot(i, key, c4);
+            const size_t off = ((size_t)g * a.slots + min(t * BK + key, n_keys - 1)) * HD + c4 * 4;
+            kpre[i] = ld4(a.kc + off);
+            vpre[i] = ld4(a.vc + off);
+        }
+    };
+    auto store_tile = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            int key, c4;
+            tile_slot(i, key, c4);
+            const bool in = t * BK + key < n_keys;
+            const float4 kv = in ? kpre[i] : zero4(), vv = in ? vpre[i] : zero4();
             st4(&sK[key * KSTR + c4 * 4], kv);
             sV[(c4 * 4 + 0) * VSTR + key] = vv.x;
             sV[(c4 * 4 + 1) * VSTR + key] = vv.y;
             sV[(c4 * 4 + 2) * VSTR + key] = vv.z;
             sV[(c4 * 4 + 3) * VSTR + key] = vv.w;
         }
+    };
+    const int t_begin = seg * a.seg_tiles;
+    const int t_end = a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles);
+    if (t_begin < t_end) load_tile(t_begin);
+    for (int t = t_begin; t < t_end; ++t) {
+        const int k0 = t * BK;
+        __syncthreads();   // every wave is done with the previous tile
+        store_tile(t);
         __syncthreads();
+        if (t + 1 < t_end) load_tile(t + 1);
         if (k0 > my_kmax) continue;
 
         floatx16 s;
@@ -619,33 +647,50 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
             s = mfma32(a4.z, qreg[4 * j + 2], s);
             s = mfma32(a4.w, qreg[4 * j + 3], s);
         }
-        // s[r] = score(query qi, key k0 + 8(r/4) + 4qg + r%4)
-        float mt = -INFINITY;
+        // s[r] = score(query qi, key k0 + 8(r/4) + 4qg + r%4), already in the
+        // log2 domain; the causal mask only matters on tiles that reach past
+        // the strip's first query position
+        if (k0 + BK - 1 > a.pos0 + 32 * strip) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 8 * (r / 4) + 4 * qg + (r % 4);
-            const float x = key > qpos ? -INFINITY : s[r] * a.scale_log2;
-            s[r] = x;
-            mt = fmaxf(mt, x);
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r / 4) + 4 * qg + (r % 4);
+                if (key > qpos) s[r] = -INFINITY;
+            }
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        float mt = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+        {
+            float lo, hi;
+            pair32(mt, lo, hi);
+            mt = fmaxf(lo, hi);
+        }
         const float m_new = fmaxf(m_run, mt);
         // a segment may start with a tile that is all masked for a row
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2f(m_run - m_use);
+        const float alpha = fast_exp2(m_run - m_use);
         float psum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s[r] = exp2f(s[r] - m_use);
+            s[r] = fast_exp2(s[r] - m_use);
             psum += s[r];
         }
-        psum += __shfl_xor(psum, 32);
+        {
+            float lo, hi;
+            pair32(psum, lo, hi);
+            psum = lo + hi;
+        }
         l_run = fmaf(l_run, alpha, psum);
         m_run = m_new;
+        // rescale only when some query's running max moved
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[tt][r] *= alpha;
+        }
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[tt][r] *= alpha;
 #pragma unroll
             for (int sb = 0; sb < 4; ++sb) {
                 const float4 a4 = ld4(&sV[(32 * tt + qi) * VSTR + 8 * sb + 4 * qg]);
