@@ -215,6 +215,7 @@ int prefill_enqueue(kore_attn *h, int layer, int pos0, int n_tok, const float *q
     pa.n_strips = (n_tok + 31) / 32;
     pa.scale_log2 = (1.0f / std::sqrt((float)h->head_dim)) * 1.4426950408889634f;
     pa.n_kseg = prefill_key_segments(n_tok, pos0, h->n_head_kv, pa.n_rep, h->num_cu, &pa.seg_tiles);
+    pa.fold = h->num_cu;
     if (pa.n_kseg > 1) {
         const size_t entries = (size_t)h->n_head_kv * pa.n_rep * pa.n_strips * pa.n_kseg * 32;
         const size_t need = entries * ((size_t)h->head_dim + 2);

@@ -76,6 +76,10 @@ struct PrefillArgs {
     int seg_tiles;
     float *part_o;        // [n_head_kv * n_rep * n_strips][n_kseg][32][hd]
     float *part_ml;       // [n_head_kv * n_rep * n_strips][n_kseg][32][2]
+    // Workgroups b and b + fold (fold = CU count) usually share a CU: the
+    // grid index is folded so that the second one runs the work list from
+    // its short end (work index grid - 1 - (b - fold) for b >= fold).
+    int fold;
 };
 
 // Counter-based synthetic inputs (identical bits to the CPU oracle's

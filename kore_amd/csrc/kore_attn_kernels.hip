@@ -523,7 +523,9 @@ __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
 // 16-byte LDS reads of 32 different rows fall in different banks.  With key
 // segments (a short chunk over a long cache has too few workgroups to fill the
 // GPU) a workgroup covers one range of key tiles and writes its rows'
-// unnormalised output with their max and sum instead.
+// unnormalised output with their max and sum instead.  The strips' causal
+// work runs from 1 to n_tok / 32 tiles; two workgroups share a CU, and the
+// grid is folded (PrefillArgs::fold) to pair long strips with short ones.
 template <int HD>
 __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int BK = 32;
@@ -536,9 +538,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nkv = a.n_head_kv;
-    const int g = blockIdx.x % nkv;
-    const int seg = (blockIdx.x / nkv) % a.n_kseg;
-    const int item = blockIdx.x / nkv / a.n_kseg;
+    // work index: items run from the longest strips down; the second part
+    // of the grid takes them from the short end, so that the two
+    // workgroups of a CU (b and b + fold) add up to about the same work
+    const int bx = blockIdx.x;
+    const int wi = bx < a.fold ? bx : (int)gridDim.x - 1 - (bx - a.fold);
+    const int g = wi % nkv;
+    const int seg = (wi / nkv) % a.n_kseg;
+    const int item = wi / nkv / a.n_kseg;
     const int total = a.n_rep * a.n_strips;
     const int e = item * 4 + wave;
     const bool active = e < total;
