@@ -188,44 +188,63 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const float *kg = a.kc + head_base;
     const float *vg = a.vc + head_base;
 
-    // ---- loads: q of head m16 at dims 16t + 4kq (+0..3) and their cos/sin,
-    // the new k/v row (pair i, i + hd/2 in lane i), then the first block
-    const int hq = min(m16, NR - 1);
-    const float *qp = a.q + (size_t)(g * a.n_rep + hq) * HD + 4 * kq;
-    const float *csp = reinterpret_cast<const float *>(a.cs) + 8 * kq;
-    float4 qf[NT], csf[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) qf[t] = ld4(qp + 16 * t);
-#pragma unroll
-    for (int t = 0; t < NT / 2; ++t) {
-        csf[2 * t] = ld4(csp + 32 * t);         // (c, s) of dims 16t + 4kq, +1
-        csf[2 * t + 1] = ld4(csp + 32 * t + 4); // ... +2, +3
+    // ---- q of the NR heads of kv-head g, roped once per workgroup and
+    // staged through LDS: thread (h, c) < NR * hd/8 loads the float4 pair
+    // (q[h][4c..4c+3], q[h][hd/2 + 4c..]) and its four (cos, sin) pairs.
+    // The MFMA operand layout repeats every q value in 16/NR lanes and every
+    // (cos, sin) pair in 16, so loading the operands directly costs each
+    // wave 16 KB of vector-memory traffic, as much as its cache rows.
+    constexpr int QS = HD + 4;                 // s_q row stride (bank spread)
+    constexpr int NC = HALF / 4;               // float4 per half row
+    static_assert(NR * NC <= kThreads, "one staging thread per q float4 pair");
+    __shared__ __align__(16) float s_q[NR * QS];   // roped q * 1/sqrt(hd) * log2(e)
+    __shared__ __align__(16) float s_cs[HD];       // (cos, sin) of dims 0 .. hd/2 - 1
+    const int sh = min(tid / NC, NR - 1), sc = tid % NC;
+    float4 sx0, sx1, scs01, scs23;
+    {
+        const float *qh = a.q + (size_t)(g * a.n_rep + sh) * HD + 4 * sc;
+        const float *csr = reinterpret_cast<const float *>(a.cs) + 8 * sc;
+        sx0 = ld4(qh);
+        sx1 = ld4(qh + HALF);
+        scs01 = ld4(csr);
+        scs23 = ld4(csr + 4);
     }
+    // the new k/v row: pair (i, i + hd/2) in lane i
     const int ni = min(lane, HALF - 1);
     const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
     const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
-    const float2 ncs = a.cs[ni];
-    // q is roped before any K/V load is issued.  Once every CU streams its
-    // K/V rows, a q load that misses the caches waits behind them in the
-    // memory controllers and arrives with the bulk of the data (measured
-    // ~3.5 us into the kernel instead of ~1 us), and the score MFMAs need q.
-    // ---- RoPE of q into the B operand, pre-scaled by 1/sqrt(hd) * log2(e)
+
+    // RoPE of the staged pairs into LDS, then the B operand: lane (m16, kq)
+    // holds head m16 at dims 16t + 4kq + e (heads past NR are zero columns).
     const float qscale = a.scale * kLog2e;
+    const int hq = min(m16, NR - 1);
     float qb[NT][4];
+    auto stage_q = [&]() {
+        if (tid < NR * NC) {
+            float y0[4], y1[4];
 #pragma unroll
-    for (int t = 0; t < NT / 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float4 c4 = csf[2 * t + e / 2];
-            const float2 cs = (e & 1) ? make_float2(c4.z, c4.w) : make_float2(c4.x, c4.y);
-            float y0, y1;
-            rope_pair(comp(qf[t], e), comp(qf[t + NT / 2], e), cs, y0, y1);
-            qb[t][e] = m16 < NR ? y0 * qscale : 0.f;
-            qb[t + NT / 2][e] = m16 < NR ? y1 * qscale : 0.f;
+            for (int e = 0; e < 4; ++e) {
+                const float4 c4 = e < 2 ? scs01 : scs23;
+                const float2 cs = (e & 1) ? make_float2(c4.z, c4.w) : make_float2(c4.x, c4.y);
+                rope_pair(comp(sx0, e), comp(sx1, e), cs, y0[e], y1[e]);
+            }
+            st4(&s_q[sh * QS + 4 * sc], make_float4(y0[0] * qscale, y0[1] * qscale, y0[2] * qscale, y0[3] * qscale));
+            st4(&s_q[sh * QS + HALF + 4 * sc],
+                make_float4(y1[0] * qscale, y1[1] * qscale, y1[2] * qscale, y1[3] * qscale));
+            if (sh == 0) {
+                st4(&s_cs[8 * sc], scs01);
+                st4(&s_cs[8 * sc + 4], scs23);
+            }
         }
-
-    __builtin_amdgcn_sched_barrier(0);   // the K/V loads come after
-
+        __syncthreads();
+        float4 qv[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) qv[t] = ld4(&s_q[hq * QS + 16 * t + 4 * kq]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qb[t][e] = m16 < NR ? comp(qv[t], e) : 0.f;
+    };
     float4 kA[NT], vA[4][NJ], kB[NT], vB[4][NJ];
     auto load_blk = [&](float4 (&kf)[NT], float4 (&vf)[4][NJ], int b) {
         const int rb = r0 + 16 * b;
@@ -250,13 +269,16 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
     const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
     if (wave + kWaves < n_blk) load_blk(kB, vB, wave + kWaves);
+    // q is staged while the cache rows stream in: its loads were issued
+    // first, so they return first, and the rotation runs under the K/V loads.
+    stage_q();
 
     // ---- the new row (owner workgroup, wave 0, while its K/V loads are in
     // flight): RoPE, append, and its score for every head (state 2 kWaves:
     // score, sum 1, output v)
     if (is_owner && wave == 0) {
         float y0, y1;
-        rope_pair(nk0, nk1, ncs, y0, y1);
+        rope_pair(nk0, nk1, make_float2(s_cs[2 * ni], s_cs[2 * ni + 1]), y0, y1);
         if (lane < HALF) {
             float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
             float *vd = a.vc + head_base + (size_t)a.new_slot * HD;
