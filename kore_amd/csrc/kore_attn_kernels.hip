@@ -153,7 +153,10 @@ __device__ __forceinline__ float sum4rows(float x) {
 // are merged in LDS into one partial per q-head, or into `out` when the
 // kv-head has a single split.
 template <int HD, int NR>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__restrict__ q_in, const float2 *cs_in,
+                                                                float *kc_in, float *vc_in, int n_rows,
+                                                                int rows_per_split, int new_slot, int slots,
+                                                                DecodeArgs a) {
     constexpr int NT = HD / 16;    // K float4 per lane per block (MFMA k-steps / 4)
     constexpr int NJ = HD / 64;    // V float4 per lane per row
     constexpr int NMB = HD / 16;   // 16-dim output blocks
@@ -173,8 +176,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m16 = lane & 15, kq = lane >> 4;
     const int split = blockIdx.x, g = blockIdx.y;
-    const int r0 = split * a.rows_per_split;
-    const int r_end = min(r0 + a.rows_per_split, a.n_rows);
+    const int r0 = split * rows_per_split;
+    const int r_end = min(r0 + rows_per_split, n_rows);
     const int n_own = max(r_end - r0, 0);
     // whole blocks, plus a last partial block of more than kWaves rows; a
     // remainder of at most kWaves rows is taken as extra rows, one per wave
@@ -182,11 +185,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const int n_blk = n_own / kDecodeBlock + (rem > kWaves ? 1 : 0);
     const int n_extra = rem > kWaves ? 0 : rem;
     const int last_row = max(r_end - 1, 0);
-    const int owner = a.n_rows == 0 ? 0 : min(a.new_slot, a.n_rows - 1) / a.rows_per_split;
+    const int owner = n_rows == 0 ? 0 : min(new_slot, n_rows - 1) / rows_per_split;
     const bool is_owner = split == owner;
-    const size_t head_base = (size_t)g * a.slots * HD;
-    const float *kg = a.kc + head_base;
-    const float *vg = a.vc + head_base;
+    const size_t head_base = (size_t)g * slots * HD;
+    const float *kg = kc_in + head_base;
+    const float *vg = vc_in + head_base;
 
     // ---- q of the NR heads of kv-head g, roped once per workgroup and
     // staged through LDS: thread (h, c) < NR * hd/8 loads the float4 pair
@@ -202,17 +205,14 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const int sh = min(tid / NC, NR - 1), sc = tid % NC;
     float4 sx0, sx1, scs01, scs23;
     {
-        const float *qh = a.q + (size_t)(g * a.n_rep + sh) * HD + 4 * sc;
-        const float *csr = reinterpret_cast<const float *>(a.cs) + 8 * sc;
+        const float *qh = q_in + (size_t)(g * NR + sh) * HD + 4 * sc;
+        const float *csr = reinterpret_cast<const float *>(cs_in) + 8 * sc;
         sx0 = ld4(qh);
         sx1 = ld4(qh + HALF);
         scs01 = ld4(csr);
         scs23 = ld4(csr + 4);
     }
-    // the new k/v row: pair (i, i + hd/2) in lane i
     const int ni = min(lane, HALF - 1);
-    const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
-    const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
 
     // RoPE of the staged pairs into LDS, then the B operand: lane (m16, kq)
     // holds head m16 at dims 16t + 4kq + e (heads past NR are zero columns).
@@ -269,6 +269,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
     const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
     if (wave + kWaves < n_blk) load_blk(kB, vB, wave + kWaves);
+    // the new k/v row, pair (i, i + hd/2) in lane i (after the cache rows:
+    // its pointers are not among the preloaded kernel arguments)
+    const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
+    const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
     // q is staged while the cache rows stream in: its loads were issued
     // first, so they return first, and the rotation runs under the K/V loads.
     stage_q();
@@ -280,8 +284,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
         float y0, y1;
         rope_pair(nk0, nk1, make_float2(s_cs[2 * ni], s_cs[2 * ni + 1]), y0, y1);
         if (lane < HALF) {
-            float *kd = a.kc + head_base + (size_t)a.new_slot * HD;
-            float *vd = a.vc + head_base + (size_t)a.new_slot * HD;
+            float *kd = kc_in + head_base + (size_t)new_slot * HD;
+            float *vd = vc_in + head_base + (size_t)new_slot * HD;
             kd[lane] = y0;
             kd[lane + HALF] = y1;
             vd[lane] = nv0;
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int row = rb + 4 * kq + v;
-            x[v] = (row < r_end && row != a.new_slot) ? s[v] : -INFINITY;
+            x[v] = (row < r_end && row != new_slot) ? s[v] : -INFINITY;
             mt = fmaxf(mt, x[v]);
         }
         const float m_new = fmaxf(m_run, max4rows(mt));
@@ -377,7 +381,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
         }
         sx = sum4rows(sx);
         if (kq == 0 && m16 < NR) {
-            s_m[(kWaves + wave) * 8 + m16] = xrow == a.new_slot ? -INFINITY : sx;
+            s_m[(kWaves + wave) * 8 + m16] = xrow == new_slot ? -INFINITY : sx;
             s_l[(kWaves + wave) * 8 + m16] = 1.f;
         }
     }
@@ -458,12 +462,13 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
 // chunk is one whole 128-byte line; every load is issued before the first
 // use (one memory round trip).
 template <int HD, int PER>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64) void decode_combine_kernel(const float *part_o, const float *part_ml, float *out,
+                                                            int n_split) {
     const int h = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
-    const int S = a.n_split;
+    const int S = n_split;
     const int sub = lane >> 3, c = lane & 7;
-    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + (size_t)h * S;
-    const float *po = a.part_o + (size_t)h * S * HD + chunk * 32 + c * 4;
+    const float2 *ml = reinterpret_cast<const float2 *>(part_ml) + (size_t)h * S;
+    const float *po = part_o + (size_t)h * S * HD + chunk * 32 + c * 4;
     float4 x[PER];
     float2 st[PER];
 #pragma unroll
@@ -499,7 +504,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
     den = sum4rows(den);
     if (sub == 0) {
         const float inv = 1.f / den;
-        st4(a.out + (size_t)h * HD + chunk * 32 + c * 4,
+        st4(out + (size_t)h * HD + chunk * 32 + c * 4,
             make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
     }
 }
@@ -841,13 +846,18 @@ __global__ void synth_kernel(SynthArgs a, uint64_t key, uint64_t okey) {
 
 template <int HD, int NR>
 hipError_t launch_decode_nr(const DecodeArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((decode_split_kernel<HD, NR>), dim3(a.n_split, a.n_head_kv), dim3(kThreads), 0, s, a);
+    // The leading scalar arguments are preloaded into SGPRs at wave launch
+    // (gfx950 kernel-argument preload), so the first loads do not wait for
+    // a kernel-argument fetch (0.24 us measured).
+    hipLaunchKernelGGL((decode_split_kernel<HD, NR>), dim3(a.n_split, a.n_head_kv), dim3(kThreads), 0, s, a.q,
+                       a.cs, a.kc, a.vc, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a);
     static_assert(kMaxDecodeSplits <= 8 * 16, "the combine takes at most 16 splits per lane");
     const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 32);
-    if (a.n_split > 64) hipLaunchKernelGGL((decode_combine_kernel<HD, 16>), cgrid, dim3(64), 0, s, a);
-    else if (a.n_split > 32) hipLaunchKernelGGL((decode_combine_kernel<HD, 8>), cgrid, dim3(64), 0, s, a);
-    else if (a.n_split > 16) hipLaunchKernelGGL((decode_combine_kernel<HD, 4>), cgrid, dim3(64), 0, s, a);
-    else if (a.n_split > 1) hipLaunchKernelGGL((decode_combine_kernel<HD, 2>), cgrid, dim3(64), 0, s, a);
+    const float *po = a.part_o, *pml = a.part_ml;
+    if (a.n_split > 64) hipLaunchKernelGGL((decode_combine_kernel<HD, 16>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
+    else if (a.n_split > 32) hipLaunchKernelGGL((decode_combine_kernel<HD, 8>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
+    else if (a.n_split > 16) hipLaunchKernelGGL((decode_combine_kernel<HD, 4>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
+    else if (a.n_split > 1) hipLaunchKernelGGL((decode_combine_kernel<HD, 2>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
     return hipGetLastError();
 }
 
