@@ -546,22 +546,30 @@ __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
 // lane owns the scores of one query, runs the online softmax in base 2 on
 // them, and accumulates O^T += V^T P^T (64 MFMAs), whose D layout again gives
 // each lane one query; the softmax statistics need one cross-lane exchange.
-// K tile rows are padded to HD+4 floats and V^T rows to 36 floats so the
-// 16-byte LDS reads of 32 different rows fall in different banks.  With key
-// segments (a short chunk over a long cache has too few workgroups to fill the
-// GPU) a workgroup covers one range of key tiles and writes its rows'
-// unnormalised output with their max and sum instead.  The strips' causal
-// work runs from 1 to n_tok / 32 tiles; two workgroups share a CU, and the
-// grid is folded (PrefillArgs::fold) to pair long strips with short ones.
+// The tiles go from HBM straight into LDS (global_load_lds_dwordx4: lane i of
+// a load writes 16 bytes at the wave's base + 16 i), double-buffered, so tile
+// t + 1 streams in while tile t is computed, with one barrier per tile and no
+// staging registers.  V is kept row-major: output block tt of a wave holds
+// dims NT i + tt (i < 32), so one 16-byte (hd 64: 8-byte) read of a V row
+// feeds all NT blocks; K's float4 columns are XOR-swizzled by (row mod 16)
+// so the 16-byte reads of 16 rows at one column fall in different banks.
+// With key segments (a short chunk over a long cache has too few workgroups
+// to fill the GPU) a workgroup covers one range of key tiles and writes its
+// rows' unnormalised output with their max and sum instead.  The strips'
+// causal work runs from 1 to n_tok / 32 tiles; two workgroups share a CU, and
+// the grid is folded (PrefillArgs::fold) to pair long strips with short ones.
 template <int HD>
 __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int BK = 32;
-    constexpr int KSTR = HD + 4;
-    constexpr int VSTR = BK + 4;
     constexpr int NT = HD / 32;
     constexpr int HALF = HD / 2;
-    __shared__ __align__(16) float sK[BK * KSTR];
-    __shared__ __align__(16) float sV[HD * VSTR];
+    constexpr int C4 = HD / 4;                 // float4 per cache row
+    constexpr int NI = BK * C4 / 64 / kWaves;  // LDS loads per wave per tensor and tile
+    static_assert(NI * 64 * kWaves == BK * C4, "whole 1 KB loads per tile");
+    // one array per buffer: the compiler tracks LDS-direct loads per LDS
+    // object, so reads of one buffer do not wait for loads into the other
+    __shared__ __align__(16) float sK0[BK * HD], sK1[BK * HD];
+    __shared__ __align__(16) float sV0[BK * HD], sV1[BK * HD];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nkv = a.n_head_kv;
@@ -619,63 +627,34 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    // K/V tiles go global -> registers -> LDS; the next tile's loads are
-    // issued before the current tile's arithmetic, so their latency hides
-    // behind it.  Every load is in bounds (keys past the cache end are
-    // clamped to its last row and zeroed; the causal mask excludes them).
-    // Copy i of wave w covers keys 16 kb + (lane % 16) and float4 columns
-    // 4 cb + lane / 16 with (kb, cb) from w * NLD + i: the transposed V
-    // stores of a wave then touch 64 different banks ((4 c4 + e) * VSTR + key
-    // = lane + const mod 64), and each global load reads 16 rows x 64 bytes.
-    constexpr int NLD = BK * HD / 4 / kThreads;   // float4 per thread per tensor
-    static_assert(BK == 32 && 4 * NLD == 2 * (HD / 16), "two 16-key halves x hd/16 column blocks");
-    float4 kpre[NLD], vpre[NLD];
-    auto tile_slot = [&](int i, int &key, int &c4) {
-        const int combo = wave * NLD + i;
-        key = 16 * (combo & 1) + (lane & 15);
-        c4 = 4 * (combo >> 1) + (lane >> 4);
-    };
-    auto load_tile = [&](int t) {
+    // Tile t into (dK, dV): load i of wave w covers float4 slots
+    // p = 64 (NI w + i) + lane, i.e. row p / C4 and position p % C4; V holds
+    // column (p % C4) there, K column (p % C4) ^ (row & 15).  Keys past the
+    // cache end are clamped to its last row (the causal mask excludes them:
+    // every query position is below n_keys).
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    auto issue_tile = [&](float *dK, float *dV, int t) {
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) {
-            int key, c4;
-            tile_slot(i, key, c4);
-            const size_t off = ((size_t)g * a.slots + min(t * BK + key, n_keys - 1)) * HD + c4 * 4;
-            kpre[i] = ld4(a.kc + off);
-            vpre[i] = ld4(a.vc + off);
+        for (int i = 0; i < NI; ++i) {
+            const int chunk = NI * wave_u + i;
+            const int p = 64 * chunk + lane;
+            const int row = p / C4, pos = p % C4;
+            const size_t base = ((size_t)g * a.slots + min(t * BK + row, n_keys - 1)) * HD;
+            __builtin_amdgcn_global_load_lds(a.kc + base + 4 * (pos ^ (row & 15)),
+                                             (void __attribute__((address_space(3))) *)(dK + 256 * chunk), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.vc + base + 4 * pos,
+                                             (void __attribute__((address_space(3))) *)(dV + 256 * chunk), 16, 0, 0);
         }
     };
-    auto store_tile = [&](int t) {
-#pragma unroll
-        for (int i = 0; i < NLD; ++i) {
-            int key, c4;
-            tile_slot(i, key, c4);
-            const bool in = t * BK + key < n_keys;
-            const float4 kv = in ? kpre[i] : zero4(), vv = in ? vpre[i] : zero4();
-            st4(&sK[key * KSTR + c4 * 4], kv);
-            sV[(c4 * 4 + 0) * VSTR + key] = vv.x;
-            sV[(c4 * 4 + 1) * VSTR + key] = vv.y;
-            sV[(c4 * 4 + 2) * VSTR + key] = vv.z;
-            sV[(c4 * 4 + 3) * VSTR + key] = vv.w;
-        }
-    };
-    const int t_begin = seg * a.seg_tiles;
-    const int t_end = a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles);
-    if (t_begin < t_end) load_tile(t_begin);
-    for (int t = t_begin; t < t_end; ++t) {
+    auto compute_tile = [&](const float *sK, const float *sV, int t) {
         const int k0 = t * BK;
-        __syncthreads();   // every wave is done with the previous tile
-        store_tile(t);
-        __syncthreads();
-        if (t + 1 < t_end) load_tile(t + 1);
-        if (k0 > my_kmax) continue;
-
+        if (k0 > my_kmax) return;
         floatx16 s;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
         for (int j = 0; j < HD / 8; ++j) {
-            const float4 a4 = ld4(&sK[qi * KSTR + 8 * j + 4 * qg]);
+            const float4 a4 = ld4(&sK[qi * HD + 4 * ((2 * j + qg) ^ (qi & 15))]);
             s = mfma32(a4.x, qreg[4 * j + 0], s);
             s = mfma32(a4.y, qreg[4 * j + 1], s);
             s = mfma32(a4.z, qreg[4 * j + 2], s);
@@ -723,46 +702,66 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[tt][r] *= alpha;
         }
+        // PV: k-step (sb, e) takes key 8sb + 4qg + e of the tile
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
+        for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
-            for (int sb = 0; sb < 4; ++sb) {
-                const float4 a4 = ld4(&sV[(32 * tt + qi) * VSTR + 8 * sb + 4 * qg]);
-                acc[tt] = mfma32(a4.x, s[4 * sb + 0], acc[tt]);
-                acc[tt] = mfma32(a4.y, s[4 * sb + 1], acc[tt]);
-                acc[tt] = mfma32(a4.z, s[4 * sb + 2], acc[tt]);
-                acc[tt] = mfma32(a4.w, s[4 * sb + 3], acc[tt]);
+            for (int e = 0; e < 4; ++e) {
+                const float *vr = &sV[(8 * sb + 4 * qg + e) * HD + NT * qi];
+                if constexpr (NT == 4) {
+                    const float4 v4 = ld4(vr);
+                    acc[0] = mfma32(v4.x, s[4 * sb + e], acc[0]);
+                    acc[1] = mfma32(v4.y, s[4 * sb + e], acc[1]);
+                    acc[2] = mfma32(v4.z, s[4 * sb + e], acc[2]);
+                    acc[3] = mfma32(v4.w, s[4 * sb + e], acc[3]);
+                } else {
+                    const float2 v2 = *reinterpret_cast<const float2 *>(vr);
+                    acc[0] = mfma32(v2.x, s[4 * sb + e], acc[0]);
+                    acc[1] = mfma32(v2.y, s[4 * sb + e], acc[1]);
+                }
             }
-        }
+    };
+
+    const int t_begin = seg * a.seg_tiles;
+    const int t_end = a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles);
+    if (t_begin < t_end) issue_tile(sK0, sV0, t_begin);
+    for (int t = t_begin; t < t_end; t += 2) {
+        // this wave's loads of tile t have landed; after the barrier every
+        // wave's have, and every wave is done with the other buffer
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 1 < t_end) issue_tile(sK1, sV1, t + 1);
+        compute_tile(sK0, sV0, t);
+        if (t + 1 >= t_end) break;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 2 < t_end) issue_tile(sK0, sV0, t + 2);
+        compute_tile(sK1, sV1, t + 1);
     }
 
+    // output: lane (qi, qg) register r of block tt is dim NT i + tt with
+    // i = 8 (r / 4) + 4 qg + r % 4, so the NT blocks give NT consecutive dims
+    auto store_row = [&](float *dst, float sc) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r / 4) + 4 * qg + (r % 4);
+            if constexpr (NT == 4)
+                st4(dst + 4 * i, make_float4(acc[0][r] * sc, acc[1][r] * sc, acc[2][r] * sc, acc[3][r] * sc));
+            else
+                *reinterpret_cast<float2 *>(dst + 2 * i) = make_float2(acc[0][r] * sc, acc[1][r] * sc);
+        }
+    };
     if (a.n_kseg > 1) {
         if (!active) return;
         const size_t pe = ((size_t)g * total + ee) * a.n_kseg + seg;
-        float *po = a.part_o + (pe * 32 + qi) * HD;
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt)
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-                st4(po + 32 * tt + 8 * rb + 4 * qg,
-                    make_float4(acc[tt][4 * rb + 0], acc[tt][4 * rb + 1], acc[tt][4 * rb + 2], acc[tt][4 * rb + 3]));
+        store_row(a.part_o + (pe * 32 + qi) * HD, 1.f);
         if (qg == 0) {
             a.part_ml[(pe * 32 + qi) * 2 + 0] = m_run;
             a.part_ml[(pe * 32 + qi) * 2 + 1] = l_run;
         }
         return;
     }
-    if (qvalid) {
-        const float inv = 1.f / l_run;
-        float *op = a.out + ((size_t)qrow * n_head + h) * HD;
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt)
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-                st4(op + 32 * tt + 8 * rb + 4 * qg,
-                    make_float4(acc[tt][4 * rb + 0] * inv, acc[tt][4 * rb + 1] * inv,
-                                acc[tt][4 * rb + 2] * inv, acc[tt][4 * rb + 3] * inv));
-    }
+    if (qvalid) store_row(a.out + ((size_t)qrow * n_head + h) * HD, 1.f / l_run);
 }
 
 // Block = one (kv-head, strip, q-head) entry of the prefill: the log-sum-exp
