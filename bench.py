@@ -54,7 +54,7 @@ PF_N, PF_SEED = 2048, 3
 # (fetch x 2.0, write x 1.0): decode layer = split + combine kernel, prefill layer =
 # append + prefill kernel.  Re-measure when a kernel changes.
 TRAFFIC_DECODE_BYTES = 19_078_000
-TRAFFIC_PREFILL_BYTES = 109_010_000
+TRAFFIC_PREFILL_BYTES = 109_052_000
 
 
 def q_stream(layer): return (1 << 32) | layer
