@@ -634,16 +634,31 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     // every query position is below n_keys).
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     auto issue_tile = [&](float *dK, float *dV, int t) {
+        if (t * BK + BK <= n_keys) {
+            const size_t tb = ((size_t)g * a.slots + t * BK) * HD;
+            const float *kb = a.kc + tb, *vb = a.vc + tb;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int chunk = NI * wave_u + i;
-            const int p = 64 * chunk + lane;
-            const int row = p / C4, pos = p % C4;
-            const size_t base = ((size_t)g * a.slots + min(t * BK + row, n_keys - 1)) * HD;
-            __builtin_amdgcn_global_load_lds(a.kc + base + 4 * (pos ^ (row & 15)),
-                                             (void __attribute__((address_space(3))) *)(dK + 256 * chunk), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(a.vc + base + 4 * pos,
-                                             (void __attribute__((address_space(3))) *)(dV + 256 * chunk), 16, 0, 0);
+            for (int i = 0; i < NI; ++i) {
+                // per-lane offsets inside a tile, the same for every tile
+                const int chunk = NI * wave_u + i;
+                const int p = 64 * chunk + lane;
+                const int row = p / C4, pos = p % C4;
+                const int koff = row * HD + 4 * (pos ^ (row & 15)), voff = row * HD + 4 * pos;
+                __builtin_amdgcn_global_load_lds(kb + koff, (void __attribute__((address_space(3))) *)(dK + 256 * chunk), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vb + voff, (void __attribute__((address_space(3))) *)(dV + 256 * chunk), 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int chunk = NI * wave_u + i;
+                const int p = 64 * chunk + lane;
+                const int row = p / C4, pos = p % C4;
+                const size_t base = ((size_t)g * a.slots + min(t * BK + row, n_keys - 1)) * HD;
+                __builtin_amdgcn_global_load_lds(a.kc + base + 4 * (pos ^ (row & 15)),
+                                                 (void __attribute__((address_space(3))) *)(dK + 256 * chunk), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(a.vc + base + 4 * pos,
+                                                 (void __attribute__((address_space(3))) *)(dV + 256 * chunk), 16, 0, 0);
+            }
         }
     };
     auto compute_tile = [&](const float *sK, const float *sV, int t) {
@@ -678,7 +693,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
             pair32(mt, lo, hi);
             mt = fmaxf(lo, hi);
         }
-        const float m_new = fmaxf(m_run, mt);
+        // Each query keeps a reference maximum and moves it only when the new
+        // maximum exceeds it by more than 8 (log2 units): the exponentials
+        // stay below 2^8 and the accumulator rescale is skipped for most
+        // tiles (any reference gives the same normalised result).
+        const float m_max = fmaxf(m_run, mt);
+        const float m_new = (m_max > m_run + 8.f || m_run == -INFINITY) ? m_max : m_run;
         // a segment may start with a tile that is all masked for a row
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
         const float alpha = fast_exp2(m_run - m_use);
