@@ -21,6 +21,13 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_BIN = os.path.join(HERE, "_ref", "kore_ref")
+REF_QMV_BIN = os.path.join(HERE, "_ref", "kore_qmv_ref")
+
+# kore's BlockQ8K (kore.cpp:415-420): d, 256 int8 values, 16 int16 sums of 16
+Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+assert Q8K_DTYPE.itemsize == 292
+TYPE_Q4K, TYPE_Q6K = 12, 14
+BLOCK_BYTES = {TYPE_Q4K: 144, TYPE_Q6K: 210}
 
 _F = C.POINTER(C.c_float)
 _D = C.POINTER(C.c_double)
@@ -78,6 +85,16 @@ def lib() -> C.CDLL:
         L.ko_synth_fill.argtypes = [_F, C.c_int, C.c_int, C.c_uint64, C.c_uint64, C.c_uint64,
                                     C.c_uint64, C.c_uint32, C.c_float]
         L.ko_cpu_has_fma.restype = C.c_int
+        _u8 = C.c_void_p
+        L.ko_f16.argtypes = [C.c_uint16]
+        L.ko_f16.restype = C.c_float
+        L.ko_quantize_q8K.argtypes = [_F, C.c_int64, _u8]
+        for name in ("ko_dot_q4K_ref", "ko_dot_q6K_ref", "ko_dot_q4K_avx2", "ko_dot_q6K_avx2"):
+            getattr(L, name).argtypes = [C.c_int64, _u8, _u8]
+            getattr(L, name).restype = C.c_float
+        L.ko_dot_q6K_avx2_v.argtypes = [C.c_int64, _u8, _u8, C.c_int]
+        L.ko_dot_q6K_avx2_v.restype = C.c_float
+        L.ko_qmatvec.argtypes = [C.c_int, C.c_int64, C.c_int64, _u8, _u8, _F, C.c_int]
         _lib = L
     return _lib
 
@@ -193,6 +210,57 @@ def synth(rows: int, dim: int, seed: int, stream: int, row0: int = 0, tensor: in
 
 def cpu_has_fma() -> bool:
     return bool(lib().ko_cpu_has_fma())
+
+
+# ------------------------------------------------- Q8_K / Q4_K / Q6_K matvec
+
+def f16(h: int) -> float:
+    return float(lib().ko_f16(h & 0xFFFF))
+
+
+def quantize_q8K(x: np.ndarray) -> np.ndarray:
+    """kore's quantize_row_q8_K (kore.cpp:422-446): ``x`` of n floats (n a
+    multiple of 256) to n/256 BlockQ8K records (``Q8K_DTYPE``)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    if x.size % 256:
+        raise ValueError("length must be a multiple of 256")
+    out = np.zeros(x.size // 256, Q8K_DTYPE)
+    lib().ko_quantize_q8K(fptr(x), x.size, out.ctypes.data)
+    return out
+
+
+def _w(weights: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(weights, np.uint8).reshape(-1)
+
+
+def dot(wtype: int, wrow: np.ndarray, xq: np.ndarray, avx2: bool = True,
+        q6k_fused_bias: int | None = None) -> float:
+    """One row's Q4_K/Q6_K x Q8_K dot product (kore.cpp:450-506, 535-632)."""
+    w = _w(wrow)
+    xq = np.ascontiguousarray(xq, Q8K_DTYPE)
+    n = 256 * xq.size
+    L = lib()
+    if wtype == TYPE_Q6K and avx2 and q6k_fused_bias is not None:
+        return float(L.ko_dot_q6K_avx2_v(n, w.ctypes.data, xq.ctypes.data, int(q6k_fused_bias)))
+    name = {(TYPE_Q4K, False): "ko_dot_q4K_ref", (TYPE_Q4K, True): "ko_dot_q4K_avx2",
+            (TYPE_Q6K, False): "ko_dot_q6K_ref", (TYPE_Q6K, True): "ko_dot_q6K_avx2"}[(wtype, bool(avx2))]
+    return float(getattr(L, name)(n, w.ctypes.data, xq.ctypes.data))
+
+
+def qmatvec(wtype: int, weights: np.ndarray, rows: int, cols: int, xq: np.ndarray,
+            avx2: bool = True) -> np.ndarray:
+    """kore's matvec_rows over all rows (kore.cpp:649-660): out[r] = row r . xq."""
+    w = _w(weights)
+    if w.size != rows * (cols // 256) * BLOCK_BYTES[wtype]:
+        raise ValueError("weights size does not match rows x cols")
+    xq = np.ascontiguousarray(xq, Q8K_DTYPE)
+    if xq.size != cols // 256:
+        raise ValueError("xq must hold cols/256 blocks")
+    out = np.zeros(rows, np.float32)
+    rc = lib().ko_qmatvec(wtype, rows, cols, w.ctypes.data, xq.ctypes.data, fptr(out), int(avx2))
+    if rc != 0:
+        raise ValueError("ko_qmatvec rejected the type or cols")
+    return out
 
 
 class KV:
