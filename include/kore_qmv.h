@@ -1,0 +1,111 @@
+/*
+ * kore_qmv.h - C ABI of the MI355X (gfx950) quantised matrix-vector product
+ * for kore: the Q8_K activation quantiser and the Q4_K / Q6_K x Q8_K row dot
+ * products that every weight matrix of kore's forward() goes through.
+ *
+ * kore's calls this replaces:
+ *   quant(e, x, xq, n)        -> quantize_row_q8_K   (kore.cpp:1392-1394, 422-446)
+ *   mv(e, t, x, xq, out)      -> matvec_mt / matvec_rows with
+ *                                dot_q4_K_q8_K_* / dot_q6_K_q8_K_*
+ *                                (kore.cpp:1387-1390, 649-682, 450-632)
+ * A weight matrix is uploaded once (kore keeps it in the mmap'ed GGUF file,
+ * Tensor::data); the activations and results move per call.
+ *
+ * Results are bit-identical to kore's on the same inputs, in either of
+ * kore's two summation orders: `avx2` = 1 reproduces dot_*_avx2 (what kore
+ * runs on a CPU with AVX2/FMA, kore.cpp:535-632), `avx2` = 0 the scalar
+ * reference dot_*_ref (kore.cpp:450-506).  The Q8_K blocks are kore's
+ * BlockQ8K records (292 bytes: float d, int8 qs[256], int16 bsums[16];
+ * kore.cpp:415-420), bit for bit.
+ *
+ * Conventions (as kore_attn.h): 0 on success, a negative KORE_QMV_E_* code
+ * otherwise; nothing throws across the ABI; kore_qmv_last_error() describes
+ * the last failure.  Host-pointer calls are synchronous; *_dev calls take
+ * device pointers on the tensor's device and are asynchronous on `stream`
+ * (a hipStream_t; NULL = the null stream).
+ */
+#ifndef KORE_QMV_H
+#define KORE_QMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef KORE_QMV_API
+#if defined(__GNUC__) || defined(__clang__)
+#define KORE_QMV_API __attribute__((visibility("default")))
+#else
+#define KORE_QMV_API
+#endif
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kore_qmv_tensor *kore_qmv_tensor_t;
+
+/* ggml type ids kore accepts in a matvec (kore.cpp:161, 650) */
+enum { KORE_QMV_Q4_K = 12, KORE_QMV_Q6_K = 14 };
+
+#define KORE_QMV_Q8K_BYTES 292   /* one BlockQ8K per 256 values */
+
+enum {
+    KORE_QMV_OK = 0,
+    KORE_QMV_E_INVALID = -1,      /* null pointer, cols not a multiple of 256, size
+                                     mismatch, misaligned device pointer        */
+    KORE_QMV_E_UNSUPPORTED = -3,  /* weight type other than Q4_K / Q6_K: kore's
+                                     matvec_rows() returns false (kore.cpp:650),
+                                     or cols above 32768                         */
+    KORE_QMV_E_HIP = -4,          /* HIP runtime failure                         */
+    KORE_QMV_E_NOMEM = -5         /* device or host allocation failed            */
+};
+
+/* Upload one weight matrix to the current HIP device.  `data` holds kore's
+ * Tensor::data for it: rows x (cols/256) blocks of 144 (Q4_K) or 210 (Q6_K)
+ * bytes, row-major (kore.cpp:652: rows of cols/256 blocks; kore's dims[0] is
+ * cols, dims[1]*dims[2]*dims[3] rows).  data_on_device = 1 when `data` is a
+ * device pointer (then it must be 2-byte aligned).  The library keeps its own
+ * copy (Q6_K blocks are stored split so every load is aligned). */
+KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_t rows, int64_t cols,
+                                        const void *data, int data_on_device);
+
+/* Release a matrix. */
+KORE_QMV_API void kore_qmv_tensor_destroy(kore_qmv_tensor_t t);
+
+/* quantize_row_q8_K (kore.cpp:422-446): x[n] (n a multiple of 256) ->
+ * n/256 BlockQ8K records in xq.  Host buffers; runs on the current device. */
+KORE_QMV_API int kore_qmv_quantize(const float *x, int64_t n, void *xq);
+
+/* Same with device buffers on the current device; xq 16-byte aligned. */
+KORE_QMV_API int kore_qmv_quantize_dev(const float *x, int64_t n, void *xq, void *stream);
+
+/* out[r] = row r . xq for every row (matvec_mt, kore.cpp:677-682); xq holds
+ * cols/256 BlockQ8K records.  Host buffers. */
+KORE_QMV_API int kore_qmv_matvec(kore_qmv_tensor_t t, const void *xq, float *out, int avx2);
+
+/* Same with device buffers on the tensor's device; xq 16-byte aligned. */
+KORE_QMV_API int kore_qmv_matvec_dev(kore_qmv_tensor_t t, const void *xq, float *out, int avx2,
+                                     void *stream);
+
+/* mv() with quant() in front (kore.cpp:1387-1394): x[cols] floats in,
+ * out[rows] out.  Host buffers. */
+KORE_QMV_API int kore_qmv_mv(kore_qmv_tensor_t t, const float *x, float *out, int avx2);
+
+/* Text of the last failure on this tensor (or, with NULL, of the last failed
+ * call without a tensor on this thread).  Never NULL. */
+KORE_QMV_API const char *kore_qmv_last_error(kore_qmv_tensor_t t);
+
+/* Shape and resources of a matrix. */
+typedef struct kore_qmv_info {
+    int type;
+    int device;
+    int64_t rows, cols;
+    size_t weight_bytes;     /* bytes one matvec streams from HBM (kore's block bytes) */
+    int rows_per_wg;         /* rows per workgroup of the matvec kernel (4, 8 or 16)   */
+} kore_qmv_info;
+KORE_QMV_API int kore_qmv_get_info(kore_qmv_tensor_t t, kore_qmv_info *info);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

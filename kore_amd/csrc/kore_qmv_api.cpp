@@ -1,0 +1,282 @@
+// kore_qmv_api.cpp - the C ABI of include/kore_qmv.h over the gfx950
+// kernels of kore_qmv_kernels.hip.
+#include "kore_qmv.h"
+#include "kore_qmv_synth.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "kore_qmv_kernels.h"
+
+using namespace kore_qmv_gpu;
+
+struct kore_qmv_tensor {
+    int type = 0;
+    int device = 0;
+    int64_t rows = 0, cols = 0;
+    int nblk = 0;
+    int rows_per_wg = 16;
+    uint8_t *w = nullptr;      // Q4_K blocks or Q6_K bodies
+    uint16_t *wd = nullptr;    // Q6_K scales
+    size_t weight_bytes = 0;
+    std::string error;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(kore_qmv_tensor *t, int code, const std::string &msg) {
+    (t ? t->error : g_error) = msg;
+    return code;
+}
+
+int hip_fail(kore_qmv_tensor *t, hipError_t e, const char *what) {
+    return fail(t, KORE_QMV_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define QMV_TRY(t, call)                                        \
+    do {                                                        \
+        hipError_t e_ = (call);                                 \
+        if (e_ != hipSuccess) return hip_fail((t), e_, #call);  \
+    } while (0)
+
+// Per-device staging buffers and stream of the synchronous host-pointer calls.
+struct HostPath {
+    std::mutex mu;
+    hipStream_t stream = nullptr;
+    void *buf = nullptr;
+    size_t cap = 0;
+};
+HostPath g_host[64];
+
+hipError_t host_path(int dev, size_t need, HostPath **out) {
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    HostPath &h = g_host[dev];
+    if (!h.stream) {
+        hipError_t e = hipStreamCreateWithFlags(&h.stream, hipStreamNonBlocking);
+        if (e != hipSuccess) return e;
+    }
+    if (h.cap < need) {
+        if (h.buf) (void)hipFree(h.buf);
+        h.buf = nullptr;
+        h.cap = 0;
+        hipError_t e = hipMalloc(&h.buf, need);
+        if (e != hipSuccess) return e;
+        h.cap = need;
+    }
+    *out = &h;
+    return hipSuccess;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Rows per workgroup: as many as still give every CU four workgroups or more;
+// fewer rows spread each row's blocks over more lanes.
+int pick_rows_per_wg(int64_t rows, int num_cu) {
+    if (const char *env = getenv("KORE_QMV_ROWS_PER_WG")) {
+        const int r = atoi(env);
+        if (r == 4 || r == 8 || r == 16) return r;
+    }
+    const int64_t want = 4LL * num_cu;
+    if (rows / 16 >= want) return 16;
+    if (rows / 8 >= want) return 8;
+    return 4;
+}
+
+int check_dev_ptr(kore_qmv_tensor *t, const void *p, size_t align, const char *what) {
+    if (!p) return fail(t, KORE_QMV_E_INVALID, std::string(what) + " is NULL");
+    if ((uintptr_t)p % align) return fail(t, KORE_QMV_E_INVALID, std::string(what) + " is not aligned");
+    return KORE_QMV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_t rows, int64_t cols,
+                                        const void *data, int data_on_device) {
+    if (!out) return fail(nullptr, KORE_QMV_E_INVALID, "out is NULL");
+    *out = nullptr;
+    if (type != KORE_QMV_Q4_K && type != KORE_QMV_Q6_K)
+        return fail(nullptr, KORE_QMV_E_UNSUPPORTED, "weight type is not Q4_K (12) or Q6_K (14)");
+    if (rows <= 0 || cols <= 0 || cols % 256 != 0)
+        return fail(nullptr, KORE_QMV_E_INVALID, "rows must be > 0 and cols a positive multiple of 256");
+    if (cols / 256 > kMaxBlocks)
+        return fail(nullptr, KORE_QMV_E_UNSUPPORTED, "cols above 32768");
+    if (rows > (int64_t)INT32_MAX) return fail(nullptr, KORE_QMV_E_UNSUPPORTED, "more than 2^31-1 rows");
+    if (!data) return fail(nullptr, KORE_QMV_E_INVALID, "data is NULL");
+    if (data_on_device && ((uintptr_t)data & 1)) return fail(nullptr, KORE_QMV_E_INVALID, "data is not 2-byte aligned");
+
+    kore_qmv_tensor *t = new (std::nothrow) kore_qmv_tensor;
+    if (!t) return fail(nullptr, KORE_QMV_E_NOMEM, "host allocation failed");
+    auto bail = [&](int code) {
+        g_error = t->error;
+        if (t->w) (void)hipFree(t->w);
+        if (t->wd) (void)hipFree(t->wd);
+        delete t;
+        return code;
+    };
+    t->type = type;
+    t->rows = rows;
+    t->cols = cols;
+    t->nblk = (int)(cols / 256);
+    hipError_t e = hipGetDevice(&t->device);
+    if (e != hipSuccess) return bail(hip_fail(t, e, "hipGetDevice"));
+    int num_cu = 0;
+    e = hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, t->device);
+    if (e != hipSuccess) return bail(hip_fail(t, e, "hipDeviceGetAttribute"));
+    t->rows_per_wg = pick_rows_per_wg(rows, num_cu);
+
+    const int64_t nblocks = rows * t->nblk;
+    const size_t bb = type == KORE_QMV_Q4_K ? kQ4Bytes : kQ6Bytes;
+    t->weight_bytes = (size_t)nblocks * bb;
+    if (type == KORE_QMV_Q4_K) {
+        if ((e = hipMalloc(&t->w, t->weight_bytes)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
+        e = hipMemcpy(t->w, data, t->weight_bytes, data_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice);
+        if (e != hipSuccess) return bail(hip_fail(t, e, "hipMemcpy"));
+        *out = t;
+        return KORE_QMV_OK;
+    }
+    if ((e = hipMalloc(&t->w, (size_t)nblocks * kQ6Body)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
+    if ((e = hipMalloc(&t->wd, (size_t)nblocks * 2)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
+    const uint8_t *raw = (const uint8_t *)data;
+    uint8_t *staged = nullptr;
+    if (!data_on_device) {
+        if ((e = hipMalloc(&staged, t->weight_bytes)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
+        e = hipMemcpy(staged, data, t->weight_bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(staged);
+            return bail(hip_fail(t, e, "hipMemcpy"));
+        }
+        raw = staged;
+    }
+    e = launch_q6k_split(raw, nblocks, t->w, t->wd, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (staged) (void)hipFree(staged);
+    if (e != hipSuccess) return bail(hip_fail(t, e, "Q6_K upload"));
+    *out = t;
+    return KORE_QMV_OK;
+}
+
+KORE_QMV_API void kore_qmv_tensor_destroy(kore_qmv_tensor_t t) {
+    if (!t) return;
+    int cur = -1;
+    (void)hipGetDevice(&cur);
+    if (cur != t->device) (void)hipSetDevice(t->device);
+    if (t->w) (void)hipFree(t->w);
+    if (t->wd) (void)hipFree(t->wd);
+    if (cur >= 0 && cur != t->device) (void)hipSetDevice(cur);
+    delete t;
+}
+
+KORE_QMV_API int kore_qmv_quantize_dev(const float *x, int64_t n, void *xq, void *stream) {
+    if (n <= 0 || n % 256 != 0) return fail(nullptr, KORE_QMV_E_INVALID, "n must be a positive multiple of 256");
+    if (int rc = check_dev_ptr(nullptr, x, 4, "x")) return rc;
+    if (int rc = check_dev_ptr(nullptr, xq, 16, "xq")) return rc;
+    hipError_t e = launch_quantize_q8k(x, n, (uint8_t *)xq, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "quantize launch");
+    return KORE_QMV_OK;
+}
+
+KORE_QMV_API int kore_qmv_quantize(const float *x, int64_t n, void *xq) {
+    if (!x || !xq) return fail(nullptr, KORE_QMV_E_INVALID, "x or xq is NULL");
+    if (n <= 0 || n % 256 != 0) return fail(nullptr, KORE_QMV_E_INVALID, "n must be a positive multiple of 256");
+    int dev = 0;
+    QMV_TRY(nullptr, hipGetDevice(&dev));
+    const size_t xb = align256((size_t)n * 4), qb = (size_t)(n / 256) * kQ8Bytes;
+    HostPath *h = nullptr;
+    std::lock_guard<std::mutex> lock(g_host[dev & 63].mu);
+    QMV_TRY(nullptr, host_path(dev, xb + qb, &h));
+    uint8_t *dx = (uint8_t *)h->buf, *dq = dx + xb;
+    QMV_TRY(nullptr, hipMemcpyAsync(dx, x, (size_t)n * 4, hipMemcpyHostToDevice, h->stream));
+    QMV_TRY(nullptr, launch_quantize_q8k((const float *)dx, n, dq, h->stream));
+    QMV_TRY(nullptr, hipMemcpyAsync(xq, dq, qb, hipMemcpyDeviceToHost, h->stream));
+    QMV_TRY(nullptr, hipStreamSynchronize(h->stream));
+    return KORE_QMV_OK;
+}
+
+KORE_QMV_API int kore_qmv_matvec_dev(kore_qmv_tensor_t t, const void *xq, float *out, int avx2, void *stream) {
+    if (!t) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
+    if (int rc = check_dev_ptr(t, xq, 16, "xq")) return rc;
+    if (int rc = check_dev_ptr(t, out, 4, "out")) return rc;
+    MatvecArgs a{t->w, t->wd, (const uint8_t *)xq, out, (int)t->rows, t->nblk};
+    hipError_t e = launch_matvec(t->type, avx2 != 0, a, t->rows_per_wg, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(t, e, "matvec launch");
+    return KORE_QMV_OK;
+}
+
+static int matvec_host(kore_qmv_tensor_t t, const float *x, const void *xq, float *out, int avx2) {
+    const size_t qb = (size_t)t->nblk * kQ8Bytes, ob = align256((size_t)t->rows * 4);
+    const size_t xb = x ? align256((size_t)t->cols * 4) : 0;
+    HostPath *h = nullptr;
+    std::lock_guard<std::mutex> lock(g_host[t->device & 63].mu);
+    QMV_TRY(t, host_path(t->device, ob + align256(qb) + xb, &h));
+    uint8_t *dout = (uint8_t *)h->buf, *dq = dout + ob, *dx = dq + align256(qb);
+    if (x) {
+        QMV_TRY(t, hipMemcpyAsync(dx, x, (size_t)t->cols * 4, hipMemcpyHostToDevice, h->stream));
+        QMV_TRY(t, launch_quantize_q8k((const float *)dx, t->cols, dq, h->stream));
+    } else {
+        QMV_TRY(t, hipMemcpyAsync(dq, xq, qb, hipMemcpyHostToDevice, h->stream));
+    }
+    MatvecArgs a{t->w, t->wd, dq, (float *)dout, (int)t->rows, t->nblk};
+    QMV_TRY(t, launch_matvec(t->type, avx2 != 0, a, t->rows_per_wg, h->stream));
+    QMV_TRY(t, hipMemcpyAsync(out, dout, (size_t)t->rows * 4, hipMemcpyDeviceToHost, h->stream));
+    QMV_TRY(t, hipStreamSynchronize(h->stream));
+    return KORE_QMV_OK;
+}
+
+KORE_QMV_API int kore_qmv_matvec(kore_qmv_tensor_t t, const void *xq, float *out, int avx2) {
+    if (!t) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
+    if (!xq || !out) return fail(t, KORE_QMV_E_INVALID, "xq or out is NULL");
+    int cur = -1;
+    QMV_TRY(t, hipGetDevice(&cur));
+    if (cur != t->device) QMV_TRY(t, hipSetDevice(t->device));
+    const int rc = matvec_host(t, nullptr, xq, out, avx2);
+    if (cur != t->device) (void)hipSetDevice(cur);
+    return rc;
+}
+
+KORE_QMV_API int kore_qmv_mv(kore_qmv_tensor_t t, const float *x, float *out, int avx2) {
+    if (!t) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
+    if (!x || !out) return fail(t, KORE_QMV_E_INVALID, "x or out is NULL");
+    int cur = -1;
+    QMV_TRY(t, hipGetDevice(&cur));
+    if (cur != t->device) QMV_TRY(t, hipSetDevice(t->device));
+    const int rc = matvec_host(t, x, nullptr, out, avx2);
+    if (cur != t->device) (void)hipSetDevice(cur);
+    return rc;
+}
+
+KORE_QMV_API const char *kore_qmv_last_error(kore_qmv_tensor_t t) {
+    return t ? t->error.c_str() : g_error.c_str();
+}
+
+KORE_QMV_API int kore_qmv_get_info(kore_qmv_tensor_t t, kore_qmv_info *info) {
+    if (!t || !info) return fail(t, KORE_QMV_E_INVALID, "tensor or info is NULL");
+    info->type = t->type;
+    info->device = t->device;
+    info->rows = t->rows;
+    info->cols = t->cols;
+    info->weight_bytes = t->weight_bytes;
+    info->rows_per_wg = t->rows_per_wg;
+    return KORE_QMV_OK;
+}
+
+KORE_QMV_API int kore_qmv_synth_dev(int type, int64_t rows, int64_t cols, uint64_t seed, void *dst, void *stream) {
+    if (type != KORE_QMV_Q4_K && type != KORE_QMV_Q6_K)
+        return fail(nullptr, KORE_QMV_E_UNSUPPORTED, "weight type is not Q4_K (12) or Q6_K (14)");
+    if (rows <= 0 || cols <= 0 || cols % 256 != 0)
+        return fail(nullptr, KORE_QMV_E_INVALID, "rows must be > 0 and cols a positive multiple of 256");
+    if (int rc = check_dev_ptr(nullptr, dst, 2, "dst")) return rc;
+    hipError_t e = launch_synth_blocks(type, rows * (cols / 256), seed, (uint8_t *)dst, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "synth launch");
+    return KORE_QMV_OK;
+}
+
+}  // extern "C"

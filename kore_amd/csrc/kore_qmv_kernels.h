@@ -1,0 +1,56 @@
+// kore_qmv_kernels.h - launch interface of the gfx950 kernels behind the
+// kore_qmv C ABI (quantised matrix-vector products).  Internal to
+// libkore_qmv.so.
+//
+// Device layouts
+//   activations  kore's BlockQ8K array (kore.cpp:415-420): per 256 values a
+//                292-byte record {float d; int8 qs[256]; int16 bsums[16]}.
+//   Q4_K weights kore's / GGUF's 144-byte blocks unchanged (kore.cpp:324-326):
+//                rows x nblk blocks, row-major; every block is 16-byte aligned.
+//   Q6_K weights the 210-byte GGUF block (kore.cpp:355-357) split in two
+//                arrays so every load is aligned: `body` holds its first 208
+//                bytes (ql[128], qh[64], int8 scales[16]) per block, `d` its
+//                f16 scale, both indexed row * nblk + block.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace kore_qmv_gpu {
+
+constexpr int kQ8Bytes = 292;
+constexpr int kQ4Bytes = 144;
+constexpr int kQ6Bytes = 210;
+constexpr int kQ6Body = 208;
+constexpr int kMaxBlocks = 128;   // cols <= 32768: the staged activations fit in LDS
+
+enum WeightType { kQ4K = 12, kQ6K = 14 };
+
+// Rows are processed by workgroups of 256 threads; a workgroup owns `rows_per_wg`
+// consecutive rows (4, 8 or 16) and walks their blocks in steps.
+struct MatvecArgs {
+    const uint8_t *w;        // Q4_K blocks, or the Q6_K 208-byte bodies
+    const uint16_t *wd;      // Q6_K f16 scales (nullptr for Q4_K)
+    const uint8_t *xq;       // nblk BlockQ8K records
+    float *out;              // [rows]
+    int rows;
+    int nblk;                // cols / 256
+};
+
+// out[r] = row r . xq with kore's summation: avx2 = true follows
+// dot_q*_K_q8_K_avx2 (kore.cpp:535-632), false dot_q*_K_q8_K_ref
+// (kore.cpp:450-506).  Bit-identical to kore's results in both orders.
+hipError_t launch_matvec(int type, bool avx2, const MatvecArgs &a, int rows_per_wg, hipStream_t s);
+
+// kore's quantize_row_q8_K (kore.cpp:422-446): x[n] -> n/256 BlockQ8K records.
+hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, hipStream_t s);
+
+// Q6_K upload: raw GGUF blocks (rows*nblk x 210 bytes, any alignment of 2)
+// -> body / d arrays above.
+hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, uint16_t *d, hipStream_t s);
+
+// Synthetic GGUF-format weights for benchmarks: nblocks raw Q4_K / Q6_K blocks
+// with hashed bytes and finite f16 scales (dst 2-byte aligned).
+hipError_t launch_synth_blocks(int type, int64_t nblocks, uint64_t seed, uint8_t *dst, hipStream_t s);
+
+}  // namespace kore_qmv_gpu

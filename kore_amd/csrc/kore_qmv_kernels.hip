@@ -1,0 +1,442 @@
+// kore_qmv_kernels.hip - gfx950 kernels of kore's quantised matrix-vector
+// product: Q8_K activation quantisation and Q4_K / Q6_K x Q8_K row dot
+// products (kore.cpp:422-682), bit-identical to kore's scalar and AVX2 code.
+//
+// The matvec is HBM-bound: every weight byte is read once, the activations
+// (at most 128 x 292 bytes) are staged in LDS by every workgroup.  A row's
+// work is cut into units (row, 256-value block) and each unit into four
+// parts handled by four adjacent lanes.  A part computes exact integer sums
+// (v_dot4_i32_i8 over 4 bytes at a time; every partial kore forms in an
+// int32 lane is reproduced exactly).  kore's float arithmetic - one fused
+// multiply-add per AVX2 lane and block, in block order, then its horizontal
+// sums - is a sequential chain per row; the integer results of a step's
+// units go through LDS to one wave that advances the chains, so blocks can
+// be spread over all lanes without changing a single rounding.
+#include "kore_qmv_kernels.h"
+
+#include <climits>
+#include <type_traits>
+
+namespace kore_qmv_gpu {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float f16_bits(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, 0, false);
+}
+
+// Products of a 6- or 8-bit scale and a sum of at most 2^16 in magnitude:
+// both fit the 24-bit multiplier (full rate, unlike v_mul_lo_u32).
+__device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
+
+__device__ __forceinline__ int quad_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true); }
+__device__ __forceinline__ int quad_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true); }
+__device__ __forceinline__ float quad_xor1f(float v) { return __int_as_float(quad_xor1(__float_as_int(v))); }
+__device__ __forceinline__ float quad_xor2f(float v) { return __int_as_float(quad_xor2(__float_as_int(v))); }
+
+// ------------------------------------------------------------------ Q8_K
+
+// One wave per 256-value block: lane l owns values 4l .. 4l+3.
+__global__ __launch_bounds__(kThreads) void quantize_q8k_kernel(const float *__restrict__ x,
+                                                                uint8_t *__restrict__ xq, int64_t nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (blk >= nblocks) return;
+    const float *xb = x + blk * 256 + 4 * lane;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = xb[e];
+    // kore keeps the first value of largest magnitude, starting from amax = 0
+    // with a strict comparison (kore.cpp:424-428): the largest |x| wins, ties
+    // go to the lowest index, NaN and zeros are never chosen.
+    float best = 0.f, bval = 0.f;
+    int bidx = 256;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float ax = fabsf(v[e]);
+        if (ax > best) {
+            best = ax;
+            bval = v[e];
+            bidx = 4 * lane + e;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ob = __shfl_xor(best, off);
+        const float ov = __shfl_xor(bval, off);
+        const int oi = __shfl_xor(bidx, off);
+        if (ob > best || (ob == best && oi < bidx)) {
+            best = ob;
+            bval = ov;
+            bidx = oi;
+        }
+    }
+    uint8_t *rec = xq + blk * kQ8Bytes;
+    uint32_t packed = 0;
+    int sum4 = 0;
+    float d = 0.f;
+    if (best != 0.f) {
+        const float iscale = -127.0f / bval;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // (int) of an out-of-range or NaN value is x86's 0x80000000 in kore
+            const float t = rintf(iscale * v[e]);
+            int q = fabsf(t) < 2147483648.0f ? (int)t : INT_MIN;
+            q = q > 127 ? 127 : q;
+            const int q8 = (int)(int8_t)(q & 0xFF);
+            packed |= (uint32_t)(q8 & 0xFF) << (8 * e);
+            sum4 += q8;
+        }
+        d = 1.0f / iscale;
+    }
+    *(uint32_t *)(rec + 4 + 4 * lane) = packed;
+    sum4 += __shfl_xor(sum4, 1);
+    sum4 += __shfl_xor(sum4, 2);
+    if ((lane & 3) == 0) *(int16_t *)(rec + 260 + 2 * (lane >> 2)) = (int16_t)sum4;
+    if (lane == 0) *(float *)rec = d;
+}
+
+// ------------------------------------------------------------------ units
+
+// Staged activations: kore's BlockQ8K records copied verbatim into LDS.
+struct Q8View {
+    const uint8_t *p;
+    __device__ float d(int i) const { return *(const float *)(p + i * kQ8Bytes); }
+    __device__ uint2 qs8(int i, int byte) const {   // 8 bytes of qs (byte % 4 == 0)
+        const uint32_t *q = (const uint32_t *)(p + i * kQ8Bytes + 4 + byte);
+        return make_uint2(q[0], q[1]);
+    }
+    __device__ int bsum(int i, int j) const { return *(const int16_t *)(p + i * kQ8Bytes + 260 + 2 * j); }
+};
+
+// Raw bytes of one unit part, loaded a step ahead.
+struct Q4Raw { uint4 hdr; uint2 qs[4]; };
+struct Q6Raw { uint2 a[2], b[2], h[2]; uint4 sc; uint32_t d; };
+
+__device__ __forceinline__ Q4Raw load_q4(const uint8_t *w, int64_t unit, int j) {
+    const uint8_t *b = w + unit * kQ4Bytes;
+    Q4Raw r;
+    r.hdr = *(const uint4 *)b;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r.qs[c] = *(const uint2 *)(b + 16 + 32 * c + 8 * j);
+    return r;
+}
+
+__device__ __forceinline__ Q6Raw load_q6(const uint8_t *w, const uint16_t *wd, int64_t unit, int j) {
+    const uint8_t *b = w + unit * kQ6Body;
+    Q6Raw r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        r.a[h] = *(const uint2 *)(b + 64 * h + 8 * j);
+        r.b[h] = *(const uint2 *)(b + 64 * h + 32 + 8 * j);
+        r.h[h] = *(const uint2 *)(b + 128 + 32 * h + 8 * j);
+    }
+    r.sc = *(const uint4 *)(b + 192);
+    r.d = wd[unit];
+    return r;
+}
+
+// Per-part record handed to the chain wave (16 bytes).
+//   AVX2 Q4_K: s[2j], s[2j+1] (AVX2 lanes 2j, 2j+1), min product of lane j,
+//              then d (j even) or dmin (j odd)
+//   AVX2 Q6_K: s[2j], s[2j+1], the block's bias sum, d
+//   scalar:    part 0 holds isum, imin (Q4_K), d, dmin for the whole unit
+struct Rec { int a, b, c; float x; };
+
+// Q4_K block (kore.cpp:324-326): 6-bit scale / min of sub-block j from the
+// 12 packed bytes q[0..11] (kore.cpp:327-335).
+__device__ __forceinline__ int q4_scale(const uint4 &h, int j) {
+    if (j < 4) return (h.y >> (8 * j)) & 63;
+    const int s = 8 * (j - 4);
+    return ((h.w >> s) & 0x0F) | (((h.y >> (s + 6)) & 3) << 4);
+}
+__device__ __forceinline__ int q4_min(const uint4 &h, int j) {
+    if (j < 4) return (h.z >> (8 * j)) & 63;
+    const int s = 8 * (j - 4);
+    return ((h.w >> (s + 4)) & 0x0F) | (((h.z >> (s + 6)) & 3) << 4);
+}
+
+// Part j of a Q4_K unit: AVX2 lanes k = 2j, 2j+1 hold bytes 4k..4k+3 of each
+// 32-byte group c of the nibbles (kore.cpp:548-575); lane j of the 4-lane
+// minimum sum holds sub-blocks 2j, 2j+1 (kore.cpp:556-560).
+template <bool AVX2>
+__device__ __forceinline__ Rec part_q4(const Q4Raw &r, const Q8View &x, int i, int j) {
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int sl = q4_scale(r.hdr, 2 * c), sh = q4_scale(r.hdr, 2 * c + 1);
+        const uint2 lo8 = x.qs8(i, 64 * c + 8 * j), hi8 = x.qs8(i, 64 * c + 32 + 8 * j);
+        const uint32_t w0 = r.qs[c].x, w1 = r.qs[c].y;
+        s0 += mul24(sl, dot4(w0 & 0x0F0F0F0Fu, lo8.x)) + mul24(sh, dot4((w0 >> 4) & 0x0F0F0F0Fu, hi8.x));
+        s1 += mul24(sl, dot4(w1 & 0x0F0F0F0Fu, lo8.y)) + mul24(sh, dot4((w1 >> 4) & 0x0F0F0F0Fu, hi8.y));
+    }
+    const int prod = mul24(q4_min(r.hdr, 2 * j), x.bsum(i, 4 * j) + x.bsum(i, 4 * j + 1)) +
+                     mul24(q4_min(r.hdr, 2 * j + 1), x.bsum(i, 4 * j + 2) + x.bsum(i, 4 * j + 3));
+    const float yd = x.d(i);
+    const float d = f16_bits(r.hdr.x & 0xFFFFu) * yd;
+    const float dmin = f16_bits(r.hdr.x >> 16) * yd;
+    if (AVX2) return Rec{s0, s1, prod, (j & 1) ? dmin : d};
+    int isum = s0 + s1, imin = prod;
+    isum += quad_xor1(isum);
+    isum += quad_xor2(isum);
+    imin += quad_xor1(imin);
+    imin += quad_xor2(imin);
+    return Rec{isum, imin, __float_as_int(dmin), d};
+}
+
+// Part j of a Q6_K unit: AVX2 lanes m = 2j, 2j+1 hold values 4m..4m+3 of each
+// 32-value group (h, k) (kore.cpp:606-627), scale sc[8h + 2k + (m >= 4)].
+template <bool AVX2>
+__device__ __forceinline__ Rec part_q6(const Q6Raw &r, const Q8View &x, int i, int j) {
+    const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+    const int g = j >> 1;
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint2 A = r.a[h], B = r.b[h], Q = r.h[h];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int bi = 8 * h + 2 * k + g;
+            const int sc = (int)(int8_t)((scw[bi >> 2] >> (8 * (bi & 3))) & 0xFF);
+            uint32_t u0, u1;
+            if (k == 0) {
+                u0 = (A.x & 0x0F0F0F0Fu) | ((Q.x << 4) & 0x30303030u);
+                u1 = (A.y & 0x0F0F0F0Fu) | ((Q.y << 4) & 0x30303030u);
+            } else if (k == 1) {
+                u0 = (B.x & 0x0F0F0F0Fu) | ((Q.x << 2) & 0x30303030u);
+                u1 = (B.y & 0x0F0F0F0Fu) | ((Q.y << 2) & 0x30303030u);
+            } else if (k == 2) {
+                u0 = ((A.x >> 4) & 0x0F0F0F0Fu) | (Q.x & 0x30303030u);
+                u1 = ((A.y >> 4) & 0x0F0F0F0Fu) | (Q.y & 0x30303030u);
+            } else {
+                u0 = ((B.x >> 4) & 0x0F0F0F0Fu) | ((Q.x >> 2) & 0x30303030u);
+                u1 = ((B.y >> 4) & 0x0F0F0F0Fu) | ((Q.y >> 2) & 0x30303030u);
+            }
+            const uint2 q8 = x.qs8(i, 128 * h + 32 * k + 8 * j);
+            s0 += mul24(sc, dot4(u0, q8.x));
+            s1 += mul24(sc, dot4(u1, q8.y));
+        }
+    }
+    // bias sum over the 16 sub-blocks (kore.cpp:605): part j takes 4j .. 4j+3
+    int ibias = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        ibias += mul24((int)(int8_t)((scw[j] >> (8 * e)) & 0xFF), x.bsum(i, 4 * j + e));
+    ibias += quad_xor1(ibias);
+    ibias += quad_xor2(ibias);
+    const float d = f16_bits(r.d) * x.d(i);
+    if (AVX2) return Rec{s0, s1, ibias, d};
+    // kore's scalar reference sums (q6 - 32) * q8 (kore.cpp:480-506): the same
+    // integer as sum(sc * q6 * q8) - 32 * sum(sc * bsums)
+    int isum = s0 + s1;
+    isum += quad_xor1(isum);
+    isum += quad_xor2(isum);
+    return Rec{isum - 32 * ibias, 0, 0, d};
+}
+
+// ------------------------------------------------------------------ matvec
+
+// Workgroup: R rows, P = 64 / R blocks per step.  Thread t: part j = t % 4,
+// row (t / 4) % R, block phase t / (4R); its record lands in recs[t].
+template <int TYPE, bool AVX2, int R>
+__global__ __launch_bounds__(kThreads) void matvec_kernel(MatvecArgs a) {
+    constexpr int P = 64 / R;
+    extern __shared__ __align__(16) uint8_t smem[];
+    Rec *recs = (Rec *)smem;                               // [2][256]
+    uint8_t *xs = smem + 2 * kThreads * sizeof(Rec);       // nblk BlockQ8K records
+
+    const int t = threadIdx.x;
+    const int j = t & 3, rho = (t >> 2) % R, ph = t / (4 * R);
+    const int row0 = blockIdx.x * R;
+    const int nblk = a.nblk;
+    const int row = min(row0 + rho, a.rows - 1);
+    const int nsteps = (nblk + P - 1) / P;
+
+    auto unit_of = [&](int s) -> int64_t {
+        const int i = min(s * P + ph, nblk - 1);
+        return (int64_t)row * nblk + i;
+    };
+    using Raw = std::conditional_t<TYPE == kQ4K, Q4Raw, Q6Raw>;
+    auto load = [&](int s) -> Raw {
+        if constexpr (TYPE == kQ4K) return load_q4(a.w, unit_of(s), j);
+        else return load_q6(a.w, a.wd, unit_of(s), j);
+    };
+
+    Raw cur = load(0);
+
+    // stage the activations: whole 16-byte chunks, then the 4-byte tail
+    {
+        const int bytes = nblk * kQ8Bytes, n16 = bytes >> 4;
+        const uint4 *src = (const uint4 *)a.xq;
+        for (int c = t; c < n16; c += kThreads) ((uint4 *)xs)[c] = src[c];
+        for (int c = 4 * n16 + t; c < (bytes >> 2); c += kThreads)
+            ((uint32_t *)xs)[c] = ((const uint32_t *)a.xq)[c];
+    }
+    __syncthreads();
+    const Q8View x{xs};
+
+    // chain state of wave 0, lane l < 4R: row l / 4, part l % 4
+    float acc0 = 0.f, acc1 = 0.f, accm = 0.f;
+    const bool chain = t < 4 * R;
+
+    for (int s = 0; s < nsteps; ++s) {
+        Raw nxt;
+        if (s + 1 < nsteps) nxt = load(s + 1);
+        const int i = min(s * P + ph, nblk - 1);
+        Rec r;
+        if constexpr (TYPE == kQ4K) r = part_q4<AVX2>(cur, x, i, j);
+        else r = part_q6<AVX2>(cur, x, i, j);
+        Rec *buf = recs + (s & 1) * kThreads;
+        buf[t] = r;
+        __syncthreads();
+        if (chain) {
+            const int nb = min(P, nblk - s * P);
+            for (int b = 0; b < nb; ++b) {
+                const int base = (b * R + rho) * 4;
+                const Rec q = buf[base + j];
+                if constexpr (AVX2) {
+                    if constexpr (TYPE == kQ4K) {
+                        const float d = buf[base].x, dmin = buf[base + 1].x;
+                        acc0 = fmaf(d, (float)q.a, acc0);
+                        acc1 = fmaf(d, (float)q.b, acc1);
+                        accm = fmaf(-dmin, (float)q.c, accm);
+                    } else {
+                        acc0 = fmaf(q.x, (float)q.a, acc0);
+                        acc1 = fmaf(q.x, (float)q.b, acc1);
+                        accm = fmaf(-(q.x * 32.0f), (float)q.c, accm);   // summ (kore.cpp:606)
+                    }
+                } else {
+                    const Rec u = buf[base];
+                    if constexpr (TYPE == kQ4K) {
+                        const float t1 = u.x * (float)u.a;
+                        const float t2 = __int_as_float(u.c) * (float)u.b;
+                        acc0 = acc0 + (t1 - t2);
+                    } else {
+                        acc0 = acc0 + u.x * (float)u.a;
+                    }
+                }
+            }
+        }
+        if (s + 1 < nsteps) cur = nxt;
+    }
+
+    if (!chain) return;
+    float res;
+    if constexpr (AVX2) {
+        // kore's hsum256 (kore.cpp:521-528): lanes k and k+4 first, then
+        // (l0 + l2) + (l1 + l3); lane 2j / 2j+1 live in part j
+        const float u = acc0 + quad_xor2f(acc0);     // part 0: l0, part 1: l2
+        const float v = acc1 + quad_xor2f(acc1);     // part 0: l1, part 1: l3
+        const float h8 = (u + quad_xor1f(u)) + (v + quad_xor1f(v));
+        if constexpr (TYPE == kQ4K) {
+            const float m = accm + quad_xor2f(accm); // hsum128 (kore.cpp:537-541)
+            res = h8 + (m + quad_xor1f(m));
+        } else {
+            res = h8 + accm;
+        }
+    } else {
+        res = acc0;
+    }
+    if (j == 0 && row0 + rho < a.rows) a.out[row0 + rho] = res;
+}
+
+// Q6_K upload: thread per output dword (52 body dwords + the scale per block).
+__global__ __launch_bounds__(kThreads) void q6k_split_kernel(const uint16_t *__restrict__ raw, int64_t nblocks,
+                                                             uint32_t *__restrict__ body,
+                                                             uint16_t *__restrict__ d) {
+    const int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (g >= nblocks * 53) return;
+    const int64_t blk = g / 53;
+    const int q = (int)(g % 53);
+    const uint16_t *src = raw + blk * (kQ6Bytes / 2);
+    if (q < 52) body[blk * 52 + q] = (uint32_t)src[2 * q] | ((uint32_t)src[2 * q + 1] << 16);
+    else d[blk] = src[104];
+}
+
+// Synthetic GGUF blocks: every 16-bit word a hash of (seed, index), the f16
+// scales replaced by finite values in [2^-8, 2^-7) (d) and [2^-9, 2^-8) (dmin).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(kThreads) void synth_blocks_kernel(uint16_t *__restrict__ dst, int64_t n16,
+                                                                int words_per_block, int d_word, int dmin_word,
+                                                                uint64_t key) {
+    const int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (g >= n16) return;
+    const uint32_t h = (uint32_t)splitmix64(key ^ (uint64_t)g);
+    const int wi = (int)(g % words_per_block);
+    uint16_t v = (uint16_t)h;
+    if (wi == d_word) v = (uint16_t)(0x1C00u | (h & 0x3FFu));
+    else if (wi == dmin_word) v = (uint16_t)(0x1800u | (h & 0x3FFu));
+    dst[g] = v;
+}
+
+template <int TYPE, bool AVX2, int R>
+hipError_t launch_r(const MatvecArgs &a, hipStream_t s) {
+    const int grid = (a.rows + R - 1) / R;
+    const size_t lds = 2 * kThreads * sizeof(Rec) + (size_t)a.nblk * kQ8Bytes;
+    hipLaunchKernelGGL((matvec_kernel<TYPE, AVX2, R>), dim3(grid), dim3(kThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int TYPE, bool AVX2>
+hipError_t launch_t(const MatvecArgs &a, int r, hipStream_t s) {
+    switch (r) {
+        case 4: return launch_r<TYPE, AVX2, 4>(a, s);
+        case 8: return launch_r<TYPE, AVX2, 8>(a, s);
+        default: return launch_r<TYPE, AVX2, 16>(a, s);
+    }
+}
+
+uint64_t splitmix64_host(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+
+hipError_t launch_matvec(int type, bool avx2, const MatvecArgs &a, int rows_per_wg, hipStream_t s) {
+    if (a.rows <= 0 || a.nblk <= 0 || a.nblk > kMaxBlocks) return hipErrorInvalidValue;
+    if (type == kQ4K) return avx2 ? launch_t<kQ4K, true>(a, rows_per_wg, s) : launch_t<kQ4K, false>(a, rows_per_wg, s);
+    if (type == kQ6K) return avx2 ? launch_t<kQ6K, true>(a, rows_per_wg, s) : launch_t<kQ6K, false>(a, rows_per_wg, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, hipStream_t s) {
+    const int64_t nb = n / 256;
+    if (nb <= 0) return hipSuccess;
+    const int64_t grid = (nb + 3) / 4;
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_blocks(int type, int64_t nblocks, uint64_t seed, uint8_t *dst, hipStream_t s) {
+    if (nblocks <= 0) return hipSuccess;
+    const int wpb = (type == kQ4K ? kQ4Bytes : kQ6Bytes) / 2;
+    const int64_t n16 = nblocks * wpb;
+    const int64_t grid = (n16 + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(synth_blocks_kernel, dim3((unsigned)grid), dim3(kThreads), 0, s, (uint16_t *)dst, n16, wpb,
+                       type == kQ4K ? 0 : 104, type == kQ4K ? 1 : -1, splitmix64_host(seed));
+    return hipGetLastError();
+}
+
+hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, uint16_t *d, hipStream_t s) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t grid = (nblocks * 53 + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(q6k_split_kernel, dim3((unsigned)grid), dim3(kThreads), 0, s, (const uint16_t *)raw,
+                       nblocks, (uint32_t *)body, d);
+    return hipGetLastError();
+}
+
+}  // namespace kore_qmv_gpu

@@ -1,0 +1,163 @@
+"""Quantised matrix-vector product of kore on the MI355X (libkore_qmv.so).
+
+Mirrors kore's ``quant()`` / ``mv()`` pair (kore.cpp:1387-1394): activations
+are quantised to Q8_K blocks (``quantize_row_q8_K``, kore.cpp:422-446) and
+every row of a Q4_K or Q6_K weight matrix is dotted with them
+(``matvec_mt``, kore.cpp:649-682).  Results are kore's, bit for bit, in its
+AVX2 summation order (``avx2=True``, what kore runs on an AVX2/FMA CPU) or its
+scalar reference order (``avx2=False``)::
+
+    w = QMat(KORE_QMV_Q4_K, rows, cols, gguf_block_bytes)
+    xq = quantize(x)                 # kore's BlockQ8K records (Q8K_DTYPE)
+    out = w.matvec(xq)               # kore's matvec_mt(t, xq, out, avx2, nth)
+    out = w.mv(x)                    # quant() + mv()
+
+There is no CPU fallback: without the built library or a GPU every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkore_qmv.so")
+
+KORE_QMV_Q4_K, KORE_QMV_Q6_K = 12, 14
+BLOCK_BYTES = {KORE_QMV_Q4_K: 144, KORE_QMV_Q6_K: 210}
+KORE_QMV_OK, KORE_QMV_E_INVALID, KORE_QMV_E_UNSUPPORTED, KORE_QMV_E_HIP, KORE_QMV_E_NOMEM = 0, -1, -3, -4, -5
+
+# kore's BlockQ8K (kore.cpp:415-420)
+Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+assert Q8K_DTYPE.itemsize == 292
+
+_vp, _i, _i64 = C.c_void_p, C.c_int, C.c_int64
+
+
+class QmvInfo(C.Structure):
+    _fields_ = [("type", C.c_int), ("device", C.c_int), ("rows", C.c_int64), ("cols", C.c_int64),
+                ("weight_bytes", C.c_size_t), ("rows_per_wg", C.c_int)]
+
+
+SYMBOLS = [
+    ("kore_qmv_tensor_create", _i, [C.POINTER(_vp), _i, _i64, _i64, _vp, _i]),
+    ("kore_qmv_tensor_destroy", None, [_vp]),
+    ("kore_qmv_quantize", _i, [_vp, _i64, _vp]),
+    ("kore_qmv_quantize_dev", _i, [_vp, _i64, _vp, _vp]),
+    ("kore_qmv_matvec", _i, [_vp, _vp, _vp, _i]),
+    ("kore_qmv_matvec_dev", _i, [_vp, _vp, _vp, _i, _vp]),
+    ("kore_qmv_mv", _i, [_vp, _vp, _vp, _i]),
+    ("kore_qmv_last_error", C.c_char_p, [_vp]),
+    ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
+    ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),
+]
+
+_lib = None
+
+
+class QmvError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            from ._lib import LibraryMissing
+            raise LibraryMissing(f"{LIB_PATH} is not built; run `make -C kore_amd/csrc` (or __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SYMBOLS:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc: int, t=None):
+    if rc != KORE_QMV_OK:
+        raise QmvError(rc, lib().kore_qmv_last_error(t).decode())
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a).view(np.uint8) if np.asarray(a).dtype != np.uint8 else a,
+                                np.uint8).reshape(-1)
+
+
+def quantize(x) -> np.ndarray:
+    """kore's quantize_row_q8_K on the GPU: x (n floats, n % 256 == 0) ->
+    n/256 BlockQ8K records."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(max(x.size // 256, 1), Q8K_DTYPE)
+    _check(lib().kore_qmv_quantize(x.ctypes.data, x.size, out.ctypes.data))
+    return out[:x.size // 256]
+
+
+def quantize_dev(x_ptr: int, n: int, xq_ptr: int, stream=None) -> None:
+    _check(lib().kore_qmv_quantize_dev(x_ptr, n, xq_ptr, stream))
+
+
+def synth_dev(wtype: int, rows: int, cols: int, seed: int, dst_ptr: int, stream=None) -> None:
+    """Synthetic GGUF blocks straight into device memory (include/kore_qmv_synth.h)."""
+    _check(lib().kore_qmv_synth_dev(wtype, rows, cols, seed, dst_ptr, stream))
+
+
+class QMat:
+    """A device-resident Q4_K / Q6_K weight matrix (kore's Tensor)."""
+
+    def __init__(self, wtype: int, rows: int, cols: int, data=None, *, device_ptr: int | None = None):
+        self.handle = C.c_void_p()
+        self.type, self.rows, self.cols = wtype, rows, cols
+        if device_ptr is not None:
+            _check(lib().kore_qmv_tensor_create(C.byref(self.handle), wtype, rows, cols, device_ptr, 1))
+        else:
+            w = _u8(data)
+            bb = BLOCK_BYTES.get(wtype)
+            if bb is not None and cols % 256 == 0 and w.size != rows * (cols // 256) * bb:
+                raise ValueError(f"expected {rows * (cols // 256) * bb} weight bytes, got {w.size}")
+            _check(lib().kore_qmv_tensor_create(C.byref(self.handle), wtype, rows, cols, w.ctypes.data, 0))
+
+    def close(self):
+        if self.handle:
+            lib().kore_qmv_tensor_destroy(self.handle)
+            self.handle = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self) -> QmvInfo:
+        inf = QmvInfo()
+        _check(lib().kore_qmv_get_info(self.handle, C.byref(inf)), self.handle)
+        return inf
+
+    def matvec(self, xq: np.ndarray, avx2: bool = True) -> np.ndarray:
+        xq = np.ascontiguousarray(xq, Q8K_DTYPE)
+        if xq.size != self.cols // 256:
+            raise ValueError(f"xq must hold {self.cols // 256} blocks")
+        out = np.zeros(self.rows, np.float32)
+        _check(lib().kore_qmv_matvec(self.handle, xq.ctypes.data, out.ctypes.data, int(avx2)), self.handle)
+        return out
+
+    def mv(self, x, avx2: bool = True) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        if x.size != self.cols:
+            raise ValueError(f"x must hold {self.cols} floats")
+        out = np.zeros(self.rows, np.float32)
+        _check(lib().kore_qmv_mv(self.handle, x.ctypes.data, out.ctypes.data, int(avx2)), self.handle)
+        return out
+
+    def matvec_dev(self, xq_ptr: int, out_ptr: int, avx2: bool = True, stream=None) -> None:
+        _check(lib().kore_qmv_matvec_dev(self.handle, xq_ptr, out_ptr, int(avx2), stream), self.handle)

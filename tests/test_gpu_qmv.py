@@ -1,0 +1,248 @@
+"""GPU parity of the quantised matvec (libkore_qmv.so) through its C ABI.
+
+Bar: bit-identical to kore.  The Q8_K blocks must equal kore's
+quantize_row_q8_K byte for byte and every row result must equal kore's
+dot_q*_K_q8_K_avx2 (avx2=1) or dot_q*_K_q8_K_ref (avx2=0) bit for bit: on
+kore's own golden outputs (tests/golden/qmv_*.npz), against the oracle (the
+C restatement pinned to those outputs) on random shapes that exercise every
+workgroup layout and tail, and on the full Qwen2.5-7B matrix shapes.  Every
+test names its case before it touches the GPU.
+"""
+import ctypes as C
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+FIXTURES = sorted(f[4:-5] for f in os.listdir(GOLD) if f.startswith("qmv_") and f.endswith(".json"))
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _assert_bits(out, ref, what):
+    bad = np.flatnonzero(_bits(out) != _bits(ref))
+    assert bad.size == 0, (f"{what}: {bad.size} rows differ, first row {bad[0]}: "
+                           f"{out[bad[0]]!r} vs kore {ref[bad[0]]!r}")
+
+
+def _weights(wtype, rows, nblk, rng):
+    """Random blocks with finite f16 scales, some of them subnormal, zero or
+    negative."""
+    bb = oracle.BLOCK_BYTES[wtype]
+    w = rng.integers(0, 256, size=(rows, nblk, bb), dtype=np.uint8)
+    d = np.abs(rng.standard_normal((rows, nblk))) * 3e-3
+    d[rng.random((rows, nblk)) < 0.05] *= -1.0
+    d[rng.random((rows, nblk)) < 0.03] = 3e-6                  # f16 subnormal
+    d[rng.random((rows, nblk)) < 0.02] = 0.0
+    db = d.astype(np.float16).view(np.uint8).reshape(rows, nblk, 2)
+    if wtype == oracle.TYPE_Q4K:
+        w[:, :, 0:2] = db
+        w[:, :, 2:4] = (np.abs(rng.standard_normal((rows, nblk))) * 1e-3).astype(np.float16).view(
+            np.uint8).reshape(rows, nblk, 2)
+    else:
+        w[:, :, 208:210] = db
+    return w.reshape(-1)
+
+
+def _x(cols, rng):
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[rng.random(cols) < 0.01] *= 20.0
+    return x
+
+
+# ---------------------------------------------------------------- golden
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_golden_replay(name):
+    from kore_amd import qmv
+    man = json.load(open(os.path.join(GOLD, f"qmv_{name}.json")))
+    z = np.load(os.path.join(GOLD, f"qmv_{name}.npz"))
+    _say(f"qmv golden {name}: type {man['type']}, {man['rows']} x {man['cols']}")
+    xq = qmv.quantize(z["x"])
+    assert xq.view(np.uint8).tobytes() == z["xq"].tobytes(), "Q8_K blocks differ from kore's"
+    kore_xq = np.frombuffer(z["xq"].tobytes(), qmv.Q8K_DTYPE)
+    with qmv.QMat(man["type"], man["rows"], man["cols"], z["weights"]) as w:
+        _assert_bits(w.matvec(kore_xq, avx2=True), z["out_avx2"], f"{name} avx2")
+        _assert_bits(w.matvec(kore_xq, avx2=False), z["out_ref"], f"{name} scalar")
+        _assert_bits(w.mv(z["x"], avx2=True), z["out_avx2"], f"{name} mv avx2")
+        _assert_bits(w.mv(z["x"], avx2=False), z["out_ref"], f"{name} mv scalar")
+
+
+# ---------------------------------------------------------------- random shapes
+
+SHAPES = [(1, 1), (37, 3), (129, 14), (64, 74), (21, 128), (300, 17), (16, 16)]
+
+
+@pytest.mark.parametrize("rpw", [4, 8, 16])
+@pytest.mark.parametrize("wtype", [oracle.TYPE_Q4K, oracle.TYPE_Q6K])
+def test_random_shapes_vs_oracle(wtype, rpw, monkeypatch):
+    from kore_amd import qmv
+    monkeypatch.setenv("KORE_QMV_ROWS_PER_WG", str(rpw))
+    for si, (rows, nblk) in enumerate(SHAPES):
+        _say(f"qmv random type {wtype} rows_per_wg {rpw}: {rows} x {nblk * 256}")
+        rng = np.random.default_rng(1000 * wtype + 10 * rpw + si)
+        w = _weights(wtype, rows, nblk, rng)
+        x = _x(nblk * 256, rng)
+        xq = oracle.quantize_q8K(x)
+        with qmv.QMat(wtype, rows, nblk * 256, w) as m:
+            assert m.info().rows_per_wg == rpw
+            for avx2 in (True, False):
+                ref = oracle.qmatvec(wtype, w, rows, nblk * 256, xq, avx2=avx2)
+                _assert_bits(m.matvec(xq, avx2=avx2), ref, f"{rows}x{nblk} avx2={avx2}")
+
+
+# ---------------------------------------------------------------- quantiser
+
+def test_quantize_edge_cases():
+    from kore_amd import qmv
+    _say("qmv quantize edge cases")
+    rng = np.random.default_rng(77)
+    blocks = []
+    blocks.append(np.zeros(256))                                   # zero block
+    blocks.append(np.full(256, 0.3))                               # constant
+    b = rng.standard_normal(256); b[10], b[99] = -5.0, 5.0; blocks.append(b)    # tie: first wins
+    b = rng.standard_normal(256); b[10], b[99] = 5.0, -5.0; blocks.append(b)
+    blocks.append(rng.standard_normal(256) * 1e-39)                # subnormal inputs
+    b = rng.standard_normal(256) * 1e-41; b[3] = 1e-39; blocks.append(b)  # -127/max overflows: x86 int path
+    blocks.append(rng.standard_normal(256) * 3e38)                 # near FLT_MAX
+    b = rng.standard_normal(256); b[7] = np.nan; blocks.append(b)  # NaN never wins
+    b = rng.standard_normal(256); b[8] = np.inf; blocks.append(b)  # inf wins: iscale -0
+    b = np.round(rng.standard_normal(256) * 16) / 16; b[0] = -127 / 16; blocks.append(b)  # halves
+    b = rng.standard_normal(256); b[:128] = -0.0; blocks.append(b)
+    x = np.concatenate(blocks).astype(np.float32)
+    with np.errstate(all="ignore"):
+        ref = oracle.quantize_q8K(x)
+    got = qmv.quantize(x)
+    for i in range(len(blocks)):
+        assert got[i].tobytes() == ref[i].tobytes(), f"block {i} differs from kore's quantiser"
+
+
+def test_quantize_many_random_blocks():
+    from kore_amd import qmv
+    _say("qmv quantize 4096 random blocks")
+    rng = np.random.default_rng(78)
+    x = (rng.standard_normal(4096 * 256) * np.repeat(10.0 ** rng.uniform(-6, 6, 4096), 256)).astype(np.float32)
+    assert qmv.quantize(x).tobytes() == oracle.quantize_q8K(x).tobytes()
+
+
+# ---------------------------------------------------------------- device API
+
+def test_device_api_matches_host_api():
+    from kore_amd import hip, qmv
+    _say("qmv device-pointer API, Q6_K 200 x 4608")
+    rng = np.random.default_rng(79)
+    rows, cols = 200, 4608
+    w = _weights(oracle.TYPE_Q6K, rows, cols // 256, rng)
+    x = _x(cols, rng)
+    dx = hip.DeviceBuffer.from_array(x)
+    dq = hip.DeviceBuffer((cols // 256 * 292 + 3) // 4)
+    do = hip.DeviceBuffer(rows)
+    # the tensor from a device copy of the raw blocks
+    draw = hip.DeviceBuffer((w.size + 3) // 4)
+    hip.check(hip.lib().hipMemcpy(draw.ptr, w.ctypes.data, w.size, hip.H2D), "upload")
+    with qmv.QMat(oracle.TYPE_Q6K, rows, cols, device_ptr=draw.ptr) as m:
+        qmv.quantize_dev(dx.ptr, cols, dq.ptr)
+        for avx2 in (True, False):
+            m.matvec_dev(dq.ptr, do.ptr, avx2=avx2)
+            hip.synchronize()
+            _assert_bits(do.download(), m.mv(x, avx2=avx2), f"dev vs host avx2={avx2}")
+        # misaligned activations are refused before any launch
+        with pytest.raises(qmv.QmvError) as e:
+            m.matvec_dev(dq.ptr + 4, do.ptr)
+        assert e.value.code == qmv.KORE_QMV_E_INVALID
+    for b in (dx, dq, do, draw):
+        b.free()
+
+
+def _splitmix64(z):
+    z = (z + np.uint64(0x9E3779B97F4A7C15)).astype(np.uint64)
+    z = ((z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)).astype(np.uint64)
+    z = ((z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)).astype(np.uint64)
+    return z ^ (z >> np.uint64(31))
+
+
+def test_synth_matches_its_definition():
+    from kore_amd import hip, qmv
+    for wtype, rows, cols, seed in ((oracle.TYPE_Q4K, 3, 512, 5), (oracle.TYPE_Q6K, 5, 768, 6)):
+        _say(f"qmv synth type {wtype} {rows} x {cols}")
+        nbytes = rows * cols // 256 * oracle.BLOCK_BYTES[wtype]
+        buf = hip.DeviceBuffer((nbytes + 3) // 4)
+        qmv.synth_dev(wtype, rows, cols, seed, buf.ptr)
+        hip.synchronize()
+        got = np.zeros(nbytes, np.uint8)
+        hip.check(hip.lib().hipMemcpy(got.ctypes.data, buf.ptr, nbytes, hip.D2H), "download")
+        buf.free()
+        with np.errstate(over="ignore"):
+            key = _splitmix64(np.array([seed], np.uint64))[0]
+            h = _splitmix64(key ^ np.arange(nbytes // 2, dtype=np.uint64)).astype(np.uint64)
+        words = (h & np.uint64(0xFFFF)).astype(np.uint16)
+        wpb = oracle.BLOCK_BYTES[wtype] // 2
+        wi = np.arange(nbytes // 2) % wpb
+        low = (h & np.uint64(0x3FF)).astype(np.uint16)
+        if wtype == oracle.TYPE_Q4K:
+            words = np.where(wi == 0, 0x1C00 | low, np.where(wi == 1, 0x1800 | low, words))
+        else:
+            words = np.where(wi == 104, 0x1C00 | low, words)
+        assert np.array_equal(got.view(np.uint16), words.astype(np.uint16))
+
+
+# ---------------------------------------------------------------- 7B shapes
+
+# Qwen2.5-7B: n_embd 3584, n_ff 18944, 4 kv-heads x 128, vocab 152064
+SHAPES_7B = [
+    ("attn_q", oracle.TYPE_Q4K, 3584, 3584),
+    ("attn_k", oracle.TYPE_Q4K, 512, 3584),
+    ("attn_v", oracle.TYPE_Q6K, 512, 3584),
+    ("attn_output", oracle.TYPE_Q4K, 3584, 3584),
+    ("ffn_gate", oracle.TYPE_Q4K, 18944, 3584),
+    ("ffn_down", oracle.TYPE_Q6K, 3584, 18944),
+    ("ffn_down_q4k", oracle.TYPE_Q4K, 3584, 18944),
+    ("output", oracle.TYPE_Q6K, 152064, 3584),
+]
+
+
+@pytest.mark.parametrize("name,wtype,rows,cols", SHAPES_7B)
+def test_7b_matrix_every_row_bitwise(name, wtype, rows, cols):
+    from kore_amd import hip, qmv
+    _say(f"qmv 7B {name}: type {wtype}, {rows} x {cols}")
+    nbytes = rows * cols // 256 * oracle.BLOCK_BYTES[wtype]
+    raw = hip.DeviceBuffer((nbytes + 3) // 4)
+    qmv.synth_dev(wtype, rows, cols, 4242 + rows, raw.ptr)
+    hip.synchronize()
+    w = np.zeros(nbytes, np.uint8)
+    hip.check(hip.lib().hipMemcpy(w.ctypes.data, raw.ptr, nbytes, hip.D2H), "download")
+    x = _x(cols, np.random.default_rng(rows + cols))
+    with qmv.QMat(wtype, rows, cols, device_ptr=raw.ptr) as m:
+        raw.free()
+        xq = qmv.quantize(x)
+        ref_xq = oracle.quantize_q8K(x)
+        assert xq.tobytes() == ref_xq.tobytes()
+        for avx2 in (True, False):
+            _assert_bits(m.matvec(xq, avx2=avx2), oracle.qmatvec(wtype, w, rows, cols, ref_xq, avx2=avx2),
+                         f"{name} avx2={avx2}")
+
+
+def test_repeated_calls_are_identical():
+    from kore_amd import qmv
+    _say("qmv repeated calls, Q4_K 1000 x 3584")
+    rng = np.random.default_rng(80)
+    w = _weights(oracle.TYPE_Q4K, 1000, 14, rng)
+    x = _x(3584, rng)
+    with qmv.QMat(oracle.TYPE_Q4K, 1000, 3584, w) as m:
+        first = m.mv(x)
+        for _ in range(5):
+            assert np.array_equal(_bits(m.mv(x)), _bits(first))
