@@ -10,6 +10,12 @@ one kore_attn_decode_dev call (kore's per-layer attention block,
 kore.cpp:1405-1455), driven from C++ (libkore_attn_bench.so) so no Python
 runs between launches.
 
+Also reported (under "matvec"): the Q4_K/Q6_K x Q8_K matrix-vector products
+of one Qwen2.5-7B-shape token (libkore_qmv.so): 28 layers x (q, k, v, o, gate,
+up, down) plus the output head, 197 matrices / 4.37 GB of weights, each
+quant() + mv() pair of kore's forward() (kore.cpp:1418-1477), bit-identical
+to kore's AVX2 results; with kore's own multithreaded matvec timed on the host.
+
 Reported next to it: Qwen2.5-7B-shape causal prefill attention of a
 2048-token prompt at position 0 over 28 layers (kore.cpp:1503-1563), and the
 CPU restatement of kore's attention (bit-identical to kore's own code) timed
@@ -55,6 +61,37 @@ PF_N, PF_SEED = 2048, 3
 # append + prefill kernel.  Re-measure when a kernel changes.
 TRAFFIC_DECODE_BYTES = 19_078_000
 TRAFFIC_PREFILL_BYTES = 109_052_000
+# the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
+# of weights, activations and outputs algorithmic)
+TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_366_000}
+
+# Qwen2.5-7B matrix shapes of the matvec leg
+QMV_FF, QMV_VOCAB = 18944, 152064
+QMV_Q4K, QMV_Q6K = 12, 14
+QMV_SEED = 17
+
+
+def _more_bits(i: int, n: int) -> bool:
+    # layers whose attn_v and ffn_down a Q4_K_M file keeps in Q6_K (llama.cpp's
+    # use_more_bits rule); the others are Q4_K, like attn_q/k/o and ffn_gate/up
+    return i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2
+
+
+def qmv_token_matrices():
+    """(name, type, rows, cols) of every weight matrix one 7B token multiplies."""
+    mats = []
+    for l in range(NL):
+        hi = QMV_Q6K if _more_bits(l, NL) else QMV_Q4K
+        mats += [(f"blk.{l}.attn_q", QMV_Q4K, E, E), (f"blk.{l}.attn_k", QMV_Q4K, KVD, E),
+                 (f"blk.{l}.attn_v", hi, KVD, E), (f"blk.{l}.attn_output", QMV_Q4K, E, E),
+                 (f"blk.{l}.ffn_gate", QMV_Q4K, QMV_FF, E), (f"blk.{l}.ffn_up", QMV_Q4K, QMV_FF, E),
+                 (f"blk.{l}.ffn_down", hi, E, QMV_FF)]
+    mats.append(("output", QMV_Q6K, QMV_VOCAB, E))
+    return mats
+
+
+def qmv_weight_bytes(wtype: int, rows: int, cols: int) -> int:
+    return rows * (cols // 256) * (144 if wtype == QMV_Q4K else 210)
 
 
 def q_stream(layer): return (1 << 32) | layer
@@ -291,6 +328,184 @@ def gpu_other_workloads(quick: bool):
     return res
 
 
+class _KqbOp(C.Structure):
+    _fields_ = [("kind", C.c_int), ("n_t", C.c_int), ("t", C.c_int * 4), ("x", C.c_void_p), ("n", C.c_longlong),
+                ("xq", C.c_void_p), ("out", C.c_void_p * 4)]
+
+
+def _op(kind, tensors=(), x=None, n=0, xq=None, outs=()):
+    o = _KqbOp()
+    o.kind, o.n_t, o.x, o.n, o.xq = kind, len(tensors), x, n, xq
+    for k, t in enumerate(tensors):
+        o.t[k] = t
+    for k, p in enumerate(outs):
+        o.out[k] = p
+    return o
+
+
+def gpu_matvec(tokens: int, warmup: int):
+    """One 7B token's quant() + mv() sequence (kore.cpp:1418-1477) over 28
+    distinct layers plus the output head, replayed `tokens` times from C++."""
+    from kore_amd import hip, qmv
+    path = os.path.join(ROOT, "kore_amd", "libkore_qmv_bench.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run `make -C kore_amd/csrc`")
+    qmv.lib()
+    B = C.CDLL(path)
+    B.kqb_run.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                          C.POINTER(C.c_float), C.POINTER(C.c_double)]
+    mats = qmv_token_matrices()
+    biggest = max(qmv_weight_bytes(t, r, c) for _, t, r, c in mats)
+    raw = hip.DeviceBuffer((biggest + 3) // 4)
+    tensors, first_raw = [], None
+    print(f"[bench] matvec: creating {len(mats)} synthetic weight matrices", file=sys.stderr, flush=True)
+    for idx, (name, t, r, c) in enumerate(mats):
+        qmv.synth_dev(t, r, c, QMV_SEED * 1000 + idx, raw.ptr)
+        if idx == 0:   # kept for the bitwise check against kore's arithmetic
+            hip.synchronize()
+            first_raw = np.zeros(qmv_weight_bytes(t, r, c), np.uint8)
+            hip.check(hip.lib().hipMemcpy(first_raw.ctypes.data, raw.ptr, first_raw.size, hip.D2H), "download")
+        tensors.append(qmv.QMat(t, r, c, device_ptr=raw.ptr))
+    raw.free()
+    rng = np.random.default_rng(QMV_SEED)
+
+    def act(n):
+        x = rng.standard_normal(n).astype(np.float32)
+        x[rng.random(n) < 0.01] *= 20.0
+        return x
+
+    xs = [act(E) for _ in range(4)] + [act(QMV_FF)]
+    dx = [hip.DeviceBuffer.from_array(x) for x in xs]
+    dqE, dqF = hip.DeviceBuffer(E // 256 * 73), hip.DeviceBuffer(QMV_FF // 256 * 73)
+    outs = [hip.DeviceBuffer(r) for _, _, r, _ in mats]
+    # kore's forward(): quant(xb) -> q, k, v; quant(att) -> o; quant(xb) -> gate, up;
+    # quant(gate) -> down; quant(xb) -> output (kore.cpp:1418-1477).  Matrices that
+    # share an input go in one launch (kore_qmv_mv_group_dev), the quantisation
+    # fused into it where that is cheaper.
+    ops, op_mats = [], []
+    for l in range(NL):
+        b = 7 * l
+        for ts, x in (((b, b + 1, b + 2), dx[0]), ((b + 3,), dx[1]), ((b + 4, b + 5), dx[2]), ((b + 6,), dx[4])):
+            ops.append(_op(2, ts, x.ptr, outs=[outs[i].ptr for i in ts]))
+            op_mats.append(ts)
+    ops.append(_op(2, (7 * NL,), dx[3].ptr, outs=[outs[7 * NL].ptr]))
+    op_mats.append((7 * NL,))
+    arr = (_KqbOp * len(ops))(*ops)
+    handles = (C.c_void_p * len(tensors))(*[m.handle.value for m in tensors])
+    wall, region = C.c_double(0), C.c_float(0)
+
+    def run(n, op_ms=None, reg=None):
+        rc = B.kqb_run(arr, len(ops), handles, 1, n, None, op_ms, reg, C.byref(wall))
+        if rc != 0:
+            raise RuntimeError(f"kqb_run failed ({rc}): {qmv.lib().kore_qmv_last_error(None).decode()}")
+
+    if warmup:
+        run(warmup)
+    print(f"[bench] matvec: {tokens} timed tokens x {len(ops)} launches", file=sys.stderr, flush=True)
+    run(tokens, reg=C.byref(region))
+    wall_ms, region_ms = wall.value, region.value
+    # per-launch durations (a second pass with an event pair around every launch)
+    n_ev = min(tokens, 4)
+    op_ms = np.zeros(n_ev * len(ops), np.float32)
+    run(n_ev, op_ms=op_ms.ctypes.data)
+    # bitwise check of the first matrix against kore's arithmetic (the oracle)
+    got = outs[0].download()
+    for m in tensors:
+        m.close()
+    for b in dx + [dqE, dqF] + outs:
+        b.free()
+    return dict(mats=mats, op_mats=op_mats, wall_ms=wall_ms, region_ms=region_ms,
+                op_ms=op_ms.reshape(n_ev, len(ops)), first_raw=first_raw, first_x=xs[0], first_out=got)
+
+
+def matvec_report(g, tokens: int):
+    mats, op_mats = g["mats"], g["op_mats"]
+    wbytes = sum(qmv_weight_bytes(t, r, c) for _, t, r, c in mats)
+    tok_s = g["region_ms"] / 1e3 / tokens
+    per = {}
+    for i, ts in enumerate(op_mats):
+        parts = []
+        alg = 0
+        for ti in ts:
+            name, t, r, c = mats[ti]
+            parts.append(name.split(".")[-1] + ("" if name == "output" else ("_q6k" if t == QMV_Q6K else "_q4k")))
+            alg += qmv_weight_bytes(t, r, c) + r * 4
+        alg += mats[ts[0]][3] * 4          # the fp32 input, read once
+        key = "+".join(parts)
+        d = per.setdefault(key, {"launches_per_token": 0, "ms": [], "bytes": alg})
+        d["launches_per_token"] += 1
+        d["ms"].extend(g["op_ms"][:, i].tolist())
+    table = {}
+    for key, d in per.items():
+        us = float(np.mean(d["ms"])) * 1e3
+        gbs = d["bytes"] / (us / 1e6) / 1e9
+        table[key] = {"launches_per_token": d["launches_per_token"], "us_mean": round(us, 2),
+                      "algorithmic_bytes": d["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                      "us_per_token": round(us * d["launches_per_token"], 1)}
+    dom = max(table, key=lambda k: table[k]["us_per_token"])
+    return {
+        "workload": "Qwen2.5-7B-shape token, matvec half: 28 layers x (attn_q, attn_k, attn_v, attn_output, "
+                    "ffn_gate, ffn_up, ffn_down) + output head = 197 matrices, Q4_K with attn_v/ffn_down in Q6_K on "
+                    "14 layers (Q4_K_M's use_more_bits rule) and a Q6_K output head; each preceded by kore's Q8_K "
+                    "quantisation of its input; synthetic weights (hashed bytes, finite f16 scales), activations "
+                    "N(0,1) with 1% x20; kore's AVX2 summation order; per layer 4 calls: q+k+v and gate+up "
+                    "as one grouped launch each",
+        "weight_bytes_per_token": wbytes,
+        "launches_per_token": len(op_mats),
+        "ms_per_token_gpu": round(tok_s * 1e3, 4),
+        "ms_per_token_wall": round(g["wall_ms"] / tokens, 4),
+        "weight_gbs": round(wbytes / tok_s / 1e9, 1),
+        "weight_frac_of_hbm_peak": round(wbytes / tok_s / 1e9 / HBM_PEAK_GBS, 4),
+        "tokens": tokens,
+        "per_matrix": table,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": table[dom]["frac"], "traffic": TRAFFIC_MATVEC_BYTES.get(dom)},
+    }
+
+
+def cpu_matvec(seconds: float, threads: int):
+    """kore's own quant() + mv() (oracle/_ref/kore_qmv_ref, built from
+    kore.cpp) on the 7B ffn_gate shape, cycling over 16 copies so the weights
+    come from DRAM; falls back to the oracle's restatement (one thread) where
+    that build is absent."""
+    import struct
+    import subprocess
+    import tempfile
+
+    import oracle
+    rows, cols = QMV_FF, E
+    rng = np.random.default_rng(5)
+    w = rng.integers(0, 256, size=(rows, cols // 256, 144), dtype=np.uint8)
+    w[:, :, 0:2] = np.frombuffer(np.float16(3e-3).tobytes(), np.uint8)
+    w[:, :, 2:4] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
+    x = rng.standard_normal(cols).astype(np.float32)
+    if os.path.exists(oracle.REF_QMV_BIN):
+        with tempfile.TemporaryDirectory() as td:
+            job = os.path.join(td, "job.bin")
+            with open(job, "wb") as f:
+                f.write(struct.pack("<3i", QMV_Q4K, rows, cols))
+                f.write(w.tobytes())
+                f.write(x.tobytes())
+            r = subprocess.run([oracle.REF_QMV_BIN, "--time", str(threads), str(seconds), "16", job],
+                               capture_output=True, text=True, check=True)
+        j = json.loads(r.stdout)
+        gbs = j["weight_bytes"] * j["reps"] / j["seconds"] / 1e9
+        return {"value": round(gbs, 2), "unit": "GB/s", "cores": j["threads"], "kind": "reference",
+                "sample": f"kore's own quantize_row_q8_K + matvec_mt (kore.cpp:422-446, 677-682, AVX2 dot "
+                          f"products: {bool(j['avx2'])}) built from kore.cpp with kore's flags, {j['threads']} "
+                          f"threads, on the 7B ffn_gate shape ({rows} x {cols} Q4_K, 38.2 MB) cycling over 16 "
+                          f"copies: {j['reps']} matvecs in {j['seconds']:.1f} s; host {_cpu_model()}"}
+    xq = oracle.quantize_q8K(x)
+    t0, n = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        oracle.qmatvec(QMV_Q4K, w, rows, cols, xq, avx2=True)
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": round(w.size * n / el / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"the oracle's restatement of kore's AVX2 Q4_K dot product, one thread, 7B ffn_gate "
+                      f"shape, {n} matvecs in {el:.1f} s; host {_cpu_model()}"}
+
+
 # ------------------------------------------------------------------ CPU legs
 
 def _rel_err(out, ref):
@@ -382,6 +597,12 @@ def main(argv=None):
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the 0.5B / 3B / 1.5B workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="decode time budget of the CPU sample")
+    ap.add_argument("--no-matvec", action="store_true", help="skip the 7B-token matvec leg")
+    ap.add_argument("--matvec-only", action="store_true", help="run only the matvec leg (for profiling)")
+    ap.add_argument("--matvec-tokens", type=int, default=10, help="timed 7B tokens of the matvec leg")
+    ap.add_argument("--matvec-warmup", type=int, default=2)
+    ap.add_argument("--cpu-threads", type=int, default=16,
+                    help="threads of kore's own matvec in the CPU baseline (the GPU box's CPU share)")
     ap.add_argument("--cpu-prefill-layers", type=int, default=2)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 8 device-to-device copies of 256 MiB (the runtime's copy kernel), "
@@ -409,11 +630,16 @@ def main(argv=None):
     clk = C.c_int(0)
     hip.lib().hipDeviceGetAttribute(C.byref(clk), 5, 0)   # hipDeviceAttributeClockRate (kHz)
 
+    if args.matvec_only:
+        g = gpu_matvec(args.matvec_tokens, args.matvec_warmup)
+        print(json.dumps({"matvec": matvec_report(g, args.matvec_tokens)}), flush=True)
+        return 0
     pf = None
     if not args.no_prefill:
         pf = gpu_prefill(args.prefill_steps, args.prefill_warmup)
     dec = gpu_decode(args.steps, args.warmup)
     other = None if args.no_other else gpu_other_workloads(quick=args.steps < 64)
+    mv = None if args.no_matvec else gpu_matvec(args.matvec_tokens, args.matvec_warmup)
 
     K, W = args.steps, args.warmup
     total_bytes = sum(decode_bytes(DEC_POS0 + s + 1) for s in range(K)) * NL
@@ -481,6 +707,8 @@ def main(argv=None):
         }
     if other is not None:
         res["other_workloads"] = other
+    if mv is not None:
+        res["matvec"] = matvec_report(mv, args.matvec_tokens)
     if not args.no_cpu:
         print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
               flush=True)
@@ -497,6 +725,14 @@ def main(argv=None):
         }
         res["parity"] = {"decode_max_rel_err": cd["max_rel_err"], "decode_kv_bitwise": cd["kv_bitwise"],
                          "tolerance": 1e-4}
+        if mv is not None:
+            import oracle
+            print(f"[bench] cpu baseline: kore's matvec, {args.cpu_threads} threads", file=sys.stderr, flush=True)
+            res["matvec"]["cpu_baseline"] = cpu_matvec(args.cpu_seconds, args.cpu_threads)
+            t, r, c = mv["mats"][0][1:]
+            ref = oracle.qmatvec(t, mv["first_raw"], r, c, oracle.quantize_q8K(mv["first_x"]), avx2=True)
+            res["parity"]["matvec_first_matrix_bitwise"] = bool(
+                np.array_equal(ref.view(np.uint32), mv["first_out"].view(np.uint32)))
         if pf is not None:
             print(f"[bench] cpu baseline: prefill sample ({args.cpu_prefill_layers} layers)", file=sys.stderr,
                   flush=True)

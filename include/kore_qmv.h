@@ -76,7 +76,7 @@ KORE_QMV_API void kore_qmv_tensor_destroy(kore_qmv_tensor_t t);
  * n/256 BlockQ8K records in xq.  Host buffers; runs on the current device. */
 KORE_QMV_API int kore_qmv_quantize(const float *x, int64_t n, void *xq);
 
-/* Same with device buffers on the current device; xq 16-byte aligned. */
+/* Same with device buffers on the current device; x and xq 16-byte aligned. */
 KORE_QMV_API int kore_qmv_quantize_dev(const float *x, int64_t n, void *xq, void *stream);
 
 /* out[r] = row r . xq for every row (matvec_mt, kore.cpp:677-682); xq holds
@@ -91,6 +91,19 @@ KORE_QMV_API int kore_qmv_matvec_dev(kore_qmv_tensor_t t, const void *xq, float 
  * out[rows] out.  Host buffers. */
 KORE_QMV_API int kore_qmv_mv(kore_qmv_tensor_t t, const float *x, float *out, int avx2);
 
+/* Same with device buffers: x[cols] (16-byte aligned) -> out[rows].  The
+ * quantisation runs inside the matvec launch when that is cheaper, else as a
+ * launch of its own into a buffer of the tensor (so calls on one tensor from
+ * different streams must not overlap).  Results equal quant() + mv(). */
+KORE_QMV_API int kore_qmv_mv_dev(kore_qmv_tensor_t t, const float *x, float *out, int avx2, void *stream);
+
+/* n (1..4) matrices with the same cols and input x in one launch: kore's
+ * quant() followed by mv() of q, k and v (kore.cpp:1418-1421) or of gate and
+ * up (kore.cpp:1462-1464).  outs[k] receives tensors[k]'s rows.  Same results
+ * as n separate kore_qmv_mv_dev calls. */
+KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *tensors, const float *x,
+                                       float *const *outs, int avx2, void *stream);
+
 /* Text of the last failure on this tensor (or, with NULL, of the last failed
  * call without a tensor on this thread).  Never NULL. */
 KORE_QMV_API const char *kore_qmv_last_error(kore_qmv_tensor_t t);
@@ -101,7 +114,7 @@ typedef struct kore_qmv_info {
     int device;
     int64_t rows, cols;
     size_t weight_bytes;     /* bytes one matvec streams from HBM (kore's block bytes) */
-    int rows_per_wg;         /* rows per workgroup of the matvec kernel (4, 8 or 16)   */
+    int rows_per_wave;       /* rows one wave of the matvec kernel owns (1 .. 16)      */
 } kore_qmv_info;
 KORE_QMV_API int kore_qmv_get_info(kore_qmv_tensor_t t, kore_qmv_info *info);
 

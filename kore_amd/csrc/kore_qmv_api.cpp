@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -20,9 +21,11 @@ struct kore_qmv_tensor {
     int device = 0;
     int64_t rows = 0, cols = 0;
     int nblk = 0;
-    int rows_per_wg = 16;
+    int rows_per_wave = 16;
+    int num_cu = 0;
     uint8_t *w = nullptr;      // Q4_K blocks or Q6_K bodies
     uint16_t *wd = nullptr;    // Q6_K scales
+    uint8_t *xq = nullptr;     // Q8_K blocks of the activations when kore_qmv_mv_dev quantises apart
     size_t weight_bytes = 0;
     std::string error;
 };
@@ -76,17 +79,36 @@ hipError_t host_path(int dev, size_t need, HostPath **out) {
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Rows per workgroup: as many as still give every CU four workgroups or more;
-// fewer rows spread each row's blocks over more lanes.
-int pick_rows_per_wg(int64_t rows, int num_cu) {
-    if (const char *env = getenv("KORE_QMV_ROWS_PER_WG")) {
+// Rows per wave: as many as still give every SIMD of the device (four per
+// CU) two waves or more; with fewer rows each wave spreads a row's blocks
+// over more lanes.
+int pick_rows_per_wave(int64_t rows, int num_cu) {
+    if (const char *env = getenv("KORE_QMV_ROWS_PER_WAVE")) {
         const int r = atoi(env);
-        if (r == 4 || r == 8 || r == 16) return r;
+        if (r == 1 || r == 2 || r == 4 || r == 8 || r == 16) return r;
     }
-    const int64_t want = 4LL * num_cu;
-    if (rows / 16 >= want) return 16;
-    if (rows / 8 >= want) return 8;
-    return 4;
+    const int64_t want = 8LL * std::max(num_cu, 1);
+    for (int r = 16; r > 1; r /= 2)
+        if (rows / r >= want) return r;
+    return 1;
+}
+
+// Workgroups of one matvec launch: one per tile of 4 x rows-per-wave rows
+// (0), or about k per CU, each walking a contiguous run of tiles.
+int max_workgroups(int num_cu) {
+    if (const char *env = getenv("KORE_QMV_WGS_PER_CU")) {
+        const int k = atoi(env);
+        if (k > 0 && k <= 64) return k * num_cu;
+    }
+    return 0;
+}
+
+// Quantise inside the matvec workgroups (one launch instead of two) when
+// every workgroup's share of it is small: few blocks per row and not so many
+// workgroups that re-reading the activations costs more than a launch.
+bool fuse_quantisation(int nblk, int64_t workgroups) {
+    if (const char *env = getenv("KORE_QMV_FUSE")) return atoi(env) != 0;
+    return nblk <= 16 && workgroups * nblk <= 65536;
 }
 
 int check_dev_ptr(kore_qmv_tensor *t, const void *p, size_t align, const char *what) {
@@ -119,6 +141,7 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
         g_error = t->error;
         if (t->w) (void)hipFree(t->w);
         if (t->wd) (void)hipFree(t->wd);
+        if (t->xq) (void)hipFree(t->xq);
         delete t;
         return code;
     };
@@ -131,7 +154,9 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
     int num_cu = 0;
     e = hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, t->device);
     if (e != hipSuccess) return bail(hip_fail(t, e, "hipDeviceGetAttribute"));
-    t->rows_per_wg = pick_rows_per_wg(rows, num_cu);
+    t->num_cu = num_cu;
+    t->rows_per_wave = pick_rows_per_wave(rows, num_cu);
+    if ((e = hipMalloc(&t->xq, (size_t)t->nblk * kQ8Bytes)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
 
     const int64_t nblocks = rows * t->nblk;
     const size_t bb = type == KORE_QMV_Q4_K ? kQ4Bytes : kQ6Bytes;
@@ -171,13 +196,14 @@ KORE_QMV_API void kore_qmv_tensor_destroy(kore_qmv_tensor_t t) {
     if (cur != t->device) (void)hipSetDevice(t->device);
     if (t->w) (void)hipFree(t->w);
     if (t->wd) (void)hipFree(t->wd);
+    if (t->xq) (void)hipFree(t->xq);
     if (cur >= 0 && cur != t->device) (void)hipSetDevice(cur);
     delete t;
 }
 
 KORE_QMV_API int kore_qmv_quantize_dev(const float *x, int64_t n, void *xq, void *stream) {
     if (n <= 0 || n % 256 != 0) return fail(nullptr, KORE_QMV_E_INVALID, "n must be a positive multiple of 256");
-    if (int rc = check_dev_ptr(nullptr, x, 4, "x")) return rc;
+    if (int rc = check_dev_ptr(nullptr, x, 16, "x")) return rc;
     if (int rc = check_dev_ptr(nullptr, xq, 16, "xq")) return rc;
     hipError_t e = launch_quantize_q8k(x, n, (uint8_t *)xq, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(nullptr, e, "quantize launch");
@@ -201,14 +227,63 @@ KORE_QMV_API int kore_qmv_quantize(const float *x, int64_t n, void *xq) {
     return KORE_QMV_OK;
 }
 
+static MatDesc desc_of(kore_qmv_tensor *t, float *out) {
+    return MatDesc{t->w, t->wd, out, (int)t->rows, t->type, 0, 0};
+}
+
+// One grouped launch: xq given (fused = false) or x quantised in the kernel.
+static int launch_group(int n, kore_qmv_tensor *const *ts, const void *xq, const float *x, float *const *outs,
+                        int avx2, hipStream_t s) {
+    GroupArgs a{};
+    int64_t rows = 0;
+    for (int k = 0; k < n; ++k) {
+        a.m[k] = desc_of(ts[k], outs[k]);
+        rows += ts[k]->rows;
+    }
+    a.n_mat = n;
+    a.nblk = ts[0]->nblk;
+    a.xq = (const uint8_t *)xq;
+    a.x = x;
+    const int r = n == 1 ? ts[0]->rows_per_wave : pick_rows_per_wave(rows, ts[0]->num_cu);
+    hipError_t e = launch_matvec_group(avx2 != 0, a, r, max_workgroups(ts[0]->num_cu), s);
+    if (e != hipSuccess) return hip_fail(ts[0], e, "matvec launch");
+    return KORE_QMV_OK;
+}
+
 KORE_QMV_API int kore_qmv_matvec_dev(kore_qmv_tensor_t t, const void *xq, float *out, int avx2, void *stream) {
     if (!t) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
     if (int rc = check_dev_ptr(t, xq, 16, "xq")) return rc;
     if (int rc = check_dev_ptr(t, out, 4, "out")) return rc;
-    MatvecArgs a{t->w, t->wd, (const uint8_t *)xq, out, (int)t->rows, t->nblk};
-    hipError_t e = launch_matvec(t->type, avx2 != 0, a, t->rows_per_wg, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(t, e, "matvec launch");
-    return KORE_QMV_OK;
+    return launch_group(1, &t, xq, nullptr, &out, avx2, (hipStream_t)stream);
+}
+
+KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *ts, const float *x, float *const *outs,
+                                       int avx2, void *stream) {
+    if (n < 1 || n > kMaxGroup || !ts || !outs)
+        return fail(nullptr, KORE_QMV_E_INVALID, "n must be 1..4 with tensors and outputs");
+    for (int k = 0; k < n; ++k) {
+        if (!ts[k]) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
+        if (ts[k]->cols != ts[0]->cols || ts[k]->device != ts[0]->device)
+            return fail(ts[0], KORE_QMV_E_INVALID, "tensors of a group must share cols and device");
+        if (int rc = check_dev_ptr(ts[0], outs[k], 4, "out")) return rc;
+    }
+    kore_qmv_tensor *t0 = ts[0];
+    if (int rc = check_dev_ptr(t0, x, 16, "x")) return rc;
+    int64_t rows = 0;
+    for (int k = 0; k < n; ++k) rows += ts[k]->rows;
+    const int r = n == 1 ? t0->rows_per_wave : pick_rows_per_wave(rows, t0->num_cu);
+    int64_t wgs = 0;
+    for (int k = 0; k < n; ++k) wgs += (ts[k]->rows + 4 * r - 1) / (4 * r);
+    if (const int cap = max_workgroups(t0->num_cu)) wgs = std::min<int64_t>(wgs, cap);
+    hipStream_t s = (hipStream_t)stream;
+    if (fuse_quantisation(t0->nblk, wgs)) return launch_group(n, ts, nullptr, x, outs, avx2, s);
+    hipError_t e = launch_quantize_q8k(x, t0->cols, t0->xq, s);
+    if (e != hipSuccess) return hip_fail(t0, e, "quantize launch");
+    return launch_group(n, ts, t0->xq, nullptr, outs, avx2, s);
+}
+
+KORE_QMV_API int kore_qmv_mv_dev(kore_qmv_tensor_t t, const float *x, float *out, int avx2, void *stream) {
+    return kore_qmv_mv_group_dev(1, &t, x, &out, avx2, stream);
 }
 
 static int matvec_host(kore_qmv_tensor_t t, const float *x, const void *xq, float *out, int avx2) {
@@ -220,12 +295,12 @@ static int matvec_host(kore_qmv_tensor_t t, const float *x, const void *xq, floa
     uint8_t *dout = (uint8_t *)h->buf, *dq = dout + ob, *dx = dq + align256(qb);
     if (x) {
         QMV_TRY(t, hipMemcpyAsync(dx, x, (size_t)t->cols * 4, hipMemcpyHostToDevice, h->stream));
-        QMV_TRY(t, launch_quantize_q8k((const float *)dx, t->cols, dq, h->stream));
+        float *o = (float *)dout;
+        if (int rc = kore_qmv_mv_group_dev(1, &t, (const float *)dx, &o, avx2, h->stream)) return rc;
     } else {
         QMV_TRY(t, hipMemcpyAsync(dq, xq, qb, hipMemcpyHostToDevice, h->stream));
+        if (int rc = launch_group(1, &t, dq, nullptr, (float *const *)&dout, avx2, h->stream)) return rc;
     }
-    MatvecArgs a{t->w, t->wd, dq, (float *)dout, (int)t->rows, t->nblk};
-    QMV_TRY(t, launch_matvec(t->type, avx2 != 0, a, t->rows_per_wg, h->stream));
     QMV_TRY(t, hipMemcpyAsync(out, dout, (size_t)t->rows * 4, hipMemcpyDeviceToHost, h->stream));
     QMV_TRY(t, hipStreamSynchronize(h->stream));
     return KORE_QMV_OK;
@@ -264,7 +339,7 @@ KORE_QMV_API int kore_qmv_get_info(kore_qmv_tensor_t t, kore_qmv_info *info) {
     info->rows = t->rows;
     info->cols = t->cols;
     info->weight_bytes = t->weight_bytes;
-    info->rows_per_wg = t->rows_per_wg;
+    info->rows_per_wave = t->rows_per_wave;
     return KORE_QMV_OK;
 }
 

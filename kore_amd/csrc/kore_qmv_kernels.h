@@ -26,21 +26,40 @@ constexpr int kMaxBlocks = 128;   // cols <= 32768: the staged activations fit i
 
 enum WeightType { kQ4K = 12, kQ6K = 14 };
 
-// Rows are processed by workgroups of 256 threads; a workgroup owns `rows_per_wg`
-// consecutive rows (4, 8 or 16) and walks their blocks in steps.
-struct MatvecArgs {
+// Rows are processed by waves: a wave owns `rows_per_wave` rows (1, 2, 4, 8
+// or 16) of one matrix and walks their blocks in order; the four waves of a
+// 256-thread workgroup take consecutive row groups and share the activations.
+// One launch may cover up to kMaxGroup matrices that multiply the same
+// activations (kore's q/k/v and gate/up matvecs share one quant(),
+// kore.cpp:1418-1421, 1462-1464).
+constexpr int kMaxGroup = 4;
+
+struct MatDesc {
     const uint8_t *w;        // Q4_K blocks, or the Q6_K 208-byte bodies
     const uint16_t *wd;      // Q6_K f16 scales (nullptr for Q4_K)
-    const uint8_t *xq;       // nblk BlockQ8K records
     float *out;              // [rows]
     int rows;
-    int nblk;                // cols / 256
+    int type;                // kQ4K or kQ6K
+    int wg_begin;            // first workgroup of this matrix   (set by the launcher)
+    int wg_count;            // its number of workgroups          (set by the launcher)
 };
 
-// out[r] = row r . xq with kore's summation: avx2 = true follows
-// dot_q*_K_q8_K_avx2 (kore.cpp:535-632), false dot_q*_K_q8_K_ref
-// (kore.cpp:450-506).  Bit-identical to kore's results in both orders.
-hipError_t launch_matvec(int type, bool avx2, const MatvecArgs &a, int rows_per_wg, hipStream_t s);
+struct GroupArgs {
+    MatDesc m[kMaxGroup];
+    int n_mat;
+    int nblk;                // cols / 256, shared by the group
+    const uint8_t *xq;       // nblk BlockQ8K records (16-byte aligned), or
+    const float *x;          // nblk*256 floats (16-byte aligned) that every workgroup
+                             // quantises into LDS itself (then xq is unused)
+};
+
+// out[r] = row r . xq for every matrix of the group, with kore's summation:
+// avx2 = true follows dot_q*_K_q8_K_avx2 (kore.cpp:535-632), false
+// dot_q*_K_q8_K_ref (kore.cpp:450-506).  Bit-identical to kore's results in
+// both orders, with or without the fused quantisation.  Tiles are 4 x
+// rows_per_wave rows; about max_wgs workgroups (0: one per tile) share them,
+// each a contiguous run.
+hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int max_wgs, hipStream_t s);
 
 // kore's quantize_row_q8_K (kore.cpp:422-446): x[n] -> n/256 BlockQ8K records.
 hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, hipStream_t s);

@@ -14,6 +14,7 @@
 // be spread over all lanes without changing a single rounding.
 #include "kore_qmv_kernels.h"
 
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 
@@ -21,6 +22,11 @@ namespace kore_qmv_gpu {
 namespace {
 
 constexpr int kThreads = 256;
+
+// Steps of weight loads in flight per thread.
+#ifndef KQMV_DEPTH
+#define KQMV_DEPTH 2
+#endif
 
 __device__ __forceinline__ float f16_bits(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -41,64 +47,83 @@ __device__ __forceinline__ float quad_xor2f(float v) { return __int_as_float(qua
 
 // ------------------------------------------------------------------ Q8_K
 
-// One wave per 256-value block: lane l owns values 4l .. 4l+3.
-__global__ __launch_bounds__(kThreads) void quantize_q8k_kernel(const float *__restrict__ x,
-                                                                uint8_t *__restrict__ xq, int64_t nblocks) {
-    const int lane = threadIdx.x & 63;
-    const int64_t blk = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    if (blk >= nblocks) return;
-    const float *xb = x + blk * 256 + 4 * lane;
-    float v[4];
+// Row-of-16 DPP moves: lane i of each 16-lane row reads lane i ^ 1, i ^ 2
+// (quad permutations) or lane (i - 4) / (i - 8) mod 16 (row rotations).
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+
+// kore's quantisation of one 256-value block (kore.cpp:422-446) by the 16
+// lanes of a DPP row: lane m owns values 16m .. 16m+15 (x 16-byte aligned),
+// which are also exactly bsums[m].  Writes the 292-byte BlockQ8K record.
+__device__ __forceinline__ void quantize_block(const float *xb, int m, uint8_t *rec) {
+    float v[16];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = xb[e];
+    for (int k = 0; k < 4; ++k) {
+        const float4 f = *(const float4 *)(xb + 16 * m + 4 * k);
+        v[4 * k] = f.x;
+        v[4 * k + 1] = f.y;
+        v[4 * k + 2] = f.z;
+        v[4 * k + 3] = f.w;
+    }
     // kore keeps the first value of largest magnitude, starting from amax = 0
     // with a strict comparison (kore.cpp:424-428): the largest |x| wins, ties
     // go to the lowest index, NaN and zeros are never chosen.
     float best = 0.f, bval = 0.f;
     int bidx = 256;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 16; ++e) {
         const float ax = fabsf(v[e]);
         if (ax > best) {
             best = ax;
             bval = v[e];
-            bidx = 4 * lane + e;
+            bidx = 16 * m + e;
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ob = __shfl_xor(best, off);
-        const float ov = __shfl_xor(bval, off);
-        const int oi = __shfl_xor(bidx, off);
+    auto merge = [&](float ob, float ov, int oi) {
         if (ob > best || (ob == best && oi < bidx)) {
             best = ob;
             bval = ov;
             bidx = oi;
         }
-    }
-    uint8_t *rec = xq + blk * kQ8Bytes;
-    uint32_t packed = 0;
-    int sum4 = 0;
+    };
+    merge(__int_as_float(dpp<0xB1>(__float_as_int(best))), __int_as_float(dpp<0xB1>(__float_as_int(bval))),
+          dpp<0xB1>(bidx));
+    merge(__int_as_float(dpp<0x4E>(__float_as_int(best))), __int_as_float(dpp<0x4E>(__float_as_int(bval))),
+          dpp<0x4E>(bidx));
+    merge(__int_as_float(dpp<0x124>(__float_as_int(best))), __int_as_float(dpp<0x124>(__float_as_int(bval))),
+          dpp<0x124>(bidx));
+    merge(__int_as_float(dpp<0x128>(__float_as_int(best))), __int_as_float(dpp<0x128>(__float_as_int(bval))),
+          dpp<0x128>(bidx));
+    uint32_t packed[4] = {0, 0, 0, 0};
+    int bsum = 0;
     float d = 0.f;
     if (best != 0.f) {
         const float iscale = -127.0f / bval;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 16; ++e) {
             // (int) of an out-of-range or NaN value is x86's 0x80000000 in kore
             const float t = rintf(iscale * v[e]);
             int q = fabsf(t) < 2147483648.0f ? (int)t : INT_MIN;
             q = q > 127 ? 127 : q;
             const int q8 = (int)(int8_t)(q & 0xFF);
-            packed |= (uint32_t)(q8 & 0xFF) << (8 * e);
-            sum4 += q8;
+            packed[e >> 2] |= (uint32_t)(q8 & 0xFF) << (8 * (e & 3));
+            bsum += q8;
         }
         d = 1.0f / iscale;
     }
-    *(uint32_t *)(rec + 4 + 4 * lane) = packed;
-    sum4 += __shfl_xor(sum4, 1);
-    sum4 += __shfl_xor(sum4, 2);
-    if ((lane & 3) == 0) *(int16_t *)(rec + 260 + 2 * (lane >> 2)) = (int16_t)sum4;
-    if (lane == 0) *(float *)rec = d;
+    uint32_t *qw = (uint32_t *)(rec + 4 + 16 * m);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qw[k] = packed[k];
+    *(int16_t *)(rec + 260 + 2 * m) = (int16_t)bsum;
+    if (m == 0) *(float *)rec = d;
+}
+
+// Sixteen blocks per workgroup, one per 16-lane row.
+__global__ __launch_bounds__(kThreads) void quantize_q8k_kernel(const float *__restrict__ x,
+                                                                uint8_t *__restrict__ xq, int64_t nblocks) {
+    const int64_t blk = (int64_t)blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+    if (blk >= nblocks) return;
+    quantize_block(x + blk * 256, threadIdx.x & 15, xq + blk * kQ8Bytes);
 }
 
 // ------------------------------------------------------------------ units
@@ -118,8 +143,7 @@ struct Q8View {
 struct Q4Raw { uint4 hdr; uint2 qs[4]; };
 struct Q6Raw { uint2 a[2], b[2], h[2]; uint4 sc; uint32_t d; };
 
-__device__ __forceinline__ Q4Raw load_q4(const uint8_t *w, int64_t unit, int j) {
-    const uint8_t *b = w + unit * kQ4Bytes;
+__device__ __forceinline__ Q4Raw load_q4(const uint8_t *b, int j) {
     Q4Raw r;
     r.hdr = *(const uint4 *)b;
 #pragma unroll
@@ -127,8 +151,7 @@ __device__ __forceinline__ Q4Raw load_q4(const uint8_t *w, int64_t unit, int j) 
     return r;
 }
 
-__device__ __forceinline__ Q6Raw load_q6(const uint8_t *w, const uint16_t *wd, int64_t unit, int j) {
-    const uint8_t *b = w + unit * kQ6Body;
+__device__ __forceinline__ Q6Raw load_q6(const uint8_t *b, const uint16_t *dp, int j) {
     Q6Raw r;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -137,7 +160,7 @@ __device__ __forceinline__ Q6Raw load_q6(const uint8_t *w, const uint16_t *wd, i
         r.h[h] = *(const uint2 *)(b + 128 + 32 * h + 8 * j);
     }
     r.sc = *(const uint4 *)(b + 192);
-    r.d = wd[unit];
+    r.d = *dp;
     return r;
 }
 
@@ -156,9 +179,11 @@ __device__ __forceinline__ int q4_scale(const uint4 &h, int j) {
     return ((h.w >> s) & 0x0F) | (((h.y >> (s + 6)) & 3) << 4);
 }
 __device__ __forceinline__ int q4_min(const uint4 &h, int j) {
-    if (j < 4) return (h.z >> (8 * j)) & 63;
-    const int s = 8 * (j - 4);
-    return ((h.w >> (s + 4)) & 0x0F) | (((h.z >> (s + 6)) & 3) << 4);
+    // j may differ between lanes: both forms, then a select (no branch)
+    const int s = 8 * (j & 3);
+    const int lo = (h.z >> s) & 63;
+    const int hi = ((h.w >> (s + 4)) & 0x0F) | (((h.z >> (s + 6)) & 3) << 4);
+    return j < 4 ? lo : hi;
 }
 
 // Part j of a Q4_K unit: AVX2 lanes k = 2j, 2j+1 hold bytes 4k..4k+3 of each
@@ -241,36 +266,57 @@ __device__ __forceinline__ Rec part_q6(const Q6Raw &r, const Q8View &x, int i, i
 
 // ------------------------------------------------------------------ matvec
 
-// Workgroup: R rows, P = 64 / R blocks per step.  Thread t: part j = t % 4,
-// row (t / 4) % R, block phase t / (4R); its record lands in recs[t].
-template <int TYPE, bool AVX2, int R>
-__global__ __launch_bounds__(kThreads) void matvec_kernel(MatvecArgs a) {
-    constexpr int P = 64 / R;
-    extern __shared__ __align__(16) uint8_t smem[];
-    Rec *recs = (Rec *)smem;                               // [2][256]
-    uint8_t *xs = smem + 2 * kThreads * sizeof(Rec);       // nblk BlockQ8K records
+// Wave layout: RW rows of one matrix, P = 16 / RW blocks per step, four parts
+// per unit.  Lane l: part j = l % 4, row (l / 4) % RW, block phase l / (4 RW).
+// A workgroup's four waves take consecutive row groups of a tile (4 RW rows)
+// and share only the staged activations; each wave walks its rows' blocks in
+// order on its own.  With P = 1 a lane's part feeds its own chain directly;
+// with P > 1 the parts of a step go through the wave's LDS records to the
+// lanes of phase 0, which advance the chains block by block.  The weight
+// loads of the next D steps are in flight while a step is computed, across
+// the tiles of the workgroup's run [tile_begin, tile_end).
+template <int TYPE, bool AVX2, int RW, bool FUSED, int D>
+__device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, int tile_end, const GroupArgs &a,
+                                            uint8_t *smem) {
+    constexpr int P = 16 / RW;
+    constexpr int BB = TYPE == kQ4K ? kQ4Bytes : kQ6Body;
+    const int t = threadIdx.x, wave = t >> 6, l = t & 63;
+    const int j = l & 3, rho = (l >> 2) % RW, ph = l / (4 * RW);
+    Rec *recs = (Rec *)smem + wave * 128;                   // [2][64] per wave
+    uint8_t *xs = smem + 2 * kThreads * sizeof(Rec);        // nblk BlockQ8K records
 
-    const int t = threadIdx.x;
-    const int j = t & 3, rho = (t >> 2) % R, ph = t / (4 * R);
-    const int row0 = blockIdx.x * R;
     const int nblk = a.nblk;
-    const int row = min(row0 + rho, a.rows - 1);
     const int nsteps = (nblk + P - 1) / P;
+    const int total = (tile_end - tile_begin) * nsteps;
+    const int rows = md.rows;
+    auto row_of = [&](int tile) { return min((tile * 4 + wave) * RW + rho, rows - 1); };
 
-    auto unit_of = [&](int s) -> int64_t {
-        const int i = min(s * P + ph, nblk - 1);
-        return (int64_t)row * nblk + i;
-    };
     using Raw = std::conditional_t<TYPE == kQ4K, Q4Raw, Q6Raw>;
-    auto load = [&](int s) -> Raw {
-        if constexpr (TYPE == kQ4K) return load_q4(a.w, unit_of(s), j);
-        else return load_q6(a.w, a.wd, unit_of(s), j);
+    // load cursor: saturates at the last step, so every load is unconditional
+    int lk = 0, lt = tile_begin, ls = 0;
+    const uint8_t *lrow = md.w + (int64_t)row_of(lt) * nblk * BB;
+    const uint16_t *ldrow = TYPE == kQ6K ? md.wd + (int64_t)row_of(lt) * nblk : nullptr;
+    auto load_next = [&]() -> Raw {
+        const int i = min(ls * P + ph, nblk - 1);
+        Raw r;
+        if constexpr (TYPE == kQ4K) r = load_q4(lrow + i * kQ4Bytes, j);
+        else r = load_q6(lrow + i * kQ6Body, ldrow + i, j);
+        if (lk + 1 < total) {
+            ++lk;
+            if (++ls == nsteps) {
+                ls = 0;
+                ++lt;
+                lrow = md.w + (int64_t)row_of(lt) * nblk * BB;
+                if constexpr (TYPE == kQ6K) ldrow = md.wd + (int64_t)row_of(lt) * nblk;
+            }
+        }
+        return r;
     };
 
-    Raw cur = load(0);
-
-    // stage the activations: whole 16-byte chunks, then the 4-byte tail
-    {
+    // the activations
+    if constexpr (FUSED) {
+        for (int b = t >> 4; b < nblk; b += kThreads / 16) quantize_block(a.x + (int64_t)b * 256, t & 15, xs + b * kQ8Bytes);
+    } else {
         const int bytes = nblk * kQ8Bytes, n16 = bytes >> 4;
         const uint4 *src = (const uint4 *)a.xq;
         for (int c = t; c < n16; c += kThreads) ((uint4 *)xs)[c] = src[c];
@@ -280,69 +326,123 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MatvecArgs a) {
     __syncthreads();
     const Q8View x{xs};
 
-    // chain state of wave 0, lane l < 4R: row l / 4, part l % 4
-    float acc0 = 0.f, acc1 = 0.f, accm = 0.f;
-    const bool chain = t < 4 * R;
+    float acc0 = 0.f, acc1 = 0.f, accm = 0.f;               // chain state of the phase-0 lanes
+    const bool chain = ph == 0;
+    int ct = tile_begin, cs = 0;                            // compute cursor
 
-    for (int s = 0; s < nsteps; ++s) {
-        Raw nxt;
-        if (s + 1 < nsteps) nxt = load(s + 1);
-        const int i = min(s * P + ph, nblk - 1);
-        Rec r;
-        if constexpr (TYPE == kQ4K) r = part_q4<AVX2>(cur, x, i, j);
-        else r = part_q6<AVX2>(cur, x, i, j);
-        Rec *buf = recs + (s & 1) * kThreads;
-        buf[t] = r;
-        __syncthreads();
-        if (chain) {
-            const int nb = min(P, nblk - s * P);
-            for (int b = 0; b < nb; ++b) {
-                const int base = (b * R + rho) * 4;
-                const Rec q = buf[base + j];
-                if constexpr (AVX2) {
-                    if constexpr (TYPE == kQ4K) {
-                        const float d = buf[base].x, dmin = buf[base + 1].x;
-                        acc0 = fmaf(d, (float)q.a, acc0);
-                        acc1 = fmaf(d, (float)q.b, acc1);
-                        accm = fmaf(-dmin, (float)q.c, accm);
-                    } else {
-                        acc0 = fmaf(q.x, (float)q.a, acc0);
-                        acc1 = fmaf(q.x, (float)q.b, acc1);
-                        accm = fmaf(-(q.x * 32.0f), (float)q.c, accm);   // summ (kore.cpp:606)
+    auto advance = [&](const Rec &q, const Rec &q0, const Rec &q1) {
+        // one block of kore's per-lane float arithmetic; q is this lane's
+        // part, q0 / q1 parts 0 / 1 of the same unit
+        if constexpr (AVX2) {
+            if constexpr (TYPE == kQ4K) {
+                acc0 = fmaf(q0.x, (float)q.a, acc0);
+                acc1 = fmaf(q0.x, (float)q.b, acc1);
+                accm = fmaf(-q1.x, (float)q.c, accm);
+            } else {
+                acc0 = fmaf(q.x, (float)q.a, acc0);
+                acc1 = fmaf(q.x, (float)q.b, acc1);
+                accm = fmaf(-(q.x * 32.0f), (float)q.c, accm);   // summ (kore.cpp:606)
+            }
+        } else {
+            if constexpr (TYPE == kQ4K) {
+                const float t1 = q0.x * (float)q0.a;
+                const float t2 = __int_as_float(q0.c) * (float)q0.b;
+                acc0 = acc0 + (t1 - t2);
+            } else {
+                acc0 = acc0 + q0.x * (float)q0.a;
+            }
+        }
+    };
+
+    for (int k0 = 0; k0 < total; k0 += D) {
+        // the loads of D steps first (a step past the end repeats the last
+        // one's clamped addresses and is discarded); nothing loaded is carried
+        // from one iteration to the next, so no register copy has to wait for
+        // loads in flight
+        Raw buf[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) buf[d] = load_next();
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int k = k0 + d;
+            const int i = min(cs * P + ph, nblk - 1);
+            Rec r;
+            if constexpr (TYPE == kQ4K) r = part_q4<AVX2>(buf[d], x, i, j);
+            else r = part_q6<AVX2>(buf[d], x, i, j);
+            if (k < total) {
+                if constexpr (P == 1) {
+                    // the unit's four parts are this lane's quad: d / dmin from parts 0 / 1
+                    Rec q0 = r, q1 = r;
+                    if constexpr (TYPE == kQ4K && AVX2) {
+                        // part j holds d (j even) or dmin (j odd): take both from the quad
+                        const float other = quad_xor1f(r.x);
+                        q0.x = (j & 1) ? other : r.x;
+                        q1.x = (j & 1) ? r.x : other;
                     }
+                    advance(r, q0, q1);
                 } else {
-                    const Rec u = buf[base];
-                    if constexpr (TYPE == kQ4K) {
-                        const float t1 = u.x * (float)u.a;
-                        const float t2 = __int_as_float(u.c) * (float)u.b;
-                        acc0 = acc0 + (t1 - t2);
-                    } else {
-                        acc0 = acc0 + u.x * (float)u.a;
+                    Rec *rb = recs + (k & 1) * 64;
+                    rb[l] = r;
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    if (chain) {
+                        const int nb = min(P, nblk - cs * P);
+                        for (int b = 0; b < nb; ++b) {
+                            const int base = (b * RW + rho) * 4;
+                            advance(rb[base + j], rb[base], rb[base + 1]);
+                        }
                     }
+                }
+                if (++cs == nsteps) {
+                    // the tile's rows are complete
+                    if (chain) {
+                        float res;
+                        if constexpr (AVX2) {
+                            // kore's hsum256 (kore.cpp:521-528): lanes k and k+4 first,
+                            // then (l0 + l2) + (l1 + l3); lanes 2j / 2j+1 live in part j
+                            const float u = acc0 + quad_xor2f(acc0);     // part 0: l0, part 1: l2
+                            const float v = acc1 + quad_xor2f(acc1);     // part 0: l1, part 1: l3
+                            const float h8 = (u + quad_xor1f(u)) + (v + quad_xor1f(v));
+                            if constexpr (TYPE == kQ4K) {
+                                const float m = accm + quad_xor2f(accm); // hsum128 (kore.cpp:537-541)
+                                res = h8 + (m + quad_xor1f(m));
+                            } else {
+                                res = h8 + accm;
+                            }
+                        } else {
+                            res = acc0;
+                        }
+                        const int orow = (ct * 4 + wave) * RW + rho;
+                        if (j == 0 && orow < rows) md.out[orow] = res;
+                        acc0 = acc1 = accm = 0.f;
+                    }
+                    cs = 0;
+                    ++ct;
                 }
             }
         }
-        if (s + 1 < nsteps) cur = nxt;
     }
+}
 
-    if (!chain) return;
-    float res;
-    if constexpr (AVX2) {
-        // kore's hsum256 (kore.cpp:521-528): lanes k and k+4 first, then
-        // (l0 + l2) + (l1 + l3); lane 2j / 2j+1 live in part j
-        const float u = acc0 + quad_xor2f(acc0);     // part 0: l0, part 1: l2
-        const float v = acc1 + quad_xor2f(acc1);     // part 0: l1, part 1: l3
-        const float h8 = (u + quad_xor1f(u)) + (v + quad_xor1f(v));
-        if constexpr (TYPE == kQ4K) {
-            const float m = accm + quad_xor2f(accm); // hsum128 (kore.cpp:537-541)
-            res = h8 + (m + quad_xor1f(m));
-        } else {
-            res = h8 + accm;
-        }
-    } else {
-        res = acc0;
-    }
-    if (j == 0 && row0 + rho < a.rows) a.out[row0 + rho] = res;
+// One launch over up to kMaxGroup matrices that read the same activations:
+// workgroups [m.wg_begin, m.wg_begin + m.wg_count) belong to matrix m and
+// split its tiles of 4 RW rows evenly in contiguous runs.
+template <bool AVX2, int RW, bool FUSED>
+__global__ __launch_bounds__(kThreads) void matvec_group_kernel(GroupArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int D = KQMV_DEPTH;
+    const int g = blockIdx.x;
+    MatDesc md = a.m[0];
+#pragma unroll
+    for (int k = 1; k < kMaxGroup; ++k)
+        if (k < a.n_mat && g >= a.m[k].wg_begin) md = a.m[k];
+    const int w = g - md.wg_begin;
+    const int64_t tiles = (md.rows + 4 * RW - 1) / (4 * RW);
+    const int tb = (int)(tiles * w / md.wg_count), te = (int)(tiles * (w + 1) / md.wg_count);
+    if (tb >= te) return;
+    if (md.type == kQ4K) matvec_body<kQ4K, AVX2, RW, FUSED, D>(md, tb, te, a, smem);
+    else matvec_body<kQ6K, AVX2, RW, FUSED, D>(md, tb, te, a, smem);
 }
 
 // Q6_K upload: thread per output dword (52 body dwords + the scale per block).
@@ -380,20 +480,21 @@ __global__ __launch_bounds__(kThreads) void synth_blocks_kernel(uint16_t *__rest
     dst[g] = v;
 }
 
-template <int TYPE, bool AVX2, int R>
-hipError_t launch_r(const MatvecArgs &a, hipStream_t s) {
-    const int grid = (a.rows + R - 1) / R;
+template <bool AVX2, int RW, bool FUSED>
+hipError_t launch_group_r(const GroupArgs &a, int grid, hipStream_t s) {
     const size_t lds = 2 * kThreads * sizeof(Rec) + (size_t)a.nblk * kQ8Bytes;
-    hipLaunchKernelGGL((matvec_kernel<TYPE, AVX2, R>), dim3(grid), dim3(kThreads), lds, s, a);
+    hipLaunchKernelGGL((matvec_group_kernel<AVX2, RW, FUSED>), dim3(grid), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
 
-template <int TYPE, bool AVX2>
-hipError_t launch_t(const MatvecArgs &a, int r, hipStream_t s) {
-    switch (r) {
-        case 4: return launch_r<TYPE, AVX2, 4>(a, s);
-        case 8: return launch_r<TYPE, AVX2, 8>(a, s);
-        default: return launch_r<TYPE, AVX2, 16>(a, s);
+template <bool AVX2, bool FUSED>
+hipError_t launch_group_f(const GroupArgs &a, int rw, int grid, hipStream_t s) {
+    switch (rw) {
+        case 1: return launch_group_r<AVX2, 1, FUSED>(a, grid, s);
+        case 2: return launch_group_r<AVX2, 2, FUSED>(a, grid, s);
+        case 4: return launch_group_r<AVX2, 4, FUSED>(a, grid, s);
+        case 8: return launch_group_r<AVX2, 8, FUSED>(a, grid, s);
+        default: return launch_group_r<AVX2, 16, FUSED>(a, grid, s);
     }
 }
 
@@ -406,17 +507,46 @@ uint64_t splitmix64_host(uint64_t z) {
 
 }  // namespace
 
-hipError_t launch_matvec(int type, bool avx2, const MatvecArgs &a, int rows_per_wg, hipStream_t s) {
-    if (a.rows <= 0 || a.nblk <= 0 || a.nblk > kMaxBlocks) return hipErrorInvalidValue;
-    if (type == kQ4K) return avx2 ? launch_t<kQ4K, true>(a, rows_per_wg, s) : launch_t<kQ4K, false>(a, rows_per_wg, s);
-    if (type == kQ6K) return avx2 ? launch_t<kQ6K, true>(a, rows_per_wg, s) : launch_t<kQ6K, false>(a, rows_per_wg, s);
-    return hipErrorInvalidValue;
+hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int max_wgs, hipStream_t s) {
+    if (a.n_mat < 1 || a.n_mat > kMaxGroup || a.nblk <= 0 || a.nblk > kMaxBlocks) return hipErrorInvalidValue;
+    const int rw = rows_per_wave;
+    if (rw != 1 && rw != 2 && rw != 4 && rw != 8 && rw != 16) return hipErrorInvalidValue;
+    const int rows_per_tile = 4 * rw;
+    const bool fused = a.x != nullptr;
+    if (!fused && !a.xq) return hipErrorInvalidValue;
+    // workgroups per matrix: in proportion to its weight bytes, at least one,
+    // at most one per row tile, about max_wgs in all
+    int64_t tiles[kMaxGroup], bytes[kMaxGroup], all_tiles = 0, all_bytes = 0;
+    for (int k = 0; k < a.n_mat; ++k) {
+        const MatDesc &m = a.m[k];
+        if (m.rows <= 0 || !m.w || !m.out || (m.type != kQ4K && m.type != kQ6K) || (m.type == kQ6K && !m.wd))
+            return hipErrorInvalidValue;
+        tiles[k] = (m.rows + rows_per_tile - 1) / rows_per_tile;
+        bytes[k] = (int64_t)m.rows * (m.type == kQ4K ? kQ4Bytes : kQ6Bytes);
+        all_tiles += tiles[k];
+        all_bytes += bytes[k];
+    }
+    const int64_t target = max_wgs > 0 ? std::min<int64_t>(max_wgs, all_tiles) : all_tiles;
+    int64_t wg = 0;
+    for (int k = 0; k < a.n_mat; ++k) {
+        MatDesc &m = a.m[k];
+        int64_t n = (target * bytes[k] + all_bytes / 2) / all_bytes;
+        n = std::max<int64_t>(1, std::min<int64_t>(n, tiles[k]));
+        m.wg_begin = (int)wg;
+        m.wg_count = (int)n;
+        wg += n;
+    }
+    for (int k = a.n_mat; k < kMaxGroup; ++k) a.m[k] = a.m[a.n_mat - 1];
+    if (wg > INT32_MAX) return hipErrorInvalidValue;
+    const int grid = (int)wg;
+    if (avx2) return fused ? launch_group_f<true, true>(a, rw, grid, s) : launch_group_f<true, false>(a, rw, grid, s);
+    return fused ? launch_group_f<false, true>(a, rw, grid, s) : launch_group_f<false, false>(a, rw, grid, s);
 }
 
 hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, hipStream_t s) {
     const int64_t nb = n / 256;
     if (nb <= 0) return hipSuccess;
-    const int64_t grid = (nb + 3) / 4;
+    const int64_t grid = (nb + kThreads / 16 - 1) / (kThreads / 16);
     hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb);
     return hipGetLastError();
 }

@@ -37,7 +37,7 @@ _vp, _i, _i64 = C.c_void_p, C.c_int, C.c_int64
 
 class QmvInfo(C.Structure):
     _fields_ = [("type", C.c_int), ("device", C.c_int), ("rows", C.c_int64), ("cols", C.c_int64),
-                ("weight_bytes", C.c_size_t), ("rows_per_wg", C.c_int)]
+                ("weight_bytes", C.c_size_t), ("rows_per_wave", C.c_int)]
 
 
 SYMBOLS = [
@@ -48,6 +48,8 @@ SYMBOLS = [
     ("kore_qmv_matvec", _i, [_vp, _vp, _vp, _i]),
     ("kore_qmv_matvec_dev", _i, [_vp, _vp, _vp, _i, _vp]),
     ("kore_qmv_mv", _i, [_vp, _vp, _vp, _i]),
+    ("kore_qmv_mv_dev", _i, [_vp, _vp, _vp, _i, _vp]),
+    ("kore_qmv_mv_group_dev", _i, [_i, _vp, _vp, _vp, _i, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
     ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),
@@ -161,3 +163,14 @@ class QMat:
 
     def matvec_dev(self, xq_ptr: int, out_ptr: int, avx2: bool = True, stream=None) -> None:
         _check(lib().kore_qmv_matvec_dev(self.handle, xq_ptr, out_ptr, int(avx2), stream), self.handle)
+
+    def mv_dev(self, x_ptr: int, out_ptr: int, avx2: bool = True, stream=None) -> None:
+        _check(lib().kore_qmv_mv_dev(self.handle, x_ptr, out_ptr, int(avx2), stream), self.handle)
+
+
+def mv_group_dev(mats, x_ptr: int, out_ptrs, avx2: bool = True, stream=None) -> None:
+    """One launch of up to 4 matrices sharing the input x (device pointers)."""
+    n = len(mats)
+    hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
+    outs = (C.c_void_p * n)(*out_ptrs)
+    _check(lib().kore_qmv_mv_group_dev(n, hs, x_ptr, outs, int(avx2), stream))

@@ -11,16 +11,81 @@
 // Result file: the Q8_K blocks of x (cols/256 x 292 bytes, kore's BlockQ8K),
 //   then out_ref[rows], then out_avx2[rows] (float32; out_avx2 equals out_ref
 //   where the CPU has no AVX2/FMA).
+//
+// Timing mode (the CPU baseline of the benchmark):
+//   kore_qmv_ref --time THREADS MIN_SECONDS COPIES job.bin
+// keeps COPIES copies of the job's matrix (so that the weights streamed exceed
+// the host's caches, as a model's do) and runs kore's own quant() + mv() pair
+// on them in turn - quantize_row_q8_K then matvec_mt over all rows with
+// THREADS threads and the AVX2 dot products where the CPU has them
+// (kore.cpp:1387-1394, 677-682) - until MIN_SECONDS have passed; prints one
+// JSON line {"reps", "seconds", "rows", "cols", "weight_bytes", "avx2",
+// "threads", "copies"}.
 
 #define main kore_ref_main
 #include "kore.cpp"
 #undef main
 
+#include <chrono>
 #include <cstdio>
+#include <cstdlib>
+#include <string>
 #include <vector>
 
+static int time_mode(unsigned nth, double min_s, int copies, const char *job) {
+    FILE *in = fopen(job, "rb");
+    if (!in) { perror("open"); return 2; }
+    int32_t hdr[3];
+    if (fread(hdr, 4, 3, in) != 3) return 3;
+    const int type = hdr[0];
+    const int64_t rows = hdr[1], cols = hdr[2];
+    if (cols % 256 != 0 || (type != GGML_Q4_K && type != GGML_Q6_K)) return 3;
+    const int64_t nb = cols / 256, bb = type == GGML_Q4_K ? 144 : 210;
+    if (copies < 1) copies = 1;
+    const size_t wb = (size_t)(rows * nb * bb);
+    std::vector<std::vector<uint8_t>> w((size_t)copies, std::vector<uint8_t>(wb));
+    std::vector<float> x((size_t)cols), out((size_t)rows);
+    if (fread(w[0].data(), 1, wb, in) != wb) return 3;
+    if (fread(x.data(), 4, x.size(), in) != x.size()) return 3;
+    fclose(in);
+    for (int c = 1; c < copies; ++c) memcpy(w[(size_t)c].data(), w[0].data(), wb);
+    std::vector<Tensor> t((size_t)copies);
+    for (int c = 0; c < copies; ++c) {
+        t[(size_t)c].type = (uint32_t)type;
+        t[(size_t)c].n_dims = 2;
+        t[(size_t)c].dims[0] = (uint64_t)cols;
+        t[(size_t)c].dims[1] = (uint64_t)rows;
+        t[(size_t)c].nbytes = wb;
+        t[(size_t)c].data = w[(size_t)c].data();
+    }
+    std::vector<BlockQ8K> xq((size_t)nb);
+    const bool avx2 = cpu_has_avx2();
+    for (int c = 0; c < copies; ++c) {   // warm-up: touch every copy once
+        quantize_row_q8_K(x.data(), xq.data(), cols);
+        matvec_mt(t[(size_t)c], xq.data(), out.data(), avx2, nth);
+    }
+    int reps = 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    double el = 0;
+    do {
+        quantize_row_q8_K(x.data(), xq.data(), cols);
+        matvec_mt(t[(size_t)(reps % copies)], xq.data(), out.data(), avx2, nth);
+        ++reps;
+        el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    } while (el < min_s);
+    printf("{\"reps\": %d, \"seconds\": %.6f, \"rows\": %lld, \"cols\": %lld, \"weight_bytes\": %zu, "
+           "\"avx2\": %d, \"threads\": %u, \"copies\": %d, \"checksum\": %.9g}\n",
+           reps, el, (long long)rows, (long long)cols, wb, (int)avx2, nth, copies, (double)out[(size_t)rows / 2]);
+    return 0;
+}
+
 int main(int argc, char **argv) {
-    if (argc != 3) { fprintf(stderr, "usage: kore_qmv_ref job.bin result.bin\n"); return 2; }
+    if (argc == 6 && std::string(argv[1]) == "--time")
+        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), argv[5]);
+    if (argc != 3) {
+        fprintf(stderr, "usage: kore_qmv_ref job.bin result.bin | --time THREADS SECONDS COPIES job.bin\n");
+        return 2;
+    }
     FILE *in = fopen(argv[1], "rb");
     FILE *out = fopen(argv[2], "wb");
     if (!in || !out) { perror("open"); return 2; }

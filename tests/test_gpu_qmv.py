@@ -87,19 +87,23 @@ def test_golden_replay(name):
 SHAPES = [(1, 1), (37, 3), (129, 14), (64, 74), (21, 128), (300, 17), (16, 16)]
 
 
-@pytest.mark.parametrize("rpw", [4, 8, 16])
+@pytest.mark.parametrize("wgs", ["0", "1"])
+@pytest.mark.parametrize("rpw", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("wtype", [oracle.TYPE_Q4K, oracle.TYPE_Q6K])
-def test_random_shapes_vs_oracle(wtype, rpw, monkeypatch):
+def test_random_shapes_vs_oracle(wtype, rpw, wgs, monkeypatch):
+    """Every wave layout (rows per wave), one tile per workgroup or long
+    runs of tiles per workgroup (one workgroup per CU)."""
     from kore_amd import qmv
-    monkeypatch.setenv("KORE_QMV_ROWS_PER_WG", str(rpw))
+    monkeypatch.setenv("KORE_QMV_ROWS_PER_WAVE", str(rpw))
+    monkeypatch.setenv("KORE_QMV_WGS_PER_CU", wgs)
     for si, (rows, nblk) in enumerate(SHAPES):
-        _say(f"qmv random type {wtype} rows_per_wg {rpw}: {rows} x {nblk * 256}")
+        _say(f"qmv random type {wtype} rows_per_wave {rpw} wgs/cu {wgs}: {rows} x {nblk * 256}")
         rng = np.random.default_rng(1000 * wtype + 10 * rpw + si)
         w = _weights(wtype, rows, nblk, rng)
         x = _x(nblk * 256, rng)
         xq = oracle.quantize_q8K(x)
         with qmv.QMat(wtype, rows, nblk * 256, w) as m:
-            assert m.info().rows_per_wg == rpw
+            assert m.info().rows_per_wave == rpw
             for avx2 in (True, False):
                 ref = oracle.qmatvec(wtype, w, rows, nblk * 256, xq, avx2=avx2)
                 _assert_bits(m.matvec(xq, avx2=avx2), ref, f"{rows}x{nblk} avx2={avx2}")
@@ -166,6 +170,46 @@ def test_device_api_matches_host_api():
         assert e.value.code == qmv.KORE_QMV_E_INVALID
     for b in (dx, dq, do, draw):
         b.free()
+
+
+@pytest.mark.parametrize("fuse", ["0", "1"])
+def test_grouped_and_fused_launches(fuse, monkeypatch):
+    """kore's q/k/v (and gate/up) matvecs share one quant(): one grouped launch,
+    with the quantisation inside it (fuse 1) or apart (fuse 0), gives kore's
+    bits for every matrix of the group."""
+    from kore_amd import hip, qmv
+    monkeypatch.setenv("KORE_QMV_FUSE", fuse)
+    groups = [
+        [(oracle.TYPE_Q4K, 300), (oracle.TYPE_Q4K, 64), (oracle.TYPE_Q6K, 64)],      # q, k, v
+        [(oracle.TYPE_Q4K, 1000), (oracle.TYPE_Q4K, 1000)],                         # gate, up
+        [(oracle.TYPE_Q6K, 77), (oracle.TYPE_Q4K, 5), (oracle.TYPE_Q6K, 130), (oracle.TYPE_Q4K, 16)],
+    ]
+    for gi, (group, nblk) in enumerate(zip(groups, (14, 14, 74))):
+        for extra in ((), (128,)) if gi == 2 else ((),):
+            nb = extra[0] if extra else nblk
+            cols = nb * 256
+            _say(f"qmv group {gi} fuse {fuse}: {[(t, r) for t, r in group]} x {cols}")
+            rng = np.random.default_rng(300 + gi + nb)
+            ws = [_weights(t, r, nb, rng) for t, r in group]
+            x = _x(cols, rng)
+            xq = oracle.quantize_q8K(x)
+            mats = [qmv.QMat(t, r, cols, w) for (t, r), w in zip(group, ws)]
+            dx = hip.DeviceBuffer.from_array(x)
+            douts = [hip.DeviceBuffer(r) for _, r in group]
+            for avx2 in (True, False):
+                qmv.mv_group_dev(mats, dx.ptr, [d.ptr for d in douts], avx2=avx2)
+                hip.synchronize()
+                for (t, r), w, d in zip(group, ws, douts):
+                    _assert_bits(d.download(), oracle.qmatvec(t, w, r, cols, xq, avx2=avx2),
+                                 f"group {gi} type {t} rows {r} avx2={avx2}")
+                mats[0].mv_dev(dx.ptr, douts[0].ptr, avx2=avx2)
+                hip.synchronize()
+                t, r = group[0]
+                _assert_bits(douts[0].download(), oracle.qmatvec(t, ws[0], r, cols, xq, avx2=avx2), "mv_dev")
+            for m in mats:
+                m.close()
+            for d in douts + [dx]:
+                d.free()
 
 
 def _splitmix64(z):
