@@ -63,7 +63,7 @@ TRAFFIC_DECODE_BYTES = 19_078_000
 TRAFFIC_PREFILL_BYTES = 109_052_000
 # the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
 # of weights, activations and outputs algorithmic)
-TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_366_000}
+TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_416_000}
 
 # Qwen2.5-7B matrix shapes of the matvec leg
 QMV_FF, QMV_VOCAB = 18944, 152064
@@ -506,6 +506,43 @@ def cpu_matvec(seconds: float, threads: int):
                       f"shape, {n} matvecs in {el:.1f} s; host {_cpu_model()}"}
 
 
+def read_calibration():
+    """What one launch of a plain streaming read (kore_hbm_probe.hip) moves per
+    size on this device, and the time of an empty dependent launch."""
+    from kore_amd import hip, qmv
+    qmv.lib()
+    B = C.CDLL(os.path.join(ROOT, "kore_amd", "libkore_qmv_bench.so"))
+    B.kqb_read_probe.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                 C.POINTER(C.c_float)]
+    total = 4 << 30
+    buf = hip.DeviceBuffer(total // 4)
+    hip.check(hip.lib().hipMemset(buf.ptr, 1, total), "hipMemset")
+    sink = hip.DeviceBuffer(8192 * 256)
+    out = {"kernel": "grid-stride read of 16-byte chunks, 4 loads in flight per thread, 256 threads per "
+                     "workgroup; launches back to back on one stream, buffer copies rotated",
+           "sizes": []}
+    us = C.c_float(0)
+    for mb in (8, 17, 38, 76, 150, 447, 1024, 4096):
+        nbytes = mb << 20
+        rot = max(1, min(total // nbytes, 8))
+        row = {"mbytes": mb}
+        for grid in (1024, 2048, 4096):
+            reps = 10 if mb >= 1024 else 100
+            rc = B.kqb_read_probe(buf.ptr, nbytes, rot, grid, reps, sink.ptr, C.byref(us))
+            if rc != 0:
+                raise RuntimeError(f"kqb_read_probe failed ({rc})")
+            row[f"grid{grid}"] = {"us": round(us.value, 2), "gbs": round(nbytes / (us.value * 1e-6) / 1e9, 1)}
+        out["sizes"].append(row)
+        print(f"[bench] read calibration {mb} MB done", file=sys.stderr, flush=True)
+    rc = B.kqb_read_probe(buf.ptr, 16, 1, 0, 1000, sink.ptr, C.byref(us))
+    if rc != 0:
+        raise RuntimeError(f"kqb_read_probe failed ({rc})")
+    out["empty_launch_us"] = round(us.value, 3)
+    buf.free()
+    sink.free()
+    return out
+
+
 # ------------------------------------------------------------------ CPU legs
 
 def _rel_err(out, ref):
@@ -604,6 +641,9 @@ def main(argv=None):
     ap.add_argument("--cpu-threads", type=int, default=16,
                     help="threads of kore's own matvec in the CPU baseline (the GPU box's CPU share)")
     ap.add_argument("--cpu-prefill-layers", type=int, default=2)
+    ap.add_argument("--read-calibration", action="store_true",
+                    help="only time a plain streaming read kernel per launch size (the yardstick of the "
+                         "HBM-bound kernels) and an empty launch")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 8 device-to-device copies of 256 MiB (the runtime's copy kernel), "
                          "the known-size reference for HBM byte counters")
@@ -625,6 +665,9 @@ def main(argv=None):
             hip.check(hip.lib().hipMemcpy(dst.ptr, src.ptr, n * 4, hip.D2D), "hipMemcpy D2D")
         hip.synchronize()
         print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 8}), flush=True)
+        return 0
+    if args.read_calibration:
+        print(json.dumps(read_calibration()), flush=True)
         return 0
     dev_name = hip.device_name(0)
     clk = C.c_int(0)

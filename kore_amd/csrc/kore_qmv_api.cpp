@@ -25,7 +25,7 @@ struct kore_qmv_tensor {
     int num_cu = 0;
     uint8_t *w = nullptr;      // Q4_K blocks or Q6_K bodies
     uint16_t *wd = nullptr;    // Q6_K scales
-    uint8_t *xq = nullptr;     // Q8_K blocks of the activations when kore_qmv_mv_dev quantises apart
+    uint8_t *xq = nullptr;     // quantised activations (the matvec's layout) when quantised apart
     size_t weight_bytes = 0;
     std::string error;
 };
@@ -156,7 +156,7 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
     if (e != hipSuccess) return bail(hip_fail(t, e, "hipDeviceGetAttribute"));
     t->num_cu = num_cu;
     t->rows_per_wave = pick_rows_per_wave(rows, num_cu);
-    if ((e = hipMalloc(&t->xq, (size_t)t->nblk * kQ8Bytes)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
+    if ((e = hipMalloc(&t->xq, (size_t)t->nblk * 308)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
 
     const int64_t nblocks = rows * t->nblk;
     const size_t bb = type == KORE_QMV_Q4_K ? kQ4Bytes : kQ6Bytes;
@@ -205,7 +205,7 @@ KORE_QMV_API int kore_qmv_quantize_dev(const float *x, int64_t n, void *xq, void
     if (n <= 0 || n % 256 != 0) return fail(nullptr, KORE_QMV_E_INVALID, "n must be a positive multiple of 256");
     if (int rc = check_dev_ptr(nullptr, x, 16, "x")) return rc;
     if (int rc = check_dev_ptr(nullptr, xq, 16, "xq")) return rc;
-    hipError_t e = launch_quantize_q8k(x, n, (uint8_t *)xq, (hipStream_t)stream);
+    hipError_t e = launch_quantize_q8k(x, n, (uint8_t *)xq, false, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(nullptr, e, "quantize launch");
     return KORE_QMV_OK;
 }
@@ -221,7 +221,7 @@ KORE_QMV_API int kore_qmv_quantize(const float *x, int64_t n, void *xq) {
     QMV_TRY(nullptr, host_path(dev, xb + qb, &h));
     uint8_t *dx = (uint8_t *)h->buf, *dq = dx + xb;
     QMV_TRY(nullptr, hipMemcpyAsync(dx, x, (size_t)n * 4, hipMemcpyHostToDevice, h->stream));
-    QMV_TRY(nullptr, launch_quantize_q8k((const float *)dx, n, dq, h->stream));
+    QMV_TRY(nullptr, launch_quantize_q8k((const float *)dx, n, dq, false, h->stream));
     QMV_TRY(nullptr, hipMemcpyAsync(xq, dq, qb, hipMemcpyDeviceToHost, h->stream));
     QMV_TRY(nullptr, hipStreamSynchronize(h->stream));
     return KORE_QMV_OK;
@@ -233,7 +233,7 @@ static MatDesc desc_of(kore_qmv_tensor *t, float *out) {
 
 // One grouped launch: xq given (fused = false) or x quantised in the kernel.
 static int launch_group(int n, kore_qmv_tensor *const *ts, const void *xq, const float *x, float *const *outs,
-                        int avx2, hipStream_t s) {
+                        int avx2, hipStream_t s, bool xq_image = false) {
     GroupArgs a{};
     int64_t rows = 0;
     for (int k = 0; k < n; ++k) {
@@ -244,6 +244,7 @@ static int launch_group(int n, kore_qmv_tensor *const *ts, const void *xq, const
     a.nblk = ts[0]->nblk;
     a.xq = (const uint8_t *)xq;
     a.x = x;
+    a.xq_image = xq_image ? 1 : 0;
     const int r = n == 1 ? ts[0]->rows_per_wave : pick_rows_per_wave(rows, ts[0]->num_cu);
     hipError_t e = launch_matvec_group(avx2 != 0, a, r, max_workgroups(ts[0]->num_cu), s);
     if (e != hipSuccess) return hip_fail(ts[0], e, "matvec launch");
@@ -277,9 +278,9 @@ KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *ts, const
     if (const int cap = max_workgroups(t0->num_cu)) wgs = std::min<int64_t>(wgs, cap);
     hipStream_t s = (hipStream_t)stream;
     if (fuse_quantisation(t0->nblk, wgs)) return launch_group(n, ts, nullptr, x, outs, avx2, s);
-    hipError_t e = launch_quantize_q8k(x, t0->cols, t0->xq, s);
+    hipError_t e = launch_quantize_q8k(x, t0->cols, t0->xq, true, s);
     if (e != hipSuccess) return hip_fail(t0, e, "quantize launch");
-    return launch_group(n, ts, t0->xq, nullptr, outs, avx2, s);
+    return launch_group(n, ts, t0->xq, nullptr, outs, avx2, s, true);
 }
 
 KORE_QMV_API int kore_qmv_mv_dev(kore_qmv_tensor_t t, const float *x, float *out, int avx2, void *stream) {

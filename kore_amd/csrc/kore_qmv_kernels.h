@@ -51,6 +51,7 @@ struct GroupArgs {
     const uint8_t *xq;       // nblk BlockQ8K records (16-byte aligned), or
     const float *x;          // nblk*256 floats (16-byte aligned) that every workgroup
                              // quantises into LDS itself (then xq is unused)
+    int xq_image;            // xq holds launch_quantize_q8k(..., image = true)'s layout
 };
 
 // out[r] = row r . xq for every matrix of the group, with kore's summation:
@@ -61,8 +62,10 @@ struct GroupArgs {
 // each a contiguous run.
 hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int max_wgs, hipStream_t s);
 
-// kore's quantize_row_q8_K (kore.cpp:422-446): x[n] -> n/256 BlockQ8K records.
-hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, hipStream_t s);
+// kore's quantize_row_q8_K (kore.cpp:422-446): x[n] -> n/256 BlockQ8K records,
+// or (image) the same values in the matvec's own layout (n/256 * 308 bytes,
+// n/256 <= kMaxBlocks) for a following launch_matvec_group with xq_image.
+hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool image, hipStream_t s);
 
 // Q6_K upload: raw GGUF blocks (rows*nblk x 210 bytes, any alignment of 2)
 // -> body / d arrays above.

@@ -52,10 +52,17 @@ __device__ __forceinline__ float quad_xor2f(float v) { return __int_as_float(qua
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
 
+// What lane m of a 16-lane DPP row holds of a quantised block: its 16 int8
+// values (16m .. 16m+15), their sum (bsums[m]) and the block's d.
+struct Q8Lane {
+    uint4 qs;
+    int bsum;
+    float d;
+};
+
 // kore's quantisation of one 256-value block (kore.cpp:422-446) by the 16
-// lanes of a DPP row: lane m owns values 16m .. 16m+15 (x 16-byte aligned),
-// which are also exactly bsums[m].  Writes the 292-byte BlockQ8K record.
-__device__ __forceinline__ void quantize_block(const float *xb, int m, uint8_t *rec) {
+// lanes of a DPP row: lane m owns values 16m .. 16m+15 (x 16-byte aligned).
+__device__ __forceinline__ Q8Lane quantize_lane(const float *xb, int m) {
     float v[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -111,102 +118,149 @@ __device__ __forceinline__ void quantize_block(const float *xb, int m, uint8_t *
         }
         d = 1.0f / iscale;
     }
-    uint32_t *qw = (uint32_t *)(rec + 4 + 16 * m);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) qw[k] = packed[k];
-    *(int16_t *)(rec + 260 + 2 * m) = (int16_t)bsum;
-    if (m == 0) *(float *)rec = d;
+    return Q8Lane{make_uint4(packed[0], packed[1], packed[2], packed[3]), bsum, d};
 }
 
-// Sixteen blocks per workgroup, one per 16-lane row.
+// Activations in LDS, laid out for 16-byte reads: the 256 int8 values of
+// block i at i * 272 (a 16-byte pad between blocks spreads them over the
+// banks), bsums at nblk * 272 + 32 i, d at nblk * 304 + 4 i.
+constexpr int kXsQs = 272;
+__host__ __device__ constexpr size_t xs_bytes(int nblk) { return (size_t)nblk * 308; }
+
+struct Q8View {
+    const uint8_t *p;
+    int nblk;
+    __device__ uint4 qs16(int i, int byte) const { return *(const uint4 *)(p + i * kXsQs + byte); }
+    __device__ int bsum(int i, int j) const { return *(const int16_t *)(p + nblk * kXsQs + 32 * i + 2 * j); }
+    __device__ float d(int i) const { return *(const float *)(p + nblk * 304 + 4 * i); }
+};
+
+__device__ __forceinline__ void xs_store(uint8_t *xs, int nblk, int i, int m, const Q8Lane &q) {
+    *(uint4 *)(xs + i * kXsQs + 16 * m) = q.qs;
+    *(int16_t *)(xs + nblk * kXsQs + 32 * i + 2 * m) = (int16_t)q.bsum;
+    if (m == 0) *(float *)(xs + nblk * 304 + 4 * i) = q.d;
+}
+
+// Sixteen blocks per workgroup, one per 16-lane row, written as kore's records
+// or (IMAGE) in the matvec's LDS layout, which workgroups then copy verbatim.
+template <bool IMAGE>
 __global__ __launch_bounds__(kThreads) void quantize_q8k_kernel(const float *__restrict__ x,
                                                                 uint8_t *__restrict__ xq, int64_t nblocks) {
     const int64_t blk = (int64_t)blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
     if (blk >= nblocks) return;
-    quantize_block(x + blk * 256, threadIdx.x & 15, xq + blk * kQ8Bytes);
+    const int m = threadIdx.x & 15;
+    const Q8Lane q = quantize_lane(x + blk * 256, m);
+    if constexpr (IMAGE) {
+        xs_store(xq, (int)nblocks, (int)blk, m, q);
+        return;
+    }
+    uint8_t *rec = xq + blk * kQ8Bytes;
+    uint32_t *qw = (uint32_t *)(rec + 4 + 16 * m);
+    qw[0] = q.qs.x;
+    qw[1] = q.qs.y;
+    qw[2] = q.qs.z;
+    qw[3] = q.qs.w;
+    *(int16_t *)(rec + 260 + 2 * m) = (int16_t)q.bsum;
+    if (m == 0) *(float *)rec = q.d;
 }
 
 // ------------------------------------------------------------------ units
 
-// Staged activations: kore's BlockQ8K records copied verbatim into LDS.
-struct Q8View {
-    const uint8_t *p;
-    __device__ float d(int i) const { return *(const float *)(p + i * kQ8Bytes); }
-    __device__ uint2 qs8(int i, int byte) const {   // 8 bytes of qs (byte % 4 == 0)
-        const uint32_t *q = (const uint32_t *)(p + i * kQ8Bytes + 4 + byte);
-        return make_uint2(q[0], q[1]);
-    }
-    __device__ int bsum(int i, int j) const { return *(const int16_t *)(p + i * kQ8Bytes + 260 + 2 * j); }
-};
-
-// Raw bytes of one unit part, loaded a step ahead.
-struct Q4Raw { uint4 hdr; uint2 qs[4]; };
-struct Q6Raw { uint2 a[2], b[2], h[2]; uint4 sc; uint32_t d; };
+// Raw bytes of one unit part: whole 16-byte chunks.
+//   Q4_K part j: the header (d, dmin, 12 scale bytes) and nibble chunks j and
+//   j + 4 of the block, i.e. groups c = j/2 and 2 + j/2 (32 bytes each), half
+//   j % 2 of each: the bytes of kore's AVX2 lanes 4(j%2) .. 4(j%2)+3.
+//   Q6_K part j (g = j % 2, kp = j / 2): the ql chunks of groups (h, kp) for
+//   h = 0, 1, lanes 4g .. 4g+3 (their high nibbles are groups (h, kp+2)), the
+//   matching qh chunks, the 16 scales and the block's f16 d.
+struct Q4Raw { uint4 hdr, a, b; };
+struct Q6Raw { uint4 a0, a1, h0, h1, sc; uint32_t d; };
 
 __device__ __forceinline__ Q4Raw load_q4(const uint8_t *b, int j) {
     Q4Raw r;
     r.hdr = *(const uint4 *)b;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) r.qs[c] = *(const uint2 *)(b + 16 + 32 * c + 8 * j);
+    r.a = *(const uint4 *)(b + 16 + 16 * j);
+    r.b = *(const uint4 *)(b + 80 + 16 * j);
     return r;
 }
 
 __device__ __forceinline__ Q6Raw load_q6(const uint8_t *b, const uint16_t *dp, int j) {
+    const int q = 16 * (2 * (j >> 1) + (j & 1)), qh = 16 * (j & 1);
     Q6Raw r;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        r.a[h] = *(const uint2 *)(b + 64 * h + 8 * j);
-        r.b[h] = *(const uint2 *)(b + 64 * h + 32 + 8 * j);
-        r.h[h] = *(const uint2 *)(b + 128 + 32 * h + 8 * j);
-    }
+    r.a0 = *(const uint4 *)(b + q);
+    r.a1 = *(const uint4 *)(b + 64 + q);
+    r.h0 = *(const uint4 *)(b + 128 + qh);
+    r.h1 = *(const uint4 *)(b + 160 + qh);
     r.sc = *(const uint4 *)(b + 192);
     r.d = *dp;
     return r;
 }
 
-// Per-part record handed to the chain wave (16 bytes).
-//   AVX2 Q4_K: s[2j], s[2j+1] (AVX2 lanes 2j, 2j+1), min product of lane j,
-//              then d (j even) or dmin (j odd)
-//   AVX2 Q6_K: s[2j], s[2j+1], the block's bias sum, d
-//   scalar:    part 0 holds isum, imin (Q4_K), d, dmin for the whole unit
+// Per-part record handed to the chain lanes (16 bytes).
+//   AVX2 Q4_K: s[k0], s[k0+1] (the part's two AVX2 lanes), min product of
+//              lane j, then d (j even) or dmin (j odd)
+//   AVX2 Q6_K: s[k0], s[k0+1], the block's bias sum, d
+//   scalar:    isum, imin (Q4_K), dmin bits, d, the same in all four parts
 struct Rec { int a, b, c; float x; };
 
 // Q4_K block (kore.cpp:324-326): 6-bit scale / min of sub-block j from the
-// 12 packed bytes q[0..11] (kore.cpp:327-335).
+// 12 packed bytes (kore.cpp:327-335); j may differ between lanes: both forms,
+// then a select (no branch).
 __device__ __forceinline__ int q4_scale(const uint4 &h, int j) {
-    if (j < 4) return (h.y >> (8 * j)) & 63;
-    const int s = 8 * (j - 4);
-    return ((h.w >> s) & 0x0F) | (((h.y >> (s + 6)) & 3) << 4);
+    const int s = 8 * (j & 3);
+    const int lo = (h.y >> s) & 63;
+    const int hi = ((h.w >> s) & 0x0F) | (((h.y >> (s + 6)) & 3) << 4);
+    return j < 4 ? lo : hi;
 }
 __device__ __forceinline__ int q4_min(const uint4 &h, int j) {
-    // j may differ between lanes: both forms, then a select (no branch)
     const int s = 8 * (j & 3);
     const int lo = (h.z >> s) & 63;
     const int hi = ((h.w >> (s + 4)) & 0x0F) | (((h.z >> (s + 6)) & 3) << 4);
     return j < 4 ? lo : hi;
 }
 
-// Part j of a Q4_K unit: AVX2 lanes k = 2j, 2j+1 hold bytes 4k..4k+3 of each
-// 32-byte group c of the nibbles (kore.cpp:548-575); lane j of the 4-lane
-// minimum sum holds sub-blocks 2j, 2j+1 (kore.cpp:556-560).
+__device__ __forceinline__ uint32_t w4(const uint4 &v, int k) {
+    return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
+}
+
+// The two AVX2 lanes part j keeps: its four lane sums S cover the groups it
+// loaded, part j ^ 2 holds the other groups of the same four lanes; one DPP
+// exchange gives part j lanes 2 sel, 2 sel + 1 of its four (sel = j / 2).
+__device__ __forceinline__ void own_lanes(const int S[4], int sel, int &s0, int &s1) {
+    const int give0 = sel ? S[0] : S[2], give1 = sel ? S[1] : S[3];
+    const int keep0 = sel ? S[2] : S[0], keep1 = sel ? S[3] : S[1];
+    s0 = keep0 + quad_xor2(give0);
+    s1 = keep1 + quad_xor2(give1);
+}
+
+// Part j of a Q4_K unit (kore.cpp:535-587): lanes k = 4(j%2) .. +3 over
+// groups c = j/2 and 2 + j/2; kept: lanes 4(j%2) + 2(j/2) + {0, 1}.  The
+// 4-lane minimum sum: lane j = sub-blocks 2j, 2j+1 (kore.cpp:556-560).
 template <bool AVX2>
 __device__ __forceinline__ Rec part_q4(const Q4Raw &r, const Q8View &x, int i, int j) {
-    int s0 = 0, s1 = 0;
+    const int hh = j & 1, c1 = j >> 1, c2 = c1 + 2;
+    const int sl1 = q4_scale(r.hdr, 2 * c1), sh1 = q4_scale(r.hdr, 2 * c1 + 1);
+    const int sl2 = q4_scale(r.hdr, 2 * c2), sh2 = q4_scale(r.hdr, 2 * c2 + 1);
+    const uint4 lo1 = x.qs16(i, 64 * c1 + 16 * hh), hi1 = x.qs16(i, 64 * c1 + 32 + 16 * hh);
+    const uint4 lo2 = x.qs16(i, 64 * c2 + 16 * hh), hi2 = x.qs16(i, 64 * c2 + 32 + 16 * hh);
+    int S[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int sl = q4_scale(r.hdr, 2 * c), sh = q4_scale(r.hdr, 2 * c + 1);
-        const uint2 lo8 = x.qs8(i, 64 * c + 8 * j), hi8 = x.qs8(i, 64 * c + 32 + 8 * j);
-        const uint32_t w0 = r.qs[c].x, w1 = r.qs[c].y;
-        s0 += mul24(sl, dot4(w0 & 0x0F0F0F0Fu, lo8.x)) + mul24(sh, dot4((w0 >> 4) & 0x0F0F0F0Fu, hi8.x));
-        s1 += mul24(sl, dot4(w1 & 0x0F0F0F0Fu, lo8.y)) + mul24(sh, dot4((w1 >> 4) & 0x0F0F0F0Fu, hi8.y));
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t a = w4(r.a, k), b = w4(r.b, k);
+        S[k] = mul24(sl1, dot4(a & 0x0F0F0F0Fu, w4(lo1, k))) + mul24(sh1, dot4((a >> 4) & 0x0F0F0F0Fu, w4(hi1, k))) +
+               mul24(sl2, dot4(b & 0x0F0F0F0Fu, w4(lo2, k))) + mul24(sh2, dot4((b >> 4) & 0x0F0F0F0Fu, w4(hi2, k)));
     }
     const int prod = mul24(q4_min(r.hdr, 2 * j), x.bsum(i, 4 * j) + x.bsum(i, 4 * j + 1)) +
                      mul24(q4_min(r.hdr, 2 * j + 1), x.bsum(i, 4 * j + 2) + x.bsum(i, 4 * j + 3));
     const float yd = x.d(i);
     const float d = f16_bits(r.hdr.x & 0xFFFFu) * yd;
     const float dmin = f16_bits(r.hdr.x >> 16) * yd;
-    if (AVX2) return Rec{s0, s1, prod, (j & 1) ? dmin : d};
-    int isum = s0 + s1, imin = prod;
+    if constexpr (AVX2) {
+        int s0, s1;
+        own_lanes(S, c1, s0, s1);
+        return Rec{s0, s1, prod, (j & 1) ? dmin : d};
+    }
+    int isum = (S[0] + S[1]) + (S[2] + S[3]), imin = prod;
     isum += quad_xor1(isum);
     isum += quad_xor2(isum);
     imin += quad_xor1(imin);
@@ -214,51 +268,49 @@ __device__ __forceinline__ Rec part_q4(const Q4Raw &r, const Q8View &x, int i, i
     return Rec{isum, imin, __float_as_int(dmin), d};
 }
 
-// Part j of a Q6_K unit: AVX2 lanes m = 2j, 2j+1 hold values 4m..4m+3 of each
-// 32-value group (h, k) (kore.cpp:606-627), scale sc[8h + 2k + (m >= 4)].
+// Part j of a Q6_K unit (kore.cpp:591-632): lanes m = 4g .. 4g+3 of groups
+// (h, kp) and (h, kp + 2), h = 0, 1 (g = j % 2, kp = j / 2), scale
+// sc[8h + 2k + g]; kept: lanes 4g + 2kp + {0, 1}.
 template <bool AVX2>
 __device__ __forceinline__ Rec part_q6(const Q6Raw &r, const Q8View &x, int i, int j) {
-    const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
-    const int g = j >> 1;
-    int s0 = 0, s1 = 0;
+    const int g = j & 1, kp = j >> 1;
+    const int sb = 8 * (2 * kp + g);
+    // scales of groups (h, k) = (0, kp), (0, kp+2), (1, kp), (1, kp+2)
+    const int s0 = (int)(int8_t)((r.sc.x >> sb) & 0xFF), s1 = (int)(int8_t)((r.sc.y >> sb) & 0xFF);
+    const int s2 = (int)(int8_t)((r.sc.z >> sb) & 0xFF), s3 = (int)(int8_t)((r.sc.w >> sb) & 0xFF);
+    const uint4 q0l = x.qs16(i, 32 * kp + 16 * g), q0h = x.qs16(i, 32 * (kp + 2) + 16 * g);
+    const uint4 q1l = x.qs16(i, 128 + 32 * kp + 16 * g), q1h = x.qs16(i, 128 + 32 * (kp + 2) + 16 * g);
+    const int shq = 2 * kp;
+    int S[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint2 A = r.a[h], B = r.b[h], Q = r.h[h];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int bi = 8 * h + 2 * k + g;
-            const int sc = (int)(int8_t)((scw[bi >> 2] >> (8 * (bi & 3))) & 0xFF);
-            uint32_t u0, u1;
-            if (k == 0) {
-                u0 = (A.x & 0x0F0F0F0Fu) | ((Q.x << 4) & 0x30303030u);
-                u1 = (A.y & 0x0F0F0F0Fu) | ((Q.y << 4) & 0x30303030u);
-            } else if (k == 1) {
-                u0 = (B.x & 0x0F0F0F0Fu) | ((Q.x << 2) & 0x30303030u);
-                u1 = (B.y & 0x0F0F0F0Fu) | ((Q.y << 2) & 0x30303030u);
-            } else if (k == 2) {
-                u0 = ((A.x >> 4) & 0x0F0F0F0Fu) | (Q.x & 0x30303030u);
-                u1 = ((A.y >> 4) & 0x0F0F0F0Fu) | (Q.y & 0x30303030u);
-            } else {
-                u0 = ((B.x >> 4) & 0x0F0F0F0Fu) | ((Q.x >> 2) & 0x30303030u);
-                u1 = ((B.y >> 4) & 0x0F0F0F0Fu) | ((Q.y >> 2) & 0x30303030u);
-            }
-            const uint2 q8 = x.qs8(i, 128 * h + 32 * k + 8 * j);
-            s0 += mul24(sc, dot4(u0, q8.x));
-            s1 += mul24(sc, dot4(u1, q8.y));
-        }
+    for (int k = 0; k < 4; ++k) {
+        // two high bits of group k at bit 2k of qh: shifted once, bits 4-5 of
+        // (q >> 2kp) << 4 are group kp's, bits 4-5 of q >> 2kp group kp+2's
+        const uint32_t a0 = w4(r.a0, k), a1 = w4(r.a1, k);
+        const uint32_t qq0 = w4(r.h0, k) >> shq, qq1 = w4(r.h1, k) >> shq;
+        const uint32_t u0l = (a0 & 0x0F0F0F0Fu) | ((qq0 << 4) & 0x30303030u);
+        const uint32_t u0h = ((a0 >> 4) & 0x0F0F0F0Fu) | (qq0 & 0x30303030u);
+        const uint32_t u1l = (a1 & 0x0F0F0F0Fu) | ((qq1 << 4) & 0x30303030u);
+        const uint32_t u1h = ((a1 >> 4) & 0x0F0F0F0Fu) | (qq1 & 0x30303030u);
+        S[k] = mul24(s0, dot4(u0l, w4(q0l, k))) + mul24(s1, dot4(u0h, w4(q0h, k))) +
+               mul24(s2, dot4(u1l, w4(q1l, k))) + mul24(s3, dot4(u1h, w4(q1h, k)));
     }
     // bias sum over the 16 sub-blocks (kore.cpp:605): part j takes 4j .. 4j+3
     int ibias = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        ibias += mul24((int)(int8_t)((scw[j] >> (8 * e)) & 0xFF), x.bsum(i, 4 * j + e));
+        ibias += mul24((int)(int8_t)((w4(r.sc, j) >> (8 * e)) & 0xFF), x.bsum(i, 4 * j + e));
     ibias += quad_xor1(ibias);
     ibias += quad_xor2(ibias);
     const float d = f16_bits(r.d) * x.d(i);
-    if (AVX2) return Rec{s0, s1, ibias, d};
+    if constexpr (AVX2) {
+        int s0, s1;
+        own_lanes(S, kp, s0, s1);
+        return Rec{s0, s1, ibias, d};
+    }
     // kore's scalar reference sums (q6 - 32) * q8 (kore.cpp:480-506): the same
     // integer as sum(sc * q6 * q8) - 32 * sum(sc * bsums)
-    int isum = s0 + s1;
+    int isum = (S[0] + S[1]) + (S[2] + S[3]);
     isum += quad_xor1(isum);
     isum += quad_xor2(isum);
     return Rec{isum - 32 * ibias, 0, 0, d};
@@ -315,16 +367,27 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
 
     // the activations
     if constexpr (FUSED) {
-        for (int b = t >> 4; b < nblk; b += kThreads / 16) quantize_block(a.x + (int64_t)b * 256, t & 15, xs + b * kQ8Bytes);
-    } else {
-        const int bytes = nblk * kQ8Bytes, n16 = bytes >> 4;
-        const uint4 *src = (const uint4 *)a.xq;
-        for (int c = t; c < n16; c += kThreads) ((uint4 *)xs)[c] = src[c];
-        for (int c = 4 * n16 + t; c < (bytes >> 2); c += kThreads)
+        for (int b = t >> 4; b < nblk; b += kThreads / 16)
+            xs_store(xs, nblk, b, t & 15, quantize_lane(a.x + (int64_t)b * 256, t & 15));
+    } else if (a.xq_image) {
+        // already in the LDS layout (xs_bytes(nblk) is a multiple of 4 bytes)
+        const int n16 = (int)(xs_bytes(nblk) >> 4);
+        for (int c = t; c < n16; c += kThreads) ((uint4 *)xs)[c] = ((const uint4 *)a.xq)[c];
+        for (int c = 4 * n16 + t; c < (int)(xs_bytes(nblk) >> 2); c += kThreads)
             ((uint32_t *)xs)[c] = ((const uint32_t *)a.xq)[c];
+    } else {
+        // kore's records (dword-aligned) into the LDS layout: per block, the
+        // 64 qs dwords by 64 lanes, then the 8 bsums dwords and d
+        const int w = t >> 6, l = t & 63;
+        for (int b = w; b < nblk; b += kThreads / 64) {
+            const uint32_t *src = (const uint32_t *)(a.xq + b * kQ8Bytes);
+            *(uint32_t *)(xs + b * kXsQs + 4 * l) = src[1 + l];
+            if (l < 8) *(uint32_t *)(xs + nblk * kXsQs + 32 * b + 4 * l) = src[65 + l];
+            else if (l == 8) *(float *)(xs + nblk * 304 + 4 * b) = __uint_as_float(src[0]);
+        }
     }
     __syncthreads();
-    const Q8View x{xs};
+    const Q8View x{xs, nblk};
 
     float acc0 = 0.f, acc1 = 0.f, accm = 0.f;               // chain state of the phase-0 lanes
     const bool chain = ph == 0;
@@ -400,10 +463,11 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
                         float res;
                         if constexpr (AVX2) {
                             // kore's hsum256 (kore.cpp:521-528): lanes k and k+4 first,
-                            // then (l0 + l2) + (l1 + l3); lanes 2j / 2j+1 live in part j
-                            const float u = acc0 + quad_xor2f(acc0);     // part 0: l0, part 1: l2
-                            const float v = acc1 + quad_xor2f(acc1);     // part 0: l1, part 1: l3
-                            const float h8 = (u + quad_xor1f(u)) + (v + quad_xor1f(v));
+                            // then (l0 + l2) + (l1 + l3); parts 0..3 hold lanes {0,1},
+                            // {4,5}, {2,3}, {6,7}
+                            const float u = acc0 + quad_xor1f(acc0);     // part 0: l0, part 2: l2
+                            const float v = acc1 + quad_xor1f(acc1);     // part 0: l1, part 2: l3
+                            const float h8 = (u + quad_xor2f(u)) + (v + quad_xor2f(v));
                             if constexpr (TYPE == kQ4K) {
                                 const float m = accm + quad_xor2f(accm); // hsum128 (kore.cpp:537-541)
                                 res = h8 + (m + quad_xor1f(m));
@@ -482,7 +546,7 @@ __global__ __launch_bounds__(kThreads) void synth_blocks_kernel(uint16_t *__rest
 
 template <bool AVX2, int RW, bool FUSED>
 hipError_t launch_group_r(const GroupArgs &a, int grid, hipStream_t s) {
-    const size_t lds = 2 * kThreads * sizeof(Rec) + (size_t)a.nblk * kQ8Bytes;
+    const size_t lds = 2 * kThreads * sizeof(Rec) + xs_bytes(a.nblk);
     hipLaunchKernelGGL((matvec_group_kernel<AVX2, RW, FUSED>), dim3(grid), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
@@ -543,11 +607,13 @@ hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int ma
     return fused ? launch_group_f<false, true>(a, rw, grid, s) : launch_group_f<false, false>(a, rw, grid, s);
 }
 
-hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, hipStream_t s) {
+hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool image, hipStream_t s) {
     const int64_t nb = n / 256;
     if (nb <= 0) return hipSuccess;
+    if (image && nb > kMaxBlocks) return hipErrorInvalidValue;
     const int64_t grid = (nb + kThreads / 16 - 1) / (kThreads / 16);
-    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb);
+    if (image) hipLaunchKernelGGL(quantize_q8k_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb);
+    else hipLaunchKernelGGL(quantize_q8k_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb);
     return hipGetLastError();
 }
 
