@@ -95,6 +95,8 @@ def lib() -> C.CDLL:
         L.ko_dot_q6K_avx2_v.argtypes = [C.c_int64, _u8, _u8, C.c_int]
         L.ko_dot_q6K_avx2_v.restype = C.c_float
         L.ko_qmatvec.argtypes = [C.c_int, C.c_int64, C.c_int64, _u8, _u8, _F, C.c_int]
+        L.ko_dequant_row.argtypes = [C.c_int, C.c_int64, _u8, _F]
+        L.ko_matmul_batch.argtypes = [C.c_int, C.c_int64, C.c_int64, _u8, _F, C.c_int, _F, C.c_int]
         _lib = L
     return _lib
 
@@ -260,6 +262,25 @@ def qmatvec(wtype: int, weights: np.ndarray, rows: int, cols: int, xq: np.ndarra
     rc = lib().ko_qmatvec(wtype, rows, cols, w.ctypes.data, xq.ctypes.data, fptr(out), int(avx2))
     if rc != 0:
         raise ValueError("ko_qmatvec rejected the type or cols")
+    return out
+
+
+def dequant_row(wtype: int, wrow: np.ndarray, cols: int) -> np.ndarray:
+    """kore's dequant_block_q4_K / _q6_K over one row (kore.cpp:337-381)."""
+    out = np.zeros(cols, np.float32)
+    lib().ko_dequant_row(wtype, cols, _w(wrow).ctypes.data, fptr(out))
+    return out
+
+
+def matmul_batch(wtype: int, weights: np.ndarray, rows: int, cols: int, x: np.ndarray,
+                 avx2: bool = True) -> np.ndarray:
+    """kore's matmul_batch_float (kore.cpp:783-845): x [B][cols] -> out [B][rows]."""
+    w = _w(weights)
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    out = np.zeros((x.shape[0], rows), np.float32)
+    rc = lib().ko_matmul_batch(wtype, rows, cols, w.ctypes.data, fptr(x), x.shape[0], fptr(out), int(avx2))
+    if rc != 0:
+        raise ValueError("ko_matmul_batch rejected the type, cols or B")
     return out
 
 

@@ -20,6 +20,8 @@
  *   ko_dot_q6K_avx2    kore.cpp:591-632
  *   ko_qmatvec         kore.cpp:649-682   (one dot product per row; the row
  *                      partition over threads does not change any result)
+ *   ko_dequant_row     kore.cpp:337-381   (dequant_block_q4_K / _q6_K)
+ *   ko_matmul_batch    kore.cpp:744-845   (matmul_batch_float, AVX2 and scalar)
  * Every AVX2 lane sum is an exact integer; the float steps are restated with
  * explicit fmaf() where kore uses _mm256_fmadd_ps / _mm_fmadd_ps, and the
  * file is compiled with -ffp-contract=off so no other product is fused.
@@ -250,6 +252,77 @@ int ko_qmatvec(int type, int64_t rows, int64_t cols, const uint8_t *w, const KoQ
         const uint8_t *wr = w + r * row_bytes;
         if (type == KO_TYPE_Q4K) out[r] = avx2 ? ko_dot_q4K_avx2(cols, wr, xq) : ko_dot_q4K_ref(cols, wr, xq);
         else out[r] = avx2 ? ko_dot_q6K_avx2(cols, wr, xq) : ko_dot_q6K_ref(cols, wr, xq);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ batched
+ * kore's matmul_batch_float (kore.cpp:783-845): out[b * rows + r] = row r of
+ * the dequantised weights . x[b], B activations at once.
+ *   dequantisation (kore.cpp:337-381): Q4_K value = d1 * q - m1 with
+ *     d1 = d * scale, m1 = dmin * min (each product rounded); Q6_K value =
+ *     (d * scale) * (q - 32); plain float arithmetic (no fused steps: the
+ *     dequantisers are compiled without FMA).
+ *   AVX2 (kore.cpp:744-779): per (row, b) one fused multiply-add chain over
+ *     the columns in order, starting from 0.
+ *   scalar (kore.cpp:820-839): per 256-column block a double sum in column
+ *     order, added to a float accumulator.
+ */
+static void dequant_q4K_block(const uint8_t *b, float *y) {
+    const float d = rd16(b), dmin = rd16(b + 2);
+    const uint8_t *q = b + 16;
+    for (int c = 0; c < 4; c++) {
+        int sc, mn;
+        q4k_scale_min(2 * c, b + 4, &sc, &mn);
+        const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+        q4k_scale_min(2 * c + 1, b + 4, &sc, &mn);
+        const float d2 = d * (float)sc, m2 = dmin * (float)mn;
+        for (int l = 0; l < 32; l++) y[64 * c + l] = d1 * (float)(q[32 * c + l] & 0x0F) - m1;
+        for (int l = 0; l < 32; l++) y[64 * c + 32 + l] = d2 * (float)(q[32 * c + l] >> 4) - m2;
+    }
+}
+
+static void dequant_q6K_block(const uint8_t *b, float *y) {
+    const int8_t *sc = (const int8_t *)(b + 192);
+    const float d = rd16(b + 208);
+    for (int v = 0; v < 256; v++) {
+        const int h = v / 128, k = (v % 128) / 32, l = v % 32;
+        const float ds = d * (float)sc[8 * h + 2 * k + l / 16];
+        y[v] = ds * (float)(q6k_u6(b, v) - 32);
+    }
+}
+
+void ko_dequant_row(int type, int64_t cols, const uint8_t *w, float *y) {
+    const int64_t nb = cols / 256;
+    for (int64_t i = 0; i < nb; i++) {
+        if (type == KO_TYPE_Q4K) dequant_q4K_block(w + i * KO_Q4K_BYTES, y + 256 * i);
+        else dequant_q6K_block(w + i * KO_Q6K_BYTES, y + 256 * i);
+    }
+}
+
+int ko_matmul_batch(int type, int64_t rows, int64_t cols, const uint8_t *w, const float *x, int B, float *out,
+                    int avx2) {
+    if (cols % 256 != 0 || B <= 0 || (type != KO_TYPE_Q4K && type != KO_TYPE_Q6K)) return -1;
+    const int64_t nb = cols / 256, rb = nb * (type == KO_TYPE_Q4K ? KO_Q4K_BYTES : KO_Q6K_BYTES);
+    float wf[256];
+    for (int64_t r = 0; r < rows; r++) {
+        for (int b = 0; b < B; b++) out[(size_t)b * rows + r] = 0.f;
+        for (int64_t i = 0; i < nb; i++) {
+            ko_dequant_row(type, 256, w + r * rb + i * (rb / nb), wf);
+            for (int b = 0; b < B; b++) {
+                const float *xb = x + (size_t)b * cols + 256 * i;
+                float *o = &out[(size_t)b * rows + r];
+                if (avx2) {
+                    float acc = *o;
+                    for (int j = 0; j < 256; j++) acc = fmaf(wf[j], xb[j], acc);
+                    *o = acc;
+                } else {
+                    double s = 0;
+                    for (int j = 0; j < 256; j++) s += (double)wf[j] * xb[j];
+                    *o = *o + (float)s;
+                }
+            }
+        }
     }
     return 0;
 }

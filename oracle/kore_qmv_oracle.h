@@ -48,6 +48,14 @@ float ko_dot_q6K_avx2_v(int64_t n, const uint8_t *w, const KoQ8K *y, int fused_b
 int   ko_qmatvec(int type, int64_t rows, int64_t cols, const uint8_t *w, const KoQ8K *xq, float *out,
                  int avx2);
 
+/* kore's dequantisers (kore.cpp:337-381): cols values of one row */
+void  ko_dequant_row(int type, int64_t cols, const uint8_t *w, float *y);
+/* kore's matmul_batch_float (kore.cpp:783-845): out[b * rows + r] for B
+ * activations x[b * cols + j]; avx2 = 1: one fused multiply-add chain per
+ * output, 0: per-block double sums; -1 for a bad type, cols or B */
+int   ko_matmul_batch(int type, int64_t rows, int64_t cols, const uint8_t *w, const float *x, int B, float *out,
+                      int avx2);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,6 +12,12 @@
 //   then out_ref[rows], then out_avx2[rows] (float32; out_avx2 equals out_ref
 //   where the CPU has no AVX2/FMA).
 //
+// Batch mode (kore's matmul_batch_float, kore.cpp:783-845):
+//   kore_qmv_ref --batch job.bin result.bin
+// job: int32 type, rows, cols, B; the weights; x as B rows of cols float32.
+// result: out[b * rows + r] of the AVX2 path, then of the scalar path (the
+// AVX2 one equals the scalar one where the CPU has no AVX2/FMA).
+//
 // Timing mode (the CPU baseline of the benchmark):
 //   kore_qmv_ref --time THREADS MIN_SECONDS COPIES job.bin
 // keeps COPIES copies of the job's matrix (so that the weights streamed exceed
@@ -79,7 +85,41 @@ static int time_mode(unsigned nth, double min_s, int copies, const char *job) {
     return 0;
 }
 
+static int batch_mode(const char *job, const char *res) {
+    FILE *in = fopen(job, "rb");
+    FILE *out = fopen(res, "wb");
+    if (!in || !out) { perror("open"); return 2; }
+    int32_t hdr[4];
+    if (fread(hdr, 4, 4, in) != 4) return 3;
+    const int type = hdr[0], B = hdr[3];
+    const int64_t rows = hdr[1], cols = hdr[2];
+    if (cols % 256 != 0 || (type != GGML_Q4_K && type != GGML_Q6_K) || B <= 0 || B > KORE_BMAX) return 3;
+    const int64_t nb = cols / 256, bb = type == GGML_Q4_K ? 144 : 210;
+    std::vector<uint8_t> w((size_t)(rows * nb * bb));
+    std::vector<float> x((size_t)(B * cols));
+    if (fread(w.data(), 1, w.size(), in) != w.size()) return 3;
+    if (fread(x.data(), 4, x.size(), in) != x.size()) return 3;
+    fclose(in);
+    Tensor t;
+    t.type = (uint32_t)type;
+    t.n_dims = 2;
+    t.dims[0] = (uint64_t)cols;
+    t.dims[1] = (uint64_t)rows;
+    t.nbytes = w.size();
+    t.data = w.data();
+    const int B8 = (B + 7) & ~7;
+    std::vector<float> xT((size_t)(cols * B8)), o1((size_t)(rows * B)), o2((size_t)(rows * B));
+    const bool avx2 = cpu_has_avx2();
+    matmul_batch_float(t, x.data(), B, xT.data(), o1.data(), avx2, 1);
+    matmul_batch_float(t, x.data(), B, xT.data(), o2.data(), false, 1);
+    if (fwrite(o1.data(), 4, o1.size(), out) != o1.size()) return 4;
+    if (fwrite(o2.data(), 4, o2.size(), out) != o2.size()) return 4;
+    fclose(out);
+    return avx2 ? 0 : 10;
+}
+
 int main(int argc, char **argv) {
+    if (argc == 4 && std::string(argv[1]) == "--batch") return batch_mode(argv[2], argv[3]);
     if (argc == 6 && std::string(argv[1]) == "--time")
         return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), argv[5]);
     if (argc != 3) {

@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Write the golden fixtures of kore's quantised matvec.
+"""Write the golden fixtures of kore's quantised matvec and batched matmul.
 
 Runs kore's own quantize_row_q8_K and its Q4_K / Q6_K x Q8_K dot products,
 scalar and AVX2 (kore.cpp:422-632), through oracle/_ref/kore_qmv_ref (built by
@@ -8,7 +8,9 @@ oracle/ref_qmv_harness.cpp) on the cases below and stores, per case:
 
 * ``qmv_<case>.npz``: the weight bytes, the input x, kore's Q8_K blocks of x
   (292 bytes each) and kore's row results, scalar and AVX2;
-* ``qmv_<case>.json``: the case and the sha256 of every array.
+* ``qmv_<case>.json``: the case and the sha256 of every array;
+* ``qmm_<case>.npz`` / ``.json``: kore's matmul_batch_float (kore.cpp:783-845),
+  AVX2 and scalar paths, for B activations at once.
 
 The weights and inputs are synthetic (numpy PCG64, fixed seeds) and include
 the corner cases the formats and the quantiser have: an all-zero block of x, a
@@ -48,6 +50,15 @@ CASES = [
 
 def f16_bits(v) -> np.ndarray:
     return np.asarray(v, np.float16).view(np.uint16)
+
+
+BATCH_CASES = [
+    # name, type, rows, cols, B, seed
+    ("q4k_b5", oracle.TYPE_Q4K, 40, 1024, 5, 21),
+    ("q6k_b64", oracle.TYPE_Q6K, 33, 768, 64, 22),
+    ("q4k_b13_odd", oracle.TYPE_Q4K, 17, 2304, 13, 23),
+    ("q6k_b1", oracle.TYPE_Q6K, 8, 512, 1, 24),
+]
 
 
 def synth_weights(wtype: int, rows: int, nblk: int, rng: np.random.Generator) -> np.ndarray:
@@ -125,6 +136,21 @@ def run_ref(wtype: int, rows: int, cols: int, w: np.ndarray, x: np.ndarray):
     return xq, outs[:rows].copy(), outs[rows:].copy()
 
 
+def run_ref_batch(wtype: int, rows: int, cols: int, B: int, w: np.ndarray, x: np.ndarray):
+    with tempfile.TemporaryDirectory() as td:
+        job, res = os.path.join(td, "job.bin"), os.path.join(td, "res.bin")
+        with open(job, "wb") as f:
+            f.write(struct.pack("<4i", wtype, rows, cols, B))
+            f.write(w.tobytes())
+            f.write(x.astype("<f4").tobytes())
+        rc = subprocess.run([oracle.REF_QMV_BIN, "--batch", job, res]).returncode
+        if rc != 0:
+            raise RuntimeError(f"kore_qmv_ref --batch failed ({rc})")
+        outs = np.fromfile(res, "<f4")
+    assert outs.size == 2 * rows * B
+    return outs[:rows * B].copy(), outs[rows * B:].copy()
+
+
 def sha(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
@@ -146,6 +172,20 @@ def main():
         with open(os.path.join(HERE, f"qmv_{name}.json"), "w") as f:
             json.dump(man, f, indent=1)
         print(f"qmv_{name}: {rows} x {cols}, max|out| {float(np.max(np.abs(out_ref))):.4g}")
+    for name, wtype, rows, cols, B, seed in BATCH_CASES:
+        rng = np.random.default_rng(seed)
+        w = synth_weights(wtype, rows, cols // 256, rng)
+        x = np.stack([synth_x(cols, rng) for _ in range(B)])
+        out_avx2, out_ref = run_ref_batch(wtype, rows, cols, B, w, x)
+        np.savez_compressed(os.path.join(HERE, f"qmm_{name}.npz"), weights=w, x=x, out_avx2=out_avx2,
+                            out_ref=out_ref)
+        man = {"name": name, "type": wtype, "rows": rows, "cols": cols, "B": B, "seed": seed,
+               "source": "kore.cpp matmul_batch_float (AVX2 and scalar) via oracle/_ref/kore_qmv_ref --batch",
+               "sha256": {k: sha(v) for k, v in (("weights", w), ("x", x), ("out_avx2", out_avx2),
+                                                  ("out_ref", out_ref))}}
+        with open(os.path.join(HERE, f"qmm_{name}.json"), "w") as f:
+            json.dump(man, f, indent=1)
+        print(f"qmm_{name}: {rows} x {cols}, B {B}, max|out| {float(np.max(np.abs(out_avx2))):.4g}")
 
 
 if __name__ == "__main__":

@@ -186,3 +186,54 @@ def test_quantize_matches_numpy_restatement_on_random_blocks():
     qs = np.minimum(np.rint((iscale[:, None] * xb).astype(np.float32)), 127).astype(np.int8)
     assert np.array_equal(q["qs"], qs)
     assert np.array_equal(q["d"], (np.float32(1.0) / iscale).astype(np.float32))
+
+
+# ---------------------------------------------------------------- batched matmul
+
+BATCH = sorted(f[4:-5] for f in os.listdir(GOLD) if f.startswith("qmm_") and f.endswith(".json"))
+
+
+def _load_batch(name):
+    man = json.load(open(os.path.join(GOLD, f"qmm_{name}.json")))
+    z = np.load(os.path.join(GOLD, f"qmm_{name}.npz"))
+    return man, {k: z[k] for k in z.files}
+
+
+def test_batch_fixture_set_present():
+    assert {"q4k_b5", "q6k_b64", "q4k_b13_odd", "q6k_b1"} <= set(BATCH)
+
+
+@pytest.mark.parametrize("name", BATCH)
+@pytest.mark.parametrize("avx2", [False, True])
+def test_matmul_batch_matches_kore_bits(name, avx2):
+    man, z = _load_batch(name)
+    out = oracle.matmul_batch(man["type"], z["weights"], man["rows"], man["cols"], z["x"], avx2=avx2)
+    assert _bits_equal(out.reshape(-1), z["out_avx2" if avx2 else "out_ref"])
+
+
+def test_matmul_batch_orders_differ():
+    for name in BATCH:
+        man, z = _load_batch(name)
+        assert not _bits_equal(z["out_avx2"], z["out_ref"]), name
+
+
+@pytest.mark.parametrize("name", BATCH)
+def test_dequant_and_batch_against_float64(name):
+    """kore's float dequantisation equals the block layout's values to fp32
+    rounding, and every output is the float64 dot product of those values
+    with x to within fp32 accumulation error."""
+    man, z = _load_batch(name)
+    t, rows, cols = man["type"], man["rows"], man["cols"]
+    nb, bb = cols // 256, oracle.BLOCK_BYTES[t]
+    deq = dequant_q4k if t == oracle.TYPE_Q4K else dequant_q6k
+    w = z["weights"].reshape(rows, nb, bb)
+    x = z["x"].astype(np.float64)
+    for r in range(rows):
+        exact = np.concatenate([deq(w[r, i]) for i in range(nb)])
+        got = oracle.dequant_row(t, w[r].reshape(-1), cols).astype(np.float64)
+        assert np.all(np.abs(got - exact) <= 2.5e-7 * np.abs(exact) + 1e-30), (name, r)
+        ref = x @ exact
+        mag = np.abs(x) @ np.abs(exact) + 1e-30
+        for key in ("out_avx2", "out_ref"):
+            o = z[key].reshape(man["B"], rows)[:, r].astype(np.float64)
+            assert np.all(np.abs(o - ref) <= 1e-5 * mag), (name, key, r)
