@@ -104,6 +104,23 @@ KORE_QMV_API int kore_qmv_mv_dev(kore_qmv_tensor_t t, const float *x, float *out
 KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *tensors, const float *x,
                                        float *const *outs, int avx2, void *stream);
 
+/* kore's batched prefill matmul, matmul_batch_float (kore.cpp:783-845), as
+ * forward_batch() calls it for q/k/v, Wo, gate/up and down (kore.cpp:1524-1583):
+ * x [nb][cols] fp32 activations, 1 <= nb <= 64 (kore's KORE_BMAX,
+ * kore.cpp:690) -> out [nb][rows] (out[b * rows + r], kore's layout).  fp32
+ * MFMA on weights dequantised as kore does (kore.cpp:337-381): the results
+ * agree with kore's to fp32 rounding, max|d| <= 1e-4 * max|ref| + 1e-6 (kore's
+ * own tolerance, kore_kernels.cpp:742), not bit for bit (kore sums each
+ * output in one FMA chain over the columns).  Host buffers, synchronous. */
+KORE_QMV_API int kore_qmv_matmul_batch(kore_qmv_tensor_t t, const float *x, int nb, float *out);
+
+/* Same with device buffers (x 16-byte aligned).  Row-poor matrices split
+ * their columns over several workgroups and add the partial sums in a second
+ * launch, through a workspace of the device that tensor creation sizes: calls
+ * that overlap on different streams of one device race on it. */
+KORE_QMV_API int kore_qmv_matmul_batch_dev(kore_qmv_tensor_t t, const float *x, int nb, float *out,
+                                           void *stream);
+
 /* Text of the last failure on this tensor (or, with NULL, of the last failed
  * call without a tensor on this thread).  Never NULL. */
 KORE_QMV_API const char *kore_qmv_last_error(kore_qmv_tensor_t t);

@@ -26,6 +26,7 @@ struct kore_qmv_tensor {
     uint8_t *w = nullptr;      // Q4_K blocks or Q6_K bodies
     uint16_t *wd = nullptr;    // Q6_K scales
     uint8_t *xq = nullptr;     // quantised activations (the matvec's layout) when quantised apart
+    int gemm_splits = 1;       // split-K of the batched matmul
     size_t weight_bytes = 0;
     std::string error;
 };
@@ -48,6 +49,15 @@ int hip_fail(kore_qmv_tensor *t, hipError_t e, const char *what) {
         hipError_t e_ = (call);                                 \
         if (e_ != hipSuccess) return hip_fail((t), e_, #call);  \
     } while (0)
+
+// Per-device workspace of the batched matmul's split-K partial sums, grown when
+// a tensor that needs more is created (never inside a call).
+struct GemmScratch {
+    std::mutex mu;
+    void *p = nullptr;
+    size_t cap = 0;
+};
+GemmScratch g_gemm[64];
 
 // Per-device staging buffers and stream of the synchronous host-pointer calls.
 struct HostPath {
@@ -157,6 +167,23 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
     t->num_cu = num_cu;
     t->rows_per_wave = pick_rows_per_wave(rows, num_cu);
     if ((e = hipMalloc(&t->xq, (size_t)t->nblk * 308)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
+    t->gemm_splits = gemm_splits((int)rows, t->nblk, num_cu);
+    if (t->gemm_splits > 1) {
+        if (t->device < 0 || t->device >= 64) return bail(fail(t, KORE_QMV_E_UNSUPPORTED, "device ordinal above 63"));
+        GemmScratch &g = g_gemm[t->device];
+        std::lock_guard<std::mutex> lock(g.mu);
+        const size_t need = (size_t)t->gemm_splits * kGemmMaxB * (size_t)rows * sizeof(float);
+        if (g.cap < need) {
+            void *np = nullptr;
+            if ((e = hipMalloc(&np, need)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
+            if (g.p) {
+                (void)hipDeviceSynchronize();   // no call may still use the old workspace
+                (void)hipFree(g.p);
+            }
+            g.p = np;
+            g.cap = need;
+        }
+    }
 
     const int64_t nblocks = rows * t->nblk;
     const size_t bb = type == KORE_QMV_Q4_K ? kQ4Bytes : kQ6Bytes;
@@ -325,6 +352,46 @@ KORE_QMV_API int kore_qmv_mv(kore_qmv_tensor_t t, const float *x, float *out, in
     QMV_TRY(t, hipGetDevice(&cur));
     if (cur != t->device) QMV_TRY(t, hipSetDevice(t->device));
     const int rc = matvec_host(t, x, nullptr, out, avx2);
+    if (cur != t->device) (void)hipSetDevice(cur);
+    return rc;
+}
+
+KORE_QMV_API int kore_qmv_matmul_batch_dev(kore_qmv_tensor_t t, const float *x, int nb, float *out, void *stream) {
+    if (!t) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
+    if (nb < 1 || nb > kGemmMaxB) return fail(t, KORE_QMV_E_INVALID, "nb must be 1..64 (kore's KORE_BMAX)");
+    if (int rc = check_dev_ptr(t, x, 16, "x")) return rc;
+    if (int rc = check_dev_ptr(t, out, 4, "out")) return rc;
+    GemmArgs a{t->w, t->wd, t->type, x, nullptr, (int)t->rows, t->nblk, nb, t->gemm_splits};
+    hipError_t e = launch_gemm(a, out, t->gemm_splits > 1 ? (float *)g_gemm[t->device & 63].p : nullptr,
+                               (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(t, e, "matmul launch");
+    return KORE_QMV_OK;
+}
+
+KORE_QMV_API int kore_qmv_matmul_batch(kore_qmv_tensor_t t, const float *x, int nb, float *out) {
+    if (!t) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
+    if (!x || !out) return fail(t, KORE_QMV_E_INVALID, "x or out is NULL");
+    if (nb < 1 || nb > kGemmMaxB) return fail(t, KORE_QMV_E_INVALID, "nb must be 1..64 (kore's KORE_BMAX)");
+    int cur = -1;
+    QMV_TRY(t, hipGetDevice(&cur));
+    if (cur != t->device) QMV_TRY(t, hipSetDevice(t->device));
+    int rc = KORE_QMV_OK;
+    {
+        const size_t xb = align256((size_t)nb * t->cols * 4), ob = align256((size_t)nb * t->rows * 4);
+        HostPath *h = nullptr;
+        std::lock_guard<std::mutex> lock(g_host[t->device & 63].mu);
+        hipError_t e = host_path(t->device, xb + ob, &h);
+        if (e != hipSuccess) rc = hip_fail(t, e, "host staging");
+        if (!rc) {
+            float *dx = (float *)h->buf, *dout = (float *)((uint8_t *)h->buf + xb);
+            if ((e = hipMemcpyAsync(dx, x, (size_t)nb * t->cols * 4, hipMemcpyHostToDevice, h->stream)) != hipSuccess)
+                rc = hip_fail(t, e, "hipMemcpyAsync");
+            if (!rc) rc = kore_qmv_matmul_batch_dev(t, dx, nb, dout, h->stream);
+            if (!rc && (e = hipMemcpyAsync(out, dout, (size_t)nb * t->rows * 4, hipMemcpyDeviceToHost, h->stream)) != hipSuccess)
+                rc = hip_fail(t, e, "hipMemcpyAsync");
+            if (!rc && (e = hipStreamSynchronize(h->stream)) != hipSuccess) rc = hip_fail(t, e, "hipStreamSynchronize");
+        }
+    }
     if (cur != t->device) (void)hipSetDevice(cur);
     return rc;
 }

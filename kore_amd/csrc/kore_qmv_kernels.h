@@ -15,6 +15,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <type_traits>
 
 namespace kore_qmv_gpu {
 
@@ -74,5 +75,22 @@ hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, 
 // Synthetic GGUF-format weights for benchmarks: nblocks raw Q4_K / Q6_K blocks
 // with hashed bytes and finite f16 scales (dst 2-byte aligned).
 hipError_t launch_synth_blocks(int type, int64_t nblocks, uint64_t seed, uint8_t *dst, hipStream_t s);
+
+// Batched prefill matmul (kore's matmul_batch_float, kore.cpp:783-845):
+// out[b * rows + r] = dequantised row r . x[b], b < B <= kGemmMaxB; fp32 MFMA,
+// equal to kore's results to fp32 rounding.
+constexpr int kGemmMaxB = 64;            // kore's KORE_BMAX (kore.cpp:690)
+struct GemmArgs {
+    const uint8_t *w;        // Q4_K blocks or Q6_K bodies
+    const uint16_t *wd;      // Q6_K f16 scales
+    int type;
+    const float *x;          // [B][nblk * 256], 16-byte aligned
+    float *out;              // set by launch_gemm
+    int rows, nblk, B;
+    int splits;              // workgroups per row tile along the blocks (gemm_splits)
+};
+int gemm_splits(int rows, int nblk, int num_cu);
+// partials: splits * B * rows floats when splits > 1
+hipError_t launch_gemm(GemmArgs a, float *out, float *partials, hipStream_t s);
 
 }  // namespace kore_qmv_gpu

@@ -50,6 +50,8 @@ SYMBOLS = [
     ("kore_qmv_mv", _i, [_vp, _vp, _vp, _i]),
     ("kore_qmv_mv_dev", _i, [_vp, _vp, _vp, _i, _vp]),
     ("kore_qmv_mv_group_dev", _i, [_i, _vp, _vp, _vp, _i, _vp]),
+    ("kore_qmv_matmul_batch", _i, [_vp, _vp, _i, _vp]),
+    ("kore_qmv_matmul_batch_dev", _i, [_vp, _vp, _i, _vp, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
     ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),
@@ -160,6 +162,16 @@ class QMat:
         out = np.zeros(self.rows, np.float32)
         _check(lib().kore_qmv_mv(self.handle, x.ctypes.data, out.ctypes.data, int(avx2)), self.handle)
         return out
+
+    def matmul_batch(self, x) -> np.ndarray:
+        """kore's matmul_batch_float: x [nb][cols] (nb <= 64) -> [nb][rows]."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.cols)
+        out = np.zeros((x.shape[0], self.rows), np.float32)
+        _check(lib().kore_qmv_matmul_batch(self.handle, x.ctypes.data, x.shape[0], out.ctypes.data), self.handle)
+        return out
+
+    def matmul_batch_dev(self, x_ptr: int, nb: int, out_ptr: int, stream=None) -> None:
+        _check(lib().kore_qmv_matmul_batch_dev(self.handle, x_ptr, nb, out_ptr, stream), self.handle)
 
     def matvec_dev(self, xq_ptr: int, out_ptr: int, avx2: bool = True, stream=None) -> None:
         _check(lib().kore_qmv_matvec_dev(self.handle, xq_ptr, out_ptr, int(avx2), stream), self.handle)

@@ -290,3 +290,97 @@ def test_repeated_calls_are_identical():
         first = m.mv(x)
         for _ in range(5):
             assert np.array_equal(_bits(m.mv(x)), _bits(first))
+
+
+# ---------------------------------------------------------------- batched matmul
+
+QMM = sorted(f[4:-5] for f in os.listdir(GOLD) if f.startswith("qmm_") and f.endswith(".json"))
+
+
+def _close_kore(out, ref, what):
+    """kore's own comparison (kore_kernels.cpp:742): max|d| <= 1e-4 * max|ref| + 1e-6."""
+    out = np.asarray(out, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    err = float(np.max(np.abs(out - ref)))
+    bound = 1e-4 * float(np.max(np.abs(ref))) + 1e-6
+    assert err <= bound, f"{what}: max|d| {err:.3e} > {bound:.3e}"
+
+
+@pytest.mark.parametrize("name", QMM)
+def test_matmul_batch_golden(name):
+    from kore_amd import qmv
+    man = json.load(open(os.path.join(GOLD, f"qmm_{name}.json")))
+    z = np.load(os.path.join(GOLD, f"qmm_{name}.npz"))
+    _say(f"qmm golden {name}: type {man['type']}, {man['rows']} x {man['cols']}, B {man['B']}")
+    with qmv.QMat(man["type"], man["rows"], man["cols"], z["weights"]) as m:
+        out = m.matmul_batch(z["x"])
+    _close_kore(out, z["out_avx2"], f"{name} vs kore avx2")
+    _close_kore(out, z["out_ref"], f"{name} vs kore scalar")
+
+
+GEMM_SHAPES = [  # type, rows, nblk, B
+    (oracle.TYPE_Q4K, 1, 1, 1), (oracle.TYPE_Q6K, 100, 3, 17), (oracle.TYPE_Q4K, 257, 2, 16),
+    (oracle.TYPE_Q4K, 3584, 14, 64), (oracle.TYPE_Q6K, 200, 74, 33), (oracle.TYPE_Q6K, 65, 14, 48),
+    (oracle.TYPE_Q4K, 130, 128, 5),
+]
+
+
+@pytest.mark.parametrize("wtype,rows,nblk,B", GEMM_SHAPES)
+def test_matmul_batch_vs_oracle(wtype, rows, nblk, B):
+    from kore_amd import qmv
+    _say(f"qmm random type {wtype}: {rows} x {nblk * 256}, B {B}")
+    rng = np.random.default_rng(rows * 7 + nblk * 3 + B)
+    w = _weights(wtype, rows, nblk, rng)
+    x = np.stack([_x(nblk * 256, rng) for _ in range(B)])
+    with qmv.QMat(wtype, rows, nblk * 256, w) as m:
+        out = m.matmul_batch(x)
+        again = m.matmul_batch(x)
+    assert np.array_equal(_bits(out), _bits(again)), "repeated calls differ"
+    _close_kore(out, oracle.matmul_batch(wtype, w, rows, nblk * 256, x, avx2=True), "vs oracle")
+
+
+def test_matmul_batch_device_api_and_rejections():
+    from kore_amd import hip, qmv
+    _say("qmm device API, Q4_K 600 x 2048, B 40")
+    rng = np.random.default_rng(91)
+    rows, cols, B = 600, 2048, 40
+    w = _weights(oracle.TYPE_Q4K, rows, cols // 256, rng)
+    x = np.stack([_x(cols, rng) for _ in range(B)])
+    with qmv.QMat(oracle.TYPE_Q4K, rows, cols, w) as m:
+        dx = hip.DeviceBuffer.from_array(x)
+        do = hip.DeviceBuffer(B * rows)
+        m.matmul_batch_dev(dx.ptr, B, do.ptr)
+        hip.synchronize()
+        assert np.array_equal(_bits(do.download()), _bits(m.matmul_batch(x).reshape(-1)))
+        for nb in (0, 65):
+            with pytest.raises(qmv.QmvError) as e:
+                m.matmul_batch_dev(dx.ptr, nb, do.ptr)
+            assert e.value.code == qmv.KORE_QMV_E_INVALID
+        dx.free()
+        do.free()
+
+
+@pytest.mark.parametrize("name,wtype,rows,cols", [("attn_q", oracle.TYPE_Q4K, 3584, 3584),
+                                                  ("ffn_gate", oracle.TYPE_Q4K, 18944, 3584),
+                                                  ("ffn_down", oracle.TYPE_Q6K, 3584, 18944)])
+def test_matmul_batch_7b_shapes(name, wtype, rows, cols):
+    """Full Qwen2.5-7B matrices, 64 activations; 192 sampled rows against the
+    oracle (its cost on the CPU is the bound here)."""
+    from kore_amd import hip, qmv
+    _say(f"qmm 7B {name}: type {wtype}, {rows} x {cols}, B 64")
+    nbytes = rows * cols // 256 * oracle.BLOCK_BYTES[wtype]
+    raw = hip.DeviceBuffer((nbytes + 3) // 4)
+    qmv.synth_dev(wtype, rows, cols, 777 + rows, raw.ptr)
+    hip.synchronize()
+    w = np.zeros(nbytes, np.uint8)
+    hip.check(hip.lib().hipMemcpy(w.ctypes.data, raw.ptr, nbytes, hip.D2H), "download")
+    rng = np.random.default_rng(cols)
+    x = np.stack([_x(cols, rng) for _ in range(64)])
+    with qmv.QMat(wtype, rows, cols, device_ptr=raw.ptr) as m:
+        raw.free()
+        out = m.matmul_batch(x)
+    rb = cols // 256 * oracle.BLOCK_BYTES[wtype]
+    pick = np.sort(rng.choice(rows, 192, replace=False))
+    wsub = np.concatenate([w[r * rb:(r + 1) * rb] for r in pick])
+    ref = oracle.matmul_batch(wtype, wsub, len(pick), cols, x, avx2=True)
+    _close_kore(out[:, pick], ref, name)
