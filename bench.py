@@ -64,6 +64,8 @@ TRAFFIC_PREFILL_BYTES = 109_052_000
 # the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
 # of weights, activations and outputs algorithmic)
 TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_416_000}
+# the same for the batched matmul leg's dominant launch (not yet measured: null)
+TRAFFIC_GEMM_BYTES: dict = {}
 
 # Qwen2.5-7B matrix shapes of the matvec leg
 QMV_FF, QMV_VOCAB = 18944, 152064
@@ -343,10 +345,8 @@ def _op(kind, tensors=(), x=None, n=0, xq=None, outs=()):
     return o
 
 
-def gpu_matvec(tokens: int, warmup: int):
-    """One 7B token's quant() + mv() sequence (kore.cpp:1418-1477) over 28
-    distinct layers plus the output head, replayed `tokens` times from C++."""
-    from kore_amd import hip, qmv
+def _qmv_bench_lib():
+    from kore_amd import qmv
     path = os.path.join(ROOT, "kore_amd", "libkore_qmv_bench.so")
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built; run `make -C kore_amd/csrc`")
@@ -354,29 +354,59 @@ def gpu_matvec(tokens: int, warmup: int):
     B = C.CDLL(path)
     B.kqb_run.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
                           C.POINTER(C.c_float), C.POINTER(C.c_double)]
+    return B
+
+
+def qmv_tensors():
+    """The 197 weight matrices of one 7B token (qmv_token_matrices), synthetic,
+    resident on the device; the bytes of the first are kept for the parity
+    checks against kore's arithmetic."""
+    from kore_amd import hip, qmv
     mats = qmv_token_matrices()
     biggest = max(qmv_weight_bytes(t, r, c) for _, t, r, c in mats)
     raw = hip.DeviceBuffer((biggest + 3) // 4)
     tensors, first_raw = [], None
-    print(f"[bench] matvec: creating {len(mats)} synthetic weight matrices", file=sys.stderr, flush=True)
+    print(f"[bench] creating {len(mats)} synthetic weight matrices", file=sys.stderr, flush=True)
     for idx, (name, t, r, c) in enumerate(mats):
         qmv.synth_dev(t, r, c, QMV_SEED * 1000 + idx, raw.ptr)
-        if idx == 0:   # kept for the bitwise check against kore's arithmetic
+        if idx == 0:
             hip.synchronize()
             first_raw = np.zeros(qmv_weight_bytes(t, r, c), np.uint8)
             hip.check(hip.lib().hipMemcpy(first_raw.ctypes.data, raw.ptr, first_raw.size, hip.D2H), "download")
         tensors.append(qmv.QMat(t, r, c, device_ptr=raw.ptr))
     raw.free()
+    return mats, tensors, first_raw
+
+
+def _act(rng, n):
+    x = rng.standard_normal(n).astype(np.float32)
+    x[rng.random(n) < 0.01] *= 20.0
+    return x
+
+
+def _kqb_runner(B, ops, tensors):
+    from kore_amd import qmv
+    arr = (_KqbOp * len(ops))(*ops)
+    handles = (C.c_void_p * len(tensors))(*[m.handle.value for m in tensors])
+    wall = C.c_double(0)
+
+    def run(n, op_ms=None, reg=None):
+        rc = B.kqb_run(arr, len(ops), handles, 1, n, None, op_ms, reg, C.byref(wall))
+        if rc != 0:
+            raise RuntimeError(f"kqb_run failed ({rc}): {qmv.lib().kore_qmv_last_error(None).decode()}")
+        return wall.value
+    return run
+
+
+def gpu_matvec(qt, tokens: int, warmup: int):
+    """One 7B token's quant() + mv() sequence (kore.cpp:1418-1477) over 28
+    distinct layers plus the output head, replayed `tokens` times from C++."""
+    from kore_amd import hip
+    B = _qmv_bench_lib()
+    mats, tensors, first_raw = qt
     rng = np.random.default_rng(QMV_SEED)
-
-    def act(n):
-        x = rng.standard_normal(n).astype(np.float32)
-        x[rng.random(n) < 0.01] *= 20.0
-        return x
-
-    xs = [act(E) for _ in range(4)] + [act(QMV_FF)]
+    xs = [_act(rng, E) for _ in range(4)] + [_act(rng, QMV_FF)]
     dx = [hip.DeviceBuffer.from_array(x) for x in xs]
-    dqE, dqF = hip.DeviceBuffer(E // 256 * 73), hip.DeviceBuffer(QMV_FF // 256 * 73)
     outs = [hip.DeviceBuffer(r) for _, _, r, _ in mats]
     # kore's forward(): quant(xb) -> q, k, v; quant(att) -> o; quant(xb) -> gate, up;
     # quant(gate) -> down; quant(xb) -> output (kore.cpp:1418-1477).  Matrices that
@@ -390,76 +420,109 @@ def gpu_matvec(tokens: int, warmup: int):
             op_mats.append(ts)
     ops.append(_op(2, (7 * NL,), dx[3].ptr, outs=[outs[7 * NL].ptr]))
     op_mats.append((7 * NL,))
-    arr = (_KqbOp * len(ops))(*ops)
-    handles = (C.c_void_p * len(tensors))(*[m.handle.value for m in tensors])
-    wall, region = C.c_double(0), C.c_float(0)
-
-    def run(n, op_ms=None, reg=None):
-        rc = B.kqb_run(arr, len(ops), handles, 1, n, None, op_ms, reg, C.byref(wall))
-        if rc != 0:
-            raise RuntimeError(f"kqb_run failed ({rc}): {qmv.lib().kore_qmv_last_error(None).decode()}")
-
+    run = _kqb_runner(B, ops, tensors)
+    region = C.c_float(0)
     if warmup:
         run(warmup)
     print(f"[bench] matvec: {tokens} timed tokens x {len(ops)} launches", file=sys.stderr, flush=True)
-    run(tokens, reg=C.byref(region))
-    wall_ms, region_ms = wall.value, region.value
+    wall_ms = run(tokens, reg=C.byref(region))
+    region_ms = region.value
     # per-launch durations (a second pass with an event pair around every launch)
     n_ev = min(tokens, 4)
     op_ms = np.zeros(n_ev * len(ops), np.float32)
     run(n_ev, op_ms=op_ms.ctypes.data)
-    # bitwise check of the first matrix against kore's arithmetic (the oracle)
-    got = outs[0].download()
-    for m in tensors:
-        m.close()
-    for b in dx + [dqE, dqF] + outs:
+    got = outs[0].download()      # for the bitwise check of the first matrix against kore's arithmetic
+    for b in dx + outs:
         b.free()
     return dict(mats=mats, op_mats=op_mats, wall_ms=wall_ms, region_ms=region_ms,
                 op_ms=op_ms.reshape(n_ev, len(ops)), first_raw=first_raw, first_x=xs[0], first_out=got)
 
 
-def matvec_report(g, tokens: int):
+GEMM_B = 64      # kore's prefill chunk, KORE_BMAX (kore.cpp:690)
+
+
+def gpu_gemm(qt, chunks: int, warmup: int):
+    """forward_batch()'s seven matmul_batch_float calls per layer
+    (kore.cpp:1524-1526, 1566, 1575-1576, 1585) for one 64-token chunk over
+    the 28 distinct 7B layers, replayed `chunks` times from C++."""
+    from kore_amd import hip
+    B = _qmv_bench_lib()
+    mats, tensors, first_raw = qt
+    rng = np.random.default_rng(QMV_SEED + 1)
+    xb = np.stack([_act(rng, E) for _ in range(GEMM_B)])
+    att = np.stack([_act(rng, E) for _ in range(GEMM_B)])
+    gate = np.stack([_act(rng, QMV_FF) for _ in range(GEMM_B)])
+    dxb, datt, dgate = (hip.DeviceBuffer.from_array(a) for a in (xb, att, gate))
+    # kore's per-role output buffers, reused by every layer (bq, bk, bv, bo, bgate, bup, bo)
+    douts = [hip.DeviceBuffer(GEMM_B * r) for r in (E, KVD, KVD, E, QMV_FF, QMV_FF, E)]
+    # q+k+v and gate+up share their input: one grouped launch each
+    # (kore_qmv_matmul_batch_group_dev); attn_output and ffn_down alone
+    ops, op_mats = [], []
+    for l in range(NL):
+        b = 7 * l
+        for js, x in (((0, 1, 2), dxb), ((3,), datt), ((4, 5), dxb), ((6,), dgate)):
+            ts = tuple(b + j for j in js)
+            ops.append(_op(4, ts, x.ptr, n=GEMM_B, outs=[douts[j].ptr for j in js]))
+            op_mats.append(ts)
+    run = _kqb_runner(B, ops, tensors)
+    region = C.c_float(0)
+    if warmup:
+        run(warmup)
+    print(f"[bench] gemm: {chunks} timed {GEMM_B}-token chunks x {len(ops)} launches", file=sys.stderr, flush=True)
+    wall_ms = run(chunks, reg=C.byref(region))
+    region_ms = region.value
+    n_ev = min(chunks, 3)
+    op_ms = np.zeros(n_ev * len(ops), np.float32)
+    run(n_ev, op_ms=op_ms.ctypes.data)
+    # the last layer's attn_q output is overwritten by later layers: run layer 0's alone for the check
+    one = _kqb_runner(B, ops[:1], tensors)
+    one(1)
+    got = douts[0].download().reshape(GEMM_B, E)
+    for b in [dxb, datt, dgate] + douts:
+        b.free()
+    return dict(mats=mats, op_mats=op_mats, wall_ms=wall_ms, region_ms=region_ms,
+                op_ms=op_ms.reshape(n_ev, len(ops)), first_raw=first_raw, first_x=xb, first_out=got)
+
+
+def gemm_report(g, chunks: int):
     mats, op_mats = g["mats"], g["op_mats"]
-    wbytes = sum(qmv_weight_bytes(t, r, c) for _, t, r, c in mats)
-    tok_s = g["region_ms"] / 1e3 / tokens
+    flops = sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] for ts in op_mats for ti in ts)
+    chunk_s = g["region_ms"] / 1e3 / chunks
     per = {}
     for i, ts in enumerate(op_mats):
-        parts = []
-        alg = 0
-        for ti in ts:
-            name, t, r, c = mats[ti]
-            parts.append(name.split(".")[-1] + ("" if name == "output" else ("_q6k" if t == QMV_Q6K else "_q4k")))
-            alg += qmv_weight_bytes(t, r, c) + r * 4
-        alg += mats[ts[0]][3] * 4          # the fp32 input, read once
-        key = "+".join(parts)
-        d = per.setdefault(key, {"launches_per_token": 0, "ms": [], "bytes": alg})
-        d["launches_per_token"] += 1
+        key = "+".join(mats[ti][0].split(".")[-1] + ("_q6k" if mats[ti][1] == QMV_Q6K else "_q4k") for ti in ts)
+        d = per.setdefault(key, {"launches_per_chunk": 0, "ms": [],
+                                 "flop": sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] for ti in ts),
+                                 "weight_bytes": sum(qmv_weight_bytes(*mats[ti][1:]) for ti in ts)})
+        d["launches_per_chunk"] += 1
         d["ms"].extend(g["op_ms"][:, i].tolist())
     table = {}
     for key, d in per.items():
         us = float(np.mean(d["ms"])) * 1e3
-        gbs = d["bytes"] / (us / 1e6) / 1e9
-        table[key] = {"launches_per_token": d["launches_per_token"], "us_mean": round(us, 2),
-                      "algorithmic_bytes": d["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                      "us_per_token": round(us * d["launches_per_token"], 1)}
-    dom = max(table, key=lambda k: table[k]["us_per_token"])
+        tf = d["flop"] / (us / 1e6) / 1e12
+        table[key] = {"launches_per_chunk": d["launches_per_chunk"], "us_mean": round(us, 2), "flop": d["flop"],
+                      "tflops": round(tf, 2), "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                      "weight_gbs": round(d["weight_bytes"] / (us / 1e6) / 1e9, 1),
+                      "us_per_chunk": round(us * d["launches_per_chunk"], 1)}
+    dom = max(table, key=lambda k: table[k]["us_per_chunk"])
     return {
-        "workload": "Qwen2.5-7B-shape token, matvec half: 28 layers x (attn_q, attn_k, attn_v, attn_output, "
-                    "ffn_gate, ffn_up, ffn_down) + output head = 197 matrices, Q4_K with attn_v/ffn_down in Q6_K on "
-                    "14 layers (Q4_K_M's use_more_bits rule) and a Q6_K output head; each preceded by kore's Q8_K "
-                    "quantisation of its input; synthetic weights (hashed bytes, finite f16 scales), activations "
-                    "N(0,1) with 1% x20; kore's AVX2 summation order; per layer 4 calls: q+k+v and gate+up "
-                    "as one grouped launch each",
-        "weight_bytes_per_token": wbytes,
-        "launches_per_token": len(op_mats),
-        "ms_per_token_gpu": round(tok_s * 1e3, 4),
-        "ms_per_token_wall": round(g["wall_ms"] / tokens, 4),
-        "weight_gbs": round(wbytes / tok_s / 1e9, 1),
-        "weight_frac_of_hbm_peak": round(wbytes / tok_s / 1e9 / HBM_PEAK_GBS, 4),
-        "tokens": tokens,
+        "workload": "Qwen2.5-7B-shape prefill chunk, matmul half: 28 layers x forward_batch's seven "
+                    "matmul_batch_float calls (attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down) "
+                    f"on {GEMM_B} activations at once, q+k+v and gate+up as one grouped launch each (112 launches), "
+                    "the same synthetic Q4_K / Q6_K matrices as the matvec leg, activations N(0,1) with 1% x20, "
+                    "fp32 out",
+        "flop_per_chunk": flops,
+        "tokens_per_chunk": GEMM_B,
+        "launches_per_chunk": len(op_mats),
+        "ms_per_chunk_gpu": round(chunk_s * 1e3, 4),
+        "ms_per_chunk_wall": round(g["wall_ms"] / chunks, 4),
+        "tflops": round(flops / chunk_s / 1e12, 2),
+        "prefill_tokens_per_s_matmuls": round(GEMM_B / chunk_s, 1),
+        "chunks": chunks,
         "per_matrix": table,
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["gbs"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": table[dom]["frac"], "traffic": TRAFFIC_MATVEC_BYTES.get(dom)},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": table[dom]["tflops"],
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": table[dom]["frac"],
+                     "traffic": TRAFFIC_GEMM_BYTES.get(dom)},
     }
 
 
@@ -504,6 +567,48 @@ def cpu_matvec(seconds: float, threads: int):
     return {"value": round(w.size * n / el / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"the oracle's restatement of kore's AVX2 Q4_K dot product, one thread, 7B ffn_gate "
                       f"shape, {n} matvecs in {el:.1f} s; host {_cpu_model()}"}
+
+
+def cpu_gemm(seconds: float, threads: int):
+    """kore's own matmul_batch_float (oracle/_ref/kore_qmv_ref --time-batch,
+    built from kore.cpp) on the 7B ffn_gate shape with 64 activations; falls
+    back to the oracle's restatement (one thread) where that build is absent."""
+    import struct
+    import subprocess
+    import tempfile
+
+    import oracle
+    rows, cols = QMV_FF, E
+    rng = np.random.default_rng(6)
+    w = rng.integers(0, 256, size=(rows, cols // 256, 144), dtype=np.uint8)
+    w[:, :, 0:2] = np.frombuffer(np.float16(3e-3).tobytes(), np.uint8)
+    w[:, :, 2:4] = np.frombuffer(np.float16(1e-3).tobytes(), np.uint8)
+    x = rng.standard_normal((GEMM_B, cols)).astype(np.float32)
+    flop = 2 * GEMM_B * rows * cols
+    if os.path.exists(oracle.REF_QMV_BIN):
+        with tempfile.TemporaryDirectory() as td:
+            job = os.path.join(td, "job.bin")
+            with open(job, "wb") as f:
+                f.write(struct.pack("<4i", QMV_Q4K, rows, cols, GEMM_B))
+                f.write(w.tobytes())
+                f.write(x.tobytes())
+            r = subprocess.run([oracle.REF_QMV_BIN, "--time-batch", str(threads), str(seconds), job],
+                               capture_output=True, text=True, check=True)
+        j = json.loads(r.stdout)
+        tf = flop * j["reps"] / j["seconds"] / 1e12
+        return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": j["threads"], "kind": "reference",
+                "sample": f"kore's own matmul_batch_float (kore.cpp:783-845, AVX2 path: {bool(j['avx2'])}) built "
+                          f"from kore.cpp with kore's flags, {j['threads']} threads, on the 7B ffn_gate shape "
+                          f"({rows} x {cols} Q4_K) with {GEMM_B} activations: {j['reps']} calls in "
+                          f"{j['seconds']:.1f} s; host {_cpu_model()}"}
+    t0, n = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        oracle.matmul_batch(QMV_Q4K, w.reshape(-1), rows, cols, x[:8], avx2=True)
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": round(2 * 8 * rows * cols * n / el / 1e12, 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"the oracle's restatement of kore's AVX2 matmul_batch_float, one thread, 7B ffn_gate "
+                      f"shape, 8 activations, {n} calls in {el:.1f} s; host {_cpu_model()}"}
 
 
 def read_calibration():
@@ -638,6 +743,10 @@ def main(argv=None):
     ap.add_argument("--matvec-only", action="store_true", help="run only the matvec leg (for profiling)")
     ap.add_argument("--matvec-tokens", type=int, default=10, help="timed 7B tokens of the matvec leg")
     ap.add_argument("--matvec-warmup", type=int, default=2)
+    ap.add_argument("--no-gemm", action="store_true", help="skip the 7B prefill-chunk batched matmul leg")
+    ap.add_argument("--gemm-only", action="store_true", help="run only the batched matmul leg (for profiling)")
+    ap.add_argument("--gemm-chunks", type=int, default=5, help="timed 64-token chunks of the batched matmul leg")
+    ap.add_argument("--gemm-warmup", type=int, default=1)
     ap.add_argument("--cpu-threads", type=int, default=16,
                     help="threads of kore's own matvec in the CPU baseline (the GPU box's CPU share)")
     ap.add_argument("--cpu-prefill-layers", type=int, default=2)
@@ -673,16 +782,28 @@ def main(argv=None):
     clk = C.c_int(0)
     hip.lib().hipDeviceGetAttribute(C.byref(clk), 5, 0)   # hipDeviceAttributeClockRate (kHz)
 
-    if args.matvec_only:
-        g = gpu_matvec(args.matvec_tokens, args.matvec_warmup)
-        print(json.dumps({"matvec": matvec_report(g, args.matvec_tokens)}), flush=True)
+    if args.matvec_only or args.gemm_only:
+        qt = qmv_tensors()
+        if args.matvec_only:
+            out = {"matvec": matvec_report(gpu_matvec(qt, args.matvec_tokens, args.matvec_warmup),
+                                           args.matvec_tokens)}
+        else:
+            out = {"gemm": gemm_report(gpu_gemm(qt, args.gemm_chunks, args.gemm_warmup), args.gemm_chunks)}
+        for m in qt[1]:
+            m.close()
+        print(json.dumps(out), flush=True)
         return 0
     pf = None
     if not args.no_prefill:
         pf = gpu_prefill(args.prefill_steps, args.prefill_warmup)
     dec = gpu_decode(args.steps, args.warmup)
     other = None if args.no_other else gpu_other_workloads(quick=args.steps < 64)
-    mv = None if args.no_matvec else gpu_matvec(args.matvec_tokens, args.matvec_warmup)
+    qt = None if (args.no_matvec and args.no_gemm) else qmv_tensors()
+    mv = None if args.no_matvec else gpu_matvec(qt, args.matvec_tokens, args.matvec_warmup)
+    gm = None if args.no_gemm else gpu_gemm(qt, args.gemm_chunks, args.gemm_warmup)
+    if qt is not None:
+        for m in qt[1]:
+            m.close()
 
     K, W = args.steps, args.warmup
     total_bytes = sum(decode_bytes(DEC_POS0 + s + 1) for s in range(K)) * NL
@@ -752,6 +873,8 @@ def main(argv=None):
         res["other_workloads"] = other
     if mv is not None:
         res["matvec"] = matvec_report(mv, args.matvec_tokens)
+    if gm is not None:
+        res["gemm"] = gemm_report(gm, args.gemm_chunks)
     if not args.no_cpu:
         print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
               flush=True)
@@ -776,6 +899,17 @@ def main(argv=None):
             ref = oracle.qmatvec(t, mv["first_raw"], r, c, oracle.quantize_q8K(mv["first_x"]), avx2=True)
             res["parity"]["matvec_first_matrix_bitwise"] = bool(
                 np.array_equal(ref.view(np.uint32), mv["first_out"].view(np.uint32)))
+        if gm is not None:
+            import oracle
+            print(f"[bench] cpu baseline: kore's batched matmul, {args.cpu_threads} threads", file=sys.stderr,
+                  flush=True)
+            res["gemm"]["cpu_baseline"] = cpu_gemm(args.cpu_seconds, args.cpu_threads)
+            t, r, c = gm["mats"][0][1:]
+            ref = oracle.matmul_batch(t, gm["first_raw"], r, c, gm["first_x"], avx2=True)
+            err = float(np.max(np.abs(ref.astype(np.float64) - gm["first_out"])))
+            bound = 1e-4 * float(np.max(np.abs(ref))) + 1e-6
+            res["parity"]["gemm_first_matrix_max_abs_err"] = err
+            res["parity"]["gemm_first_matrix_within_kore_tolerance"] = bool(err <= bound)
         if pf is not None:
             print(f"[bench] cpu baseline: prefill sample ({args.cpu_prefill_layers} layers)", file=sys.stderr,
                   flush=True)

@@ -114,12 +114,21 @@ KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *tensors, 
  * output in one FMA chain over the columns).  Host buffers, synchronous. */
 KORE_QMV_API int kore_qmv_matmul_batch(kore_qmv_tensor_t t, const float *x, int nb, float *out);
 
-/* Same with device buffers (x 16-byte aligned).  Row-poor matrices split
- * their columns over several workgroups and add the partial sums in a second
- * launch, through a workspace of the device that tensor creation sizes: calls
- * that overlap on different streams of one device race on it. */
+/* Same with device buffers (x 16-byte aligned; enqueued on `stream`, no
+ * allocation).  Tiles of rows whose columns are split between workgroups pass
+ * partial sums through a per-device workspace that tensor creation sizes:
+ * calls that overlap on different streams of one device race on it. */
 KORE_QMV_API int kore_qmv_matmul_batch_dev(kore_qmv_tensor_t t, const float *x, int nb, float *out,
                                            void *stream);
+
+/* n (1..4) matrices of one device and equal cols multiplied with the same x
+ * in one launch: out[k] = matmul_batch(t[k], x), as forward_batch() calls
+ * matmul_batch_float for wq, wk, wv and for w_gate, w_up on the same input
+ * (kore.cpp:1524-1526, 1575-1576).  Results equal n calls of
+ * kore_qmv_matmul_batch_dev to fp32 rounding (the split of the sums between
+ * workgroups depends on the launch).  Same workspace caveat. */
+KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
+                                                 float *const *out, void *stream);
 
 /* Text of the last failure on this tensor (or, with NULL, of the last failed
  * call without a tensor on this thread).  Never NULL. */

@@ -1,21 +1,35 @@
-// kore_gemm_kernels.hip - gfx950 kernels of kore's batched prefill matmul
+// kore_gemm_kernels.hip - gfx950 kernel of kore's batched prefill matmul
 // (matmul_batch_float, kore.cpp:783-845): out[b][r] = row r of the
-// dequantised Q4_K / Q6_K weights . x[b] for B <= 64 activations at once.
+// dequantised Q4_K / Q6_K weights . x[b] for B <= 64 activations at once, for
+// up to four matrices that share x in one launch.
 //
 // fp32 MFMA (v_mfma_f32_16x16x4f32) on weights dequantised in registers: a
-// wave owns 16 rows and up to 64 activations (NB blocks of 16); lane l
-// supplies row l % 16 and, of every 256-column block, the 64 columns of group
-// l / 16 (the order of the K sum inside a block is permuted so that each lane
-// dequantises contiguous bytes; the sum is the same up to fp32 rounding).  The
-// activations of a block are staged in LDS, each of them a 260-float row so
-// the 16-byte reads of 16 consecutive activations hit different banks.  Row-
-// poor matrices split their blocks over several workgroups (split-K) and a
-// second kernel adds the partial sums in split order.  kore sums each output
-// in one fused multiply-add chain over the columns; this sums in MFMA blocks,
-// so results agree with kore's to fp32 rounding (kore's own tolerance,
-// max|d| <= 1e-4 max|ref| + 1e-6, kore_kernels.cpp:742), not bit for bit.
+// wave owns 16 rows of a 64-row tile and up to 64 activations (NB blocks of
+// 16); lane l supplies row l % 16 and, of every 256-column block, the 64
+// columns of group l / 16 (the order of the K sum inside a block is permuted
+// so that each lane dequantises contiguous bytes; the sum is the same up to
+// fp32 rounding).  The activations of a block are staged in LDS, each of them
+// a 260-float row so the 16-byte reads of 16 consecutive activations hit
+// different banks.  The next block's activations and weights are loaded into
+// registers while the current block's MFMAs run.
+//
+// Work split: stream-K.  The iteration space (tile, block) of all matrices is
+// cut into `workers` contiguous runs of equal length, one per workgroup, so
+// every CU gets the same number of block iterations whatever the shapes.  A
+// tile split between workers leaves one partial sum per worker in a slot of
+// the workspace (slot 2p for worker p's first tile, 2p + 1 for its last), and
+// a second launch adds each split tile's slots in worker order.  (Finishing
+// split tiles inside the first launch would need device-scope fences, which
+// write back and invalidate the XCD's L2 each time and cost far more than the
+// second launch.)
+//
+// kore sums each output in one fused multiply-add chain over the columns; this
+// sums in MFMA blocks, so results agree with kore's to fp32 rounding (kore's
+// own tolerance, max|d| <= 1e-4 max|ref| + 1e-6, kore_kernels.cpp:742), not
+// bit for bit.  For one device, shape and B the result is deterministic.
 #include "kore_qmv_kernels.h"
 
+#include <algorithm>
 #include <mutex>
 
 namespace kore_qmv_gpu {
@@ -24,7 +38,6 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerWg = 64;          // 16 per wave
 constexpr int kXStride = 260;           // floats per staged activation row
 
 __device__ __forceinline__ float f16f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
@@ -44,202 +57,331 @@ __device__ __forceinline__ int q4m(const uint4 &h, int j) {   // 6-bit min of su
     return j < 4 ? (int)((h.z >> s) & 63) : (int)(((h.w >> (s + 4)) & 0x0F) | (((h.z >> (s + 6)) & 3) << 4));
 }
 
-// One lane's weights of one block: Q4_K group kk (32 nibble bytes + header);
-// Q6_K values 64 kk .. 64 kk + 63 (64 ql bytes of half kk / 2, 32 qh bytes,
-// the four scales of the lane, d).
-struct Q4G { uint4 hdr, qa, qb; };
-struct Q6G { uint4 l0, l1, l2, l3, h0, h1; uint32_t sc, d; };
+// One lane's weights of one block.  Q4_K (group kk: 32 nibble bytes + header):
+// v[0] header, v[1..2] bytes 16 + 32 kk ...; Q6_K (values 64 kk .. 64 kk + 63):
+// v[0..3] the 64 ql bytes of half kk / 2, v[4..5] its 32 qh bytes, sc the four
+// scales of the lane, d the f16 scale.
+template <bool Q6>
+struct WRaw {
+    uint4 v[Q6 ? 6 : 3];
+    uint32_t sc, d;
+};
 
-__device__ __forceinline__ Q4G load4(const uint8_t *b, int kk) {
-    Q4G g;
-    g.hdr = *(const uint4 *)b;
-    g.qa = *(const uint4 *)(b + 16 + 32 * kk);
-    g.qb = *(const uint4 *)(b + 32 + 32 * kk);
-    return g;
-}
-
-__device__ __forceinline__ Q6G load6(const uint8_t *b, const uint16_t *dp, int kk) {
-    const int h = kk >> 1;
-    Q6G g;
-    g.l0 = *(const uint4 *)(b + 64 * h);
-    g.l1 = *(const uint4 *)(b + 64 * h + 16);
-    g.l2 = *(const uint4 *)(b + 64 * h + 32);
-    g.l3 = *(const uint4 *)(b + 64 * h + 48);
-    g.h0 = *(const uint4 *)(b + 128 + 32 * h);
-    g.h1 = *(const uint4 *)(b + 128 + 32 * h + 16);
-    g.sc = *(const uint32_t *)(b + 192 + 4 * kk);   // sc[8h + 4(kk&1) + 0..3]
-    g.d = *dp;
-    return g;
-}
-
-template <int TYPE>
-using Group = std::conditional_t<TYPE == kQ4K, Q4G, Q6G>;
-
-template <int TYPE, int NB>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
-    extern __shared__ __align__(16) float xs[];      // [16 NB][kXStride]
-    constexpr int BB = TYPE == kQ4K ? kQ4Bytes : kQ6Body;
-    const int t = threadIdx.x, wave = t >> 6, l = t & 63;
-    const int i = l & 15, kk = l >> 4;
-    const int tile = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
-    const int kb0 = (int)((int64_t)a.nblk * split / a.splits);
-    const int kb1 = (int)((int64_t)a.nblk * (split + 1) / a.splits);
-    const int row = min(tile * kRowsPerWg + 16 * wave + i, a.rows - 1);
-    const int64_t cols = (int64_t)a.nblk * 256;
-    const uint8_t *wrow = a.w + (int64_t)row * a.nblk * BB;
-    const uint16_t *drow = TYPE == kQ6K ? a.wd + (int64_t)row * a.nblk : nullptr;
-
-    auto load = [&](int blk) -> Group<TYPE> {
-        if constexpr (TYPE == kQ4K) return load4(wrow + (int64_t)blk * BB, kk);
-        else return load6(wrow + (int64_t)blk * BB, drow + blk, kk);
-    };
-
-    floatx4 acc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    Group<TYPE> cur = load(min(kb0, a.nblk - 1));
-    for (int blk = kb0; blk < kb1; ++blk) {
-        __syncthreads();                                 // the previous block's reads of xs are done
-        for (int c = t; c < 16 * NB * 64; c += kThreads) {
-            const int b = c >> 6, q = c & 63;
-            if (b < a.B)
-                *(float4 *)&xs[b * kXStride + 4 * q] = *(const float4 *)(a.x + b * cols + 256 * (int64_t)blk + 4 * q);
-        }
-        const Group<TYPE> g = cur;
-        cur = load(min(blk + 1, kb1 - 1));               // the next block's weights, while this one runs
-        __syncthreads();
-
-        if constexpr (TYPE == kQ4K) {
-            // kore's dequant_block_q4_K (kore.cpp:337-353): d1 = d*sc, m1 = dmin*min, value = d1*q - m1
-            const float d = f16f(g.hdr.x & 0xFFFFu), dmin = f16f(g.hdr.x >> 16);
-            const float d1 = d * (float)q4s(g.hdr, 2 * kk), m1 = dmin * (float)q4m(g.hdr, 2 * kk);
-            const float d2 = d * (float)q4s(g.hdr, 2 * kk + 1), m2 = dmin * (float)q4m(g.hdr, 2 * kk + 1);
-#pragma unroll
-            for (int t4 = 0; t4 < 16; ++t4) {
-                float4 bx[NB];
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) bx[nb] = *(const float4 *)&xs[(16 * nb + i) * kXStride + 64 * kk + 4 * t4];
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) {
-                    const int tk = 4 * t4 + tt;              // column 64 kk + tk of the block
-                    const int byte = tk & 31;
-                    const uint32_t w = word(g.qa, g.qb, byte >> 2);
-                    const uint32_t q = (w >> (8 * (byte & 3) + (tk >= 32 ? 4 : 0))) & 15u;
-                    const float av = tk < 32 ? d1 * (float)q - m1 : d2 * (float)q - m2;
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
-                        const float bv = tt == 0 ? bx[nb].x : tt == 1 ? bx[nb].y : tt == 2 ? bx[nb].z : bx[nb].w;
-                        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[nb], 0, 0, 0);
-                    }
-                }
-            }
-        } else {
-            // kore's dequant_block_q6_K (kore.cpp:359-381): value = (d * sc) * (q6 - 32);
-            // lane kk: h = kk / 2, groups k = 2 (kk % 2) + tk / 32, low or high nibble by kk % 2
-            const float d = f16f(g.d);
-            const int kh = kk & 1;
-            float ds[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ds[e] = d * (float)(int)(int8_t)((g.sc >> (8 * e)) & 0xFF);
-#pragma unroll
-            for (int t4 = 0; t4 < 16; ++t4) {
-                float4 bx[NB];
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) bx[nb] = *(const float4 *)&xs[(16 * nb + i) * kXStride + 64 * kk + 4 * t4];
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) {
-                    const int tk = 4 * t4 + tt, l32 = tk & 31, kt = tk >> 5;
-                    const uint4 &lv = tk < 16 ? g.l0 : tk < 32 ? g.l1 : tk < 48 ? g.l2 : g.l3;
-                    const int m = (tk >> 2) & 3;
-                    const uint32_t lw = m == 0 ? lv.x : m == 1 ? lv.y : m == 2 ? lv.z : lv.w;
-                    const uint32_t hw = word(g.h0, g.h1, l32 >> 2);
-                    const uint32_t nib = (lw >> (8 * (tk & 3) + 4 * kh)) & 15u;
-                    const uint32_t hb = (hw >> (8 * (l32 & 3) + 4 * kh + 2 * kt)) & 3u;
-                    const float av = ds[2 * kt + (l32 >> 4)] * (float)((int)(nib | (hb << 4)) - 32);
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
-                        const float bv = tt == 0 ? bx[nb].x : tt == 1 ? bx[nb].y : tt == 2 ? bx[nb].z : bx[nb].w;
-                        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[nb], 0, 0, 0);
-                    }
-                }
-            }
-        }
+template <bool Q6>
+__device__ __forceinline__ void load_w(WRaw<Q6> &g, const GemmMat &m, int row, int blk, int nblk, int kk) {
+    if (!Q6 || m.type == kQ4K) {
+        const uint8_t *b = m.w + ((int64_t)row * nblk + blk) * kQ4Bytes;
+        g.v[0] = *(const uint4 *)b;
+        g.v[1] = *(const uint4 *)(b + 16 + 32 * kk);
+        g.v[2] = *(const uint4 *)(b + 32 + 32 * kk);
+    } else if constexpr (Q6) {
+        const uint8_t *b = m.w + ((int64_t)row * nblk + blk) * kQ6Body;
+        const int h = kk >> 1;
+        g.v[0] = *(const uint4 *)(b + 64 * h);
+        g.v[1] = *(const uint4 *)(b + 64 * h + 16);
+        g.v[2] = *(const uint4 *)(b + 64 * h + 32);
+        g.v[3] = *(const uint4 *)(b + 64 * h + 48);
+        g.v[4] = *(const uint4 *)(b + 128 + 32 * h);
+        g.v[5] = *(const uint4 *)(b + 128 + 32 * h + 16);
+        g.sc = *(const uint32_t *)(b + 192 + 4 * kk);   // sc[8h + 4(kk&1) + 0..3]
+        g.d = m.wd[(int64_t)row * nblk + blk];
     }
+}
 
-    // D block: lane l holds rows 4 (l / 16) + v, activation l % 16 of each 16-block
-    float *out = a.out + (int64_t)split * a.B * a.rows;
-    const int r0 = tile * kRowsPerWg + 16 * wave + 4 * kk;
+// One block: acc[nb] += W(16 rows x 256) . X(256 x 16 activations of block nb).
+// Step t4 covers columns 64 kk + 4 t4 .. + 3 of the lane: its activations are
+// read from LDS one step ahead (bx double buffer) and its four weights
+// dequantised before its 4 NB MFMAs, so neither LDS latency nor the
+// dequantisation chain sits in front of an MFMA.
+template <int NB>
+__device__ __forceinline__ void read_bx(floatx4 *bx, const float *xs, int i, int kk, int t4) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bx[nb] = *(const floatx4 *)&xs[(16 * nb + i) * kXStride + 64 * kk + 4 * t4];
+}
+
+template <int NB>
+__device__ __forceinline__ void mfma_step(const float *av, const floatx4 *bx, floatx4 *acc) {
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[tt], bx[nb][tt], acc[nb], 0, 0, 0);
+}
+
+template <int NB, bool Q6>
+__device__ __forceinline__ void block_q4(const WRaw<Q6> &g, const float *xs, int i, int kk, floatx4 *acc) {
+    // kore's dequant_block_q4_K (kore.cpp:337-353): d1 = d*sc, m1 = dmin*min, value = d1*q - m1
+    const uint4 &hdr = g.v[0];
+    const float d = f16f(hdr.x & 0xFFFFu), dmin = f16f(hdr.x >> 16);
+    const float d1 = d * (float)q4s(hdr, 2 * kk), m1 = dmin * (float)q4m(hdr, 2 * kk);
+    const float d2 = d * (float)q4s(hdr, 2 * kk + 1), m2 = dmin * (float)q4m(hdr, 2 * kk + 1);
+    floatx4 bx[2][NB];
+    read_bx<NB>(bx[0], xs, i, kk, 0);
+#pragma unroll
+    for (int t4 = 0; t4 < 16; ++t4) {
+        // the next step's reads go out first, a whole step before their use
+        __builtin_amdgcn_sched_barrier(0);
+        if (t4 + 1 < 16) read_bx<NB>(bx[(t4 + 1) & 1], xs, i, kk, t4 + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        float av[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const int tk = 4 * t4 + tt;              // column 64 kk + tk of the block
+            const int byte = tk & 31;
+            const uint32_t w = word(g.v[1], g.v[2], byte >> 2);
+            const uint32_t q = (w >> (8 * (byte & 3) + (tk >= 32 ? 4 : 0))) & 15u;
+            av[tt] = tk < 32 ? d1 * (float)q - m1 : d2 * (float)q - m2;
+        }
+        mfma_step<NB>(av, bx[t4 & 1], acc);
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ void block_q6(const WRaw<true> &g, const float *xs, int i, int kk, floatx4 *acc) {
+    // kore's dequant_block_q6_K (kore.cpp:359-381): value = (d * sc) * (q6 - 32);
+    // lane kk: h = kk / 2, groups k = 2 (kk % 2) + tk / 32, low or high nibble by kk % 2
+    const float d = f16f(g.d);
+    const int kh = kk & 1;
+    float ds[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ds[e] = d * (float)(int)(int8_t)((g.sc >> (8 * e)) & 0xFF);
+    floatx4 bx[2][NB];
+    read_bx<NB>(bx[0], xs, i, kk, 0);
+#pragma unroll
+    for (int t4 = 0; t4 < 16; ++t4) {
+        // the next step's reads go out first, a whole step before their use
+        __builtin_amdgcn_sched_barrier(0);
+        if (t4 + 1 < 16) read_bx<NB>(bx[(t4 + 1) & 1], xs, i, kk, t4 + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        float av[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const int tk = 4 * t4 + tt, l32 = tk & 31, kt = tk >> 5;
+            const uint4 &lv = g.v[tk >> 4];
+            const int m = (tk >> 2) & 3;
+            const uint32_t lw = m == 0 ? lv.x : m == 1 ? lv.y : m == 2 ? lv.z : lv.w;
+            const uint32_t hw = word(g.v[4], g.v[5], l32 >> 2);
+            const uint32_t nib = (lw >> (8 * (tk & 3) + 4 * kh)) & 15u;
+            const uint32_t hb = (hw >> (8 * (l32 & 3) + 4 * kh + 2 * kt)) & 3u;
+            av[tt] = ds[2 * kt + (l32 >> 4)] * (float)((int)(nib | (hb << 4)) - 32);
+        }
+        mfma_step<NB>(av, bx[t4 & 1], acc);
+    }
+}
+
+__device__ __forceinline__ int mat_of_tile(const GemmArgs &a, int tile) {
+    int m = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxGroup; ++k)
+        if (k < a.n_mat && tile >= a.m[k].tile0) m = k;
+    return m;
+}
+
+// First iteration of worker p's run, and the worker whose run holds iteration
+// `it` (the largest p with run_first(p) <= it; runs are never empty because
+// the host keeps workers <= iterations).
+__device__ __forceinline__ int64_t run_first(int64_t T, int P, int p) { return T * p / P; }
+__device__ __forceinline__ int run_of(int64_t T, int P, int64_t it) { return (int)(((it + 1) * P - 1) / T); }
+
+// D block of an MFMA: lane l holds rows 4 (l / 16) + v, activation l % 16 of
+// each 16-block; rows past the matrix and activations past B are dropped.
+template <int NB>
+__device__ __forceinline__ void store_tile(const GemmArgs &a, const GemmMat &mt, int tile, int wave, int i, int kk,
+                                           const floatx4 *acc) {
+    const int r0 = (tile - mt.tile0) * kGemmRowsPerTile + 16 * wave + 4 * kk;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         const int b = 16 * nb + i;
         if (b >= a.B) continue;
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-            if (r0 + v < a.rows) out[(int64_t)b * a.rows + r0 + v] = acc[nb][v];
+            if (r0 + v < mt.rows) mt.out[(int64_t)b * mt.rows + r0 + v] = acc[nb][v];
     }
 }
 
-// out[e] = sum over s of part[s][e], s in order.
-__global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(const float *__restrict__ part, int splits,
-                                                               int64_t n, float *__restrict__ out) {
-    const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (e >= n) return;
-    float s = part[e];
-    for (int k = 1; k < splits; ++k) s += part[(int64_t)k * n + e];
-    out[e] = s;
+// Fix-up launch: workgroup t finishes tile t if the main launch split it, adding
+// the partial sums of its workers in worker order.
+template <int NB>
+__global__ __launch_bounds__(kThreads) void gemm_fixup_kernel(GemmArgs a) {
+    const int tile = blockIdx.x, nblk = a.nblk, P = a.workers;
+    const int64_t T = (int64_t)a.tiles * nblk, tfirst = (int64_t)tile * nblk;
+    const int pf = run_of(T, P, tfirst), pl = run_of(T, P, tfirst + nblk - 1);
+    if (pf == pl) return;                        // one worker ran the whole tile and stored it
+    const int t = threadIdx.x, l = t & 63, wave = t >> 6, i = l & 15, kk = l >> 4;
+    floatx4 acc[NB];
+    for (int q = pf; q <= pl; ++q) {
+        const int slot = 2 * q + (run_first(T, P, q) / nblk == tile ? 0 : 1);
+        const floatx4 *src = (const floatx4 *)a.partials + (int64_t)slot * (kGemmSlotFloats / 4);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const floatx4 v = src[(wave * 4 + nb) * 64 + l];
+            acc[nb] = q == pf ? v : acc[nb] + v;
+        }
+    }
+    store_tile<NB>(a, a.m[mat_of_tile(a, tile)], tile, wave, i, kk, acc);
 }
 
+// Q6: the launch holds a Q6_K matrix (the Q4_K-only kernel keeps smaller
+// weight records in registers).
+template <int NB, bool Q6>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
+    extern __shared__ __align__(16) float xs[];      // [16 NB][kXStride]
+    const int t = threadIdx.x, l = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);   // uniform: addresses built from it stay scalar
+    const int i = l & 15, kk = l >> 4;
+    const int nblk = a.nblk, P = a.workers;
+    const int64_t T = (int64_t)a.tiles * nblk;
+    // consecutive runs on one XCD (workgroups are dealt to the 8 XCDs in turn),
+    // so the workers that share a split tile share an L2
+    const int p = (P % 8 == 0) ? (int)(blockIdx.x % 8) * (P / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int64_t it0 = run_first(T, P, p), it1 = run_first(T, P, p + 1);
+    if (it0 >= it1) return;
+    const int64_t cols = (int64_t)nblk * 256;
+
+    // activation staging: thread t moves float4 t + 256 j of the block, i.e.
+    // quad l of activation wave + 4 j (a wave-uniform row: its base address is
+    // scalar); activations past B repeat the last one (their MFMA columns are
+    // never stored)
+    const float *xrow[4 * NB];
+#pragma unroll
+    for (int j = 0; j < 4 * NB; ++j) xrow[j] = a.x + (int64_t)min(wave + 4 * j, a.B - 1) * cols;
+    floatx4 xr[4 * NB];       // native vectors: HIP's float4 is a struct whose copies stay in memory
+    auto row_of = [&](int tile, int m) {
+        return min((tile - a.m[m].tile0) * kGemmRowsPerTile + 16 * wave + i, a.m[m].rows - 1);
+    };
+
+    int tile = (int)(it0 / nblk), blk = (int)(it0 % nblk), seg0 = blk;
+    int m = mat_of_tile(a, tile);
+    WRaw<Q6> g;
+    load_w<Q6>(g, a.m[m], row_of(tile, m), blk, nblk, kk);
+#pragma unroll
+    for (int j = 0; j < 4 * NB; ++j) xr[j] = *(const floatx4 *)(xrow[j] + 256 * blk + 4 * l);
+
+    floatx4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t it = it0; it < it1; ++it) {
+        __syncthreads();                                 // every wave is done with the previous block
+#pragma unroll
+        for (int j = 0; j < 4 * NB; ++j) *(floatx4 *)&xs[(wave + 4 * j) * kXStride + 4 * l] = xr[j];
+        __syncthreads();
+        const WRaw<Q6> gc = g;
+        const int cm = m;
+        int ntile = tile, nblk_i = blk + 1;
+        if (nblk_i == nblk) { nblk_i = 0; ++ntile; }
+        if (it + 1 < it1) {                              // the next block, while this one runs
+            m = ntile == tile ? m : mat_of_tile(a, ntile);
+            load_w<Q6>(g, a.m[m], row_of(ntile, m), nblk_i, nblk, kk);
+#pragma unroll
+            for (int j = 0; j < 4 * NB; ++j) xr[j] = *(const floatx4 *)(xrow[j] + 256 * nblk_i + 4 * l);
+        }
+        if constexpr (Q6) {
+            if (a.m[cm].type == kQ4K) block_q4<NB, Q6>(gc, xs, i, kk, acc);
+            else block_q6<NB>(gc, xs, i, kk, acc);
+        } else {
+            block_q4<NB, Q6>(gc, xs, i, kk, acc);
+        }
+
+        if (it + 1 == it1 || nblk_i == 0) {              // end of this worker's part of the tile
+            if (seg0 != 0 || blk + 1 != nblk) {          // split tile: partial sums for the fix-up launch
+                const int slot = 2 * p + (it0 / nblk == tile ? 0 : 1);
+                floatx4 *mine = (floatx4 *)a.partials + (int64_t)slot * (kGemmSlotFloats / 4);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) mine[(wave * 4 + nb) * 64 + l] = acc[nb];
+            } else {
+                store_tile<NB>(a, a.m[cm], tile, wave, i, kk, acc);
+            }
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+            seg0 = 0;
+        }
+        tile = ntile;
+        blk = nblk_i;
+    }
+}
+
+constexpr size_t lds_bytes(int nbk) { return (size_t)16 * nbk * kXStride * sizeof(float); }
+
 // Dynamic LDS above 64 KiB (64 activations: 66,560 bytes) needs the kernel's
-// limit raised once; gfx950 has 160 KiB per CU.
-template <int TYPE, int NB>
-hipError_t launch_nb(const GemmArgs &a, int grid, hipStream_t s) {
-    const size_t lds = (size_t)16 * NB * kXStride * sizeof(float);
+// limit raised once; gfx950 has 160 KiB per CU.  The same call records how many
+// workgroups of the kernel fit on a CU (LDS and registers).
+template <int NB, bool Q6>
+hipError_t prepare_nb(int *per_cu) {
     static std::once_flag once;
-    static hipError_t attr = hipSuccess;
+    static hipError_t err = hipSuccess;
+    static int occ = 1;
     std::call_once(once, [&] {
-        attr = hipFuncSetAttribute((const void *)gemm_kernel<TYPE, NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)lds);
+        err = hipFuncSetAttribute((const void *)gemm_kernel<NB, Q6>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds_bytes(NB));
+        if (err == hipSuccess)
+            err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemm_kernel<NB, Q6>, kThreads, lds_bytes(NB));
+        occ = std::max(1, std::min(4, occ));
     });
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemm_kernel<TYPE, NB>), dim3(grid), dim3(kThreads), lds, s, a);
+    *per_cu = occ;
+    return err;
+}
+
+template <bool Q6>
+hipError_t prepare_t(int B, int *per_cu) {
+    switch ((B + 15) / 16) {
+        case 1: return prepare_nb<1, Q6>(per_cu);
+        case 2: return prepare_nb<2, Q6>(per_cu);
+        case 3: return prepare_nb<3, Q6>(per_cu);
+        default: return prepare_nb<4, Q6>(per_cu);
+    }
+}
+
+template <int NB, bool Q6>
+hipError_t launch_nb(const GemmArgs &a, hipStream_t s) {
+    int occ = 0;
+    if (hipError_t e = prepare_nb<NB, Q6>(&occ)) return e;
+    hipLaunchKernelGGL((gemm_kernel<NB, Q6>), dim3(a.workers), dim3(kThreads), lds_bytes(NB), s, a);
+    if (hipError_t e = hipGetLastError()) return e;
+    // every run a whole number of tiles: nothing split
+    const int64_t T = (int64_t)a.tiles * a.nblk;
+    if (T % a.workers == 0 && (T / a.workers) % a.nblk == 0) return hipSuccess;
+    hipLaunchKernelGGL((gemm_fixup_kernel<NB>), dim3(a.tiles), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
-template <int TYPE>
-hipError_t launch_t(const GemmArgs &a, int grid, hipStream_t s) {
+template <bool Q6>
+hipError_t launch_t(const GemmArgs &a, hipStream_t s) {
     switch ((a.B + 15) / 16) {
-        case 1: return launch_nb<TYPE, 1>(a, grid, s);
-        case 2: return launch_nb<TYPE, 2>(a, grid, s);
-        case 3: return launch_nb<TYPE, 3>(a, grid, s);
-        default: return launch_nb<TYPE, 4>(a, grid, s);
+        case 1: return launch_nb<1, Q6>(a, s);
+        case 2: return launch_nb<2, Q6>(a, s);
+        case 3: return launch_nb<3, Q6>(a, s);
+        default: return launch_nb<4, Q6>(a, s);
     }
 }
 
 }  // namespace
 
-int gemm_splits(int rows, int nblk, int num_cu) {
-    const int tiles = (rows + kRowsPerWg - 1) / kRowsPerWg;
-    int s = 1;
-    // two workgroups per CU, each split at least two blocks long
-    while (tiles * s * 2 < 2 * num_cu && nblk / (2 * s) >= 2) s *= 2;
-    return s;
+int gemm_max_workers(int num_cu) { return 4 * num_cu; }
+
+int gemm_workers(int tiles, int nblk, int B, bool has_q6k, int num_cu) {
+    int occ = 1;
+    if ((has_q6k ? prepare_t<true>(B, &occ) : prepare_t<false>(B, &occ)) != hipSuccess) occ = 1;
+    const int64_t T = (int64_t)tiles * nblk;
+    int64_t p = std::min<int64_t>((int64_t)occ * num_cu, std::max<int64_t>(1, T / 2));
+    if (p >= 8) p -= p % 8;
+    return (int)p;
 }
 
-hipError_t launch_gemm(GemmArgs a, float *out, float *partials, hipStream_t s) {
-    if (a.rows <= 0 || a.nblk <= 0 || a.B <= 0 || a.B > kGemmMaxB || a.splits <= 0) return hipErrorInvalidValue;
-    if (a.type != kQ4K && a.type != kQ6K) return hipErrorInvalidValue;
-    if (a.splits > 1 && !partials) return hipErrorInvalidValue;
-    const int tiles = (a.rows + kRowsPerWg - 1) / kRowsPerWg;
-    const int64_t grid = (int64_t)tiles * a.splits;
-    if (grid > INT32_MAX) return hipErrorInvalidValue;
-    a.out = a.splits > 1 ? partials : out;
-    hipError_t e = a.type == kQ4K ? launch_t<kQ4K>(a, (int)grid, s) : launch_t<kQ6K>(a, (int)grid, s);
-    if (e != hipSuccess || a.splits == 1) return e;
-    const int64_t n = (int64_t)a.B * a.rows;
-    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
-                       (const float *)partials, a.splits, n, out);
-    return hipGetLastError();
+hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
+    if (a.n_mat < 1 || a.n_mat > kMaxGroup || a.nblk <= 0 || a.B <= 0 || a.B > kGemmMaxB) return hipErrorInvalidValue;
+    if (a.workers < 1 || !a.partials) return hipErrorInvalidValue;
+    int tiles = 0;
+    for (int k = 0; k < a.n_mat; ++k) {
+        const GemmMat &m = a.m[k];
+        if (m.rows <= 0 || !m.w || !m.out || (m.type != kQ4K && m.type != kQ6K) || (m.type == kQ6K && !m.wd))
+            return hipErrorInvalidValue;
+        a.m[k].tile0 = tiles;
+        tiles += (m.rows + kGemmRowsPerTile - 1) / kGemmRowsPerTile;
+    }
+    if (tiles != a.tiles || (int64_t)tiles * a.nblk < a.workers) return hipErrorInvalidValue;
+    bool q6 = false;
+    for (int k = 0; k < a.n_mat; ++k) q6 |= a.m[k].type == kQ6K;
+    return q6 ? launch_t<true>(a, s) : launch_t<false>(a, s);
 }
 
 }  // namespace kore_qmv_gpu

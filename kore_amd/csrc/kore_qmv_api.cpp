@@ -26,7 +26,6 @@ struct kore_qmv_tensor {
     uint8_t *w = nullptr;      // Q4_K blocks or Q6_K bodies
     uint16_t *wd = nullptr;    // Q6_K scales
     uint8_t *xq = nullptr;     // quantised activations (the matvec's layout) when quantised apart
-    int gemm_splits = 1;       // split-K of the batched matmul
     size_t weight_bytes = 0;
     std::string error;
 };
@@ -50,14 +49,23 @@ int hip_fail(kore_qmv_tensor *t, hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail((t), e_, #call);  \
     } while (0)
 
-// Per-device workspace of the batched matmul's split-K partial sums, grown when
-// a tensor that needs more is created (never inside a call).
+// Per-device workspace of the batched matmul: the partial sums of split tiles,
+// sized for the largest grid at the first tensor creation, never inside a call.
 struct GemmScratch {
     std::mutex mu;
-    void *p = nullptr;
-    size_t cap = 0;
+    float *partials = nullptr;
 };
 GemmScratch g_gemm[64];
+
+int row_tiles(int64_t rows) { return (int)((rows + kGemmRowsPerTile - 1) / kGemmRowsPerTile); }
+
+hipError_t gemm_scratch_reserve(int dev, int num_cu) {
+    GemmScratch &g = g_gemm[dev];
+    std::lock_guard<std::mutex> lock(g.mu);
+    if (g.partials) return hipSuccess;
+    const size_t bytes = (size_t)2 * gemm_max_workers(num_cu) * kGemmSlotFloats * sizeof(float);
+    return hipMalloc((void **)&g.partials, bytes);
+}
 
 // Per-device staging buffers and stream of the synchronous host-pointer calls.
 struct HostPath {
@@ -167,23 +175,9 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
     t->num_cu = num_cu;
     t->rows_per_wave = pick_rows_per_wave(rows, num_cu);
     if ((e = hipMalloc(&t->xq, (size_t)t->nblk * 308)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
-    t->gemm_splits = gemm_splits((int)rows, t->nblk, num_cu);
-    if (t->gemm_splits > 1) {
-        if (t->device < 0 || t->device >= 64) return bail(fail(t, KORE_QMV_E_UNSUPPORTED, "device ordinal above 63"));
-        GemmScratch &g = g_gemm[t->device];
-        std::lock_guard<std::mutex> lock(g.mu);
-        const size_t need = (size_t)t->gemm_splits * kGemmMaxB * (size_t)rows * sizeof(float);
-        if (g.cap < need) {
-            void *np = nullptr;
-            if ((e = hipMalloc(&np, need)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
-            if (g.p) {
-                (void)hipDeviceSynchronize();   // no call may still use the old workspace
-                (void)hipFree(g.p);
-            }
-            g.p = np;
-            g.cap = need;
-        }
-    }
+    if (t->device < 0 || t->device >= 64) return bail(fail(t, KORE_QMV_E_UNSUPPORTED, "device ordinal above 63"));
+    if ((e = gemm_scratch_reserve(t->device, num_cu)) != hipSuccess)
+        return bail(hip_fail(t, e, "matmul workspace"));
 
     const int64_t nblocks = rows * t->nblk;
     const size_t bb = type == KORE_QMV_Q4_K ? kQ4Bytes : kQ6Bytes;
@@ -356,16 +350,39 @@ KORE_QMV_API int kore_qmv_mv(kore_qmv_tensor_t t, const float *x, float *out, in
     return rc;
 }
 
+KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
+                                                 float *const *out, void *stream) {
+    if (n < 1 || n > kMaxGroup || !t || !out) return fail(nullptr, KORE_QMV_E_INVALID, "n must be 1..4, t and out set");
+    for (int k = 0; k < n; ++k)
+        if (!t[k]) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
+    kore_qmv_tensor *t0 = t[0];
+    if (nb < 1 || nb > kGemmMaxB) return fail(t0, KORE_QMV_E_INVALID, "nb must be 1..64 (kore's KORE_BMAX)");
+    if (int rc = check_dev_ptr(t0, x, 16, "x")) return rc;
+    GemmArgs a{};
+    a.n_mat = n;
+    a.x = x;
+    a.B = nb;
+    a.nblk = t0->nblk;
+    for (int k = 0; k < n; ++k) {
+        if (t[k]->device != t0->device || t[k]->cols != t0->cols)
+            return fail(t0, KORE_QMV_E_INVALID, "grouped tensors must share device and cols");
+        if (int rc = check_dev_ptr(t0, out[k], 4, "out")) return rc;
+        a.m[k] = GemmMat{t[k]->w, t[k]->wd, out[k], (int)t[k]->rows, t[k]->type, a.tiles};
+        a.tiles += row_tiles(t[k]->rows);
+    }
+    GemmScratch &g = g_gemm[t0->device & 63];
+    bool q6 = false;
+    for (int k = 0; k < n; ++k) q6 |= t[k]->type == KORE_QMV_Q6_K;
+    a.workers = gemm_workers(a.tiles, a.nblk, nb, q6, t0->num_cu);
+    a.partials = g.partials;
+    hipError_t e = launch_gemm(a, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(t0, e, "matmul launch");
+    return KORE_QMV_OK;
+}
+
 KORE_QMV_API int kore_qmv_matmul_batch_dev(kore_qmv_tensor_t t, const float *x, int nb, float *out, void *stream) {
     if (!t) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
-    if (nb < 1 || nb > kGemmMaxB) return fail(t, KORE_QMV_E_INVALID, "nb must be 1..64 (kore's KORE_BMAX)");
-    if (int rc = check_dev_ptr(t, x, 16, "x")) return rc;
-    if (int rc = check_dev_ptr(t, out, 4, "out")) return rc;
-    GemmArgs a{t->w, t->wd, t->type, x, nullptr, (int)t->rows, t->nblk, nb, t->gemm_splits};
-    hipError_t e = launch_gemm(a, out, t->gemm_splits > 1 ? (float *)g_gemm[t->device & 63].p : nullptr,
-                               (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(t, e, "matmul launch");
-    return KORE_QMV_OK;
+    return kore_qmv_matmul_batch_group_dev(1, &t, x, nb, &out, stream);
 }
 
 KORE_QMV_API int kore_qmv_matmul_batch(kore_qmv_tensor_t t, const float *x, int nb, float *out) {

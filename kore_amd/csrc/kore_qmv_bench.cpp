@@ -5,7 +5,9 @@
 // calls (kore.cpp:1418-1421, 1456-1457, 1462-1464, 1469-1470, 1476-1477)
 // replayed through the public device-pointer entry points
 // kore_qmv_quantize_dev / kore_qmv_matvec_dev / kore_qmv_mv_group_dev on one
-// stream, so that a timed region contains no Python between launches.
+// stream, so that a timed region contains no Python between launches; and of
+// forward_batch()'s matmul_batch_float calls (kore.cpp:1524-1585) through
+// kore_qmv_matmul_batch_dev.
 //
 // Timing as in kore_attn_bench.cpp: steady_clock around the whole region,
 // bracketed by a stream synchronisation on both sides; optionally a HIP event
@@ -22,12 +24,14 @@
 struct KqbOp {
     int kind;              // 0: quantize x[n] -> xq; 1: matvec tensors[t[0]] . xq -> out[0];
                            // 2: quant + mv of n_t tensors sharing x (kore_qmv_mv_group_dev)
+                           // 3: batched matmul of tensors[t[0]] with x[n][cols] -> out[0]
+                           // 4: batched matmul of n_t tensors sharing x, one launch
     int n_t;               // kind 2: number of tensors (1..4)
     int t[4];              // indices into tensors
     const float *x;        // kinds 0, 2
-    long long n;           // kind 0
+    long long n;           // kind 0: elements; kind 3: activations
     void *xq;              // kinds 0, 1
-    float *out[4];         // kinds 1, 2
+    float *out[4];         // kinds 1 to 4
 };
 
 // Runs the n_ops operations `reps` times in order.  op_ms (optional) receives
@@ -61,10 +65,13 @@ KQB_API int kqb_run(const KqbOp *ops, int n_ops, kore_qmv_tensor_t *tensors, int
                 rc = kore_qmv_quantize_dev(o.x, o.n, o.xq, s);
             } else if (o.kind == 1) {
                 rc = kore_qmv_matvec_dev(tensors[o.t[0]], o.xq, o.out[0], avx2, s);
+            } else if (o.kind == 3) {
+                rc = kore_qmv_matmul_batch_dev(tensors[o.t[0]], o.x, (int)o.n, o.out[0], s);
             } else {
                 kore_qmv_tensor_t g[4];
                 for (int m = 0; m < o.n_t && m < 4; ++m) g[m] = tensors[o.t[m]];
-                rc = kore_qmv_mv_group_dev(o.n_t, g, o.x, o.out, avx2, s);
+                if (o.kind == 4) rc = kore_qmv_matmul_batch_group_dev(o.n_t, g, o.x, (int)o.n, o.out, s);
+                else rc = kore_qmv_mv_group_dev(o.n_t, g, o.x, o.out, avx2, s);
             }
             if (rc != KORE_QMV_OK) break;
             if (op_ms) (void)hipEventRecord(ev[k + 1], s);

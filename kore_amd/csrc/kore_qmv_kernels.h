@@ -78,19 +78,38 @@ hipError_t launch_synth_blocks(int type, int64_t nblocks, uint64_t seed, uint8_t
 
 // Batched prefill matmul (kore's matmul_batch_float, kore.cpp:783-845):
 // out[b * rows + r] = dequantised row r . x[b], b < B <= kGemmMaxB; fp32 MFMA,
-// equal to kore's results to fp32 rounding.
+// equal to kore's results to fp32 rounding.  One launch covers up to
+// kMaxGroup matrices that share x (same cols), each with its own output.
+//
+// Work split (stream-K): the iteration space (64-row tile, 256-column block)
+// of all the matrices is cut into `workers` equal contiguous runs, one per
+// workgroup.  A tile whose blocks fall to several workers is finished by a
+// second launch that adds their partial sums in worker order.
 constexpr int kGemmMaxB = 64;            // kore's KORE_BMAX (kore.cpp:690)
-struct GemmArgs {
+constexpr int kGemmRowsPerTile = 64;
+constexpr int kGemmSlotFloats = kGemmRowsPerTile * kGemmMaxB;   // one partial tile
+struct GemmMat {
     const uint8_t *w;        // Q4_K blocks or Q6_K bodies
     const uint16_t *wd;      // Q6_K f16 scales
-    int type;
-    const float *x;          // [B][nblk * 256], 16-byte aligned
-    float *out;              // set by launch_gemm
-    int rows, nblk, B;
-    int splits;              // workgroups per row tile along the blocks (gemm_splits)
+    float *out;              // [B][rows]
+    int rows, type;
+    int tile0;               // first tile of this matrix in the launch
 };
-int gemm_splits(int rows, int nblk, int num_cu);
-// partials: splits * B * rows floats when splits > 1
-hipError_t launch_gemm(GemmArgs a, float *out, float *partials, hipStream_t s);
+struct GemmArgs {
+    GemmMat m[kMaxGroup];
+    int n_mat;
+    const float *x;          // [B][nblk * 256], 16-byte aligned
+    int B, nblk;
+    int tiles;               // all matrices' tiles
+    int workers;             // grid size (gemm_workers)
+    float *partials;         // 2 * workers * kGemmSlotFloats floats
+};
+// Workers of one launch: as many as fit on the CUs at once (by the LDS and
+// registers of the kernel that B activations and the weight types select), at
+// least two iterations each.
+int gemm_workers(int tiles, int nblk, int B, bool has_q6k, int num_cu);
+// Largest grid any launch on a device with num_cu CUs uses (sizes partials).
+int gemm_max_workers(int num_cu);
+hipError_t launch_gemm(GemmArgs a, hipStream_t s);
 
 }  // namespace kore_qmv_gpu

@@ -52,6 +52,7 @@ SYMBOLS = [
     ("kore_qmv_mv_group_dev", _i, [_i, _vp, _vp, _vp, _i, _vp]),
     ("kore_qmv_matmul_batch", _i, [_vp, _vp, _i, _vp]),
     ("kore_qmv_matmul_batch_dev", _i, [_vp, _vp, _i, _vp, _vp]),
+    ("kore_qmv_matmul_batch_group_dev", _i, [_i, _vp, _vp, _i, _vp, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
     ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),
@@ -186,3 +187,12 @@ def mv_group_dev(mats, x_ptr: int, out_ptrs, avx2: bool = True, stream=None) -> 
     hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
     outs = (C.c_void_p * n)(*out_ptrs)
     _check(lib().kore_qmv_mv_group_dev(n, hs, x_ptr, outs, int(avx2), stream))
+
+
+def matmul_batch_group_dev(mats, x_ptr: int, nb: int, out_ptrs, stream=None) -> None:
+    """One batched-matmul launch of up to 4 matrices of equal cols sharing x
+    [nb][cols] (device pointers); out_ptrs[k] receives [nb][rows_k]."""
+    n = len(mats)
+    hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
+    outs = (C.c_void_p * n)(*out_ptrs)
+    _check(lib().kore_qmv_matmul_batch_group_dev(n, hs, x_ptr, nb, outs, stream))

@@ -27,6 +27,12 @@
 // (kore.cpp:1387-1394, 677-682) - until MIN_SECONDS have passed; prints one
 // JSON line {"reps", "seconds", "rows", "cols", "weight_bytes", "avx2",
 // "threads", "copies"}.
+//
+//   kore_qmv_ref --time-batch THREADS MIN_SECONDS job.bin
+// takes a batch-mode job and runs kore's matmul_batch_float on it with
+// THREADS threads and the AVX2 path where the CPU has it (as forward_batch()
+// calls it, kore.cpp:1524) until MIN_SECONDS have passed; prints one JSON line
+// {"reps", "seconds", "rows", "cols", "B", "avx2", "threads"}.
 
 #define main kore_ref_main
 #include "kore.cpp"
@@ -85,33 +91,70 @@ static int time_mode(unsigned nth, double min_s, int copies, const char *job) {
     return 0;
 }
 
-static int batch_mode(const char *job, const char *res) {
+struct BatchJob {
+    int type = 0, B = 0;
+    int64_t rows = 0, cols = 0;
+    std::vector<uint8_t> w;
+    std::vector<float> x;
+    Tensor t;
+};
+
+static int read_batch_job(const char *job, BatchJob &j) {
     FILE *in = fopen(job, "rb");
-    FILE *out = fopen(res, "wb");
-    if (!in || !out) { perror("open"); return 2; }
+    if (!in) { perror("open"); return 2; }
     int32_t hdr[4];
     if (fread(hdr, 4, 4, in) != 4) return 3;
-    const int type = hdr[0], B = hdr[3];
-    const int64_t rows = hdr[1], cols = hdr[2];
-    if (cols % 256 != 0 || (type != GGML_Q4_K && type != GGML_Q6_K) || B <= 0 || B > KORE_BMAX) return 3;
-    const int64_t nb = cols / 256, bb = type == GGML_Q4_K ? 144 : 210;
-    std::vector<uint8_t> w((size_t)(rows * nb * bb));
-    std::vector<float> x((size_t)(B * cols));
-    if (fread(w.data(), 1, w.size(), in) != w.size()) return 3;
-    if (fread(x.data(), 4, x.size(), in) != x.size()) return 3;
+    j.type = hdr[0];
+    j.B = hdr[3];
+    j.rows = hdr[1];
+    j.cols = hdr[2];
+    if (j.cols % 256 != 0 || (j.type != GGML_Q4_K && j.type != GGML_Q6_K) || j.B <= 0 || j.B > KORE_BMAX) return 3;
+    const int64_t nb = j.cols / 256, bb = j.type == GGML_Q4_K ? 144 : 210;
+    j.w.resize((size_t)(j.rows * nb * bb));
+    j.x.resize((size_t)(j.B * j.cols));
+    if (fread(j.w.data(), 1, j.w.size(), in) != j.w.size()) return 3;
+    if (fread(j.x.data(), 4, j.x.size(), in) != j.x.size()) return 3;
     fclose(in);
-    Tensor t;
-    t.type = (uint32_t)type;
-    t.n_dims = 2;
-    t.dims[0] = (uint64_t)cols;
-    t.dims[1] = (uint64_t)rows;
-    t.nbytes = w.size();
-    t.data = w.data();
-    const int B8 = (B + 7) & ~7;
-    std::vector<float> xT((size_t)(cols * B8)), o1((size_t)(rows * B)), o2((size_t)(rows * B));
+    j.t.type = (uint32_t)j.type;
+    j.t.n_dims = 2;
+    j.t.dims[0] = (uint64_t)j.cols;
+    j.t.dims[1] = (uint64_t)j.rows;
+    j.t.nbytes = j.w.size();
+    j.t.data = j.w.data();
+    return 0;
+}
+
+static int time_batch_mode(unsigned nth, double min_s, const char *job) {
+    BatchJob j;
+    if (int rc = read_batch_job(job, j)) return rc;
+    const int B8 = (j.B + 7) & ~7;
+    std::vector<float> xT((size_t)(j.cols * B8)), o((size_t)(j.rows * j.B));
     const bool avx2 = cpu_has_avx2();
-    matmul_batch_float(t, x.data(), B, xT.data(), o1.data(), avx2, 1);
-    matmul_batch_float(t, x.data(), B, xT.data(), o2.data(), false, 1);
+    matmul_batch_float(j.t, j.x.data(), j.B, xT.data(), o.data(), avx2, nth);   // warm-up
+    int reps = 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    double el = 0;
+    do {
+        matmul_batch_float(j.t, j.x.data(), j.B, xT.data(), o.data(), avx2, nth);
+        ++reps;
+        el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    } while (el < min_s);
+    printf("{\"reps\": %d, \"seconds\": %.6f, \"rows\": %lld, \"cols\": %lld, \"B\": %d, \"avx2\": %d, "
+           "\"threads\": %u, \"checksum\": %.9g}\n",
+           reps, el, (long long)j.rows, (long long)j.cols, j.B, (int)avx2, nth, (double)o[o.size() / 2]);
+    return 0;
+}
+
+static int batch_mode(const char *job, const char *res) {
+    BatchJob j;
+    if (int rc = read_batch_job(job, j)) return rc;
+    FILE *out = fopen(res, "wb");
+    if (!out) { perror("open"); return 2; }
+    const int B8 = (j.B + 7) & ~7;
+    std::vector<float> xT((size_t)(j.cols * B8)), o1((size_t)(j.rows * j.B)), o2((size_t)(j.rows * j.B));
+    const bool avx2 = cpu_has_avx2();
+    matmul_batch_float(j.t, j.x.data(), j.B, xT.data(), o1.data(), avx2, 1);
+    matmul_batch_float(j.t, j.x.data(), j.B, xT.data(), o2.data(), false, 1);
     if (fwrite(o1.data(), 4, o1.size(), out) != o1.size()) return 4;
     if (fwrite(o2.data(), 4, o2.size(), out) != o2.size()) return 4;
     fclose(out);
@@ -120,10 +163,13 @@ static int batch_mode(const char *job, const char *res) {
 
 int main(int argc, char **argv) {
     if (argc == 4 && std::string(argv[1]) == "--batch") return batch_mode(argv[2], argv[3]);
+    if (argc == 5 && std::string(argv[1]) == "--time-batch")
+        return time_batch_mode((unsigned)atoi(argv[2]), atof(argv[3]), argv[4]);
     if (argc == 6 && std::string(argv[1]) == "--time")
         return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), argv[5]);
     if (argc != 3) {
-        fprintf(stderr, "usage: kore_qmv_ref job.bin result.bin | --time THREADS SECONDS COPIES job.bin\n");
+        fprintf(stderr, "usage: kore_qmv_ref job.bin result.bin | --batch job.bin result.bin | --time THREADS SECONDS COPIES "
+                        "job.bin | --time-batch THREADS SECONDS job.bin\n");
         return 2;
     }
     FILE *in = fopen(argv[1], "rb");

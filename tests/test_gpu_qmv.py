@@ -322,6 +322,9 @@ GEMM_SHAPES = [  # type, rows, nblk, B
     (oracle.TYPE_Q4K, 1, 1, 1), (oracle.TYPE_Q6K, 100, 3, 17), (oracle.TYPE_Q4K, 257, 2, 16),
     (oracle.TYPE_Q4K, 3584, 14, 64), (oracle.TYPE_Q6K, 200, 74, 33), (oracle.TYPE_Q6K, 65, 14, 48),
     (oracle.TYPE_Q4K, 130, 128, 5),
+    (oracle.TYPE_Q6K, 64, 74, 64),     # one tile whose 74 blocks are split among 37 workgroups
+    (oracle.TYPE_Q4K, 5000, 3, 20),    # 79 tiles of 3 blocks
+    (oracle.TYPE_Q4K, 64, 1, 64),      # a single iteration
 ]
 
 
@@ -384,3 +387,59 @@ def test_matmul_batch_7b_shapes(name, wtype, rows, cols):
     wsub = np.concatenate([w[r * rb:(r + 1) * rb] for r in pick])
     ref = oracle.matmul_batch(wtype, wsub, len(pick), cols, x, avx2=True)
     _close_kore(out[:, pick], ref, name)
+
+
+@pytest.mark.parametrize("shapes,B", [
+    ([(oracle.TYPE_Q4K, 300), (oracle.TYPE_Q4K, 64), (oracle.TYPE_Q6K, 65)], 37),   # q, k, v with v in Q6_K
+    ([(oracle.TYPE_Q4K, 700), (oracle.TYPE_Q4K, 700)], 64),                          # gate, up
+    ([(oracle.TYPE_Q6K, 17), (oracle.TYPE_Q4K, 1), (oracle.TYPE_Q6K, 129), (oracle.TYPE_Q4K, 64)], 16),
+])
+def test_matmul_batch_group(shapes, B):
+    """One grouped launch: every output within kore's tolerance of the oracle
+    and of the matrix's own single launch."""
+    from kore_amd import hip, qmv
+    cols = 2048
+    _say(f"qmm group {shapes}, cols {cols}, B {B}")
+    rng = np.random.default_rng(len(shapes) * 100 + B)
+    ws = [_weights(t, r, cols // 256, rng) for t, r in shapes]
+    x = np.stack([_x(cols, rng) for _ in range(B)])
+    mats = [qmv.QMat(t, r, cols, w) for (t, r), w in zip(shapes, ws)]
+    try:
+        dx = hip.DeviceBuffer.from_array(x)
+        outs = [hip.DeviceBuffer(B * r) for _, r in shapes]
+        for rep in range(2):
+            qmv.matmul_batch_group_dev(mats, dx.ptr, B, [o.ptr for o in outs])
+            hip.synchronize()
+            got = [o.download().reshape(B, r) for o, (_, r) in zip(outs, shapes)]
+            if rep == 0:
+                first = [g.copy() for g in got]
+            else:
+                for g0, g1 in zip(first, got):
+                    assert np.array_equal(_bits(g0), _bits(g1)), "repeated grouped calls differ"
+        for k, ((t, r), w) in enumerate(zip(shapes, ws)):
+            _close_kore(got[k], oracle.matmul_batch(t, w, r, cols, x, avx2=True), f"group member {k} vs oracle")
+            _close_kore(got[k], mats[k].matmul_batch(x), f"group member {k} vs its single launch")
+        dx.free()
+        for o in outs:
+            o.free()
+    finally:
+        for m in mats:
+            m.close()
+
+
+def test_matmul_batch_group_rejections():
+    from kore_amd import hip, qmv
+    rng = np.random.default_rng(3)
+    a = qmv.QMat(oracle.TYPE_Q4K, 64, 512, _weights(oracle.TYPE_Q4K, 64, 2, rng))
+    b = qmv.QMat(oracle.TYPE_Q4K, 64, 768, _weights(oracle.TYPE_Q4K, 64, 3, rng))
+    try:
+        dx, do = hip.DeviceBuffer(64 * 768), hip.DeviceBuffer(64 * 64)
+        with pytest.raises(qmv.QmvError):               # unequal cols
+            qmv.matmul_batch_group_dev([a, b], dx.ptr, 4, [do.ptr, do.ptr])
+        with pytest.raises(qmv.QmvError):               # five matrices
+            qmv.matmul_batch_group_dev([a] * 5, dx.ptr, 4, [do.ptr] * 5)
+        dx.free()
+        do.free()
+    finally:
+        a.close()
+        b.close()
