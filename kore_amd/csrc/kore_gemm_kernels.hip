@@ -58,13 +58,15 @@ __device__ __forceinline__ int q4m(const uint4 &h, int j) {   // 6-bit min of su
 }
 
 // One lane's weights of one block.  Q4_K (group kk: 32 nibble bytes + header):
-// v[0] header, v[1..2] bytes 16 + 32 kk ...; Q6_K (values 64 kk .. 64 kk + 63):
-// v[0..3] the 64 ql bytes of half kk / 2, v[4..5] its 32 qh bytes, sc the four
-// scales of the lane, d the f16 scale.
+// v[0] header, v[1..2] bytes 16 + 32 kk ...  Q6_K (lane kk = 2 h + j): v[0..1]
+// the 32 ql bytes 64 h + 32 j ..., whose low and high nibbles are the low bits
+// of values 128 h + 32 j + l and 128 h + 32 (j + 2) + l; v[2..3] the 32 qh bytes
+// of half h (2 high bits of each of those values); sc the 8 scale bytes of half
+// h; d the f16 scale.
 template <bool Q6>
 struct WRaw {
-    uint4 v[Q6 ? 6 : 3];
-    uint32_t sc, d;
+    uint4 v[Q6 ? 4 : 3];
+    uint32_t sc[Q6 ? 2 : 1], d;
 };
 
 template <bool Q6>
@@ -76,14 +78,14 @@ __device__ __forceinline__ void load_w(WRaw<Q6> &g, const GemmMat &m, int row, i
         g.v[2] = *(const uint4 *)(b + 32 + 32 * kk);
     } else if constexpr (Q6) {
         const uint8_t *b = m.w + ((int64_t)row * nblk + blk) * kQ6Body;
-        const int h = kk >> 1;
-        g.v[0] = *(const uint4 *)(b + 64 * h);
-        g.v[1] = *(const uint4 *)(b + 64 * h + 16);
-        g.v[2] = *(const uint4 *)(b + 64 * h + 32);
-        g.v[3] = *(const uint4 *)(b + 64 * h + 48);
-        g.v[4] = *(const uint4 *)(b + 128 + 32 * h);
-        g.v[5] = *(const uint4 *)(b + 128 + 32 * h + 16);
-        g.sc = *(const uint32_t *)(b + 192 + 4 * kk);   // sc[8h + 4(kk&1) + 0..3]
+        const int h = kk >> 1, j = kk & 1;
+        g.v[0] = *(const uint4 *)(b + 64 * h + 32 * j);
+        g.v[1] = *(const uint4 *)(b + 64 * h + 32 * j + 16);
+        g.v[2] = *(const uint4 *)(b + 128 + 32 * h);
+        g.v[3] = *(const uint4 *)(b + 128 + 32 * h + 16);
+        const uint2 sc = *(const uint2 *)(b + 192 + 8 * h);
+        g.sc[0] = sc.x;
+        g.sc[1] = sc.y;
         g.d = m.wd[(int64_t)row * nblk + blk];
     }
 }
@@ -94,9 +96,9 @@ __device__ __forceinline__ void load_w(WRaw<Q6> &g, const GemmMat &m, int row, i
 // dequantised before its 4 NB MFMAs, so neither LDS latency nor the
 // dequantisation chain sits in front of an MFMA.
 template <int NB>
-__device__ __forceinline__ void read_bx(floatx4 *bx, const float *xs, int i, int kk, int t4) {
+__device__ __forceinline__ void read_bx(floatx4 *bx, const float *xs, int i, int col) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) bx[nb] = *(const floatx4 *)&xs[(16 * nb + i) * kXStride + 64 * kk + 4 * t4];
+    for (int nb = 0; nb < NB; ++nb) bx[nb] = *(const floatx4 *)&xs[(16 * nb + i) * kXStride + col];
 }
 
 template <int NB>
@@ -115,12 +117,12 @@ __device__ __forceinline__ void block_q4(const WRaw<Q6> &g, const float *xs, int
     const float d1 = d * (float)q4s(hdr, 2 * kk), m1 = dmin * (float)q4m(hdr, 2 * kk);
     const float d2 = d * (float)q4s(hdr, 2 * kk + 1), m2 = dmin * (float)q4m(hdr, 2 * kk + 1);
     floatx4 bx[2][NB];
-    read_bx<NB>(bx[0], xs, i, kk, 0);
+    read_bx<NB>(bx[0], xs, i, 64 * kk);
 #pragma unroll
     for (int t4 = 0; t4 < 16; ++t4) {
         // the next step's reads go out first, a whole step before their use
         __builtin_amdgcn_sched_barrier(0);
-        if (t4 + 1 < 16) read_bx<NB>(bx[(t4 + 1) & 1], xs, i, kk, t4 + 1);
+        if (t4 + 1 < 16) read_bx<NB>(bx[(t4 + 1) & 1], xs, i, 64 * kk + 4 * (t4 + 1));
         __builtin_amdgcn_sched_barrier(0);
         float av[4];
 #pragma unroll
@@ -137,32 +139,32 @@ __device__ __forceinline__ void block_q4(const WRaw<Q6> &g, const float *xs, int
 
 template <int NB>
 __device__ __forceinline__ void block_q6(const WRaw<true> &g, const float *xs, int i, int kk, floatx4 *acc) {
-    // kore's dequant_block_q6_K (kore.cpp:359-381): value = (d * sc) * (q6 - 32);
-    // lane kk: h = kk / 2, groups k = 2 (kk % 2) + tk / 32, low or high nibble by kk % 2
+    // kore's dequant_block_q6_K (kore.cpp:359-381): value = (d * sc) * (q6 - 32).  Lane
+    // kk = 2 h + j takes values tk = 0..63 at column 128 h + 32 (j + 2 a) + l, a = tk / 32,
+    // l = tk % 32: low bits from nibble a of ql byte l, high bits 2 (j + 2 a) of qh byte l,
+    // scale byte 2 (j + 2 a) + l / 16 of the half's eight
+    const int h = kk >> 1, j = kk & 1;
     const float d = f16f(g.d);
-    const int kh = kk & 1;
-    float ds[4];
+    float ds[4];                                      // [2 a + l / 16]
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ds[e] = d * (float)(int)(int8_t)((g.sc >> (8 * e)) & 0xFF);
+    for (int e = 0; e < 4; ++e) ds[e] = d * (float)(int)(int8_t)((g.sc[e >> 1] >> (8 * (2 * j + (e & 1)))) & 0xFF);
+    const int col0 = 128 * h + 32 * j;
     floatx4 bx[2][NB];
-    read_bx<NB>(bx[0], xs, i, kk, 0);
+    read_bx<NB>(bx[0], xs, i, col0);
 #pragma unroll
     for (int t4 = 0; t4 < 16; ++t4) {
-        // the next step's reads go out first, a whole step before their use
         __builtin_amdgcn_sched_barrier(0);
-        if (t4 + 1 < 16) read_bx<NB>(bx[(t4 + 1) & 1], xs, i, kk, t4 + 1);
+        if (t4 + 1 < 16) read_bx<NB>(bx[(t4 + 1) & 1], xs, i, col0 + 64 * ((t4 + 1) >> 3) + 4 * ((t4 + 1) & 7));
         __builtin_amdgcn_sched_barrier(0);
         float av[4];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
-            const int tk = 4 * t4 + tt, l32 = tk & 31, kt = tk >> 5;
-            const uint4 &lv = g.v[tk >> 4];
-            const int m = (tk >> 2) & 3;
-            const uint32_t lw = m == 0 ? lv.x : m == 1 ? lv.y : m == 2 ? lv.z : lv.w;
-            const uint32_t hw = word(g.v[4], g.v[5], l32 >> 2);
-            const uint32_t nib = (lw >> (8 * (tk & 3) + 4 * kh)) & 15u;
-            const uint32_t hb = (hw >> (8 * (l32 & 3) + 4 * kh + 2 * kt)) & 3u;
-            av[tt] = ds[2 * kt + (l32 >> 4)] * (float)((int)(nib | (hb << 4)) - 32);
+            const int tk = 4 * t4 + tt, a = tk >> 5, l = tk & 31;
+            const uint32_t lw = word(g.v[0], g.v[1], l >> 2);
+            const uint32_t hw = word(g.v[2], g.v[3], l >> 2);
+            const uint32_t nib = (lw >> (8 * (l & 3) + 4 * a)) & 15u;
+            const uint32_t hb = (hw >> (8 * (l & 3) + 2 * (j + 2 * a))) & 3u;
+            av[tt] = ds[2 * a + (l >> 4)] * (float)((int)(nib | (hb << 4)) - 32);
         }
         mfma_step<NB>(av, bx[t4 & 1], acc);
     }
@@ -184,17 +186,25 @@ __device__ __forceinline__ int run_of(int64_t T, int P, int64_t it) { return (in
 
 // D block of an MFMA: lane l holds rows 4 (l / 16) + v, activation l % 16 of
 // each 16-block; rows past the matrix and activations past B are dropped.
+// When every 4-row group is whole and 16-byte aligned (rows % 4 == 0, out
+// aligned) a lane stores its four rows of an activation as one vector.
 template <int NB>
 __device__ __forceinline__ void store_tile(const GemmArgs &a, const GemmMat &mt, int tile, int wave, int i, int kk,
                                            const floatx4 *acc) {
     const int r0 = (tile - mt.tile0) * kGemmRowsPerTile + 16 * wave + 4 * kk;
+    const bool vec = (mt.rows & 3) == 0 && ((uintptr_t)mt.out & 15) == 0;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         const int b = 16 * nb + i;
         if (b >= a.B) continue;
+        float *o = mt.out + (int64_t)b * mt.rows + r0;
+        if (vec) {
+            if (r0 < mt.rows) *(floatx4 *)o = acc[nb];
+        } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            if (r0 + v < mt.rows) mt.out[(int64_t)b * mt.rows + r0 + v] = acc[nb][v];
+            for (int v = 0; v < 4; ++v)
+                if (r0 + v < mt.rows) o[v] = acc[nb][v];
+        }
     }
 }
 
@@ -207,15 +217,24 @@ __global__ __launch_bounds__(kThreads) void gemm_fixup_kernel(GemmArgs a) {
     const int pf = run_of(T, P, tfirst), pl = run_of(T, P, tfirst + nblk - 1);
     if (pf == pl) return;                        // one worker ran the whole tile and stored it
     const int t = threadIdx.x, l = t & 63, wave = t >> 6, i = l & 15, kk = l >> 4;
+    // contributions in worker order, the loads of up to eight contributors in flight at once
+    constexpr int kBatch = 8;
     floatx4 acc[NB];
-    for (int q = pf; q <= pl; ++q) {
-        const int slot = 2 * q + (run_first(T, P, q) / nblk == tile ? 0 : 1);
-        const floatx4 *src = (const floatx4 *)a.partials + (int64_t)slot * (kGemmSlotFloats / 4);
+    for (int q0 = pf; q0 <= pl; q0 += kBatch) {
+        floatx4 v[kBatch][NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const floatx4 v = src[(wave * 4 + nb) * 64 + l];
-            acc[nb] = q == pf ? v : acc[nb] + v;
+        for (int u = 0; u < kBatch; ++u) {
+            const int q = min(q0 + u, pl);
+            const int slot = 2 * q + (run_first(T, P, q) / nblk == tile ? 0 : 1);
+            const floatx4 *src = (const floatx4 *)a.partials + (int64_t)slot * (kGemmSlotFloats / 4);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) v[u][nb] = src[(wave * 4 + nb) * 64 + l];
         }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                if (q0 + u <= pl) acc[nb] = q0 + u == pf ? v[u][nb] : acc[nb] + v[u][nb];
     }
     store_tile<NB>(a, a.m[mat_of_tile(a, tile)], tile, wave, i, kk, acc);
 }
@@ -223,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void gemm_fixup_kernel(GemmArgs a) {
 // Q6: the launch holds a Q6_K matrix (the Q4_K-only kernel keeps smaller
 // weight records in registers).
 template <int NB, bool Q6>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {   // two workgroups per CU
     extern __shared__ __align__(16) float xs[];      // [16 NB][kXStride]
     const int t = threadIdx.x, l = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);   // uniform: addresses built from it stay scalar
