@@ -526,6 +526,51 @@ def gemm_report(g, chunks: int):
     }
 
 
+def matvec_report(g, tokens: int):
+    mats, op_mats = g["mats"], g["op_mats"]
+    wbytes = sum(qmv_weight_bytes(t, r, c) for _, t, r, c in mats)
+    tok_s = g["region_ms"] / 1e3 / tokens
+    per = {}
+    for i, ts in enumerate(op_mats):
+        parts = []
+        alg = 0
+        for ti in ts:
+            name, t, r, c = mats[ti]
+            parts.append(name.split(".")[-1] + ("" if name == "output" else ("_q6k" if t == QMV_Q6K else "_q4k")))
+            alg += qmv_weight_bytes(t, r, c) + r * 4
+        alg += mats[ts[0]][3] * 4          # the fp32 input, read once
+        key = "+".join(parts)
+        d = per.setdefault(key, {"launches_per_token": 0, "ms": [], "bytes": alg})
+        d["launches_per_token"] += 1
+        d["ms"].extend(g["op_ms"][:, i].tolist())
+    table = {}
+    for key, d in per.items():
+        us = float(np.mean(d["ms"])) * 1e3
+        gbs = d["bytes"] / (us / 1e6) / 1e9
+        table[key] = {"launches_per_token": d["launches_per_token"], "us_mean": round(us, 2),
+                      "algorithmic_bytes": d["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                      "us_per_token": round(us * d["launches_per_token"], 1)}
+    dom = max(table, key=lambda k: table[k]["us_per_token"])
+    return {
+        "workload": "Qwen2.5-7B-shape token, matvec half: 28 layers x (attn_q, attn_k, attn_v, attn_output, "
+                    "ffn_gate, ffn_up, ffn_down) + output head = 197 matrices, Q4_K with attn_v/ffn_down in Q6_K on "
+                    "14 layers (Q4_K_M's use_more_bits rule) and a Q6_K output head; each preceded by kore's Q8_K "
+                    "quantisation of its input; synthetic weights (hashed bytes, finite f16 scales), activations "
+                    "N(0,1) with 1% x20; kore's AVX2 summation order; per layer 4 calls: q+k+v and gate+up "
+                    "as one grouped launch each",
+        "weight_bytes_per_token": wbytes,
+        "launches_per_token": len(op_mats),
+        "ms_per_token_gpu": round(tok_s * 1e3, 4),
+        "ms_per_token_wall": round(g["wall_ms"] / tokens, 4),
+        "weight_gbs": round(wbytes / tok_s / 1e9, 1),
+        "weight_frac_of_hbm_peak": round(wbytes / tok_s / 1e9 / HBM_PEAK_GBS, 4),
+        "tokens": tokens,
+        "per_matrix": table,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": table[dom]["frac"], "traffic": TRAFFIC_MATVEC_BYTES.get(dom)},
+    }
+
+
 def cpu_matvec(seconds: float, threads: int):
     """kore's own quant() + mv() (oracle/_ref/kore_qmv_ref, built from
     kore.cpp) on the 7B ffn_gate shape, cycling over 16 copies so the weights
