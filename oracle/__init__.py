@@ -22,6 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_BIN = os.path.join(HERE, "_ref", "kore_ref")
 REF_QMV_BIN = os.path.join(HERE, "_ref", "kore_qmv_ref")
+REF_LAYER_BIN = os.path.join(HERE, "_ref", "kore_layer_ref")
 
 # kore's BlockQ8K (kore.cpp:415-420): d, 256 int8 values, 16 int16 sums of 16
 Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
@@ -97,6 +98,8 @@ def lib() -> C.CDLL:
         L.ko_qmatvec.argtypes = [C.c_int, C.c_int64, C.c_int64, _u8, _u8, _F, C.c_int]
         L.ko_dequant_row.argtypes = [C.c_int, C.c_int64, _u8, _F]
         L.ko_matmul_batch.argtypes = [C.c_int, C.c_int64, C.c_int64, _u8, _F, C.c_int, _F, C.c_int]
+        L.ko_rmsnorm.argtypes = [_F, _F, _F, C.c_int, C.c_float]
+        L.ko_swiglu.argtypes = [_F, _F, C.c_int]
         _lib = L
     return _lib
 
@@ -341,3 +344,54 @@ class KV:
         if rc != 0:
             raise ValueError(f"ko_prefill rejected layer={layer} pos0={pos0} n={n} ({rc})")
         return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """kore's rmsnorm (kore.cpp:1367-1372)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    out = np.zeros_like(x)
+    lib().ko_rmsnorm(fptr(out), fptr(x), fptr(w), x.size, eps)
+    return out
+
+
+def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """kore's SwiGLU (kore.cpp:1465-1468): g / (1 + exp(-g)) * u."""
+    out = np.array(g, np.float32).reshape(-1)
+    u = np.ascontiguousarray(u, np.float32).reshape(-1)
+    lib().ko_swiglu(fptr(out), fptr(u), out.size)
+    return out
+
+
+class LayerWeights:
+    """One layer's weights as kore holds them: the GGUF block bytes and types of
+    wq, wk, wv, wo, w_gate, w_up, w_down, and the float norms and biases."""
+    NAMES = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+
+    def __init__(self, types, mats, attn_norm, ffn_norm, bq, bk, bv):
+        self.types, self.mats = list(types), [np.ascontiguousarray(m, np.uint8).reshape(-1) for m in mats]
+        self.attn_norm, self.ffn_norm = np.asarray(attn_norm, np.float32), np.asarray(ffn_norm, np.float32)
+        self.bq, self.bk, self.bv = (np.asarray(b, np.float32) for b in (bq, bk, bv))
+
+
+def layer_forward(kv: "KV", layer: int, pos: int, x: np.ndarray, lw: LayerWeights, n_ff: int, eps: float,
+                  avx2: bool = True) -> np.ndarray:
+    """kore's forward() body for one layer on the quantised path
+    (kore.cpp:1415-1472): returns the new residual x; the KV store gets the
+    roped k and v at pos."""
+    E, kvd = kv.E, kv.kv_dim
+    x = np.array(x, np.float32).reshape(-1)
+    shapes = [(E, E), (kvd, E), (kvd, E), (E, E), (n_ff, E), (n_ff, E), (E, n_ff)]
+
+    def mv(j, xq):
+        return qmatvec(lw.types[j], lw.mats[j], shapes[j][0], shapes[j][1], xq, avx2=avx2)
+
+    xq = quantize_q8K(rmsnorm(x, lw.attn_norm, eps))
+    q = mv(0, xq) + lw.bq
+    k = mv(1, xq) + lw.bk
+    v = mv(2, xq) + lw.bv
+    att = kv.decode(layer, pos, q, k, v)
+    x = x + mv(3, quantize_q8K(att))
+    xq = quantize_q8K(rmsnorm(x, lw.ffn_norm, eps))
+    g = swiglu(mv(4, xq), mv(5, xq))
+    return x + mv(6, quantize_q8K(g))

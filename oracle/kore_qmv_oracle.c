@@ -326,3 +326,22 @@ int ko_matmul_batch(int type, int64_t rows, int64_t cols, const uint8_t *w, cons
     }
     return 0;
 }
+
+/* ------------------------------------------------------------ around the matvecs */
+
+/* kore.cpp:1367-1372 rmsnorm: double sum of (double)x[i] * x[i] in index order,
+ * scale = 1.0f / std::sqrt((float)(ss / n) + eps), out[i] = x[i] * scale * w[i]. */
+void ko_rmsnorm(float *out, const float *x, const float *w, int n, float eps) {
+    double ss = 0;
+    for (int i = 0; i < n; i++) ss += (double)x[i] * x[i];
+    const float scale = 1.0f / sqrtf((float)(ss / n) + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * scale * w[i];
+}
+
+/* kore.cpp:1465-1468 SwiGLU in place: g = g / (1.0f + exp(-g)) * u. */
+void ko_swiglu(float *g, const float *u, int n) {
+    for (int i = 0; i < n; i++) {
+        const float gg = g[i];
+        g[i] = gg / (1.0f + expf(-gg)) * u[i];
+    }
+}

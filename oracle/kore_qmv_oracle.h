@@ -56,6 +56,10 @@ void  ko_dequant_row(int type, int64_t cols, const uint8_t *w, float *y);
 int   ko_matmul_batch(int type, int64_t rows, int64_t cols, const uint8_t *w, const float *x, int B, float *out,
                       int avx2);
 
+/* kore's rmsnorm (kore.cpp:1367-1372) and SwiGLU (kore.cpp:1465-1468, in place). */
+void  ko_rmsnorm(float *out, const float *x, const float *w, int n, float eps);
+void  ko_swiglu(float *g, const float *u, int n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,140 @@
+// ref_layer_harness.cpp - drives kore's own forward() (kore.cpp:1397-1484) over
+// layers with real Q4_K / Q6_K weights, norms and biases, to record what it
+// produces.  TEST INFRASTRUCTURE ONLY: built by oracle/Makefile (target `ref`)
+// from the kore.cpp found at $(KORE_SRC) into oracle/_ref/kore_layer_ref, and
+// used to write tests/golden/layer_*.npz, which pin the oracle's composition
+// of rmsnorm, quantisation, matvecs, biases, RoPE, attention, SwiGLU and the
+// residual adds.
+//
+//   kore_layer_ref job.bin result.bin
+//
+// Job (little endian):
+//   int32 n_layer, n_head, n_head_kv, head_dim, n_ff, ctx, avx2, n_steps;
+//   float32 rope_base, rms_eps;
+//   per layer: int32 types[7] (12 Q4_K / 14 Q6_K for wq wk wv wo w_gate w_up
+//              w_down), float32 attn_norm[E], ffn_norm[E], bq[E], bk[kvd],
+//              bv[kvd], then the 7 matrices' GGUF block bytes (rows x cols/256
+//              blocks);
+//   float32 emb[n_steps][E] (step s runs token s, whose embedding row is emb[s]);
+//   int32 pos[n_steps].
+// Result: float32 x[n_steps][E] (the residual after the last layer, kore's
+//   e.x: forward() is called without logits), then the K and V caches
+//   ([n_layer][ctx][kvd] each).
+#define main kore_ref_main
+#include "kore.cpp"
+#undef main
+
+#include <cstdio>
+#include <vector>
+
+namespace {
+
+bool rd(FILE *f, void *p, size_t n) { return fread(p, 1, n, f) == n; }
+bool wr(FILE *f, const void *p, size_t n) { return fwrite(p, 1, n, f) == n; }
+
+struct OwnedTensor {
+    std::vector<uint8_t> bytes;
+    Tensor t;
+};
+
+bool read_tensor(FILE *f, OwnedTensor &o, uint32_t type, uint64_t cols, uint64_t rows) {
+    const uint64_t bb = type == GGML_Q4_K ? 144 : type == GGML_Q6_K ? 210 : type == GGML_F32 ? 1024 : 0;
+    if (!bb || cols % 256) return false;
+    o.bytes.resize(cols / 256 * bb * rows);
+    o.t.type = type;
+    o.t.n_dims = 2;
+    o.t.dims[0] = cols;
+    o.t.dims[1] = rows;
+    o.t.nbytes = o.bytes.size();
+    return rd(f, o.bytes.data(), o.bytes.size());
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    if (argc != 3) { fprintf(stderr, "usage: kore_layer_ref job.bin result.bin\n"); return 2; }
+    FILE *in = fopen(argv[1], "rb");
+    FILE *out = fopen(argv[2], "wb");
+    if (!in || !out) { perror("open"); return 2; }
+    int32_t hdr[8];
+    float fp[2];
+    if (!rd(in, hdr, sizeof hdr) || !rd(in, fp, sizeof fp)) return 3;
+    const int n_layer = hdr[0], nh = hdr[1], nkv = hdr[2], hd = hdr[3], FF = hdr[4], ctx = hdr[5];
+    const int avx2 = hdr[6], n_steps = hdr[7];
+    const int E = nh * hd, kvd = nkv * hd;
+    if (E % 256 || FF % 256 || nh % nkv || n_steps < 1) return 3;
+
+    Engine e;
+    e.hp.n_layer = (uint32_t)n_layer; e.hp.n_embd = (uint32_t)E; e.hp.n_ff = (uint32_t)FF;
+    e.hp.n_head = (uint32_t)nh; e.hp.n_head_kv = (uint32_t)nkv; e.hp.n_ctx = (uint32_t)ctx;
+    e.hp.n_vocab = (uint32_t)n_steps; e.hp.rope_base = fp[0]; e.hp.rms_eps = fp[1];
+    e.head_dim = hd; e.kv_dim = kvd; e.n_rep = nh / nkv; e.ctx = ctx; e.n_vocab = n_steps;
+    e.nth = 4; e.use_float = false;
+    e.avx2 = KORE_HAVE_AVX2 && cpu_has_avx2() && avx2;
+
+    std::vector<std::vector<float>> vecs((size_t)n_layer * 5);
+    std::vector<OwnedTensor> mats((size_t)n_layer * 7);
+    const uint64_t rows_of[7] = {(uint64_t)E, (uint64_t)kvd, (uint64_t)kvd, (uint64_t)E, (uint64_t)FF, (uint64_t)FF,
+                                 (uint64_t)E};
+    const uint64_t cols_of[7] = {(uint64_t)E, (uint64_t)E, (uint64_t)E, (uint64_t)E, (uint64_t)E, (uint64_t)E,
+                                 (uint64_t)FF};
+    for (int l = 0; l < n_layer; l++) {
+        int32_t types[7];
+        if (!rd(in, types, sizeof types)) return 3;
+        const size_t sizes[5] = {(size_t)E, (size_t)E, (size_t)E, (size_t)kvd, (size_t)kvd};
+        for (int j = 0; j < 5; j++) {
+            std::vector<float> &v = vecs[(size_t)l * 5 + j];
+            v.resize(sizes[j]);
+            if (!rd(in, v.data(), v.size() * 4)) return 3;
+        }
+        for (int j = 0; j < 7; j++)
+            if (!read_tensor(in, mats[(size_t)l * 7 + j], (uint32_t)types[j], cols_of[j], rows_of[j])) return 3;
+    }
+    OwnedTensor tok;
+    tok.bytes.resize((size_t)n_steps * E * 4);
+    if (!rd(in, tok.bytes.data(), tok.bytes.size())) return 3;
+    tok.t.type = GGML_F32; tok.t.n_dims = 2; tok.t.dims[0] = (uint64_t)E; tok.t.dims[1] = (uint64_t)n_steps;
+    tok.t.nbytes = tok.bytes.size(); tok.t.data = tok.bytes.data();
+    std::vector<int32_t> pos((size_t)n_steps);
+    if (!rd(in, pos.data(), pos.size() * 4)) return 3;
+
+    std::vector<float> ones((size_t)E, 1.0f);
+    e.tok_embd = &tok.t;
+    e.out_norm = ones.data();
+    for (int l = 0; l < n_layer; l++) {
+        OwnedTensor *m = &mats[(size_t)l * 7];
+        for (int j = 0; j < 7; j++) m[j].t.data = m[j].bytes.data();
+        Layer L;
+        L.wq = &m[0].t; L.wk = &m[1].t; L.wv = &m[2].t; L.wo = &m[3].t;
+        L.w_gate = &m[4].t; L.w_up = &m[5].t; L.w_down = &m[6].t;
+        std::vector<float> *v = &vecs[(size_t)l * 5];
+        L.attn_norm = v[0].data(); L.ffn_norm = v[1].data();
+        L.bq = v[2].data(); L.bk = v[3].data(); L.bv = v[4].data();
+        e.layers.push_back(L);
+    }
+
+    // Buffer sizes as engine_init gives them (kore.cpp:1336-1363).
+    const int half = hd / 2;
+    e.inv_freq.resize((size_t)half);
+    for (int i = 0; i < half; i++) e.inv_freq[(size_t)i] = (float)std::pow((double)e.hp.rope_base, -2.0 * i / hd);
+    e.rope_c.resize((size_t)half); e.rope_s.resize((size_t)half);
+    e.kcache.assign((size_t)n_layer * ctx * kvd, 0.0f);
+    e.vcache.assign((size_t)n_layer * ctx * kvd, 0.0f);
+    e.emb.resize((size_t)E); e.x.resize((size_t)E); e.xb.resize((size_t)E); e.q.resize((size_t)E);
+    e.att.resize((size_t)E); e.o.resize((size_t)E);
+    e.k.resize((size_t)kvd); e.v.resize((size_t)kvd);
+    e.gate.resize((size_t)FF); e.up.resize((size_t)FF);
+    e.scores.resize((size_t)ctx); e.logits.resize(1);
+    e.xq_e.resize((size_t)(E / 256 + 1)); e.xq_f.resize((size_t)FF / 256);
+    e.scratch.resize((size_t)E);
+
+    for (int st = 0; st < n_steps; st++) {
+        if (!forward(e, st, pos[(size_t)st], false)) { fprintf(stderr, "forward failed at step %d\n", st); return 5; }
+        if (!wr(out, e.x.data(), sizeof(float) * E)) return 6;
+    }
+    if (!wr(out, e.kcache.data(), sizeof(float) * e.kcache.size()) ||
+        !wr(out, e.vcache.data(), sizeof(float) * e.vcache.size())) return 6;
+    fclose(out);
+    fclose(in);
+    return 0;
+}
