@@ -130,6 +130,30 @@ KORE_QMV_API int kore_qmv_matmul_batch_dev(kore_qmv_tensor_t t, const float *x, 
 KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
                                                  float *const *out, void *stream);
 
+/* The matvec with kore's elementwise steps around it fused into the same
+ * launches (kore's forward(), kore.cpp:1417-1471).  Before quantising x:
+ *   norm_w  != NULL: kore's rmsnorm(x, norm_w, norm_eps) (kore.cpp:1367-1372),
+ *                    bit-identical to kore's sequential double sum;
+ *   up      != NULL: kore's SwiGLU, x / (1 + exp(-x)) * up (kore.cpp:1465-1468),
+ *                    exp rounded from double (glibc's expf can differ in the last
+ *                    bit on rare inputs, so this step holds to kore's tolerance);
+ * and in the final store of matrix k:
+ *   bias[k] != NULL: out = W.x + bias (kore's q/k/v biases, kore.cpp:1422-1423);
+ *   accumulate:      out = out + W.x (kore's residual adds, kore.cpp:1458, 1471).
+ * norm_w, up, bias are device arrays (norm_w and up 16-byte aligned, cols long;
+ * bias rows long); at most one of norm_w and up. */
+typedef struct kore_qmv_mv_opts {
+    const float *norm_w;
+    float norm_eps;
+    const float *up;
+    const float *bias[4];
+    int accumulate;
+} kore_qmv_mv_opts;
+
+KORE_QMV_API int kore_qmv_mv_group_ex_dev(int n, const kore_qmv_tensor_t *t, const float *x,
+                                          const kore_qmv_mv_opts *opts, float *const *out, int avx2,
+                                          void *stream);
+
 /* Text of the last failure on this tensor (or, with NULL, of the last failed
  * call without a tensor on this thread).  Never NULL. */
 KORE_QMV_API const char *kore_qmv_last_error(kore_qmv_tensor_t t);

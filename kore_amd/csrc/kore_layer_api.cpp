@@ -1,0 +1,142 @@
+// kore_layer_api.cpp - the C ABI of include/kore_layer.h: one layer of kore's
+// forward() chained from libkore_qmv's fused matvec launches and libkore_attn's
+// decode, all on one stream.
+#include "kore_layer.h"
+
+#include <hip/hip_runtime.h>
+
+#include <new>
+#include <string>
+
+struct kore_layer {
+    int E = 0, FF = 0, n_head = 0, n_head_kv = 0, head_dim = 0, kvd = 0;
+    float eps = 0.f;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    float *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *gate = nullptr, *up = nullptr;
+    std::string error;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(kore_layer *L, int code, const std::string &msg) {
+    (L ? L->error : g_error) = msg;
+    return code;
+}
+
+void release(kore_layer *L) {
+    for (float *p : {L->q, L->k, L->v, L->att, L->gate, L->up})
+        if (p) (void)hipFree(p);
+    if (L->stream) (void)hipStreamDestroy(L->stream);
+    delete L;
+}
+
+bool shape_is(kore_qmv_tensor_t t, int64_t rows, int64_t cols) {
+    kore_qmv_info info{};
+    return t && kore_qmv_get_info(t, &info) == KORE_QMV_OK && info.rows == rows && info.cols == cols;
+}
+
+}  // namespace
+
+extern "C" {
+
+KORE_LAYER_API int kore_layer_create(kore_layer_t *out, int n_embd, int n_ff, int n_head, int n_head_kv,
+                                     float rms_eps) {
+    if (!out) return fail(nullptr, KORE_LAYER_E_INVALID, "out is NULL");
+    *out = nullptr;
+    if (n_embd <= 0 || n_ff <= 0 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || n_embd % n_head ||
+        n_embd % 256 || n_ff % 256)
+        return fail(nullptr, KORE_LAYER_E_INVALID,
+                    "n_embd, n_ff multiples of 256; n_head dividing n_embd; n_head_kv dividing n_head");
+    kore_layer *L = new (std::nothrow) kore_layer;
+    if (!L) return fail(nullptr, KORE_LAYER_E_HIP, "out of host memory");
+    L->E = n_embd;
+    L->FF = n_ff;
+    L->n_head = n_head;
+    L->n_head_kv = n_head_kv;
+    L->head_dim = n_embd / n_head;
+    L->kvd = n_head_kv * L->head_dim;
+    L->eps = rms_eps;
+    hipError_t e = hipGetDevice(&L->device);
+    // a blocking stream: ordered with the null stream, so a caller's plain
+    // hipMemcpy of x before a call is seen by it
+    if (e == hipSuccess) e = hipStreamCreate(&L->stream);
+    const size_t sizes[6] = {(size_t)L->E, (size_t)L->kvd, (size_t)L->kvd, (size_t)L->E, (size_t)L->FF,
+                             (size_t)L->FF};
+    float **bufs[6] = {&L->q, &L->k, &L->v, &L->att, &L->gate, &L->up};
+    for (int i = 0; i < 6 && e == hipSuccess; ++i) e = hipMalloc((void **)bufs[i], sizes[i] * sizeof(float));
+    if (e != hipSuccess) {
+        g_error = std::string("kore_layer_create: ") + hipGetErrorString(e);
+        release(L);
+        return KORE_LAYER_E_HIP;
+    }
+    *out = L;
+    return KORE_LAYER_OK;
+}
+
+KORE_LAYER_API void kore_layer_destroy(kore_layer_t L) {
+    if (L) release(L);
+}
+
+KORE_LAYER_API int kore_layer_decode_dev(kore_layer_t L, const kore_layer_weights *w, kore_attn_t attn, int layer,
+                                         int pos, float *x, int avx2, void *stream) {
+    if (!L) return fail(nullptr, KORE_LAYER_E_INVALID, "layer handle is NULL");
+    if (!w || !attn || !x || ((uintptr_t)x & 15)) return fail(L, KORE_LAYER_E_INVALID, "w, attn or x missing or x unaligned");
+    if (!w->attn_norm || !w->ffn_norm) return fail(L, KORE_LAYER_E_INVALID, "attn_norm and ffn_norm are required");
+    const int64_t E = L->E, FF = L->FF, kvd = L->kvd;
+    if (!shape_is(w->wq, E, E) || !shape_is(w->wk, kvd, E) || !shape_is(w->wv, kvd, E) || !shape_is(w->wo, E, E) ||
+        !shape_is(w->w_gate, FF, E) || !shape_is(w->w_up, FF, E) || !shape_is(w->w_down, E, FF))
+        return fail(L, KORE_LAYER_E_INVALID, "a weight tensor's shape does not match the layer geometry");
+    kore_attn_info ai{};
+    if (kore_attn_get_info(attn, &ai) != KORE_ATTN_OK || ai.n_head != L->n_head || ai.n_head_kv != L->n_head_kv ||
+        ai.head_dim != L->head_dim)
+        return fail(L, KORE_LAYER_E_INVALID, "the attention handle's geometry differs from the layer's");
+    void *s = stream ? stream : (void *)L->stream;
+    auto qmv_err = [&](kore_qmv_tensor_t t, const char *what) {
+        return fail(L, KORE_LAYER_E_STEP, std::string(what) + ": " + kore_qmv_last_error(t));
+    };
+
+    // 1. rmsnorm + quant + wq/wk/wv + biases (kore.cpp:1417-1423)
+    kore_qmv_mv_opts o1{};
+    o1.norm_w = w->attn_norm;
+    o1.norm_eps = L->eps;
+    o1.bias[0] = w->bq;
+    o1.bias[1] = w->bk;
+    o1.bias[2] = w->bv;
+    kore_qmv_tensor_t qkv[3] = {w->wq, w->wk, w->wv};
+    float *qkv_out[3] = {L->q, L->k, L->v};
+    if (kore_qmv_mv_group_ex_dev(3, qkv, x, &o1, qkv_out, avx2, s) != KORE_QMV_OK) return qmv_err(w->wq, "q/k/v");
+    // 2. RoPE + append + attention (kore.cpp:1424-1455)
+    if (kore_attn_decode_dev(attn, layer, pos, L->n_head, L->n_head_kv, L->head_dim, L->q, L->k, L->v, L->att, s) !=
+        KORE_ATTN_OK)
+        return fail(L, KORE_LAYER_E_STEP, std::string("attention: ") + kore_attn_last_error(attn));
+    // 3. quant + Wo, x += o (kore.cpp:1456-1458)
+    kore_qmv_mv_opts o3{};
+    o3.accumulate = 1;
+    if (kore_qmv_mv_group_ex_dev(1, &w->wo, L->att, &o3, &x, avx2, s) != KORE_QMV_OK) return qmv_err(w->wo, "wo");
+    // 4. rmsnorm + quant + gate/up (kore.cpp:1461-1464)
+    kore_qmv_mv_opts o4{};
+    o4.norm_w = w->ffn_norm;
+    o4.norm_eps = L->eps;
+    kore_qmv_tensor_t gu[2] = {w->w_gate, w->w_up};
+    float *gu_out[2] = {L->gate, L->up};
+    if (kore_qmv_mv_group_ex_dev(2, gu, x, &o4, gu_out, avx2, s) != KORE_QMV_OK) return qmv_err(w->w_gate, "gate/up");
+    // 5. SwiGLU + quant + down, x += o (kore.cpp:1465-1471)
+    kore_qmv_mv_opts o5{};
+    o5.up = L->up;
+    o5.accumulate = 1;
+    if (kore_qmv_mv_group_ex_dev(1, &w->w_down, L->gate, &o5, &x, avx2, s) != KORE_QMV_OK) return qmv_err(w->w_down, "down");
+    return KORE_LAYER_OK;
+}
+
+KORE_LAYER_API int kore_layer_sync(kore_layer_t L) {
+    if (!L) return fail(nullptr, KORE_LAYER_E_INVALID, "layer handle is NULL");
+    const hipError_t e = hipStreamSynchronize(L->stream);
+    return e == hipSuccess ? KORE_LAYER_OK : fail(L, KORE_LAYER_E_HIP, hipGetErrorString(e));
+}
+
+KORE_LAYER_API const char *kore_layer_last_error(kore_layer_t L) { return L ? L->error.c_str() : g_error.c_str(); }
+
+}  // extern "C"

@@ -248,17 +248,18 @@ KORE_QMV_API int kore_qmv_quantize(const float *x, int64_t n, void *xq) {
     return KORE_QMV_OK;
 }
 
-static MatDesc desc_of(kore_qmv_tensor *t, float *out) {
-    return MatDesc{t->w, t->wd, out, (int)t->rows, t->type, 0, 0};
+static MatDesc desc_of(kore_qmv_tensor *t, float *out, const float *bias = nullptr, int accumulate = 0) {
+    return MatDesc{t->w, t->wd, out, (int)t->rows, t->type, 0, 0, bias, accumulate};
 }
 
-// One grouped launch: xq given (fused = false) or x quantised in the kernel.
+// One grouped launch: xq given (fused = false) or x quantised in the kernel
+// (after the pre-op of opts, if any); opts also carries the store epilogue.
 static int launch_group(int n, kore_qmv_tensor *const *ts, const void *xq, const float *x, float *const *outs,
-                        int avx2, hipStream_t s, bool xq_image = false) {
+                        int avx2, hipStream_t s, bool xq_image = false, const kore_qmv_mv_opts *opts = nullptr) {
     GroupArgs a{};
     int64_t rows = 0;
     for (int k = 0; k < n; ++k) {
-        a.m[k] = desc_of(ts[k], outs[k]);
+        a.m[k] = desc_of(ts[k], outs[k], opts ? opts->bias[k] : nullptr, opts ? opts->accumulate : 0);
         rows += ts[k]->rows;
     }
     a.n_mat = n;
@@ -266,6 +267,11 @@ static int launch_group(int n, kore_qmv_tensor *const *ts, const void *xq, const
     a.xq = (const uint8_t *)xq;
     a.x = x;
     a.xq_image = xq_image ? 1 : 0;
+    if (opts && x) {
+        a.norm_w = opts->norm_w;
+        a.norm_eps = opts->norm_eps;
+        a.up = opts->up;
+    }
     const int r = n == 1 ? ts[0]->rows_per_wave : pick_rows_per_wave(rows, ts[0]->num_cu);
     hipError_t e = launch_matvec_group(avx2 != 0, a, r, max_workgroups(ts[0]->num_cu), s);
     if (e != hipSuccess) return hip_fail(ts[0], e, "matvec launch");
@@ -279,8 +285,8 @@ KORE_QMV_API int kore_qmv_matvec_dev(kore_qmv_tensor_t t, const void *xq, float 
     return launch_group(1, &t, xq, nullptr, &out, avx2, (hipStream_t)stream);
 }
 
-KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *ts, const float *x, float *const *outs,
-                                       int avx2, void *stream) {
+KORE_QMV_API int kore_qmv_mv_group_ex_dev(int n, const kore_qmv_tensor_t *ts, const float *x,
+                                          const kore_qmv_mv_opts *opts, float *const *outs, int avx2, void *stream) {
     if (n < 1 || n > kMaxGroup || !ts || !outs)
         return fail(nullptr, KORE_QMV_E_INVALID, "n must be 1..4 with tensors and outputs");
     for (int k = 0; k < n; ++k) {
@@ -291,6 +297,13 @@ KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *ts, const
     }
     kore_qmv_tensor *t0 = ts[0];
     if (int rc = check_dev_ptr(t0, x, 16, "x")) return rc;
+    PreOp pre{nullptr, 0.f, nullptr};
+    if (opts) {
+        if (opts->norm_w && opts->up) return fail(t0, KORE_QMV_E_INVALID, "rmsnorm and SwiGLU together");
+        if (opts->norm_w && check_dev_ptr(t0, opts->norm_w, 16, "norm_w")) return KORE_QMV_E_INVALID;
+        if (opts->up && check_dev_ptr(t0, opts->up, 16, "up")) return KORE_QMV_E_INVALID;
+        pre = PreOp{opts->norm_w, opts->norm_eps, opts->up};
+    }
     int64_t rows = 0;
     for (int k = 0; k < n; ++k) rows += ts[k]->rows;
     const int r = n == 1 ? t0->rows_per_wave : pick_rows_per_wave(rows, t0->num_cu);
@@ -298,10 +311,15 @@ KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *ts, const
     for (int k = 0; k < n; ++k) wgs += (ts[k]->rows + 4 * r - 1) / (4 * r);
     if (const int cap = max_workgroups(t0->num_cu)) wgs = std::min<int64_t>(wgs, cap);
     hipStream_t s = (hipStream_t)stream;
-    if (fuse_quantisation(t0->nblk, wgs)) return launch_group(n, ts, nullptr, x, outs, avx2, s);
-    hipError_t e = launch_quantize_q8k(x, t0->cols, t0->xq, true, s);
+    if (fuse_quantisation(t0->nblk, wgs)) return launch_group(n, ts, nullptr, x, outs, avx2, s, false, opts);
+    hipError_t e = launch_quantize_q8k(x, t0->cols, t0->xq, true, s, pre);
     if (e != hipSuccess) return hip_fail(t0, e, "quantize launch");
-    return launch_group(n, ts, t0->xq, nullptr, outs, avx2, s, true);
+    return launch_group(n, ts, t0->xq, nullptr, outs, avx2, s, true, opts);
+}
+
+KORE_QMV_API int kore_qmv_mv_group_dev(int n, const kore_qmv_tensor_t *ts, const float *x, float *const *outs,
+                                       int avx2, void *stream) {
+    return kore_qmv_mv_group_ex_dev(n, ts, x, nullptr, outs, avx2, stream);
 }
 
 KORE_QMV_API int kore_qmv_mv_dev(kore_qmv_tensor_t t, const float *x, float *out, int avx2, void *stream) {

@@ -43,6 +43,8 @@ struct MatDesc {
     int type;                // kQ4K or kQ6K
     int wg_begin;            // first workgroup of this matrix   (set by the launcher)
     int wg_count;            // its number of workgroups          (set by the launcher)
+    const float *bias;       // out = dot + bias[r] (kore's q/k/v biases), or nullptr
+    int accumulate;          // out = out + dot (kore's residual adds)
 };
 
 struct GroupArgs {
@@ -53,6 +55,17 @@ struct GroupArgs {
     const float *x;          // nblk*256 floats (16-byte aligned) that every workgroup
                              // quantises into LDS itself (then xq is unused)
     int xq_image;            // xq holds launch_quantize_q8k(..., image = true)'s layout
+    // applied to x before the in-kernel quantisation (not with xq):
+    const float *norm_w;     // kore's rmsnorm with these weights (kore.cpp:1367-1372), or nullptr
+    float norm_eps;
+    const float *up;         // kore's SwiGLU, x = gate (kore.cpp:1465-1468), or nullptr
+};
+
+// What a quantiser does to its input first (at most one of the two).
+struct PreOp {
+    const float *norm_w;     // rmsnorm: x[i] * scale * norm_w[i]
+    float norm_eps;
+    const float *up;         // SwiGLU: x[i] / (1 + exp(-x[i])) * up[i]
 };
 
 // out[r] = row r . xq for every matrix of the group, with kore's summation:
@@ -66,7 +79,8 @@ hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int ma
 // kore's quantize_row_q8_K (kore.cpp:422-446): x[n] -> n/256 BlockQ8K records,
 // or (image) the same values in the matvec's own layout (n/256 * 308 bytes,
 // n/256 <= kMaxBlocks) for a following launch_matvec_group with xq_image.
-hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool image, hipStream_t s);
+hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool image, hipStream_t s,
+                               PreOp pre = PreOp{nullptr, 0.f, nullptr});
 
 // Q6_K upload: raw GGUF blocks (rows*nblk x 210 bytes, any alignment of 2)
 // -> body / d arrays above.

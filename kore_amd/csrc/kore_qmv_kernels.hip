@@ -60,9 +60,87 @@ struct Q8Lane {
     float d;
 };
 
+// ------------------------------------------------------------------ pre-ops
+
+// kore's rmsnorm scale from the sum of squares ss (kore.cpp:1370):
+// 1.0f / std::sqrt((float)(ss / n) + eps).  sqrt and the reciprocal are taken
+// in double and rounded once to float, which is the correctly rounded float
+// result (53 >= 2 * 24 + 2 bits) whatever the compiler does with float sqrt
+// and division.
+__device__ __forceinline__ float kore_rms_scale(double ss, int n, float eps) {
+    const float a = (float)(ss / (double)n) + eps;
+    const float r = (float)sqrt((double)a);
+    return (float)(1.0 / (double)r);
+}
+
+__device__ __forceinline__ void two_sum(double a, double b, double &s, double &e) {
+    s = a + b;
+    const double bb = s - a;
+    e = (a - (s - bb)) + (b - bb);
+}
+
+// kore's rmsnorm scale of x[0..n) for a whole workgroup (every thread gets it).
+// kore sums (double)x[i] * x[i] in index order in double (kore.cpp:1368-1369);
+// here a double-double sum in parallel gives the exact sum S to ~2^-100, and
+// every order's double sum of n nonnegative terms lies within gamma(n-1) * S of
+// it.  When the float scale is the same at both ends of that interval it is
+// kore's (the scale is monotone in ss); otherwise one thread runs kore's loop.
+// red: 2 * kThreads doubles of LDS.
+__device__ float block_rms_scale(const float *x, int n, float eps, double *red) {
+    const int t = threadIdx.x;
+    double hi = 0.0, lo = 0.0;
+    for (int i = t; i < n; i += kThreads) {
+        double s, e;
+        two_sum(hi, (double)x[i] * (double)x[i], s, e);
+        hi = s;
+        lo += e;
+    }
+    red[t] = hi;
+    red[kThreads + t] = lo;
+    __syncthreads();
+    for (int off = kThreads / 2; off > 0; off >>= 1) {
+        if (t < off) {
+            double s, e;
+            two_sum(red[t], red[t + off], s, e);
+            red[t] = s;
+            red[kThreads + t] = (red[kThreads + t] + red[kThreads + t + off]) + e;
+        }
+        __syncthreads();
+    }
+    const double S = red[0] + red[kThreads];
+    const double g = (double)(n - 1) * 0x1p-53 / (1.0 - (double)(n - 1) * 0x1p-53);
+    const double m = 2.0 * g + 0x1p-50;   // + the double-double and final roundings
+    const float lo_s = kore_rms_scale(S * (1.0 - m), n, eps), hi_s = kore_rms_scale(S * (1.0 + m), n, eps);
+    __syncthreads();                       // red is reused below
+    if (__float_as_uint(lo_s) == __float_as_uint(hi_s)) return lo_s;
+    if (t == 0) {                          // kore's own loop
+        double ss = 0.0;
+        for (int i = 0; i < n; ++i) ss += (double)x[i] * x[i];
+        red[0] = ss;
+    }
+    __syncthreads();
+    const float sc = kore_rms_scale(red[0], n, eps);
+    __syncthreads();
+    return sc;
+}
+
+// kore's SwiGLU of one value (kore.cpp:1466-1467): g / (1.0f + std::exp(-g)) * u.
+// exp is taken in double and rounded to float (glibc's expf agrees with that
+// correctly rounded value except in rare hard cases); the division is rounded
+// once from double like kore's float division.
+__device__ __forceinline__ float kore_swiglu(float g, float u) {
+    const float ex = (float)exp(-(double)g);
+    const float den = 1.0f + ex;
+    const float q = (float)((double)g / (double)den);
+    return q * u;
+}
+
 // kore's quantisation of one 256-value block (kore.cpp:422-446) by the 16
-// lanes of a DPP row: lane m owns values 16m .. 16m+15 (x 16-byte aligned).
-__device__ __forceinline__ Q8Lane quantize_lane(const float *xb, int m) {
+// lanes of a DPP row: lane m owns values 16m .. 16m+15 (x 16-byte aligned),
+// after the pre-op (rmsnorm with `scale`, or SwiGLU) of the values at xb[i] =
+// x[base + i].
+__device__ __forceinline__ Q8Lane quantize_lane(const float *xb, int m, const PreOp &pre = PreOp{nullptr, 0.f, nullptr},
+                                                float scale = 1.f, int64_t base = 0) {
     float v[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -71,6 +149,25 @@ __device__ __forceinline__ Q8Lane quantize_lane(const float *xb, int m) {
         v[4 * k + 1] = f.y;
         v[4 * k + 2] = f.z;
         v[4 * k + 3] = f.w;
+    }
+    if (pre.norm_w) {                      // kore.cpp:1371: x[i] * scale * w[i]
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 w = *(const float4 *)(pre.norm_w + base + 16 * m + 4 * k);
+            v[4 * k] = (v[4 * k] * scale) * w.x;
+            v[4 * k + 1] = (v[4 * k + 1] * scale) * w.y;
+            v[4 * k + 2] = (v[4 * k + 2] * scale) * w.z;
+            v[4 * k + 3] = (v[4 * k + 3] * scale) * w.w;
+        }
+    } else if (pre.up) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 u = *(const float4 *)(pre.up + base + 16 * m + 4 * k);
+            v[4 * k] = kore_swiglu(v[4 * k], u.x);
+            v[4 * k + 1] = kore_swiglu(v[4 * k + 1], u.y);
+            v[4 * k + 2] = kore_swiglu(v[4 * k + 2], u.z);
+            v[4 * k + 3] = kore_swiglu(v[4 * k + 3], u.w);
+        }
     }
     // kore keeps the first value of largest magnitude, starting from amax = 0
     // with a strict comparison (kore.cpp:424-428): the largest |x| wins, ties
@@ -145,11 +242,15 @@ __device__ __forceinline__ void xs_store(uint8_t *xs, int nblk, int i, int m, co
 // or (IMAGE) in the matvec's LDS layout, which workgroups then copy verbatim.
 template <bool IMAGE>
 __global__ __launch_bounds__(kThreads) void quantize_q8k_kernel(const float *__restrict__ x,
-                                                                uint8_t *__restrict__ xq, int64_t nblocks) {
+                                                                uint8_t *__restrict__ xq, int64_t nblocks,
+                                                                PreOp pre) {
+    __shared__ double red[2 * kThreads];
+    // rmsnorm needs the whole vector's scale: every workgroup computes it
+    const float scale = pre.norm_w ? block_rms_scale(x, (int)(nblocks * 256), pre.norm_eps, red) : 1.f;
     const int64_t blk = (int64_t)blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
     if (blk >= nblocks) return;
     const int m = threadIdx.x & 15;
-    const Q8Lane q = quantize_lane(x + blk * 256, m);
+    const Q8Lane q = quantize_lane(x + blk * 256, m, pre, scale, blk * 256);
     if constexpr (IMAGE) {
         xs_store(xq, (int)nblocks, (int)blk, m, q);
         return;
@@ -367,8 +468,11 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
 
     // the activations
     if constexpr (FUSED) {
+        const PreOp pre{a.norm_w, a.norm_eps, a.up};
+        // rmsnorm's scale: the records area is free until the blocks start
+        const float scale = a.norm_w ? block_rms_scale(a.x, nblk * 256, a.norm_eps, (double *)smem) : 1.f;
         for (int b = t >> 4; b < nblk; b += kThreads / 16)
-            xs_store(xs, nblk, b, t & 15, quantize_lane(a.x + (int64_t)b * 256, t & 15));
+            xs_store(xs, nblk, b, t & 15, quantize_lane(a.x + (int64_t)b * 256, t & 15, pre, scale, (int64_t)b * 256));
     } else if (a.xq_image) {
         // already in the LDS layout (xs_bytes(nblk) is a multiple of 4 bytes)
         const int n16 = (int)(xs_bytes(nblk) >> 4);
@@ -478,7 +582,11 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
                             res = acc0;
                         }
                         const int orow = (ct * 4 + wave) * RW + rho;
-                        if (j == 0 && orow < rows) md.out[orow] = res;
+                        if (j == 0 && orow < rows) {
+                            // kore's q += bq (kore.cpp:1422-1423), x += o (kore.cpp:1458, 1471)
+                            const float v = md.bias ? res + md.bias[orow] : res;
+                            md.out[orow] = md.accumulate ? md.out[orow] + v : v;
+                        }
                         acc0 = acc1 = accm = 0.f;
                     }
                     cs = 0;
@@ -578,6 +686,8 @@ hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int ma
     const int rows_per_tile = 4 * rw;
     const bool fused = a.x != nullptr;
     if (!fused && !a.xq) return hipErrorInvalidValue;
+    if ((a.norm_w || a.up) && !fused) return hipErrorInvalidValue;   // pre-ops act on x
+    if (a.norm_w && a.up) return hipErrorInvalidValue;
     // workgroups per matrix: in proportion to its weight bytes, at least one,
     // at most one per row tile, about max_wgs in all
     int64_t tiles[kMaxGroup], bytes[kMaxGroup], all_tiles = 0, all_bytes = 0;
@@ -607,13 +717,15 @@ hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int ma
     return fused ? launch_group_f<false, true>(a, rw, grid, s) : launch_group_f<false, false>(a, rw, grid, s);
 }
 
-hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool image, hipStream_t s) {
+hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool image, hipStream_t s, PreOp pre) {
     const int64_t nb = n / 256;
     if (nb <= 0) return hipSuccess;
     if (image && nb > kMaxBlocks) return hipErrorInvalidValue;
+    if (pre.norm_w && pre.up) return hipErrorInvalidValue;
+    if (pre.norm_w && n > INT32_MAX) return hipErrorInvalidValue;
     const int64_t grid = (nb + kThreads / 16 - 1) / (kThreads / 16);
-    if (image) hipLaunchKernelGGL(quantize_q8k_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb);
-    else hipLaunchKernelGGL(quantize_q8k_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb);
+    if (image) hipLaunchKernelGGL(quantize_q8k_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb, pre);
+    else hipLaunchKernelGGL(quantize_q8k_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb, pre);
     return hipGetLastError();
 }
 

@@ -53,6 +53,7 @@ SYMBOLS = [
     ("kore_qmv_matmul_batch", _i, [_vp, _vp, _i, _vp]),
     ("kore_qmv_matmul_batch_dev", _i, [_vp, _vp, _i, _vp, _vp]),
     ("kore_qmv_matmul_batch_group_dev", _i, [_i, _vp, _vp, _i, _vp, _vp]),
+    ("kore_qmv_mv_group_ex_dev", _i, [_i, _vp, _vp, _vp, _vp, _i, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
     ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),
@@ -196,3 +197,24 @@ def matmul_batch_group_dev(mats, x_ptr: int, nb: int, out_ptrs, stream=None) -> 
     hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
     outs = (C.c_void_p * n)(*out_ptrs)
     _check(lib().kore_qmv_matmul_batch_group_dev(n, hs, x_ptr, nb, outs, stream))
+
+
+class MvOpts(C.Structure):
+    """kore_qmv_mv_opts: the steps fused around a matvec launch."""
+    _fields_ = [("norm_w", C.c_void_p), ("norm_eps", C.c_float), ("up", C.c_void_p), ("bias", C.c_void_p * 4),
+                ("accumulate", C.c_int)]
+
+
+def mv_group_ex_dev(mats, x_ptr: int, out_ptrs, norm_w: int = None, norm_eps: float = 0.0, up: int = None,
+                    bias=None, accumulate: bool = False, avx2: bool = True, stream=None) -> None:
+    """kore_qmv_mv_group_ex_dev: rmsnorm (norm_w) or SwiGLU (up) on x before
+    the quantisation, bias per matrix and/or out += in the store (device
+    pointers)."""
+    n = len(mats)
+    o = MvOpts()
+    o.norm_w, o.norm_eps, o.up, o.accumulate = norm_w, norm_eps, up, int(accumulate)
+    for k, b in enumerate(bias or ()):
+        o.bias[k] = b
+    hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
+    outs = (C.c_void_p * n)(*out_ptrs)
+    _check(lib().kore_qmv_mv_group_ex_dev(n, hs, x_ptr, C.byref(o), outs, int(avx2), stream))
