@@ -485,6 +485,103 @@ def gpu_gemm(qt, chunks: int, warmup: int):
                 op_ms=op_ms.reshape(n_ev, len(ops)), first_raw=first_raw, first_x=xb, first_out=got)
 
 
+def gpu_token(qt, tokens: int, warmup: int):
+    """Whole 7B decode tokens as kore's forward() runs them (kore.cpp:1397-1484):
+    28 layers through kore_layer_decode_dev (rmsnorm+quant+q/k/v+bias, RoPE +
+    append + attention, Wo + residual, rmsnorm+quant+gate/up, SwiGLU+quant+down
+    + residual) and the logits (rmsnorm+quant+output head), at positions
+    4096.. over a cache filled to 4096, driven from C++."""
+    from kore_amd import KoreAttn, hip
+    from kore_amd.layer import Layer, LayerWeights, _Weights
+    from kore_amd.layer import lib as layer_lib
+    layer_lib()
+    path = os.path.join(ROOT, "kore_amd", "libkore_layer_bench.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run `make -C kore_amd/csrc`")
+    B = C.CDLL(path)
+    vp = C.c_void_p
+    B.klb_tokens.argtypes = [vp, C.POINTER(_Weights), C.c_int, vp, vp, vp, C.c_float, vp, C.c_int, C.c_int, C.c_int,
+                             vp, vp, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_double)]
+    mats, tensors, _ = qt
+    rng = np.random.default_rng(QMV_SEED + 2)
+    attn = KoreAttn(NL, DEC_CTX, NH, NKV, HD, ROPE_BASE)
+    print("[bench] token: filling the 28-layer cache to 4096", file=sys.stderr, flush=True)
+    _fill_cache(attn, NL, DEC_POS0, KVD, 11, None)
+    lws, bufs = [], []
+    for l in range(NL):
+        lw = LayerWeights()
+        lw.mats = tensors[7 * l:7 * l + 7]
+        for name, n, scale in (("attn_norm", E, 0.1), ("ffn_norm", E, 0.1), ("bq", E, 0.5), ("bk", KVD, 0.5),
+                               ("bv", KVD, 0.5)):
+            a = (rng.standard_normal(n) * scale + (1.0 if "norm" in name else 0.0)).astype(np.float32)
+            lw.bufs[name] = hip.DeviceBuffer.from_array(a)
+            bufs.append(lw.bufs[name])
+        lws.append(lw)
+    warr = (_Weights * NL)(*[lw.struct() for lw in lws])
+    out_norm = hip.DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(E)).astype(np.float32))
+    emb = hip.DeviceBuffer.from_array(np.stack([_act(rng, E) for _ in range(tokens)]))
+    x, logits = hip.DeviceBuffer(E), hip.DeviceBuffer(QMV_VOCAB)
+    L = Layer(E, QMV_FF, NH, NKV, 1e-6)
+    region, wall = C.c_float(0), C.c_double(0)
+
+    def run(reps, reg=None):
+        rc = B.klb_tokens(L._h, warr, NL, attn.handle, tensors[7 * NL].handle, out_norm.ptr, 1e-6, emb.ptr, E,
+                          tokens, DEC_POS0, x.ptr, logits.ptr, 1, reps, reg, C.byref(wall))
+        if rc != 0:
+            raise RuntimeError(f"klb_tokens failed ({rc}): {layer_lib().kore_layer_last_error(L._h).decode()}")
+
+    if warmup:
+        run(warmup)
+    print(f"[bench] token: {tokens} timed 7B tokens at positions {DEC_POS0}..", file=sys.stderr, flush=True)
+    run(1, C.byref(region))
+    res = dict(region_ms=region.value, wall_ms=wall.value, tokens=tokens)
+    L.close()
+    for b in bufs + [out_norm, emb, x, logits]:
+        b.free()
+    attn.close()
+    return res
+
+
+def token_report(t, mats):
+    wbytes = sum(qmv_weight_bytes(tp, r, c) for _, tp, r, c in mats)
+    kv = sum(2 * (DEC_POS0 + i + 1) * KVD * 4 * NL for i in range(t["tokens"])) / t["tokens"]
+    s_tok = t["region_ms"] / 1e3 / t["tokens"]
+    return {
+        "workload": "Qwen2.5-7B-shape decode tokens as kore's forward() with logits runs them: embedding row in, "
+                    "28 layers (rmsnorm + Q8_K + q/k/v + bias in one launch, RoPE + append + attention, Wo + "
+                    "residual, rmsnorm + Q8_K + gate/up, SwiGLU + Q8_K + down + residual) and the output head "
+                    "(rmsnorm + Q8_K + 152064-row Q6_K matvec); 4.37 GB of synthetic Q4_K/Q6_K weights, fp32 KV "
+                    f"cache filled to {DEC_POS0}, {t['tokens']} tokens at positions {DEC_POS0}.., kore's AVX2 "
+                    "matvec order",
+        "ms_per_token_gpu": round(s_tok * 1e3, 4),
+        "ms_per_token_wall": round(t["wall_ms"] / t["tokens"], 4),
+        "tokens_per_s": round(1.0 / s_tok, 1),
+        "weight_bytes_per_token": wbytes,
+        "kv_bytes_per_token": int(kv),
+        "gbs": round((wbytes + kv) / s_tok / 1e9, 1),
+        "frac_of_hbm_peak": round((wbytes + kv) / s_tok / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+
+def cpu_token(seconds: float, threads: int):
+    """kore's own forward() with logits (oracle/_ref/kore_layer_ref --time, built
+    from kore.cpp) on a synthetic 7B engine at position 4096."""
+    import subprocess
+
+    import oracle
+    if not os.path.exists(oracle.REF_LAYER_BIN):
+        return None
+    r = subprocess.run([oracle.REF_LAYER_BIN, "--time", str(threads), str(seconds), str(DEC_POS0)],
+                       capture_output=True, text=True, check=True)
+    j = json.loads(r.stdout)
+    return {"value": round(j["tokens"] / j["seconds"], 3), "unit": "tokens/s", "cores": j["threads"],
+            "kind": "reference",
+            "sample": f"kore's own forward() with logits (kore.cpp:1397-1484, AVX2 matvecs: {bool(j['avx2'])}, "
+                      f"attention on one thread as in kore) built from kore.cpp with kore's flags, {j['threads']} "
+                      f"threads, on a synthetic Qwen2.5-7B-shape engine at positions {j['pos']}..: {j['tokens']} "
+                      f"tokens in {j['seconds']:.1f} s; host {_cpu_model()}"}
+
+
 def gemm_report(g, chunks: int):
     mats, op_mats = g["mats"], g["op_mats"]
     flops = sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] for ts in op_mats for ti in ts)
@@ -793,6 +890,9 @@ def main(argv=None):
     ap.add_argument("--gemm-only", action="store_true", help="run only the batched matmul leg (for profiling)")
     ap.add_argument("--gemm-chunks", type=int, default=5, help="timed 64-token chunks of the batched matmul leg")
     ap.add_argument("--gemm-warmup", type=int, default=1)
+    ap.add_argument("--no-token", action="store_true", help="skip the whole-token decode leg")
+    ap.add_argument("--token-only", action="store_true", help="run only the whole-token decode leg")
+    ap.add_argument("--token-count", type=int, default=32, help="timed 7B decode tokens of the whole-token leg")
     ap.add_argument("--cpu-threads", type=int, default=16,
                     help="threads of kore's own matvec in the CPU baseline (the GPU box's CPU share)")
     ap.add_argument("--cpu-prefill-layers", type=int, default=2)
@@ -828,9 +928,11 @@ def main(argv=None):
     clk = C.c_int(0)
     hip.lib().hipDeviceGetAttribute(C.byref(clk), 5, 0)   # hipDeviceAttributeClockRate (kHz)
 
-    if args.matvec_only or args.gemm_only:
+    if args.matvec_only or args.gemm_only or args.token_only:
         qt = qmv_tensors()
-        if args.matvec_only:
+        if args.token_only:
+            out = {"token": token_report(gpu_token(qt, args.token_count, 1), qt[0])}
+        elif args.matvec_only:
             out = {"matvec": matvec_report(gpu_matvec(qt, args.matvec_tokens, args.matvec_warmup),
                                            args.matvec_tokens)}
         else:
@@ -847,6 +949,7 @@ def main(argv=None):
     qt = None if (args.no_matvec and args.no_gemm) else qmv_tensors()
     mv = None if args.no_matvec else gpu_matvec(qt, args.matvec_tokens, args.matvec_warmup)
     gm = None if args.no_gemm else gpu_gemm(qt, args.gemm_chunks, args.gemm_warmup)
+    tk = None if (args.no_token or qt is None) else gpu_token(qt, args.token_count, 1)
     if qt is not None:
         for m in qt[1]:
             m.close()
@@ -921,6 +1024,8 @@ def main(argv=None):
         res["matvec"] = matvec_report(mv, args.matvec_tokens)
     if gm is not None:
         res["gemm"] = gemm_report(gm, args.gemm_chunks)
+    if tk is not None:
+        res["token"] = token_report(tk, qt[0])
     if not args.no_cpu:
         print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
               flush=True)
@@ -956,6 +1061,9 @@ def main(argv=None):
             bound = 1e-4 * float(np.max(np.abs(ref))) + 1e-6
             res["parity"]["gemm_first_matrix_max_abs_err"] = err
             res["parity"]["gemm_first_matrix_within_kore_tolerance"] = bool(err <= bound)
+        if tk is not None:
+            print(f"[bench] cpu baseline: kore's forward(), {args.cpu_threads} threads", file=sys.stderr, flush=True)
+            res["token"]["cpu_baseline"] = cpu_token(args.cpu_seconds, args.cpu_threads)
         if pf is not None:
             print(f"[bench] cpu baseline: prefill sample ({args.cpu_prefill_layers} layers)", file=sys.stderr,
                   flush=True)

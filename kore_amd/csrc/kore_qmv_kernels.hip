@@ -85,9 +85,9 @@ __device__ __forceinline__ void two_sum(double a, double b, double &s, double &e
 // every order's double sum of n nonnegative terms lies within gamma(n-1) * S of
 // it.  When the float scale is the same at both ends of that interval it is
 // kore's (the scale is monotone in ss); otherwise one thread runs kore's loop.
-// red: 2 * kThreads doubles of LDS.
+// red: 2 * kThreads / 64 doubles of LDS (at least one).
 __device__ float block_rms_scale(const float *x, int n, float eps, double *red) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     double hi = 0.0, lo = 0.0;
     for (int i = t; i < n; i += kThreads) {
         double s, e;
@@ -95,23 +95,34 @@ __device__ float block_rms_scale(const float *x, int n, float eps, double *red) 
         hi = s;
         lo += e;
     }
-    red[t] = hi;
-    red[kThreads + t] = lo;
-    __syncthreads();
-    for (int off = kThreads / 2; off > 0; off >>= 1) {
-        if (t < off) {
-            double s, e;
-            two_sum(red[t], red[t + off], s, e);
-            red[t] = s;
-            red[kThreads + t] = (red[kThreads + t] + red[kThreads + t + off]) + e;
-        }
-        __syncthreads();
+    // wave, then the four waves in order: one barrier
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const double ohi = __shfl_xor(hi, off), olo = __shfl_xor(lo, off);
+        double s, e;
+        two_sum(hi, ohi, s, e);
+        hi = s;
+        lo = (lo + olo) + e;
     }
-    const double S = red[0] + red[kThreads];
+    if (lane == 0) {
+        red[2 * wave] = hi;
+        red[2 * wave + 1] = lo;
+    }
+    __syncthreads();
+    hi = red[0];
+    lo = red[1];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) {
+        double s, e;
+        two_sum(hi, red[2 * w], s, e);
+        hi = s;
+        lo = (lo + red[2 * w + 1]) + e;
+    }
+    const double S = hi + lo;
     const double g = (double)(n - 1) * 0x1p-53 / (1.0 - (double)(n - 1) * 0x1p-53);
     const double m = 2.0 * g + 0x1p-50;   // + the double-double and final roundings
     const float lo_s = kore_rms_scale(S * (1.0 - m), n, eps), hi_s = kore_rms_scale(S * (1.0 + m), n, eps);
-    __syncthreads();                       // red is reused below
+    __syncthreads();                       // red is reused below and by the caller
     if (__float_as_uint(lo_s) == __float_as_uint(hi_s)) return lo_s;
     if (t == 0) {                          // kore's own loop
         double ss = 0.0;

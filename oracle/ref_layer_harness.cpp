@@ -20,11 +20,23 @@
 // Result: float32 x[n_steps][E] (the residual after the last layer, kore's
 //   e.x: forward() is called without logits), then the K and V caches
 //   ([n_layer][ctx][kvd] each).
+//
+// Timing mode (the CPU baseline of the benchmark's whole-token leg):
+//   kore_layer_ref --time THREADS MIN_SECONDS POS
+// builds a Qwen2.5-7B-shape engine (28 layers, 3584 / 18944, 28 / 4 heads of
+// 128, 152064-row Q6_K output head; Q4_K weights with attn_v and ffn_down in
+// Q6_K on the layers Q4_K_M files keep them there) from synthetic block bytes,
+// then runs kore's forward() with logits for tokens at positions POS, POS + 1,
+// ... with THREADS threads until MIN_SECONDS have passed; prints one JSON line
+// {"tokens", "seconds", "threads", "avx2", "pos"}.
 #define main kore_ref_main
 #include "kore.cpp"
 #undef main
 
+#include <chrono>
 #include <cstdio>
+#include <cstdlib>
+#include <string>
 #include <vector>
 
 namespace {
@@ -49,10 +61,105 @@ bool read_tensor(FILE *f, OwnedTensor &o, uint32_t type, uint64_t cols, uint64_t
     return rd(f, o.bytes.data(), o.bytes.size());
 }
 
+uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// Hashed block bytes with f16 scales of a trained model's size (subnormal f16:
+// Q4_K d 2.0e-5, dmin 5.0e-6; Q6_K d 4.0e-6).
+void synth(OwnedTensor &o, uint32_t type, uint64_t cols, uint64_t rows, uint64_t seed) {
+    const uint64_t bb = type == GGML_Q4_K ? 144 : 210;
+    o.bytes.resize(cols / 256 * bb * rows);
+    for (size_t i = 0; i < o.bytes.size(); i += 8) {
+        const uint64_t r = mix64(seed * 0x100000001b3ull + i);
+        memcpy(o.bytes.data() + i, &r, std::min<size_t>(8, o.bytes.size() - i));
+    }
+    for (size_t b = 0; b < o.bytes.size(); b += bb) {
+        uint8_t *p = o.bytes.data() + b;
+        if (type == GGML_Q4_K) { p[0] = 0x4F; p[1] = 0x01; p[2] = 0x54; p[3] = 0x00; }
+        else { p[208] = 0x43; p[209] = 0x00; }
+    }
+    o.t.type = type;
+    o.t.n_dims = 2;
+    o.t.dims[0] = cols;
+    o.t.dims[1] = rows;
+    o.t.nbytes = o.bytes.size();
+    o.t.data = o.bytes.data();
+}
+
+int time_mode(unsigned nth, double min_s, int pos0) {
+    const int NL = 28, E = 3584, FF = 18944, NH = 28, NKV = 4, HD = 128, VOCAB = 152064;
+    const int kvd = NKV * HD, ctx = pos0 + 256;
+    Engine e;
+    e.hp.n_layer = NL; e.hp.n_embd = E; e.hp.n_ff = FF; e.hp.n_head = NH; e.hp.n_head_kv = NKV;
+    e.hp.n_ctx = (uint32_t)ctx; e.hp.n_vocab = VOCAB; e.hp.rope_base = 1e6f; e.hp.rms_eps = 1e-6f;
+    e.head_dim = HD; e.kv_dim = kvd; e.n_rep = NH / NKV; e.ctx = ctx; e.n_vocab = VOCAB;
+    e.nth = nth; e.use_float = false;
+    e.avx2 = KORE_HAVE_AVX2 && cpu_has_avx2();
+    std::vector<OwnedTensor> mats((size_t)NL * 7);
+    std::vector<float> ones((size_t)E, 1.0f), zeros((size_t)E, 0.0f);
+    for (int l = 0; l < NL; l++) {
+        const bool more = l < NL / 8 || l >= 7 * NL / 8 || (l - NL / 8) % 3 == 2;
+        const uint32_t hi = more ? GGML_Q6_K : GGML_Q4_K;
+        const uint32_t types[7] = {GGML_Q4_K, GGML_Q4_K, hi, GGML_Q4_K, GGML_Q4_K, GGML_Q4_K, hi};
+        const uint64_t rows[7] = {(uint64_t)E, (uint64_t)kvd, (uint64_t)kvd, (uint64_t)E, (uint64_t)FF, (uint64_t)FF,
+                                  (uint64_t)E};
+        const uint64_t cols[7] = {(uint64_t)E, (uint64_t)E, (uint64_t)E, (uint64_t)E, (uint64_t)E, (uint64_t)E,
+                                  (uint64_t)FF};
+        OwnedTensor *m = &mats[(size_t)l * 7];
+        for (int j = 0; j < 7; j++) synth(m[j], types[j], cols[j], rows[j], (uint64_t)l * 7 + j + 1);
+        Layer L;
+        L.wq = &m[0].t; L.wk = &m[1].t; L.wv = &m[2].t; L.wo = &m[3].t;
+        L.w_gate = &m[4].t; L.w_up = &m[5].t; L.w_down = &m[6].t;
+        L.attn_norm = ones.data(); L.ffn_norm = ones.data();
+        L.bq = zeros.data(); L.bk = zeros.data(); L.bv = zeros.data();
+        e.layers.push_back(L);
+    }
+    OwnedTensor head, tok;
+    synth(head, GGML_Q6_K, (uint64_t)E, (uint64_t)VOCAB, 999);
+    tok.bytes.assign((size_t)E * 4, 0);
+    for (int i = 0; i < E; i++) { const float v = (float)((int)(mix64(7 + i) % 2001) - 1000) * 1e-3f; memcpy(&tok.bytes[(size_t)i * 4], &v, 4); }
+    tok.t.type = GGML_F32; tok.t.n_dims = 2; tok.t.dims[0] = (uint64_t)E; tok.t.dims[1] = 1;
+    tok.t.nbytes = tok.bytes.size(); tok.t.data = tok.bytes.data();
+    e.tok_embd = &tok.t;
+    e.out_w = &head.t;
+    e.out_norm = ones.data();
+    const int half = HD / 2;
+    e.inv_freq.resize((size_t)half);
+    for (int i = 0; i < half; i++) e.inv_freq[(size_t)i] = (float)std::pow((double)e.hp.rope_base, -2.0 * i / HD);
+    e.rope_c.resize((size_t)half); e.rope_s.resize((size_t)half);
+    e.kcache.assign((size_t)NL * ctx * kvd, 0.0f);
+    e.vcache.assign((size_t)NL * ctx * kvd, 0.0f);
+    e.emb.resize((size_t)E); e.x.resize((size_t)E); e.xb.resize((size_t)E); e.q.resize((size_t)E);
+    e.att.resize((size_t)E); e.o.resize((size_t)E);
+    e.k.resize((size_t)kvd); e.v.resize((size_t)kvd);
+    e.gate.resize((size_t)FF); e.up.resize((size_t)FF);
+    e.scores.resize((size_t)ctx); e.logits.resize((size_t)VOCAB);
+    e.xq_e.resize((size_t)(E / 256 + 1)); e.xq_f.resize((size_t)FF / 256);
+    e.scratch.resize((size_t)E);
+    if (!forward(e, 0, pos0, true)) return 5;                  // warm-up
+    int tokens = 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    double el = 0;
+    do {
+        if (!forward(e, 0, pos0 + 1 + tokens % 200, true)) return 5;
+        ++tokens;
+        el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    } while (el < min_s);
+    printf("{\"tokens\": %d, \"seconds\": %.6f, \"threads\": %u, \"avx2\": %d, \"pos\": %d, \"checksum\": %.9g}\n",
+           tokens, el, nth, (int)e.avx2, pos0, (double)e.logits[(size_t)VOCAB / 2]);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
-    if (argc != 3) { fprintf(stderr, "usage: kore_layer_ref job.bin result.bin\n"); return 2; }
+    if (argc == 5 && std::string(argv[1]) == "--time")
+        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]));
+    if (argc != 3) { fprintf(stderr, "usage: kore_layer_ref job.bin result.bin | --time THREADS SECONDS POS\n"); return 2; }
     FILE *in = fopen(argv[1], "rb");
     FILE *out = fopen(argv[2], "wb");
     if (!in || !out) { perror("open"); return 2; }

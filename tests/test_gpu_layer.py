@@ -154,8 +154,10 @@ def test_layers_against_kore_forward(tag, avx2):
         with KoreAttn(man["n_layer"], man["ctx"], man["n_head"], man["n_head_kv"], man["head_dim"],
                       man["rope_base"]) as attn, Layer(E, FF, man["n_head"], man["n_head_kv"], man["rms_eps"]) as L:
             dx = hip.DeviceBuffer(E)
+            emb = np.ascontiguousarray(z["emb"], np.float32)   # held: hipMemcpy reads it after the call starts
             for st in range(man["steps"]):
-                hip.check(hip.lib().hipMemcpy(dx.ptr, z["emb"][st].ctypes.data, E * 4, hip.H2D), "H2D")
+                row = np.ascontiguousarray(emb[st])
+                hip.check(hip.lib().hipMemcpy(dx.ptr, row.ctypes.data, E * 4, hip.H2D), "H2D")
                 for l in range(man["n_layer"]):
                     L.decode_dev(ws[l], attn, l, st, dx.ptr, avx2=avx2)
                 L.sync()
