@@ -127,6 +127,13 @@ class QMat:
                 raise ValueError(f"expected {rows * (cols // 256) * bb} weight bytes, got {w.size}")
             _check(lib().kore_qmv_tensor_create(C.byref(self.handle), wtype, rows, cols, w.ctypes.data, 0))
 
+    @classmethod
+    def adopt(cls, handle: C.c_void_p, wtype: int, rows: int, cols: int) -> "QMat":
+        """Wrap a tensor another library created (kore_gguf_to_qmv); it is destroyed on close."""
+        m = cls.__new__(cls)
+        m.handle, m.type, m.rows, m.cols = handle, wtype, int(rows), int(cols)
+        return m
+
     def close(self):
         if self.handle:
             lib().kore_qmv_tensor_destroy(self.handle)

@@ -28,6 +28,13 @@
 // JSON line {"reps", "seconds", "rows", "cols", "weight_bytes", "avx2",
 // "threads", "copies"}.
 //
+//   kore_qmv_ref --gguf file.gguf
+// runs kore's load_model (kore.cpp:188-285) on the file and prints one JSON
+// line: {"ok", "hp": {...}, "data_start", "tensors": [{"name", "type",
+// "n_dims", "dims", "nbytes", "has_data", "fnv"}...]} with the tensors sorted
+// by name and fnv the 64-bit FNV-1a hash of the nbytes bytes the tensor points
+// to (kore's stderr messages pass through).
+//
 //   kore_qmv_ref --time-batch THREADS MIN_SECONDS job.bin
 // takes a batch-mode job and runs kore's matmul_batch_float on it with
 // THREADS threads and the AVX2 path where the CPU has it (as forward_batch()
@@ -41,6 +48,7 @@
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -161,7 +169,39 @@ static int batch_mode(const char *job, const char *res) {
     return avx2 ? 0 : 10;
 }
 
+static int gguf_mode(const char *path) {
+    Model m;
+    const bool ok = load_model(path, m);
+    printf("{\"ok\": %s", ok ? "true" : "false");
+    if (ok) {
+        const Hparams &h = m.hp;
+        printf(", \"hp\": {\"n_layer\": %u, \"n_embd\": %u, \"n_ff\": %u, \"n_head\": %u, \"n_head_kv\": %u, "
+               "\"n_ctx\": %u, \"n_vocab\": %u, \"rope_base\": %.9g, \"rms_eps\": %.9g}, \"data_start\": %llu, "
+               "\"tensors\": [",
+               h.n_layer, h.n_embd, h.n_ff, h.n_head, h.n_head_kv, h.n_ctx, h.n_vocab, (double)h.rope_base,
+               (double)h.rms_eps, (unsigned long long)m.data_start);
+        std::vector<std::string> names;
+        for (const auto &kv : m.tensors) names.push_back(kv.first);
+        std::sort(names.begin(), names.end());
+        for (size_t i = 0; i < names.size(); ++i) {
+            const Tensor &t = m.tensors.at(names[i]);
+            uint64_t fnv = 0xcbf29ce484222325ull;
+            if (t.data)
+                for (uint64_t b = 0; b < t.nbytes; ++b) fnv = (fnv ^ t.data[b]) * 0x100000001b3ull;
+            printf("%s{\"name\": \"%s\", \"type\": %u, \"n_dims\": %u, \"dims\": [%llu, %llu, %llu, %llu], "
+                   "\"nbytes\": %llu, \"has_data\": %s, \"fnv\": \"%016llx\"}",
+                   i ? ", " : "", names[i].c_str(), t.type, t.n_dims, (unsigned long long)t.dims[0],
+                   (unsigned long long)t.dims[1], (unsigned long long)t.dims[2], (unsigned long long)t.dims[3],
+                   (unsigned long long)t.nbytes, t.data ? "true" : "false", (unsigned long long)fnv);
+        }
+        printf("]");
+    }
+    printf("}\n");
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc == 3 && std::string(argv[1]) == "--gguf") return gguf_mode(argv[2]);
     if (argc == 4 && std::string(argv[1]) == "--batch") return batch_mode(argv[2], argv[3]);
     if (argc == 5 && std::string(argv[1]) == "--time-batch")
         return time_batch_mode((unsigned)atoi(argv[2]), atof(argv[3]), argv[4]);
