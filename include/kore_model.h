@@ -1,0 +1,67 @@
+/* kore_model.h - a whole kore engine on an MI355X: kore's engine_init
+ * (kore.cpp:1274-1365) over a GGUF file with every tensor in HBM, and its
+ * forward() (kore.cpp:1397-1484) for one token on the GPU: the token's
+ * embedding row (kore_qmv_get_row_dev), every layer (kore_layer_decode_dev)
+ * and, when asked, the logits (rmsnorm with output_norm, quant, output head).
+ *
+ * Loading applies engine_init's checks (Qwen2 hyper-parameters present and
+ * consistent, n_embd and n_ff multiples of 256, even head_dim, matrices Q4_K or
+ * Q6_K, norms and biases F32, token_embd and output with the same vocabulary)
+ * and its context: min(qwen2.context_length, ctx_max), or ctx_max when the file
+ * has none.  Part of libkore_layer.so. */
+#ifndef KORE_MODEL_H
+#define KORE_MODEL_H
+
+#include "kore_attn.h"
+#include "kore_gguf.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef KORE_MODEL_API
+#if defined(__GNUC__)
+#define KORE_MODEL_API __attribute__((visibility("default")))
+#else
+#define KORE_MODEL_API
+#endif
+#endif
+
+#define KORE_MODEL_OK 0
+#define KORE_MODEL_E_LOAD 1        /* the file: kore_gguf_open failed, or engine_init would refuse it */
+#define KORE_MODEL_E_RANGE 2       /* token or position outside what forward() accepts (kore.cpp:1400) */
+#define KORE_MODEL_E_DEVICE 3      /* a HIP call or a device step failed */
+
+typedef struct kore_model *kore_model_t;
+
+typedef struct kore_model_info {
+    kore_gguf_hparams hp;
+    int ctx;                 /* positions per layer of the KV cache */
+    int n_vocab;             /* rows of output.weight */
+    int head_dim, kv_dim;
+    size_t weight_bytes;     /* device bytes of all tensors */
+} kore_model_info;
+
+KORE_MODEL_API int kore_model_load(const char *gguf_path, int ctx_max, kore_model_t *out);
+KORE_MODEL_API void kore_model_destroy(kore_model_t m);
+KORE_MODEL_API int kore_model_get_info(kore_model_t m, kore_model_info *info);
+
+/* kore's forward(e, token, pos, want_logits) with the result in HBM: the logits
+ * (n_vocab floats) at kore_model_logits_dev when want_logits.  Enqueued on
+ * `stream` (NULL: the model's own stream, ordered with the null stream). */
+KORE_MODEL_API int kore_model_decode_dev(kore_model_t m, int token, int pos, int want_logits, void *stream);
+KORE_MODEL_API const float *kore_model_logits_dev(kore_model_t m);
+
+/* Same, synchronous, with the logits copied to host memory (NULL: no logits). */
+KORE_MODEL_API int kore_model_decode(kore_model_t m, int token, int pos, float *logits);
+
+/* The model's KV cache (for kore_attn_read_kv and the like). */
+KORE_MODEL_API kore_attn_t kore_model_attn(kore_model_t m);
+
+KORE_MODEL_API const char *kore_model_last_error(kore_model_t m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

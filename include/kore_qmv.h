@@ -154,6 +154,13 @@ KORE_QMV_API int kore_qmv_mv_group_ex_dev(int n, const kore_qmv_tensor_t *t, con
                                           const kore_qmv_mv_opts *opts, float *const *out, int avx2,
                                           void *stream);
 
+/* kore's get_row (kore.cpp:384-407) on the device, as forward() uses it for the
+ * token embedding: row `row` of `table` (device memory in the file's layout:
+ * rows of n values of ggml type 0 F32, 1 F16, 30 BF16, 12 Q4_K or 14 Q6_K with
+ * kore's 144 / 210-byte blocks) dequantised with kore's expressions into out[n]
+ * (device), bit-identical to kore.  Enqueued on `stream`. */
+KORE_QMV_API int kore_qmv_get_row_dev(int type, const void *table, int64_t row, int64_t n, float *out, void *stream);
+
 /* Text of the last failure on this tensor (or, with NULL, of the last failed
  * call without a tensor on this thread).  Never NULL. */
 KORE_QMV_API const char *kore_qmv_last_error(kore_qmv_tensor_t t);

@@ -431,6 +431,15 @@ KORE_QMV_API int kore_qmv_matmul_batch(kore_qmv_tensor_t t, const float *x, int 
     return rc;
 }
 
+KORE_QMV_API int kore_qmv_get_row_dev(int type, const void *table, int64_t row, int64_t n, float *out, void *stream) {
+    if (!table || !out) return fail(nullptr, KORE_QMV_E_INVALID, "table or out is NULL");
+    if (type != 0 && type != 1 && type != 30 && type != KORE_QMV_Q4_K && type != KORE_QMV_Q6_K)
+        return fail(nullptr, KORE_QMV_E_UNSUPPORTED, "get_row takes F32, F16, BF16, Q4_K or Q6_K");
+    const hipError_t e = launch_get_row(type, (const uint8_t *)table, row, n, out, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(nullptr, KORE_QMV_E_INVALID, std::string("get_row: ") + hipGetErrorString(e));
+    return KORE_QMV_OK;
+}
+
 KORE_QMV_API const char *kore_qmv_last_error(kore_qmv_tensor_t t) {
     return t ? t->error.c_str() : g_error.c_str();
 }

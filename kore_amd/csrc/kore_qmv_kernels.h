@@ -86,6 +86,10 @@ hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool imag
 // -> body / d arrays above.
 hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, uint16_t *d, hipStream_t s);
 
+// kore's get_row (kore.cpp:384-407): row `row` of a table of rows of n values
+// of type F32 / F16 / BF16 / Q4_K / Q6_K (kore's block bytes) -> out[n] floats.
+hipError_t launch_get_row(int type, const uint8_t *data, int64_t row, int64_t n, float *out, hipStream_t s);
+
 // Synthetic GGUF-format weights for benchmarks: nblocks raw Q4_K / Q6_K blocks
 // with hashed bytes and finite f16 scales (dst 2-byte aligned).
 hipError_t launch_synth_blocks(int type, int64_t nblocks, uint64_t seed, uint8_t *dst, hipStream_t s);

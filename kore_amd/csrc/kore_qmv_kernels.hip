@@ -759,3 +759,64 @@ hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, 
 }
 
 }  // namespace kore_qmv_gpu
+
+// ------------------------------------------------------------------ get_row
+
+namespace kore_qmv_gpu {
+namespace {
+
+__device__ __forceinline__ float f16_at(const uint8_t *p) { return f16_bits((uint32_t)p[0] | ((uint32_t)p[1] << 8)); }
+
+// kore's get_row (kore.cpp:384-407): value i of a row of n values, one thread
+// per value.  Q4_K / Q6_K follow kore's dequantisers (kore.cpp:337-381) with
+// their separate roundings (no fused multiply-add).
+__global__ __launch_bounds__(kThreads) void get_row_kernel(int type, const uint8_t *__restrict__ row, int64_t n,
+                                                           float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    float v = 0.f;
+    if (type == 0) {                                     // F32
+        v = ((const float *)row)[i];
+    } else if (type == 1) {                              // F16
+        v = f16_at(row + 2 * i);
+    } else if (type == 30) {                             // BF16: the high half of a float
+        v = __uint_as_float(((uint32_t)row[2 * i] | ((uint32_t)row[2 * i + 1] << 8)) << 16);
+    } else if (type == kQ4K) {
+        const uint8_t *b = row + (i / 256) * kQ4Bytes;
+        const int e = (int)(i % 256), j = e / 32, l = e % 32;   // sub-block j, value l
+        const uint8_t *s = b + 4;
+        const int sc = j < 4 ? (s[j] & 63) : ((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+        const int mn = j < 4 ? (s[j + 4] & 63) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+        const float d1 = f16_at(b) * (float)sc, m1 = f16_at(b + 2) * (float)mn;
+        const uint8_t qb = b[16 + 32 * (j / 2) + l];
+        const int q = (j & 1) ? (qb >> 4) : (qb & 0xF);
+        v = d1 * (float)q - m1;
+    } else {                                             // Q6_K, kore's 210-byte blocks
+        const uint8_t *b = row + (i / 256) * kQ6Bytes;
+        const int e = (int)(i % 256), h = e / 128, k = (e % 128) / 32, l = e % 32;
+        const uint8_t lo = b[64 * h + 32 * (k & 1) + l];
+        const int ql = k < 2 ? (lo & 0xF) : (lo >> 4);
+        const int qh = (b[128 + 32 * h + l] >> (2 * k)) & 3;
+        const float sc = (float)(int8_t)b[192 + 8 * h + 2 * k + l / 16];
+        v = (f16_at(b + 208) * sc) * (float)((ql | (qh << 4)) - 32);
+    }
+    out[i] = v;
+}
+
+}  // namespace
+
+hipError_t launch_get_row(int type, const uint8_t *data, int64_t row, int64_t n, float *out, hipStream_t s) {
+    int64_t per = 1, bytes = 4;
+    if (type == 1 || type == 30) bytes = 2;
+    else if (type == kQ4K) { per = 256; bytes = kQ4Bytes; }
+    else if (type == kQ6K) { per = 256; bytes = kQ6Bytes; }
+    else if (type != 0) return hipErrorInvalidValue;
+    if (n <= 0 || n % per || row < 0) return hipErrorInvalidValue;
+    const uint8_t *p = data + row * (n / per * bytes);
+    hipLaunchKernelGGL(get_row_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, type, p,
+                       n, out);
+    return hipGetLastError();
+}
+
+}  // namespace kore_qmv_gpu

@@ -54,6 +54,7 @@ SYMBOLS = [
     ("kore_qmv_matmul_batch_dev", _i, [_vp, _vp, _i, _vp, _vp]),
     ("kore_qmv_matmul_batch_group_dev", _i, [_i, _vp, _vp, _i, _vp, _vp]),
     ("kore_qmv_mv_group_ex_dev", _i, [_i, _vp, _vp, _vp, _vp, _i, _vp]),
+    ("kore_qmv_get_row_dev", _i, [_i, _vp, _i64, _i64, _vp, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
     ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),

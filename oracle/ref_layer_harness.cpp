@@ -21,6 +21,13 @@
 //   e.x: forward() is called without logits), then the K and V caches
 //   ([n_layer][ctx][kvd] each).
 //
+// GGUF mode (pins the loader and the whole token on a real file):
+//   kore_layer_ref --gguf-forward file.gguf CTX_MAX TOKEN...
+// runs kore's load_model + engine_init(ctx_max, 4 threads, quantised path) and
+// forward(token, pos, logits) for the tokens at positions 0, 1, ...; prints one
+// JSON line {"ok", "ctx", "n_vocab", "avx2", "logits": [[...], ...]} (logits as
+// the hex of their float bits), or {"ok": false} when kore refuses the file.
+//
 // Timing mode (the CPU baseline of the benchmark's whole-token leg):
 //   kore_layer_ref --time THREADS MIN_SECONDS POS
 // builds a Qwen2.5-7B-shape engine (28 layers, 3584 / 18944, 28 / 4 heads of
@@ -156,7 +163,31 @@ int time_mode(unsigned nth, double min_s, int pos0) {
 
 }  // namespace
 
+int gguf_forward(const char *path, int ctx_max, int n, char **toks) {
+    Model m;
+    Engine e;
+    if (!load_model(path, m) || !engine_init(e, m, ctx_max, 4, false)) {
+        printf("{\"ok\": false}\n");
+        return 0;
+    }
+    printf("{\"ok\": true, \"ctx\": %d, \"n_vocab\": %d, \"avx2\": %d, \"logits\": [", e.ctx, e.n_vocab, (int)e.avx2);
+    for (int i = 0; i < n; ++i) {
+        if (!forward(e, atoi(toks[i]), i, true)) { printf("]}\n"); return 5; }
+        printf("%s[", i ? ", " : "");
+        for (int v = 0; v < e.n_vocab; ++v) {
+            uint32_t u;
+            memcpy(&u, &e.logits[(size_t)v], 4);
+            printf("%s\"%08x\"", v ? ", " : "", u);
+        }
+        printf("]");
+    }
+    printf("]}\n");
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc >= 4 && std::string(argv[1]) == "--gguf-forward")
+        return gguf_forward(argv[2], atoi(argv[3]), argc - 4, argv + 4);
     if (argc == 5 && std::string(argv[1]) == "--time")
         return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]));
     if (argc != 3) { fprintf(stderr, "usage: kore_layer_ref job.bin result.bin | --time THREADS SECONDS POS\n"); return 2; }

@@ -1,6 +1,7 @@
 #!/usr/bin/env python3
 """Write small GGUF files and kore's own parse of each: tests/golden/gguf_*.gguf
-and gguf_*.json.
+and gguf_*.json; and kore's whole engine on the tiny model's file
+(gguf_tiny_qwen2_forward.json: logits of four decode tokens).
 
 The files are written here from the GGUF layout (magic, version, tensor and
 metadata counts, typed key/value pairs, the tensor table, data aligned to
@@ -130,6 +131,19 @@ def main():
             json.dump({"file": f"gguf_{name}.gguf", "bytes": len(data), "kore": kore,
                        "kore_stderr": r.stderr.strip()}, f, indent=1)
         print(name, len(data), "ok" if kore["ok"] else "rejected", r.stderr.strip()[:60])
+    # kore's whole engine on the tiny model: engine_init (ctx_max 64) and
+    # forward() with logits for four tokens at positions 0..3
+    if not os.path.exists(oracle.REF_LAYER_BIN):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref"], check=True)
+    tokens = [3, 7, 0, 11]
+    r = subprocess.run([oracle.REF_LAYER_BIN, "--gguf-forward", os.path.join(HERE, "gguf_tiny_qwen2.gguf"), "64"] +
+                       [str(t) for t in tokens], capture_output=True, text=True, check=True)
+    fwd = json.loads(r.stdout)
+    with open(os.path.join(HERE, "gguf_tiny_qwen2_forward.json"), "w") as f:
+        json.dump({"file": "gguf_tiny_qwen2.gguf", "ctx_max": 64, "tokens": tokens,
+                   "source": "kore.cpp load_model + engine_init + forward(logits) via oracle/_ref/kore_layer_ref",
+                   "kore": fwd}, f, indent=1)
+    print("forward:", fwd["ok"], fwd["ctx"], fwd["n_vocab"])
 
 
 if __name__ == "__main__":

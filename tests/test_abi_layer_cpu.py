@@ -6,14 +6,14 @@ import re
 import subprocess
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("kore_layer.h", "kore_gguf.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("kore_layer.h", "kore_gguf.h", "kore_model.h")]
 
 
 def _declared():
     names = set()
     for h in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= {m.group(1) for m in re.finditer(r"\b(kore_(?:layer|gguf)_[a-z_0-9]+)\s*\(", text)}
+        names |= {m.group(1) for m in re.finditer(r"\b(kore_(?:layer|gguf|model)_[a-z_0-9]+)\s*\(", text)}
     return names
 
 

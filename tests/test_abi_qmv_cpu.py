@@ -32,7 +32,8 @@ def _exported():
 def test_headers_declare_the_abi():
     assert _declared() == {"kore_qmv_tensor_create", "kore_qmv_tensor_destroy", "kore_qmv_quantize",
                            "kore_qmv_quantize_dev", "kore_qmv_matvec", "kore_qmv_matvec_dev", "kore_qmv_mv",
-                           "kore_qmv_mv_dev", "kore_qmv_mv_group_dev", "kore_qmv_mv_group_ex_dev", "kore_qmv_matmul_batch",
+                           "kore_qmv_mv_dev", "kore_qmv_mv_group_dev", "kore_qmv_mv_group_ex_dev", "kore_qmv_get_row_dev",
+                           "kore_qmv_matmul_batch",
                            "kore_qmv_matmul_batch_dev", "kore_qmv_matmul_batch_group_dev",
                            "kore_qmv_last_error", "kore_qmv_get_info", "kore_qmv_synth_dev"}
 

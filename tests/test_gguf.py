@@ -11,7 +11,8 @@ import pytest
 import oracle.gguf as ogguf
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-CASES = sorted(f[5:-5] for f in os.listdir(GOLD) if f.startswith("gguf_") and f.endswith(".json"))
+CASES = sorted(f[5:-5] for f in os.listdir(GOLD)
+               if f.startswith("gguf_") and f.endswith(".json") and not f.endswith("_forward.json"))
 
 
 def _case(name):
@@ -94,3 +95,61 @@ def test_oracle_rejects_what_breaks_the_rules():
     assert not ogguf.parse(b"GGUF")["ok"]                   # header cut short
     assert not ogguf.parse(b"XGUF" + good[4:])["ok"]        # magic
     assert not ogguf.parse(good[:-1])["ok"]                 # last tensor leaves the file by one byte
+
+
+def oracle_engine_logits(path, tokens, ctx_max=64):
+    """The oracle's kore engine over a GGUF file: engine_init's tensors
+    (kore.cpp:1274-1334), then per token get_row (kore.cpp:384-407), every
+    forward() layer and the logits (kore.cpp:1474-1478)."""
+    import oracle
+    data = open(path, "rb").read()
+    p = ogguf.parse(data)
+    hp, start = p["hp"], p["data_start"]
+    # tensor bytes by name, from the parse's offsets (first of a repeated name)
+    r = ogguf._R(data)
+    r.take(4), r.u32()
+    n_t, n_kv = r.u64(), r.u64()
+    for _ in range(n_kv):
+        r.str()
+        r.skip_value(r.u32())
+    tens = {}
+    for _ in range(n_t):
+        name, nd = r.str().decode(), r.u32()
+        dims = [r.u64() for _ in range(nd)] + [1] * (4 - nd)
+        t, off = r.u32(), r.u64()
+        if name not in tens:
+            nb = next(x["nbytes"] for x in p["tensors"] if x["name"] == name)
+            tens[name] = (t, dims, np.frombuffer(data[start + off:start + off + nb], np.uint8))
+    E, FF, NH, NKV = hp["n_embd"], hp["n_ff"], hp["n_head"], hp["n_head_kv"]
+    ctx = min(hp["n_ctx"], ctx_max) if hp["n_ctx"] else ctx_max
+    f32 = lambda n: tens[n][2].view(np.float32)                     # noqa: E731
+    layers = []
+    for l in range(hp["n_layer"]):
+        b = f"blk.{l}."
+        names = ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]
+        layers.append(oracle.LayerWeights([tens[b + n + ".weight"][0] for n in names],
+                                          [tens[b + n + ".weight"][2] for n in names],
+                                          f32(b + "attn_norm.weight"), f32(b + "ffn_norm.weight"),
+                                          f32(b + "attn_q.bias"), f32(b + "attn_k.bias"), f32(b + "attn_v.bias")))
+    kv = oracle.KV(hp["n_layer"], ctx, NH, NKV, E // NH, hp["rope_base"])
+    et, edims, eb = tens["token_embd.weight"]
+    ot, odims, ob = tens["output.weight"]
+    row_bytes = len(eb) // edims[1]
+    out = []
+    for pos, tok in enumerate(tokens):
+        x = oracle.dequant_row(et, eb[tok * row_bytes:(tok + 1) * row_bytes], E) if et in (12, 14) else \
+            eb[tok * row_bytes:(tok + 1) * row_bytes].view(np.float32).copy()
+        for l, lw in enumerate(layers):
+            x = oracle.layer_forward(kv, l, pos, x, lw, FF, hp["rms_eps"], avx2=True)
+        xq = oracle.quantize_q8K(oracle.rmsnorm(x, f32("output_norm.weight"), hp["rms_eps"]))
+        out.append(oracle.qmatvec(ot, ob, odims[1], E, xq, avx2=True))
+    return ctx, np.stack(out), kv
+
+
+def test_oracle_engine_matches_kore_logits():
+    man = json.load(open(os.path.join(GOLD, "gguf_tiny_qwen2_forward.json")))
+    kore = man["kore"]
+    ctx, logits, _ = oracle_engine_logits(os.path.join(GOLD, man["file"]), man["tokens"], man["ctx_max"])
+    assert kore["ok"] and kore["avx2"] == 1 and ctx == kore["ctx"]
+    want = np.array([[int(h, 16) for h in row] for row in kore["logits"]], np.uint32)
+    assert np.array_equal(logits.astype(np.float32).view(np.uint32), want)

@@ -1,0 +1,90 @@
+"""A whole kore engine on the GPU (include/kore_model.h) built from a GGUF file
+against kore's own engine on the same file (tests/golden/gguf_tiny_qwen2*):
+logits of four decode tokens within kore's tolerance (attention's softmax and
+SwiGLU's exp are the only steps not bit-identical), layer 0's K/V rows bit for
+bit against the oracle's engine, the device embedding lookup bit for bit, and
+forward()'s range checks."""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+from test_gguf import oracle_engine_logits  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_model_logits_against_kore_engine():
+    from kore_amd.model import Model
+    man = json.load(open(os.path.join(GOLD, "gguf_tiny_qwen2_forward.json")))
+    path = os.path.join(GOLD, man["file"])
+    want = np.array([[int(h, 16) for h in row] for row in man["kore"]["logits"]], np.uint32).view(np.float32)
+    print("[gpu-model] tiny_qwen2 engine, 4 tokens", flush=True)
+    with Model(path, man["ctx_max"]) as m:
+        assert m.info.ctx == man["kore"]["ctx"] and m.info.n_vocab == man["kore"]["n_vocab"]
+        for pos, tok in enumerate(man["tokens"]):
+            got = m.decode(tok, pos).astype(np.float64)
+            ref = want[pos].astype(np.float64)
+            assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref)), f"token {pos}"
+        # layer 0's K/V rows depend only on exact steps: bit for bit with the oracle's engine
+        k, v = m.read_kv(0, 0, len(man["tokens"]))
+    _, _, kv = oracle_engine_logits(path, man["tokens"], man["ctx_max"])
+    n = len(man["tokens"])
+    assert np.array_equal(k.view(np.uint32), kv.kcache()[0, :n].view(np.uint32))
+    assert np.array_equal(v.view(np.uint32), kv.vcache()[0, :n].view(np.uint32))
+
+
+def test_embedding_rows_bitwise():
+    from kore_amd import hip, qmv
+    rng = np.random.default_rng(4)
+    print("[gpu-model] get_row for F32, F16, BF16, Q4_K, Q6_K", flush=True)
+    for t, n in ((0, 512), (1, 512), (30, 512), (oracle.TYPE_Q4K, 768), (oracle.TYPE_Q6K, 768)):
+        rows = 5
+        if t in (oracle.TYPE_Q4K, oracle.TYPE_Q6K):
+            bb = oracle.BLOCK_BYTES[t]
+            tab = rng.integers(0, 256, size=rows * n // 256 * bb, dtype=np.uint8)
+            tab.reshape(-1, bb)[:, 0 if t == oracle.TYPE_Q4K else 208:(4 if t == oracle.TYPE_Q4K else 210)] = \
+                np.frombuffer(np.array([2e-3, 1e-3][:2 if t == oracle.TYPE_Q4K else 1], np.float16).tobytes(), np.uint8)
+            ref = [oracle.dequant_row(t, tab[r * n // 256 * bb:(r + 1) * n // 256 * bb], n) for r in range(rows)]
+        else:
+            f = rng.standard_normal(rows * n).astype(np.float32)
+            if t == 0:
+                tab, ref = f.view(np.uint8), list(f.reshape(rows, n))
+            elif t == 1:
+                h = f.astype(np.float16)
+                tab, ref = h.view(np.uint8), list(h.astype(np.float32).reshape(rows, n))
+            else:
+                b = (f.view(np.uint32) >> 16).astype(np.uint16)
+                tab, ref = b.view(np.uint8), list((b.astype(np.uint32) << 16).view(np.float32).reshape(rows, n))
+        dt = hip.DeviceBuffer((tab.size + 3) // 4)
+        hip.check(hip.lib().hipMemcpy(dt.ptr, np.ascontiguousarray(tab).ctypes.data, tab.size, hip.H2D), "H2D")
+        out = hip.DeviceBuffer(n)
+        for r in range(rows):
+            rc = qmv.lib().kore_qmv_get_row_dev(t, dt.ptr, r, n, out.ptr, None)
+            assert rc == 0
+            hip.synchronize()
+            assert np.array_equal(out.download().view(np.uint32), np.asarray(ref[r], np.float32).view(np.uint32)), (t, r)
+        dt.free()
+        out.free()
+
+
+def test_model_rejections():
+    from kore_amd.model import KORE_MODEL_E_LOAD, KORE_MODEL_E_RANGE, Model, ModelError
+    with pytest.raises(ModelError) as e:
+        Model(os.path.join(GOLD, "gguf_align64_v2.gguf"))           # hyper-parameters but no tensors
+    assert e.value.code == KORE_MODEL_E_LOAD
+    with pytest.raises(ModelError) as e:
+        Model(os.path.join(GOLD, "gguf_bad_magic.gguf"))
+    assert e.value.code == KORE_MODEL_E_LOAD
+    with Model(os.path.join(GOLD, "gguf_tiny_qwen2.gguf"), 16) as m:
+        assert m.info.ctx == 16                                      # min(context_length 4096, ctx_max 16)
+        for tok, pos in ((12, 0), (-1, 0), (0, 16), (0, -1)):
+            with pytest.raises(ModelError) as e:
+                m.decode(tok, pos)
+            assert e.value.code == KORE_MODEL_E_RANGE
