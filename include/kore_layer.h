@@ -70,6 +70,19 @@ KORE_LAYER_API void kore_layer_destroy(kore_layer_t L);
 KORE_LAYER_API int kore_layer_decode_dev(kore_layer_t L, const kore_layer_weights *w, kore_attn_t attn, int layer,
                                          int pos, float *x, int avx2, void *stream);
 
+/* kore's forward_batch() body for layer `layer` over n_tok (1..64, kore's
+ * KORE_BMAX) rows at positions pos0.. (kore.cpp:1518-1589): x (device,
+ * [n_tok][n_embd], 16-byte aligned) is the rows' residual stream, updated in
+ * place.  Batched rmsnorm, q/k/v matmul + biases, RoPE + append + causal
+ * attention (kore_attn_prefill_dev), Wo + residual, rmsnorm, gate/up matmul,
+ * SwiGLU, down + residual.  rmsnorm is bit-identical to kore's; the matmuls
+ * and attention hold kore's tolerance (max|d| <= 1e-4 * max|ref|).  Fails
+ * with KORE_LAYER_E_STEP (attention's range error) when pos0 < 0 or pos0 +
+ * n_tok > ctx, like forward_batch() (kore.cpp:1490).  Same stream and scratch
+ * rules as kore_layer_decode_dev. */
+KORE_LAYER_API int kore_layer_prefill_dev(kore_layer_t L, const kore_layer_weights *w, kore_attn_t attn, int layer,
+                                          int pos0, int n_tok, float *x, void *stream);
+
 /* Wait for the layer's own stream. */
 KORE_LAYER_API int kore_layer_sync(kore_layer_t L);
 

@@ -52,6 +52,20 @@ KORE_MODEL_API int kore_model_get_info(kore_model_t m, kore_model_info *info);
 KORE_MODEL_API int kore_model_decode_dev(kore_model_t m, int token, int pos, int want_logits, void *stream);
 KORE_MODEL_API const float *kore_model_logits_dev(kore_model_t m);
 
+/* kore's forward_batch(e, tokens, n_tok, pos0, want_logits) (kore.cpp:1486-1598)
+ * with the results in HBM: tokens is host memory; 1 <= n_tok <= min(64, ctx)
+ * (kore's e.bsz) and pos0 + n_tok <= ctx, every token < n_vocab, else
+ * KORE_MODEL_E_RANGE.  The rows' residual streams after the last layer are at
+ * kore_model_rows_dev ([n_tok][n_embd], kore's e.bx) and, when want_logits,
+ * the last row's logits at kore_model_logits_dev.  Matmuls and attention hold
+ * kore's tolerance (max|d| <= 1e-4 * max|ref|); not bit for bit. */
+KORE_MODEL_API int kore_model_prefill_dev(kore_model_t m, const int *tokens, int n_tok, int pos0, int want_logits,
+                                          void *stream);
+KORE_MODEL_API const float *kore_model_rows_dev(kore_model_t m);
+
+/* Waits for the model's own stream. */
+KORE_MODEL_API int kore_model_sync(kore_model_t m);
+
 /* Same, synchronous, with the logits copied to host memory (NULL: no logits). */
 KORE_MODEL_API int kore_model_decode(kore_model_t m, int token, int pos, float *logits);
 

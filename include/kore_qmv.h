@@ -154,6 +154,26 @@ KORE_QMV_API int kore_qmv_mv_group_ex_dev(int n, const kore_qmv_tensor_t *t, con
                                           const kore_qmv_mv_opts *opts, float *const *out, int avx2,
                                           void *stream);
 
+/* The batched matmul with kore's elementwise steps after it fused into the
+ * final stores (forward_batch(), kore.cpp:1527-1532, 1567-1570, 1586-1589):
+ * opts->bias[k] (q/k/v biases) and opts->accumulate (residual adds) as for
+ * kore_qmv_mv_group_ex_dev; opts->norm_w and opts->up must be NULL (the batched
+ * rmsnorm and SwiGLU are the two calls below).  opts may be NULL. */
+KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
+                                                    const kore_qmv_mv_opts *opts, float *const *out, void *stream);
+
+/* kore's rmsnorm of each of `rows` rows of n floats (forward_batch(),
+ * kore.cpp:1521-1522, 1572-1573; rmsnorm at kore.cpp:1367-1372): out[r] =
+ * x[r] * scale_r * w, bit-identical to kore's sequential double sum.  Device
+ * buffers (out may equal x), enqueued on `stream`. */
+KORE_QMV_API int kore_qmv_rmsnorm_rows_dev(const float *x, const float *w, int64_t n, int rows, float eps, float *out,
+                                           void *stream);
+
+/* kore's batched SwiGLU in place (kore.cpp:1577-1583): g[i] = g[i] / (1 +
+ * exp(-g[i])) * u[i] over n floats, exp rounded from double as in
+ * kore_qmv_mv_group_ex_dev.  Device buffers, enqueued on `stream`. */
+KORE_QMV_API int kore_qmv_swiglu_dev(float *g, const float *u, int64_t n, void *stream);
+
 /* kore's get_row (kore.cpp:384-407) on the device, as forward() uses it for the
  * token embedding: row `row` of `table` (device memory in the file's layout:
  * rows of n values of ggml type 0 F32, 1 F16, 30 BF16, 12 Q4_K or 14 Q6_K with

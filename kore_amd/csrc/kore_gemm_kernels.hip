@@ -192,18 +192,28 @@ template <int NB>
 __device__ __forceinline__ void store_tile(const GemmArgs &a, const GemmMat &mt, int tile, int wave, int i, int kk,
                                            const floatx4 *acc) {
     const int r0 = (tile - mt.tile0) * kGemmRowsPerTile + 16 * wave + 4 * kk;
-    const bool vec = (mt.rows & 3) == 0 && ((uintptr_t)mt.out & 15) == 0;
+    const bool vec = (mt.rows & 3) == 0 && ((uintptr_t)mt.out & 15) == 0 && ((uintptr_t)mt.bias & 15) == 0;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         const int b = 16 * nb + i;
         if (b >= a.B) continue;
         float *o = mt.out + (int64_t)b * mt.rows + r0;
+        // kore's q += bq (kore.cpp:1530-1532) and x += o (kore.cpp:1567-1570, 1586-1589)
+        floatx4 val = acc[nb];
         if (vec) {
-            if (r0 < mt.rows) *(floatx4 *)o = acc[nb];
+            if (r0 < mt.rows) {
+                if (mt.bias) val = val + *(const floatx4 *)(mt.bias + r0);
+                if (mt.accumulate) val = *(const floatx4 *)o + val;
+                *(floatx4 *)o = val;
+            }
         } else {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                if (r0 + v < mt.rows) o[v] = acc[nb][v];
+                if (r0 + v < mt.rows) {
+                    float f = val[v];
+                    if (mt.bias) f = f + mt.bias[r0 + v];
+                    o[v] = mt.accumulate ? o[v] + f : f;
+                }
         }
     }
 }

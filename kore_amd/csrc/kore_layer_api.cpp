@@ -14,12 +14,16 @@ struct kore_layer {
     int device = 0;
     hipStream_t stream = nullptr;
     float *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *gate = nullptr, *up = nullptr;
+    // forward_batch() rows (kore's e.bxb, bq, bk, bv, batt, bgate, bup), kMaxBatch each
+    float *bxb = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *batt = nullptr, *bgate = nullptr,
+          *bup = nullptr;
     std::string error;
 };
 
 namespace {
 
 thread_local std::string g_error;
+constexpr int kMaxBatch = 64;   // kore's KORE_BMAX (kore.cpp:690)
 
 int fail(kore_layer *L, int code, const std::string &msg) {
     (L ? L->error : g_error) = msg;
@@ -27,7 +31,8 @@ int fail(kore_layer *L, int code, const std::string &msg) {
 }
 
 void release(kore_layer *L) {
-    for (float *p : {L->q, L->k, L->v, L->att, L->gate, L->up})
+    for (float *p : {L->q, L->k, L->v, L->att, L->gate, L->up, L->bxb, L->bq, L->bk, L->bv, L->batt, L->bgate,
+                     L->bup})
         if (p) (void)hipFree(p);
     if (L->stream) (void)hipStreamDestroy(L->stream);
     delete L;
@@ -63,10 +68,11 @@ KORE_LAYER_API int kore_layer_create(kore_layer_t *out, int n_embd, int n_ff, in
     // a blocking stream: ordered with the null stream, so a caller's plain
     // hipMemcpy of x before a call is seen by it
     if (e == hipSuccess) e = hipStreamCreate(&L->stream);
-    const size_t sizes[6] = {(size_t)L->E, (size_t)L->kvd, (size_t)L->kvd, (size_t)L->E, (size_t)L->FF,
-                             (size_t)L->FF};
-    float **bufs[6] = {&L->q, &L->k, &L->v, &L->att, &L->gate, &L->up};
-    for (int i = 0; i < 6 && e == hipSuccess; ++i) e = hipMalloc((void **)bufs[i], sizes[i] * sizeof(float));
+    const size_t E = (size_t)L->E, kvd = (size_t)L->kvd, FF = (size_t)L->FF, B = kMaxBatch;
+    const size_t sizes[13] = {E, kvd, kvd, E, FF, FF, B * E, B * E, B * kvd, B * kvd, B * E, B * FF, B * FF};
+    float **bufs[13] = {&L->q,   &L->k,  &L->v,  &L->att,  &L->gate,  &L->up, &L->bxb,
+                        &L->bq,  &L->bk, &L->bv, &L->batt, &L->bgate, &L->bup};
+    for (int i = 0; i < 13 && e == hipSuccess; ++i) e = hipMalloc((void **)bufs[i], sizes[i] * sizeof(float));
     if (e != hipSuccess) {
         g_error = std::string("kore_layer_create: ") + hipGetErrorString(e);
         release(L);
@@ -80,9 +86,10 @@ KORE_LAYER_API void kore_layer_destroy(kore_layer_t L) {
     if (L) release(L);
 }
 
-KORE_LAYER_API int kore_layer_decode_dev(kore_layer_t L, const kore_layer_weights *w, kore_attn_t attn, int layer,
-                                         int pos, float *x, int avx2, void *stream) {
-    if (!L) return fail(nullptr, KORE_LAYER_E_INVALID, "layer handle is NULL");
+namespace {
+
+// The checks both layer steps make on their arguments.
+int check_call(kore_layer *L, const kore_layer_weights *w, kore_attn_t attn, const float *x) {
     if (!w || !attn || !x || ((uintptr_t)x & 15)) return fail(L, KORE_LAYER_E_INVALID, "w, attn or x missing or x unaligned");
     if (!w->attn_norm || !w->ffn_norm) return fail(L, KORE_LAYER_E_INVALID, "attn_norm and ffn_norm are required");
     const int64_t E = L->E, FF = L->FF, kvd = L->kvd;
@@ -93,6 +100,15 @@ KORE_LAYER_API int kore_layer_decode_dev(kore_layer_t L, const kore_layer_weight
     if (kore_attn_get_info(attn, &ai) != KORE_ATTN_OK || ai.n_head != L->n_head || ai.n_head_kv != L->n_head_kv ||
         ai.head_dim != L->head_dim)
         return fail(L, KORE_LAYER_E_INVALID, "the attention handle's geometry differs from the layer's");
+    return KORE_LAYER_OK;
+}
+
+}  // namespace
+
+KORE_LAYER_API int kore_layer_decode_dev(kore_layer_t L, const kore_layer_weights *w, kore_attn_t attn, int layer,
+                                         int pos, float *x, int avx2, void *stream) {
+    if (!L) return fail(nullptr, KORE_LAYER_E_INVALID, "layer handle is NULL");
+    if (int rc = check_call(L, w, attn, x)) return rc;
     void *s = stream ? stream : (void *)L->stream;
     auto qmv_err = [&](kore_qmv_tensor_t t, const char *what) {
         return fail(L, KORE_LAYER_E_STEP, std::string(what) + ": " + kore_qmv_last_error(t));
@@ -128,6 +144,50 @@ KORE_LAYER_API int kore_layer_decode_dev(kore_layer_t L, const kore_layer_weight
     o5.up = L->up;
     o5.accumulate = 1;
     if (kore_qmv_mv_group_ex_dev(1, &w->w_down, L->gate, &o5, &x, avx2, s) != KORE_QMV_OK) return qmv_err(w->w_down, "down");
+    return KORE_LAYER_OK;
+}
+
+KORE_LAYER_API int kore_layer_prefill_dev(kore_layer_t L, const kore_layer_weights *w, kore_attn_t attn, int layer,
+                                          int pos0, int n_tok, float *x, void *stream) {
+    if (!L) return fail(nullptr, KORE_LAYER_E_INVALID, "layer handle is NULL");
+    if (int rc = check_call(L, w, attn, x)) return rc;
+    if (n_tok < 1 || n_tok > kMaxBatch) return fail(L, KORE_LAYER_E_INVALID, "n_tok must be 1..64 (kore's KORE_BMAX)");
+    void *s = stream ? stream : (void *)L->stream;
+    const int64_t E = L->E, FF = L->FF;
+    auto qmv_err = [&](kore_qmv_tensor_t t, const char *what) {
+        return fail(L, KORE_LAYER_E_STEP, std::string(what) + ": " + kore_qmv_last_error(t));
+    };
+    // 1. rmsnorm of every row, then q/k/v + biases (kore.cpp:1521-1532)
+    if (kore_qmv_rmsnorm_rows_dev(x, w->attn_norm, E, n_tok, L->eps, L->bxb, s) != KORE_QMV_OK)
+        return qmv_err(nullptr, "attn_norm");
+    kore_qmv_mv_opts o1{};
+    o1.bias[0] = w->bq;
+    o1.bias[1] = w->bk;
+    o1.bias[2] = w->bv;
+    kore_qmv_tensor_t qkv[3] = {w->wq, w->wk, w->wv};
+    float *qkv_out[3] = {L->bq, L->bk, L->bv};
+    if (kore_qmv_matmul_batch_group_ex_dev(3, qkv, L->bxb, n_tok, &o1, qkv_out, s) != KORE_QMV_OK)
+        return qmv_err(w->wq, "q/k/v");
+    // 2. RoPE + append + causal attention of the rows (kore.cpp:1533-1563)
+    if (kore_attn_prefill_dev(attn, layer, pos0, n_tok, L->n_head, L->n_head_kv, L->head_dim, L->bq, L->bk, L->bv,
+                              L->batt, s) != KORE_ATTN_OK)
+        return fail(L, KORE_LAYER_E_STEP, std::string("attention: ") + kore_attn_last_error(attn));
+    // 3. Wo, x += o (kore.cpp:1566-1570)
+    kore_qmv_mv_opts acc{};
+    acc.accumulate = 1;
+    if (kore_qmv_matmul_batch_group_ex_dev(1, &w->wo, L->batt, n_tok, &acc, &x, s) != KORE_QMV_OK)
+        return qmv_err(w->wo, "wo");
+    // 4. rmsnorm, gate/up, SwiGLU (kore.cpp:1572-1583)
+    if (kore_qmv_rmsnorm_rows_dev(x, w->ffn_norm, E, n_tok, L->eps, L->bxb, s) != KORE_QMV_OK)
+        return qmv_err(nullptr, "ffn_norm");
+    kore_qmv_tensor_t gu[2] = {w->w_gate, w->w_up};
+    float *gu_out[2] = {L->bgate, L->bup};
+    if (kore_qmv_matmul_batch_group_ex_dev(2, gu, L->bxb, n_tok, nullptr, gu_out, s) != KORE_QMV_OK)
+        return qmv_err(w->w_gate, "gate/up");
+    if (kore_qmv_swiglu_dev(L->bgate, L->bup, (int64_t)n_tok * FF, s) != KORE_QMV_OK) return qmv_err(nullptr, "swiglu");
+    // 5. down, x += o (kore.cpp:1585-1589)
+    if (kore_qmv_matmul_batch_group_ex_dev(1, &w->w_down, L->bgate, n_tok, &acc, &x, s) != KORE_QMV_OK)
+        return qmv_err(w->w_down, "down");
     return KORE_LAYER_OK;
 }
 

@@ -25,6 +25,8 @@ struct kore_model {
     kore_attn_t attn = nullptr;
     kore_layer_t layer = nullptr;
     float *x = nullptr, *logits = nullptr;
+    int bsz = 0;                                  // kore's e.bsz = min(64, ctx) (kore.cpp:1354)
+    float *bx = nullptr;                          // forward_batch()'s rows, [bsz][n_embd]
     hipStream_t stream = nullptr;
     std::string error;
 };
@@ -41,7 +43,7 @@ int fail(kore_model *m, int code, const std::string &msg) {
 void release(kore_model *m) {
     for (kore_qmv_tensor_t t : m->mats) kore_qmv_tensor_destroy(t);
     for (float *p : m->arrays) (void)hipFree(p);
-    for (void *p : {(void *)m->embd, (void *)m->x, (void *)m->logits})
+    for (void *p : {(void *)m->embd, (void *)m->x, (void *)m->logits, (void *)m->bx})
         if (p) (void)hipFree(p);
     if (m->layer) kore_layer_destroy(m->layer);
     if (m->attn) kore_attn_destroy(m->attn);
@@ -119,6 +121,8 @@ int build(kore_model *m, kore_gguf_t g, int ctx_max) {
     if (e == hipSuccess) e = hipMemcpy(m->embd, te.data, te.nbytes, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc((void **)&m->x, h.n_embd * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&m->logits, (size_t)m->n_vocab * sizeof(float));
+    m->bsz = std::min(64, m->ctx);
+    if (e == hipSuccess) e = hipMalloc((void **)&m->bx, (size_t)m->bsz * h.n_embd * sizeof(float));
     if (e != hipSuccess) return fail(m, KORE_MODEL_E_DEVICE, std::string("device buffers: ") + hipGetErrorString(e));
     m->embd_type = (int)te.type;
     m->weight_bytes += te.nbytes;
@@ -191,6 +195,41 @@ KORE_MODEL_API int kore_model_decode_dev(kore_model_t m, int token, int pos, int
             return fail(m, KORE_MODEL_E_DEVICE, std::string("logits: ") + kore_qmv_last_error(m->head));
     }
     return KORE_MODEL_OK;
+}
+
+KORE_MODEL_API int kore_model_prefill_dev(kore_model_t m, const int *tokens, int n_tok, int pos0, int want_logits,
+                                          void *stream) {
+    if (!m) return fail(nullptr, KORE_MODEL_E_RANGE, "model is NULL");
+    if (!tokens || n_tok <= 0 || n_tok > m->bsz || pos0 < 0 || pos0 + n_tok > m->ctx)   // kore.cpp:1490
+        return fail(m, KORE_MODEL_E_RANGE, "n_tok must be 1..min(64, ctx) and pos0 + n_tok <= ctx");
+    for (int z = 0; z < n_tok; ++z)                                                       // kore.cpp:1497
+        if (tokens[z] < 0 || tokens[z] >= m->n_vocab) return fail(m, KORE_MODEL_E_RANGE, "token out of range");
+    void *s = stream ? stream : (void *)m->stream;
+    const int E = (int)m->hp.n_embd;
+    for (int z = 0; z < n_tok; ++z)                                                       // kore.cpp:1496-1501
+        if (kore_qmv_get_row_dev(m->embd_type, m->embd, tokens[z], E, m->bx + (size_t)z * E, s) != KORE_QMV_OK)
+            return fail(m, KORE_MODEL_E_DEVICE, std::string("embedding: ") + kore_qmv_last_error(nullptr));
+    for (int l = 0; l < (int)m->layers.size(); ++l)
+        if (kore_layer_prefill_dev(m->layer, &m->layers[(size_t)l], m->attn, l, pos0, n_tok, m->bx, s) !=
+            KORE_LAYER_OK)
+            return fail(m, KORE_MODEL_E_DEVICE, std::string("layer: ") + kore_layer_last_error(m->layer));
+    if (want_logits) {                                 // the last row only (kore.cpp:1592-1596)
+        kore_qmv_mv_opts o{};
+        o.norm_w = m->out_norm;
+        o.norm_eps = m->hp.rms_eps;
+        const float *last = m->bx + (size_t)(n_tok - 1) * E;
+        if (kore_qmv_mv_group_ex_dev(1, &m->head, last, &o, &m->logits, 1, s) != KORE_QMV_OK)
+            return fail(m, KORE_MODEL_E_DEVICE, std::string("logits: ") + kore_qmv_last_error(m->head));
+    }
+    return KORE_MODEL_OK;
+}
+
+KORE_MODEL_API const float *kore_model_rows_dev(kore_model_t m) { return m ? m->bx : nullptr; }
+
+KORE_MODEL_API int kore_model_sync(kore_model_t m) {
+    if (!m) return fail(nullptr, KORE_MODEL_E_RANGE, "model is NULL");
+    const hipError_t e = hipStreamSynchronize(m->stream);
+    return e == hipSuccess ? KORE_MODEL_OK : fail(m, KORE_MODEL_E_DEVICE, hipGetErrorString(e));
 }
 
 KORE_MODEL_API const float *kore_model_logits_dev(kore_model_t m) { return m ? m->logits : nullptr; }

@@ -368,13 +368,18 @@ KORE_QMV_API int kore_qmv_mv(kore_qmv_tensor_t t, const float *x, float *out, in
     return rc;
 }
 
-KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
-                                                 float *const *out, void *stream) {
+KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
+                                                    const kore_qmv_mv_opts *opts, float *const *out, void *stream) {
     if (n < 1 || n > kMaxGroup || !t || !out) return fail(nullptr, KORE_QMV_E_INVALID, "n must be 1..4, t and out set");
     for (int k = 0; k < n; ++k)
         if (!t[k]) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
     kore_qmv_tensor *t0 = t[0];
     if (nb < 1 || nb > kGemmMaxB) return fail(t0, KORE_QMV_E_INVALID, "nb must be 1..64 (kore's KORE_BMAX)");
+    if (opts && (opts->norm_w || opts->up))
+        return fail(t0, KORE_QMV_E_INVALID, "the batched matmul takes bias and accumulate only (norm_w and up must be NULL)");
+    for (int k = 0; opts && k < n; ++k)
+        if (opts->bias[k])
+            if (int rc = check_dev_ptr(t0, opts->bias[k], 4, "bias")) return rc;
     if (int rc = check_dev_ptr(t0, x, 16, "x")) return rc;
     GemmArgs a{};
     a.n_mat = n;
@@ -385,7 +390,9 @@ KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t 
         if (t[k]->device != t0->device || t[k]->cols != t0->cols)
             return fail(t0, KORE_QMV_E_INVALID, "grouped tensors must share device and cols");
         if (int rc = check_dev_ptr(t0, out[k], 4, "out")) return rc;
-        a.m[k] = GemmMat{t[k]->w, t[k]->wd, out[k], (int)t[k]->rows, t[k]->type, a.tiles};
+        a.m[k] = GemmMat{t[k]->w,        t[k]->wd,                      out[k],
+                         (int)t[k]->rows, t[k]->type,                    a.tiles,
+                         opts ? opts->bias[k] : nullptr, opts ? opts->accumulate : 0};
         a.tiles += row_tiles(t[k]->rows);
     }
     GemmScratch &g = g_gemm[t0->device & 63];
@@ -396,6 +403,25 @@ KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t 
     hipError_t e = launch_gemm(a, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(t0, e, "matmul launch");
     return KORE_QMV_OK;
+}
+
+KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
+                                                 float *const *out, void *stream) {
+    return kore_qmv_matmul_batch_group_ex_dev(n, t, x, nb, nullptr, out, stream);
+}
+
+KORE_QMV_API int kore_qmv_rmsnorm_rows_dev(const float *x, const float *w, int64_t n, int rows, float eps, float *out,
+                                           void *stream) {
+    if (!x || !w || !out || n < 1 || n > INT32_MAX || rows < 1)
+        return fail(nullptr, KORE_QMV_E_INVALID, "x, w, out set, n >= 1 and rows >= 1 required");
+    const hipError_t e = launch_rmsnorm_rows(x, w, (int)n, rows, eps, out, (hipStream_t)stream);
+    return e == hipSuccess ? KORE_QMV_OK : hip_fail(nullptr, e, "rmsnorm launch");
+}
+
+KORE_QMV_API int kore_qmv_swiglu_dev(float *g, const float *u, int64_t n, void *stream) {
+    if (!g || !u || n < 1) return fail(nullptr, KORE_QMV_E_INVALID, "g, u set and n >= 1 required");
+    const hipError_t e = launch_swiglu(g, u, n, (hipStream_t)stream);
+    return e == hipSuccess ? KORE_QMV_OK : hip_fail(nullptr, e, "swiglu launch");
 }
 
 KORE_QMV_API int kore_qmv_matmul_batch_dev(kore_qmv_tensor_t t, const float *x, int nb, float *out, void *stream) {

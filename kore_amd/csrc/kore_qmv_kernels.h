@@ -86,6 +86,12 @@ hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool imag
 // -> body / d arrays above.
 hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, uint16_t *d, hipStream_t s);
 
+// kore's rmsnorm (kore.cpp:1367-1372) of each of n_rows rows of n values
+// (out may be x), bit-identical to kore's sequential double sum; and kore's
+// SwiGLU in place over n values (kore.cpp:1577-1581, exp rounded from double).
+hipError_t launch_rmsnorm_rows(const float *x, const float *w, int n, int n_rows, float eps, float *out, hipStream_t s);
+hipError_t launch_swiglu(float *g, const float *u, int64_t n, hipStream_t s);
+
 // kore's get_row (kore.cpp:384-407): row `row` of a table of rows of n values
 // of type F32 / F16 / BF16 / Q4_K / Q6_K (kore's block bytes) -> out[n] floats.
 hipError_t launch_get_row(int type, const uint8_t *data, int64_t row, int64_t n, float *out, hipStream_t s);
@@ -112,6 +118,8 @@ struct GemmMat {
     float *out;              // [B][rows]
     int rows, type;
     int tile0;               // first tile of this matrix in the launch
+    const float *bias;       // out = dot + bias[r] (kore's q/k/v biases), or nullptr
+    int accumulate;          // out = out + dot (kore's residual adds)
 };
 struct GemmArgs {
     GemmMat m[kMaxGroup];

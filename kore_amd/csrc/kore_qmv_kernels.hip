@@ -760,6 +760,43 @@ hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, 
 
 }  // namespace kore_qmv_gpu
 
+// ------------------------------------------------------------------ row-wise steps of forward_batch
+
+namespace kore_qmv_gpu {
+namespace {
+
+// kore's rmsnorm of row blockIdx.x (kore.cpp:1367-1372, 1522, 1573): the
+// certified scale of block_rms_scale, then x * scale * w with kore's roundings.
+__global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, const float *__restrict__ w, int n,
+                                                                float eps, float *out) {
+    __shared__ double red[2 * kThreads / 64];
+    const float *xr = x + (int64_t)blockIdx.x * n;
+    float *orow = out + (int64_t)blockIdx.x * n;
+    const float scale = block_rms_scale(xr, n, eps, red);
+    for (int i = threadIdx.x; i < n; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_kernel(float *__restrict__ g, const float *__restrict__ u, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) g[i] = kore_swiglu(g[i], u[i]);
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm_rows(const float *x, const float *w, int n, int n_rows, float eps, float *out, hipStream_t s) {
+    if (n <= 0 || n_rows <= 0 || !x || !w || !out) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n_rows), dim3(kThreads), 0, s, x, w, n, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(float *g, const float *u, int64_t n, hipStream_t s) {
+    if (n <= 0 || !g || !u) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g, u, n);
+    return hipGetLastError();
+}
+
+}  // namespace kore_qmv_gpu
+
 // ------------------------------------------------------------------ get_row
 
 namespace kore_qmv_gpu {

@@ -39,6 +39,7 @@ SYMBOLS = [
     ("kore_layer_create", _i, [C.POINTER(_vp), _i, _i, _i, _i, _f]),
     ("kore_layer_destroy", None, [_vp]),
     ("kore_layer_decode_dev", _i, [_vp, C.POINTER(_Weights), _vp, _i, _i, _vp, _i, _vp]),
+    ("kore_layer_prefill_dev", _i, [_vp, C.POINTER(_Weights), _vp, _i, _i, _i, _vp, _vp]),
     ("kore_layer_sync", _i, [_vp]),
     ("kore_layer_last_error", C.c_char_p, [_vp]),
 ]
@@ -124,6 +125,13 @@ class Layer:
         s = w.struct()
         self._check(lib().kore_layer_decode_dev(self._h, C.byref(s), attn.handle, layer, pos, x_ptr, int(avx2),
                                                 stream))
+
+    def prefill_dev(self, w: LayerWeights, attn, layer: int, pos0: int, n_tok: int, x_ptr: int,
+                    stream=None) -> None:
+        """kore's forward_batch() body for `layer` over n_tok rows at pos0..:
+        x (device, [n_tok][n_embd]) updated in place."""
+        s = w.struct()
+        self._check(lib().kore_layer_prefill_dev(self._h, C.byref(s), attn.handle, layer, pos0, n_tok, x_ptr, stream))
 
     def sync(self):
         self._check(lib().kore_layer_sync(self._h))

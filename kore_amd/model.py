@@ -35,6 +35,9 @@ def lib() -> C.CDLL:
                                 ("kore_model_get_info", C.c_int, [vp, C.POINTER(Info)]),
                                 ("kore_model_decode_dev", C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
                                 ("kore_model_logits_dev", vp, [vp]),
+                                ("kore_model_prefill_dev", C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+                                ("kore_model_rows_dev", vp, [vp]),
+                                ("kore_model_sync", C.c_int, [vp]),
                                 ("kore_model_decode", C.c_int, [vp, C.c_int, C.c_int, vp]),
                                 ("kore_model_attn", vp, [vp]),
                                 ("kore_model_last_error", C.c_char_p, [vp])):
@@ -69,6 +72,23 @@ class Model:
         out = np.zeros(self.info.n_vocab, np.float32) if want_logits else None
         self._check(lib().kore_model_decode(self._h, token, pos, out.ctypes.data if want_logits else None))
         return out
+
+    def prefill(self, tokens, pos0: int, want_logits: bool = True):
+        """kore's forward_batch(tokens, pos0, want_logits): (rows [n][n_embd],
+        logits of the last row or None), host copies."""
+        from . import hip
+        t = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        self._check(lib().kore_model_prefill_dev(self._h, t.ctypes.data, t.size, pos0, int(want_logits), None))
+        self._check(lib().kore_model_sync(self._h))
+        rows = np.zeros((t.size, self.info.hp.n_embd), np.float32)
+        hip.check(hip.lib().hipMemcpy(rows.ctypes.data, lib().kore_model_rows_dev(self._h), rows.nbytes, hip.D2H),
+                  "rows")
+        logits = None
+        if want_logits:
+            logits = np.zeros(self.info.n_vocab, np.float32)
+            hip.check(hip.lib().hipMemcpy(logits.ctypes.data, lib().kore_model_logits_dev(self._h), logits.nbytes,
+                                          hip.D2H), "logits")
+        return rows, logits
 
     def read_kv(self, layer: int, pos0: int, n: int):
         from . import _lib

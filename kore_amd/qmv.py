@@ -55,6 +55,9 @@ SYMBOLS = [
     ("kore_qmv_matmul_batch_group_dev", _i, [_i, _vp, _vp, _i, _vp, _vp]),
     ("kore_qmv_mv_group_ex_dev", _i, [_i, _vp, _vp, _vp, _vp, _i, _vp]),
     ("kore_qmv_get_row_dev", _i, [_i, _vp, _i64, _i64, _vp, _vp]),
+    ("kore_qmv_matmul_batch_group_ex_dev", _i, [_i, _vp, _vp, _i, _vp, _vp, _vp]),
+    ("kore_qmv_rmsnorm_rows_dev", _i, [_vp, _vp, _i64, _i, C.c_float, _vp, _vp]),
+    ("kore_qmv_swiglu_dev", _i, [_vp, _vp, _i64, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
     ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),
@@ -226,3 +229,27 @@ def mv_group_ex_dev(mats, x_ptr: int, out_ptrs, norm_w: int = None, norm_eps: fl
     hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
     outs = (C.c_void_p * n)(*out_ptrs)
     _check(lib().kore_qmv_mv_group_ex_dev(n, hs, x_ptr, C.byref(o), outs, int(avx2), stream))
+
+
+def matmul_batch_group_ex_dev(mats, x_ptr: int, nb: int, out_ptrs, bias=None, accumulate: bool = False,
+                              stream=None) -> None:
+    """kore_qmv_matmul_batch_group_ex_dev: the batched matmul with bias per
+    matrix and/or out += in the final store (device pointers)."""
+    n = len(mats)
+    o = MvOpts()
+    o.accumulate = int(accumulate)
+    for k, b in enumerate(bias or ()):
+        o.bias[k] = b
+    hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
+    outs = (C.c_void_p * n)(*out_ptrs)
+    _check(lib().kore_qmv_matmul_batch_group_ex_dev(n, hs, x_ptr, nb, C.byref(o), outs, stream))
+
+
+def rmsnorm_rows_dev(x_ptr: int, w_ptr: int, n: int, rows: int, eps: float, out_ptr: int, stream=None) -> None:
+    """kore's rmsnorm of `rows` rows of n floats (device pointers)."""
+    _check(lib().kore_qmv_rmsnorm_rows_dev(x_ptr, w_ptr, n, rows, eps, out_ptr, stream))
+
+
+def swiglu_dev(g_ptr: int, u_ptr: int, n: int, stream=None) -> None:
+    """kore's batched SwiGLU in place over n floats (device pointers)."""
+    _check(lib().kore_qmv_swiglu_dev(g_ptr, u_ptr, n, stream))

@@ -395,3 +395,27 @@ def layer_forward(kv: "KV", layer: int, pos: int, x: np.ndarray, lw: LayerWeight
     xq = quantize_q8K(rmsnorm(x, lw.ffn_norm, eps))
     g = swiglu(mv(4, xq), mv(5, xq))
     return x + mv(6, quantize_q8K(g))
+
+
+def layer_forward_batch(kv: "KV", layer: int, pos0: int, x: np.ndarray, lw: LayerWeights, n_ff: int, eps: float,
+                        avx2: bool = True) -> np.ndarray:
+    """kore's forward_batch() body for one layer (kore.cpp:1518-1589) over the
+    rows x [nb][E] at positions pos0..: returns the new residual rows; the KV
+    store gets the roped k and v rows."""
+    E, kvd = kv.E, kv.kv_dim
+    x = np.array(x, np.float32).reshape(-1, E)
+    shapes = [(E, E), (kvd, E), (kvd, E), (E, E), (n_ff, E), (n_ff, E), (E, n_ff)]
+
+    def mm(j, a):
+        return matmul_batch(lw.types[j], lw.mats[j], shapes[j][0], shapes[j][1], a, avx2=avx2)
+
+    xb = np.stack([rmsnorm(r, lw.attn_norm, eps) for r in x])
+    q = mm(0, xb) + lw.bq
+    k = mm(1, xb) + lw.bk
+    v = mm(2, xb) + lw.bv
+    att = kv.prefill(layer, pos0, q, k, v, avx2=avx2)
+    x = x + mm(3, att)
+    xb = np.stack([rmsnorm(r, lw.ffn_norm, eps) for r in x])
+    g = swiglu(mm(4, xb).reshape(-1), mm(5, xb).reshape(-1)).reshape(x.shape[0], n_ff)
+    return x + mm(6, g)
+

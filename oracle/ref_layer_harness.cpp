@@ -23,6 +23,7 @@
 //
 // GGUF mode (pins the loader and the whole token on a real file):
 //   kore_layer_ref --gguf-forward file.gguf CTX_MAX TOKEN...
+//   kore_layer_ref --gguf-forward-batch file.gguf CTX_MAX SPLIT TOKEN...
 // runs kore's load_model + engine_init(ctx_max, 4 threads, quantised path) and
 // forward(token, pos, logits) for the tokens at positions 0, 1, ...; prints one
 // JSON line {"ok", "ctx", "n_vocab", "avx2", "logits": [[...], ...]} (logits as
@@ -185,7 +186,42 @@ int gguf_forward(const char *path, int ctx_max, int n, char **toks) {
     return 0;
 }
 
+// kore_layer_ref --gguf-forward-batch file.gguf CTX_MAX SPLIT TOKEN...: kore's
+// forward_batch() over the tokens in two chunks, [0, SPLIT) at position 0
+// without logits and the rest at position SPLIT with logits; prints the last
+// chunk's residual rows (e.bx) and the logits as float bit patterns.
+int gguf_forward_batch(const char *path, int ctx_max, int split, int n, char **toks) {
+    Model m;
+    Engine e;
+    if (!load_model(path, m) || !engine_init(e, m, ctx_max, 4, false)) {
+        printf("{\"ok\": false}\n");
+        return 0;
+    }
+    std::vector<int> t((size_t)n);
+    for (int i = 0; i < n; ++i) t[(size_t)i] = atoi(toks[i]);
+    if (split <= 0 || split >= n || !forward_batch(e, t.data(), split, 0, false) ||
+        !forward_batch(e, t.data() + split, n - split, split, true)) {
+        printf("{\"ok\": false}\n");
+        return 0;
+    }
+    auto hex = [](const float *a, size_t k) {
+        for (size_t i = 0; i < k; ++i) {
+            uint32_t u;
+            memcpy(&u, a + i, 4);
+            printf("%s\"%08x\"", i ? ", " : "", u);
+        }
+    };
+    printf("{\"ok\": true, \"ctx\": %d, \"bsz\": %d, \"avx2\": %d, \"x\": [", e.ctx, e.bsz, (int)e.avx2);
+    hex(e.bx.data(), (size_t)(n - split) * m.hp.n_embd);
+    printf("], \"logits\": [");
+    hex(e.logits.data(), (size_t)e.n_vocab);
+    printf("]}\n");
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc >= 6 && std::string(argv[1]) == "--gguf-forward-batch")
+        return gguf_forward_batch(argv[2], atoi(argv[3]), atoi(argv[4]), argc - 5, argv + 5);
     if (argc >= 4 && std::string(argv[1]) == "--gguf-forward")
         return gguf_forward(argv[2], atoi(argv[3]), argc - 4, argv + 4);
     if (argc == 5 && std::string(argv[1]) == "--time")

@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Write small GGUF files and kore's own parse of each: tests/golden/gguf_*.gguf
 and gguf_*.json; and kore's whole engine on the tiny model's file
-(gguf_tiny_qwen2_forward.json: logits of four decode tokens).
+(gguf_tiny_qwen2_forward.json: logits of four decode tokens;
+gguf_tiny_qwen2_forward_batch.json: forward_batch() of two chunks).
 
 The files are written here from the GGUF layout (magic, version, tensor and
 metadata counts, typed key/value pairs, the tensor table, data aligned to
@@ -144,6 +145,17 @@ def main():
                    "source": "kore.cpp load_model + engine_init + forward(logits) via oracle/_ref/kore_layer_ref",
                    "kore": fwd}, f, indent=1)
     print("forward:", fwd["ok"], fwd["ctx"], fwd["n_vocab"])
+    # kore's forward_batch() on the same model: tokens 0..4 at position 0, then
+    # 5..8 at position 5 with logits (the residual rows of the second chunk)
+    tokens, split = [3, 7, 0, 11, 5, 2, 9, 10, 1], 5
+    r = subprocess.run([oracle.REF_LAYER_BIN, "--gguf-forward-batch", os.path.join(HERE, "gguf_tiny_qwen2.gguf"),
+                        "64", str(split)] + [str(t) for t in tokens], capture_output=True, text=True, check=True)
+    fwd = json.loads(r.stdout)
+    with open(os.path.join(HERE, "gguf_tiny_qwen2_forward_batch.json"), "w") as f:
+        json.dump({"file": "gguf_tiny_qwen2.gguf", "ctx_max": 64, "tokens": tokens, "split": split,
+                   "source": "kore.cpp load_model + engine_init + forward_batch x2 via oracle/_ref/kore_layer_ref",
+                   "kore": fwd}, f, indent=1)
+    print("forward_batch:", fwd["ok"], fwd["ctx"], fwd["bsz"], len(fwd["x"]))
 
 
 if __name__ == "__main__":

@@ -24,7 +24,8 @@ def test_library_exports_exactly_the_declared_symbols():
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     assert _declared() == exported
-    assert {"kore_layer_decode_dev", "kore_gguf_open", "kore_gguf_to_qmv"} <= exported
+    assert {"kore_layer_decode_dev", "kore_layer_prefill_dev", "kore_model_prefill_dev", "kore_model_rows_dev",
+            "kore_model_sync", "kore_gguf_open", "kore_gguf_to_qmv"} <= exported
 
 
 def test_rejections_without_a_gpu():
@@ -36,4 +37,5 @@ def test_rejections_without_a_gpu():
     assert L.kore_layer_create(C.byref(h), 300, 512, 2, 1, 1e-6) == layer.KORE_LAYER_E_INVALID   # 300 % 256
     assert L.kore_layer_create(C.byref(h), 256, 512, 3, 2, 1e-6) == layer.KORE_LAYER_E_INVALID   # 3 % 2
     assert L.kore_layer_decode_dev(None, None, None, 0, 0, None, 1, None) == layer.KORE_LAYER_E_INVALID
+    assert L.kore_layer_prefill_dev(None, None, None, 0, 0, 1, None, None) == layer.KORE_LAYER_E_INVALID
     assert b"NULL" in L.kore_layer_last_error(None)

@@ -35,6 +35,7 @@ def test_headers_declare_the_abi():
                            "kore_qmv_mv_dev", "kore_qmv_mv_group_dev", "kore_qmv_mv_group_ex_dev", "kore_qmv_get_row_dev",
                            "kore_qmv_matmul_batch",
                            "kore_qmv_matmul_batch_dev", "kore_qmv_matmul_batch_group_dev",
+                           "kore_qmv_matmul_batch_group_ex_dev", "kore_qmv_rmsnorm_rows_dev", "kore_qmv_swiglu_dev",
                            "kore_qmv_last_error", "kore_qmv_get_info", "kore_qmv_synth_dev"}
 
 

@@ -12,7 +12,7 @@ import oracle.gguf as ogguf
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 CASES = sorted(f[5:-5] for f in os.listdir(GOLD)
-               if f.startswith("gguf_") and f.endswith(".json") and not f.endswith("_forward.json"))
+               if f.startswith("gguf_") and f.endswith(".json") and "_forward" not in f)
 
 
 def _case(name):
@@ -97,10 +97,9 @@ def test_oracle_rejects_what_breaks_the_rules():
     assert not ogguf.parse(good[:-1])["ok"]                 # last tensor leaves the file by one byte
 
 
-def oracle_engine_logits(path, tokens, ctx_max=64):
-    """The oracle's kore engine over a GGUF file: engine_init's tensors
-    (kore.cpp:1274-1334), then per token get_row (kore.cpp:384-407), every
-    forward() layer and the logits (kore.cpp:1474-1478)."""
+def _oracle_engine(path, ctx_max):
+    """engine_init's tensors (kore.cpp:1274-1334) from the oracle's parse:
+    (hp, ctx, layers, f32, embedding row, output head (type, rows, bytes), kv)."""
     import oracle
     data = open(path, "rb").read()
     p = ogguf.parse(data)
@@ -133,17 +132,49 @@ def oracle_engine_logits(path, tokens, ctx_max=64):
                                           f32(b + "attn_q.bias"), f32(b + "attn_k.bias"), f32(b + "attn_v.bias")))
     kv = oracle.KV(hp["n_layer"], ctx, NH, NKV, E // NH, hp["rope_base"])
     et, edims, eb = tens["token_embd.weight"]
-    ot, odims, ob = tens["output.weight"]
     row_bytes = len(eb) // edims[1]
+
+    def emb(tok):
+        r = eb[tok * row_bytes:(tok + 1) * row_bytes]
+        return oracle.dequant_row(et, r, E) if et in (12, 14) else r.view(np.float32).copy()
+
+    ot, odims, ob = tens["output.weight"]
+    return hp, ctx, layers, f32, emb, (ot, odims[1], ob), kv
+
+
+def _oracle_logits(hp, f32, head, x):
+    """forward()'s logits (kore.cpp:1474-1478)."""
+    import oracle
+    ot, rows, ob = head
+    xq = oracle.quantize_q8K(oracle.rmsnorm(x, f32("output_norm.weight"), hp["rms_eps"]))
+    return oracle.qmatvec(ot, ob, rows, hp["n_embd"], xq, avx2=True)
+
+
+def oracle_engine_logits(path, tokens, ctx_max=64):
+    """The oracle's kore engine over a GGUF file: engine_init, then per token
+    get_row (kore.cpp:384-407), every forward() layer and the logits."""
+    import oracle
+    hp, ctx, layers, f32, emb, head, kv = _oracle_engine(path, ctx_max)
     out = []
     for pos, tok in enumerate(tokens):
-        x = oracle.dequant_row(et, eb[tok * row_bytes:(tok + 1) * row_bytes], E) if et in (12, 14) else \
-            eb[tok * row_bytes:(tok + 1) * row_bytes].view(np.float32).copy()
+        x = emb(tok)
         for l, lw in enumerate(layers):
-            x = oracle.layer_forward(kv, l, pos, x, lw, FF, hp["rms_eps"], avx2=True)
-        xq = oracle.quantize_q8K(oracle.rmsnorm(x, f32("output_norm.weight"), hp["rms_eps"]))
-        out.append(oracle.qmatvec(ot, ob, odims[1], E, xq, avx2=True))
+            x = oracle.layer_forward(kv, l, pos, x, lw, hp["n_ff"], hp["rms_eps"], avx2=True)
+        out.append(_oracle_logits(hp, f32, head, x))
     return ctx, np.stack(out), kv
+
+
+def oracle_engine_batch(path, tokens, split, ctx_max=64):
+    """The oracle's forward_batch() (kore.cpp:1486-1600) over the tokens in two
+    chunks, [0, split) at position 0 and the rest at `split`: the second
+    chunk's residual rows and the logits of its last row."""
+    import oracle
+    hp, ctx, layers, f32, emb, head, kv = _oracle_engine(path, ctx_max)
+    for pos0, chunk in ((0, tokens[:split]), (split, tokens[split:])):
+        x = np.stack([emb(t) for t in chunk])
+        for l, lw in enumerate(layers):
+            x = oracle.layer_forward_batch(kv, l, pos0, x, lw, hp["n_ff"], hp["rms_eps"], avx2=True)
+    return ctx, x, _oracle_logits(hp, f32, head, x[-1]), kv
 
 
 def test_oracle_engine_matches_kore_logits():
@@ -153,3 +184,18 @@ def test_oracle_engine_matches_kore_logits():
     assert kore["ok"] and kore["avx2"] == 1 and ctx == kore["ctx"]
     want = np.array([[int(h, 16) for h in row] for row in kore["logits"]], np.uint32)
     assert np.array_equal(logits.astype(np.float32).view(np.uint32), want)
+
+
+def test_oracle_forward_batch_matches_kore():
+    man = json.load(open(os.path.join(GOLD, "gguf_tiny_qwen2_forward_batch.json")))
+    kore = man["kore"]
+    ctx, x, logits, _ = oracle_engine_batch(os.path.join(GOLD, man["file"]), man["tokens"], man["split"],
+                                            man["ctx_max"])
+    assert kore["ok"] and kore["avx2"] == 1 and ctx == kore["ctx"]
+    hexes = lambda a: np.array([int(h, 16) for h in a], np.uint32)   # noqa: E731
+    assert np.array_equal(x.astype(np.float32).reshape(-1).view(np.uint32), hexes(kore["x"]))
+    assert np.array_equal(logits.astype(np.float32).view(np.uint32), hexes(kore["logits"]))
+    # the batch and the token-at-a-time paths differ (matmul in float vs Q8_K matvec)
+    _, dec, _ = oracle_engine_logits(os.path.join(GOLD, man["file"]), man["tokens"], man["ctx_max"])
+    assert not np.array_equal(dec[-1].astype(np.float32), logits.astype(np.float32))
+
