@@ -485,14 +485,9 @@ def gpu_gemm(qt, chunks: int, warmup: int):
                 op_ms=op_ms.reshape(n_ev, len(ops)), first_raw=first_raw, first_x=xb, first_out=got)
 
 
-def gpu_token(qt, tokens: int, warmup: int):
-    """Whole 7B decode tokens as kore's forward() runs them (kore.cpp:1397-1484):
-    28 layers through kore_layer_decode_dev (rmsnorm+quant+q/k/v+bias, RoPE +
-    append + attention, Wo + residual, rmsnorm+quant+gate/up, SwiGLU+quant+down
-    + residual) and the logits (rmsnorm+quant+output head), at positions
-    4096.. over a cache filled to 4096, driven from C++."""
-    from kore_amd import KoreAttn, hip
-    from kore_amd.layer import Layer, LayerWeights, _Weights
+def _klb():
+    """libkore_layer_bench.so with its two drivers typed."""
+    from kore_amd.layer import _Weights
     from kore_amd.layer import lib as layer_lib
     layer_lib()
     path = os.path.join(ROOT, "kore_amd", "libkore_layer_bench.so")
@@ -502,11 +497,17 @@ def gpu_token(qt, tokens: int, warmup: int):
     vp = C.c_void_p
     B.klb_tokens.argtypes = [vp, C.POINTER(_Weights), C.c_int, vp, vp, vp, C.c_float, vp, C.c_int, C.c_int, C.c_int,
                              vp, vp, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_double)]
-    mats, tensors, _ = qt
-    rng = np.random.default_rng(QMV_SEED + 2)
-    attn = KoreAttn(NL, DEC_CTX, NH, NKV, HD, ROPE_BASE)
-    print("[bench] token: filling the 28-layer cache to 4096", file=sys.stderr, flush=True)
-    _fill_cache(attn, NL, DEC_POS0, KVD, 11, None)
+    B.klb_prefill.argtypes = [vp, C.POINTER(_Weights), C.c_int, vp, vp, vp, C.c_float, vp, C.c_int, C.c_int, C.c_int,
+                              vp, vp, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_double)]
+    return B
+
+
+def _engine_weights(qt, rng):
+    """The 28 layers' device weights (the synthetic Q4_K_M matrices of qt plus
+    norms and biases) as kore_layer_weights, and the output norm."""
+    from kore_amd import hip
+    from kore_amd.layer import LayerWeights, _Weights
+    _, tensors, _ = qt
     lws, bufs = [], []
     for l in range(NL):
         lw = LayerWeights()
@@ -519,6 +520,25 @@ def gpu_token(qt, tokens: int, warmup: int):
         lws.append(lw)
     warr = (_Weights * NL)(*[lw.struct() for lw in lws])
     out_norm = hip.DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(E)).astype(np.float32))
+    return warr, out_norm, bufs + [out_norm]
+
+
+def gpu_token(qt, tokens: int, warmup: int):
+    """Whole 7B decode tokens as kore's forward() runs them (kore.cpp:1397-1484):
+    28 layers through kore_layer_decode_dev (rmsnorm+quant+q/k/v+bias, RoPE +
+    append + attention, Wo + residual, rmsnorm+quant+gate/up, SwiGLU+quant+down
+    + residual) and the logits (rmsnorm+quant+output head), at positions
+    4096.. over a cache filled to 4096, driven from C++."""
+    from kore_amd import KoreAttn, hip
+    from kore_amd.layer import Layer
+    from kore_amd.layer import lib as layer_lib
+    B = _klb()
+    _, tensors, _ = qt
+    rng = np.random.default_rng(QMV_SEED + 2)
+    attn = KoreAttn(NL, DEC_CTX, NH, NKV, HD, ROPE_BASE)
+    print("[bench] token: filling the 28-layer cache to 4096", file=sys.stderr, flush=True)
+    _fill_cache(attn, NL, DEC_POS0, KVD, 11, None)
+    warr, out_norm, bufs = _engine_weights(qt, rng)
     emb = hip.DeviceBuffer.from_array(np.stack([_act(rng, E) for _ in range(tokens)]))
     x, logits = hip.DeviceBuffer(E), hip.DeviceBuffer(QMV_VOCAB)
     L = Layer(E, QMV_FF, NH, NKV, 1e-6)
@@ -536,10 +556,89 @@ def gpu_token(qt, tokens: int, warmup: int):
     run(1, C.byref(region))
     res = dict(region_ms=region.value, wall_ms=wall.value, tokens=tokens)
     L.close()
-    for b in bufs + [out_norm, emb, x, logits]:
+    for b in bufs + [emb, x, logits]:
         b.free()
     attn.close()
     return res
+
+
+PROMPT_NB = 64   # kore's KORE_BMAX rows per forward_batch() call (kore.cpp:690)
+
+
+def gpu_prompt(qt, chunks: int, warmup: int):
+    """A 7B prompt prefill as kore's forward_batch() runs it (kore.cpp:1486-1598)
+    in 64-token chunks at positions 0, 64, ..: per chunk 28 layers through
+    kore_layer_prefill_dev (rmsnorm rows, q/k/v matmul + bias, RoPE + append +
+    causal attention, Wo + residual, rmsnorm rows, gate/up matmul, SwiGLU, down
+    + residual) and the last row's logits, driven from C++."""
+    from kore_amd import KoreAttn, hip
+    from kore_amd.layer import Layer
+    from kore_amd.layer import lib as layer_lib
+    B = _klb()
+    _, tensors, _ = qt
+    rng = np.random.default_rng(QMV_SEED + 3)
+    n_tok = chunks * PROMPT_NB
+    attn = KoreAttn(NL, n_tok, NH, NKV, HD, ROPE_BASE)
+    warr, out_norm, bufs = _engine_weights(qt, rng)
+    emb = hip.DeviceBuffer.from_array(np.stack([_act(rng, E) for _ in range(n_tok)]))
+    x, logits = hip.DeviceBuffer(PROMPT_NB * E), hip.DeviceBuffer(QMV_VOCAB)
+    L = Layer(E, QMV_FF, NH, NKV, 1e-6)
+    region, wall = C.c_float(0), C.c_double(0)
+
+    def run(reps, reg=None):
+        rc = B.klb_prefill(L._h, warr, NL, attn.handle, tensors[7 * NL].handle, out_norm.ptr, 1e-6, emb.ptr, E,
+                           PROMPT_NB, chunks, x.ptr, logits.ptr, reps, reg, C.byref(wall))
+        if rc != 0:
+            raise RuntimeError(f"klb_prefill failed ({rc}): {layer_lib().kore_layer_last_error(L._h).decode()}")
+
+    if warmup:
+        run(warmup)
+    print(f"[bench] prompt: {n_tok} timed 7B prompt tokens in {chunks} chunks", file=sys.stderr, flush=True)
+    run(1, C.byref(region))
+    res = dict(region_ms=region.value, wall_ms=wall.value, chunks=chunks, tokens=n_tok)
+    L.close()
+    for b in bufs + [emb, x, logits]:
+        b.free()
+    attn.close()
+    return res
+
+
+def prompt_report(p, mats):
+    """Matmul flops per chunk: 2 * 64 * rows * cols over the 28 layers' seven
+    matrices (attention and the logits matvec not counted)."""
+    layer_mats = [m for m in mats if not m[0].startswith("output")]
+    flops = sum(2 * PROMPT_NB * r * c for _, _, r, c in layer_mats)
+    s_chunk = p["region_ms"] / 1e3 / p["chunks"]
+    return {
+        "workload": f"Qwen2.5-7B-shape prompt prefill as kore's forward_batch() runs it: {p['tokens']} tokens in "
+                    f"{p['chunks']} chunks of 64 at positions 0, 64, .. (28 layers: rmsnorm rows, q/k/v batched "
+                    "matmul + bias, RoPE + append + causal attention, Wo + residual, rmsnorm rows, gate/up matmul, "
+                    "SwiGLU, down + residual; then the last row's logits), synthetic Q4_K/Q6_K weights",
+        "ms_per_chunk_gpu": round(s_chunk * 1e3, 3),
+        "ms_per_chunk_wall": round(p["wall_ms"] / p["chunks"], 3),
+        "tokens_per_s": round(PROMPT_NB / s_chunk, 1),
+        "matmul_flop_per_chunk": flops,
+        "matmul_tflops_effective": round(flops / s_chunk / 1e12, 2),
+    }
+
+
+def cpu_prompt(seconds: float, threads: int):
+    """kore's own forward_batch() (oracle/_ref/kore_layer_ref --time-batch, built
+    from kore.cpp) on the synthetic 7B engine, 64-token chunks."""
+    import subprocess
+
+    import oracle
+    if not os.path.exists(oracle.REF_LAYER_BIN):
+        return None
+    r = subprocess.run([oracle.REF_LAYER_BIN, "--time-batch", str(threads), str(seconds)],
+                       capture_output=True, text=True, check=True)
+    j = json.loads(r.stdout)
+    return {"value": round(j["tokens"] / j["seconds"], 3), "unit": "tokens/s", "cores": j["threads"],
+            "kind": "reference",
+            "sample": f"kore's own forward_batch() (kore.cpp:1486-1598, matmul_batch_float with AVX2: "
+                      f"{bool(j['avx2'])}) built from kore.cpp with kore's flags, {j['threads']} threads, on a "
+                      f"synthetic Qwen2.5-7B-shape engine: {j['chunks']} chunks of 64 tokens at positions 0..511 "
+                      f"in {j['seconds']:.1f} s (after one warm-up chunk); host {_cpu_model()}"}
 
 
 def token_report(t, mats):
@@ -893,6 +992,9 @@ def main(argv=None):
     ap.add_argument("--no-token", action="store_true", help="skip the whole-token decode leg")
     ap.add_argument("--token-only", action="store_true", help="run only the whole-token decode leg")
     ap.add_argument("--token-count", type=int, default=32, help="timed 7B decode tokens of the whole-token leg")
+    ap.add_argument("--no-prompt", action="store_true", help="skip the whole-prompt prefill leg")
+    ap.add_argument("--prompt-only", action="store_true", help="run only the whole-prompt prefill leg")
+    ap.add_argument("--prompt-chunks", type=int, default=8, help="64-token chunks of the whole-prompt leg")
     ap.add_argument("--cpu-threads", type=int, default=16,
                     help="threads of kore's own matvec in the CPU baseline (the GPU box's CPU share)")
     ap.add_argument("--cpu-prefill-layers", type=int, default=2)
@@ -928,9 +1030,11 @@ def main(argv=None):
     clk = C.c_int(0)
     hip.lib().hipDeviceGetAttribute(C.byref(clk), 5, 0)   # hipDeviceAttributeClockRate (kHz)
 
-    if args.matvec_only or args.gemm_only or args.token_only:
+    if args.matvec_only or args.gemm_only or args.token_only or args.prompt_only:
         qt = qmv_tensors()
-        if args.token_only:
+        if args.prompt_only:
+            out = {"prompt": prompt_report(gpu_prompt(qt, args.prompt_chunks, 1), qt[0])}
+        elif args.token_only:
             out = {"token": token_report(gpu_token(qt, args.token_count, 1), qt[0])}
         elif args.matvec_only:
             out = {"matvec": matvec_report(gpu_matvec(qt, args.matvec_tokens, args.matvec_warmup),
@@ -950,6 +1054,7 @@ def main(argv=None):
     mv = None if args.no_matvec else gpu_matvec(qt, args.matvec_tokens, args.matvec_warmup)
     gm = None if args.no_gemm else gpu_gemm(qt, args.gemm_chunks, args.gemm_warmup)
     tk = None if (args.no_token or qt is None) else gpu_token(qt, args.token_count, 1)
+    pr = None if (args.no_prompt or qt is None) else gpu_prompt(qt, args.prompt_chunks, 1)
     if qt is not None:
         for m in qt[1]:
             m.close()
@@ -1026,6 +1131,8 @@ def main(argv=None):
         res["gemm"] = gemm_report(gm, args.gemm_chunks)
     if tk is not None:
         res["token"] = token_report(tk, qt[0])
+    if pr is not None:
+        res["prompt"] = prompt_report(pr, qt[0])
     if not args.no_cpu:
         print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
               flush=True)
@@ -1064,6 +1171,10 @@ def main(argv=None):
         if tk is not None:
             print(f"[bench] cpu baseline: kore's forward(), {args.cpu_threads} threads", file=sys.stderr, flush=True)
             res["token"]["cpu_baseline"] = cpu_token(args.cpu_seconds, args.cpu_threads)
+        if pr is not None:
+            print(f"[bench] cpu baseline: kore's forward_batch(), {args.cpu_threads} threads", file=sys.stderr,
+                  flush=True)
+            res["prompt"]["cpu_baseline"] = cpu_prompt(args.cpu_seconds, args.cpu_threads)
         if pf is not None:
             print(f"[bench] cpu baseline: prefill sample ({args.cpu_prefill_layers} layers)", file=sys.stderr,
                   flush=True)

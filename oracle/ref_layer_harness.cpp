@@ -24,6 +24,8 @@
 // GGUF mode (pins the loader and the whole token on a real file):
 //   kore_layer_ref --gguf-forward file.gguf CTX_MAX TOKEN...
 //   kore_layer_ref --gguf-forward-batch file.gguf CTX_MAX SPLIT TOKEN...
+//   kore_layer_ref --time-batch THREADS SECONDS   (forward_batch() of 64-token
+//   chunks at positions 0, 64, .., 448 on the synthetic 7B engine of --time)
 // runs kore's load_model + engine_init(ctx_max, 4 threads, quantised path) and
 // forward(token, pos, logits) for the tokens at positions 0, 1, ...; prints one
 // JSON line {"ok", "ctx", "n_vocab", "avx2", "logits": [[...], ...]} (logits as
@@ -98,9 +100,9 @@ void synth(OwnedTensor &o, uint32_t type, uint64_t cols, uint64_t rows, uint64_t
     o.t.data = o.bytes.data();
 }
 
-int time_mode(unsigned nth, double min_s, int pos0) {
+int time_mode(unsigned nth, double min_s, int pos0, bool batch) {
     const int NL = 28, E = 3584, FF = 18944, NH = 28, NKV = 4, HD = 128, VOCAB = 152064;
-    const int kvd = NKV * HD, ctx = pos0 + 256;
+    const int kvd = NKV * HD, ctx = batch ? 512 : pos0 + 256;
     Engine e;
     e.hp.n_layer = NL; e.hp.n_embd = E; e.hp.n_ff = FF; e.hp.n_head = NH; e.hp.n_head_kv = NKV;
     e.hp.n_ctx = (uint32_t)ctx; e.hp.n_vocab = VOCAB; e.hp.rope_base = 1e6f; e.hp.rms_eps = 1e-6f;
@@ -148,6 +150,28 @@ int time_mode(unsigned nth, double min_s, int pos0) {
     e.scores.resize((size_t)ctx); e.logits.resize((size_t)VOCAB);
     e.xq_e.resize((size_t)(E / 256 + 1)); e.xq_f.resize((size_t)FF / 256);
     e.scratch.resize((size_t)E);
+    if (batch) {                                               // engine_init's batch buffers (kore.cpp:1354-1363)
+        const size_t B = 64;
+        e.bsz = 64;
+        e.bemb.resize(B * E); e.bx.resize(B * E); e.bxb.resize(B * E); e.bq.resize(B * E); e.batt.resize(B * E);
+        e.bo.resize(B * E); e.bk.resize(B * kvd); e.bv.resize(B * kvd); e.bgate.resize(B * FF); e.bup.resize(B * FF);
+        e.bscores.resize(B * (size_t)ctx); e.bc_rope.resize(B * (size_t)half); e.bs_rope.resize(B * (size_t)half);
+        e.bxt.resize(B * FF);
+        std::vector<int> toks(B, 0);
+        if (!forward_batch(e, toks.data(), 64, 0, true)) return 5;   // warm-up
+        int chunks = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        double el = 0;
+        do {                                                   // 64-token chunks at 0, 64, .., 448 in turn
+            if (!forward_batch(e, toks.data(), 64, 64 * (chunks % 8), true)) return 5;
+            ++chunks;
+            el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        } while (el < min_s);
+        printf("{\"tokens\": %d, \"chunks\": %d, \"seconds\": %.6f, \"threads\": %u, \"avx2\": %d, "
+               "\"checksum\": %.9g}\n", chunks * 64, chunks, el, nth, (int)e.avx2,
+               (double)e.logits[(size_t)VOCAB / 2]);
+        return 0;
+    }
     if (!forward(e, 0, pos0, true)) return 5;                  // warm-up
     int tokens = 0;
     const auto t0 = std::chrono::steady_clock::now();
@@ -225,7 +249,9 @@ int main(int argc, char **argv) {
     if (argc >= 4 && std::string(argv[1]) == "--gguf-forward")
         return gguf_forward(argv[2], atoi(argv[3]), argc - 4, argv + 4);
     if (argc == 5 && std::string(argv[1]) == "--time")
-        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]));
+        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), false);
+    if (argc == 4 && std::string(argv[1]) == "--time-batch")
+        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), 0, true);
     if (argc != 3) { fprintf(stderr, "usage: kore_layer_ref job.bin result.bin | --time THREADS SECONDS POS\n"); return 2; }
     FILE *in = fopen(argv[1], "rb");
     FILE *out = fopen(argv[2], "wb");
