@@ -86,15 +86,10 @@ __device__ __forceinline__ void two_sum(double a, double b, double &s, double &e
 // it.  When the float scale is the same at both ends of that interval it is
 // kore's (the scale is monotone in ss); otherwise one thread runs kore's loop.
 // red: 2 * kThreads / 64 doubles of LDS (at least one).
-__device__ float block_rms_scale(const float *x, int n, float eps, double *red) {
+// The reduction and certification of block_rms_scale from each thread's
+// double-double partial sum (hi, lo) of x[t], x[t + kThreads], ...
+__device__ float block_rms_scale_from(double hi, double lo, const float *x, int n, float eps, double *red) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    double hi = 0.0, lo = 0.0;
-    for (int i = t; i < n; i += kThreads) {
-        double s, e;
-        two_sum(hi, (double)x[i] * (double)x[i], s, e);
-        hi = s;
-        lo += e;
-    }
     // wave, then the four waves in order: one barrier
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -133,6 +128,28 @@ __device__ float block_rms_scale(const float *x, int n, float eps, double *red) 
     const float sc = kore_rms_scale(red[0], n, eps);
     __syncthreads();
     return sc;
+}
+
+__device__ float block_rms_scale(const float *x, int n, float eps, double *red) {
+    // 8 loads at a time issued ahead of the dependent sum chain (clamped
+    // indexes: no load waits on a branch); a slot past n adds 0.0, which leaves
+    // hi and lo unchanged, so the order is that of one value at a time
+    constexpr int kPer = 8;
+    double hi = 0.0, lo = 0.0;
+    for (int i0 = threadIdx.x; i0 < n; i0 += kPer * kThreads) {
+        float v[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) v[j] = x[min(i0 + j * kThreads, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const float xv = i0 + j * kThreads < n ? v[j] : 0.0f;
+            double s, e;
+            two_sum(hi, (double)xv * (double)xv, s, e);
+            hi = s;
+            lo += e;
+        }
+    }
+    return block_rms_scale_from(hi, lo, x, n, eps, red);
 }
 
 // kore's SwiGLU of one value (kore.cpp:1466-1467): g / (1.0f + std::exp(-g)) * u.
@@ -772,8 +789,37 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, 
     __shared__ double red[2 * kThreads / 64];
     const float *xr = x + (int64_t)blockIdx.x * n;
     float *orow = out + (int64_t)blockIdx.x * n;
-    const float scale = block_rms_scale(xr, n, eps, red);
-    for (int i = threadIdx.x; i < n; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
+    constexpr int kPer = 16;
+    if (n > kPer * kThreads) {
+        const float scale = block_rms_scale(xr, n, eps, red);
+        for (int i = threadIdx.x; i < n; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
+        return;
+    }
+    // rows up to 4096: every load of x and w issued up front (clamped indexes,
+    // so no load waits on a branch), the sum in block_rms_scale's order; a
+    // slot past n adds 0.0, which leaves hi and lo unchanged
+    float v[kPer], wv[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = min((int)threadIdx.x + j * kThreads, n - 1);
+        v[j] = xr[i];
+        wv[j] = w[i];
+    }
+    double hi = 0.0, lo = 0.0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const float xv = (int)threadIdx.x + j * kThreads < n ? v[j] : 0.0f;
+        double s, e;
+        two_sum(hi, (double)xv * (double)xv, s, e);
+        hi = s;
+        lo += e;
+    }
+    const float scale = block_rms_scale_from(hi, lo, xr, n, eps, red);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = (int)threadIdx.x + j * kThreads;
+        if (i < n) orow[i] = (v[j] * scale) * wv[j];
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(float *__restrict__ g, const float *__restrict__ u, int64_t n) {
