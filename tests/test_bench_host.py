@@ -49,3 +49,16 @@ def test_gemm_report_fields():
     assert abs(r["tflops"] - flop / 0.01 / 1e12) < 0.01
     assert r["roofline"]["bound"] == "mfma" and r["roofline"]["peak"] == bench.FP32_MFMA_PEAK_TFLOPS
     assert r["roofline"]["kernel"] == "ffn_gate_q4k+ffn_up_q4k"
+
+
+def test_token_and_prompt_report_fields():
+    mats = _mats()
+    t = bench.token_report({"region_ms": 64.0, "wall_ms": 64.5, "tokens": 32}, mats)
+    assert t["ms_per_token_gpu"] == 2.0 and t["tokens_per_s"] == 500.0
+    assert abs(t["gbs"] - (t["weight_bytes_per_token"] + t["kv_bytes_per_token"]) / 2e-3 / 1e9) < 0.1
+    p = bench.prompt_report({"region_ms": 80.0, "wall_ms": 80.4, "chunks": 8, "tokens": 512}, mats)
+    # the seven matrices of 28 layers at 64 rows: 2 * 64 * rows * cols, the head not counted
+    flops = 2 * 64 * bench.NL * (3584 * 3584 * 2 + 512 * 3584 * 2 + 18944 * 3584 * 3)
+    assert p["matmul_flop_per_chunk"] == flops
+    assert p["ms_per_chunk_gpu"] == 10.0 and p["tokens_per_s"] == 6400.0
+    assert abs(p["matmul_tflops_effective"] - flops / 1e-2 / 1e12) < 0.01
