@@ -322,7 +322,7 @@ def gpu_other_workloads(quick: bool):
         chunk = {"us_per_layer_gpu": round(per_s * 1e6, 2), "flop_per_layer": F,
                  "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
                               "unit": "TFLOP/s", "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4)}}
-        dec = _decode_leg(a, nl, W, 1, 256, 0, nh, nkv, hd, 5, lambda s: W)
+        dec = _decode_leg(a, nl, W, 1, 256, 8, nh, nkv, hd, 5, lambda s: W)
         res["chunk_1p5b_1024_at_7168"] = dict(chunk, workload="Qwen2.5-1.5B-shape causal prefill chunk, 28 layers, "
                                                               "12/2/128, 1024 rows at 7168 onto 7168 cached rows")
         res["decode_1p5b_sliding_8192"] = dict(dec, workload="Qwen2.5-1.5B-shape decode, 28 layers, ring of 8192 "

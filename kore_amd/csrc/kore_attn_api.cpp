@@ -24,10 +24,11 @@ struct kore_attn {
     int device = 0, num_cu = 0;
     hipStream_t stream = nullptr;
     float *d_k = nullptr, *d_v = nullptr;    // [layer][kv_head][slot][head_dim]
-    float2 *d_cs = nullptr;                  // RoPE table [cs_len][head_dim/2]
-    int cs_len = 0;
+    float2 *d_cs = nullptr;                  // RoPE table [ctx][head_dim/2] (prefill, append)
     std::vector<float> inv_freq;
-    float *d_part_o = nullptr, *d_part_ml = nullptr;
+    RopeRow dec_cs{};                        // (cos, sin) of the last decode position
+    int dec_cs_pos = -1;
+    float *d_part_o = nullptr;               // decode split partials (o, then max/sum)
     int max_split = 0;
     float *d_pf_part = nullptr;              // prefill key-segment partials
     size_t pf_part_floats = 0;
@@ -78,23 +79,31 @@ void fill_rope_rows(const std::vector<float> &inv_freq, int p0, int p1, std::vec
         }
 }
 
-int ensure_rope(kore_attn *h, int need) {
-    if (need <= h->cs_len) return KORE_ATTN_OK;
+// The table of positions 0..ctx-1, built once at create: prefill and append
+// never reach past ctx (kore.cpp:1490), and a decode takes its one row by
+// value (decode_row), so nothing on a per-call path grows or reallocates it.
+int build_rope_table(kore_attn *h) {
     const int half = h->head_dim / 2;
-    int len = std::max(need, h->cs_len * 2);
     std::vector<float2> rows;
-    fill_rope_rows(h->inv_freq, 0, len, rows);
-    float2 *d = nullptr;
-    HIP_TRY(h, hipMalloc(&d, sizeof(float2) * (size_t)len * half));
-    hipError_t e = hipMemcpy(d, rows.data(), sizeof(float2) * rows.size(), hipMemcpyHostToDevice);
-    if (e != hipSuccess) { (void)hipFree(d); return hip_fail(h, e, "rope table upload"); }
-    if (h->d_cs) {
-        HIP_TRY(h, hipDeviceSynchronize());  // an older table may still be read
-        (void)hipFree(h->d_cs);
-    }
-    h->d_cs = d;
-    h->cs_len = len;
+    fill_rope_rows(h->inv_freq, 0, h->ctx, rows);
+    HIP_TRY(h, hipMalloc(&h->d_cs, sizeof(float2) * (size_t)h->ctx * half));
+    HIP_TRY(h, hipMemcpy(h->d_cs, rows.data(), sizeof(float2) * rows.size(), hipMemcpyHostToDevice));
     return KORE_ATTN_OK;
+}
+
+// (cos, sin) of one decode position (kore.cpp:1405-1410), kept for the next
+// call: kore's layer loop decodes every layer at the same position.
+const RopeRow &decode_row(kore_attn *h, int pos) {
+    if (pos != h->dec_cs_pos) {
+        const int half = h->head_dim / 2;
+        for (int i = 0; i < half; ++i) {
+            const double ang = (double)pos * h->inv_freq[(size_t)i];
+            h->dec_cs.cs[2 * i] = (float)std::cos(ang);
+            h->dec_cs.cs[2 * i + 1] = (float)std::sin(ang);
+        }
+        h->dec_cs_pos = pos;
+    }
+    return h->dec_cs;
 }
 
 int check_geometry(kore_attn *h, int n_head, int n_head_kv, int head_dim) {
@@ -141,7 +150,6 @@ void release(kore_attn *h) {
     if (h->d_v) (void)hipFree(h->d_v);
     if (h->d_cs) (void)hipFree(h->d_cs);
     if (h->d_part_o) (void)hipFree(h->d_part_o);
-    if (h->d_part_ml) (void)hipFree(h->d_part_ml);
     if (h->d_pf_part) (void)hipFree(h->d_pf_part);
     if (h->d_io) (void)hipFree(h->d_io);
     if (h->h_stage) (void)hipHostFree(h->h_stage);
@@ -153,25 +161,23 @@ hipStream_t pick_stream(kore_attn *h, void *stream) {
     return stream ? (hipStream_t)stream : h->stream;
 }
 
+// Enqueues a decode with its split partials in part (part_floats floats; a
+// decode needs n_head * splits * (head_dim + 2)).
 int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float *k, const float *v,
-                   float *out, hipStream_t s) {
+                   float *out, hipStream_t s, float *part, size_t part_floats) {
     // Cache rows read besides the new one: positions 0..pos-1 (kore.cpp:1437),
     // or every slot of a ring that has wrapped (the new slot's stale copy is
     // masked by the kernel).
     const bool wrapped = h->window && pos >= h->window;
     const int n_rows = wrapped ? h->window : pos;
     const int slot = h->window ? pos % h->window : pos;
-    if (int rc = ensure_rope(h, pos + 1)) return rc;
     DecodeArgs a{};
     a.q = q;
     a.k = k;
     a.v = v;
-    a.cs = h->d_cs + (size_t)pos * (h->head_dim / 2);
     a.kc = h->d_k + (size_t)layer * h->layer_floats();
     a.vc = h->d_v + (size_t)layer * h->layer_floats();
     a.out = out;
-    a.part_o = h->d_part_o;
-    a.part_ml = h->d_part_ml;
     a.slots = h->ctx;
     a.n_rows = n_rows;
     a.new_slot = slot;
@@ -183,13 +189,18 @@ int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float
     if (a.n_split > h->max_split)
         return fail(h, KORE_ATTN_E_UNSUPPORTED, "decode needs %d splits, scratch holds %d", a.n_split,
                     h->max_split);
-    HIP_TRY(h, launch_decode(a, h->head_dim, s));
+    const size_t np = (size_t)h->n_head * a.n_split;
+    if (np * ((size_t)h->head_dim + 2) > part_floats)
+        return fail(h, KORE_ATTN_E_UNSUPPORTED, "decode partials need %zu floats, the scratch holds %zu",
+                    np * ((size_t)h->head_dim + 2), part_floats);
+    a.part_o = part;
+    a.part_ml = part + np * h->head_dim;
+    HIP_TRY(h, launch_decode(a, decode_row(h, pos), h->head_dim, s));
     return KORE_ATTN_OK;
 }
 
 int prefill_enqueue(kore_attn *h, int layer, int pos0, int n_tok, const float *q, const float *k,
                     const float *v, float *out, hipStream_t s) {
-    if (int rc = ensure_rope(h, pos0 + n_tok)) return rc;
     AppendArgs ap{};
     ap.k = k;
     ap.v = v;
@@ -219,16 +230,9 @@ int prefill_enqueue(kore_attn *h, int layer, int pos0, int n_tok, const float *q
     if (pa.n_kseg > 1) {
         const size_t entries = (size_t)h->n_head_kv * pa.n_rep * pa.n_strips * pa.n_kseg * 32;
         const size_t need = entries * ((size_t)h->head_dim + 2);
-        if (need > h->pf_part_floats) {
-            if (h->d_pf_part) {
-                HIP_TRY(h, hipDeviceSynchronize());   // earlier launches may still read it
-                (void)hipFree(h->d_pf_part);
-                h->d_pf_part = nullptr;
-                h->pf_part_floats = 0;
-            }
-            HIP_TRY(h, hipMalloc(&h->d_pf_part, need * sizeof(float)));
-            h->pf_part_floats = need;
-        }
+        if (need > h->pf_part_floats)   // cannot happen: sized at create for the largest split
+            return fail(h, KORE_ATTN_E_UNSUPPORTED, "prefill partials need %zu floats, scratch holds %zu", need,
+                        h->pf_part_floats);
         pa.part_o = h->d_pf_part;
         pa.part_ml = h->d_pf_part + entries * h->head_dim;
     }
@@ -318,15 +322,24 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
     h->inv_freq.resize((size_t)head_dim / 2);
     for (int i = 0; i < head_dim / 2; ++i)   // kore.cpp:1339
         h->inv_freq[(size_t)i] = (float)std::pow((double)rope_base, -2.0 * i / head_dim);
-    if (ensure_rope(h, ctx) != KORE_ATTN_OK) {
+    if (build_rope_table(h) != KORE_ATTN_OK) {
         g_create_error = h->err;
         release(h);
         return KORE_ATTN_E_HIP;
     }
+    // Decode split partials: n_head * max_split * (hd + 2) floats.
     h->max_split = decode_max_split(head_dim, window ? window : ctx, n_head_kv, h->num_cu);
     const size_t np = (size_t)n_head * h->max_split;
-    if ((e = hipMalloc(&h->d_part_o, np * head_dim * sizeof(float))) != hipSuccess) return bail(e, "hipMalloc");
-    if ((e = hipMalloc(&h->d_part_ml, np * 2 * sizeof(float))) != hipSuccess) return bail(e, "hipMalloc");
+    if ((e = hipMalloc(&h->d_part_o, np * ((size_t)head_dim + 2) * sizeof(float))) != hipSuccess)
+        return bail(e, "hipMalloc");
+    // Prefill key-segment partials, sized for the largest split any chunk
+    // gets: segments are only used while a chunk has fewer workgroups than
+    // CUs, which bounds (heads x strips x segments) by 8 x num_cu
+    // (prefill_key_segments), i.e. 8 x num_cu x 32 rows of (hd + 2) floats.
+    h->pf_part_floats = (size_t)8 * h->num_cu * 32 * ((size_t)head_dim + 2);
+    if ((e = hipMalloc(&h->d_pf_part, h->pf_part_floats * sizeof(float))) != hipSuccess)
+        return bail(e, "hipMalloc");
+
     if ((e = hipStreamSynchronize(h->stream)) != hipSuccess) return bail(e, "hipStreamSynchronize");
     *out = h;
     return KORE_ATTN_OK;
@@ -339,7 +352,8 @@ int kore_attn_decode_dev(kore_attn_t h, int layer, int pos, int n_head, int n_he
     if (!h) return fail(nullptr, KORE_ATTN_E_INVALID, "null handle");
     if (int rc = check_decode(h, layer, pos, n_head, n_head_kv, head_dim, q, k, v, out)) return rc;
     HIP_TRY(h, hipSetDevice(h->device));
-    return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream));
+    return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_part_o,
+                          (size_t)h->n_head * h->max_split * ((size_t)h->head_dim + 2));
 }
 
 int kore_attn_decode(kore_attn_t h, int layer, int pos, int n_head, int n_head_kv, int head_dim,
@@ -354,7 +368,8 @@ int kore_attn_decode(kore_attn_t h, int layer, int pos, int n_head, int n_head_k
     std::memcpy(hs + E, k, kvd * sizeof(float));
     std::memcpy(hs + E + kvd, v, kvd * sizeof(float));
     HIP_TRY(h, hipMemcpyAsync(ds, hs, (E + 2 * kvd) * sizeof(float), hipMemcpyHostToDevice, h->stream));
-    if (int rc = decode_enqueue(h, layer, pos, ds, ds + E, ds + E + kvd, ds + E + 2 * kvd, h->stream))
+    if (int rc = decode_enqueue(h, layer, pos, ds, ds + E, ds + E + kvd, ds + E + 2 * kvd, h->stream,
+                                h->d_part_o, (size_t)h->n_head * h->max_split * ((size_t)h->head_dim + 2)))
         return rc;
     HIP_TRY(h, hipMemcpyAsync(hs + E + 2 * kvd, ds + E + 2 * kvd, E * sizeof(float), hipMemcpyDeviceToHost,
                               h->stream));
@@ -382,7 +397,6 @@ int kore_attn_append_dev(kore_attn_t h, int layer, int pos0, int n_tok, const fl
         return fail(h, KORE_ATTN_E_RANGE, "rows [%d, %d + %d) outside the cache (ctx %d)", pos0, pos0,
                     n_tok, h->ctx);
     HIP_TRY(h, hipSetDevice(h->device));
-    if (int rc = ensure_rope(h, pos0 + n_tok)) return rc;
     AppendArgs ap{};
     ap.k = k;
     ap.v = v;
@@ -429,7 +443,9 @@ int kore_attn_read_kv(kore_attn_t h, int layer, int pos0, int n, float *k_out, f
         return fail(h, KORE_ATTN_E_RANGE, "rows [%d, %d + %d) outside the cache (ctx %d)", pos0, pos0, n,
                     h->ctx);
     HIP_TRY(h, hipSetDevice(h->device));
-    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    // _dev calls may have been enqueued on any stream of the device: wait
+    // for all of them (this export is not on kore's per-token path)
+    HIP_TRY(h, hipDeviceSynchronize());
     const size_t hd = (size_t)h->head_dim, kvd = h->kv_dim();
     for (int which = 0; which < 2; ++which) {
         const float *base = (which ? h->d_v : h->d_k) + (size_t)layer * h->layer_floats();

@@ -26,7 +26,6 @@ struct DecodeArgs {
     const float *q;       // [n_head][hd]        post-bias, pre-RoPE
     const float *k;       // [n_head_kv][hd]     post-bias, pre-RoPE
     const float *v;       // [n_head_kv][hd]
-    const float2 *cs;     // [hd/2] (cos, sin) of this position
     float *kc, *vc;       // layer base, [n_head_kv][slots][hd]
     float *out;           // [n_head][hd]
     float *part_o;        // [n_head][n_split][hd]   split partial outputs
@@ -40,6 +39,15 @@ struct DecodeArgs {
     int n_head_kv;
     int n_rep;            // q heads per kv head
     float scale;          // 1/sqrt(hd) as kore computes it (kore.cpp:1411)
+};
+
+// (cos, sin) of dims 0 .. hd/2 - 1 at the decode position, interleaved,
+// built on the host (kore.cpp:1405-1410) and passed by value with the launch:
+// a decode needs one row, so no device table has to cover its position (a
+// ring decodes past ctx without bound).
+constexpr int kMaxRopeHalf = 64;
+struct RopeRow {
+    float cs[2 * kMaxRopeHalf];
 };
 
 // Batched RoPE + append of n_tok rows starting at position pos0
@@ -98,7 +106,7 @@ int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu);
 bool decode_supported(int head_dim, int n_rep);
 bool prefill_supported(int head_dim, int n_rep);
 
-hipError_t launch_decode(const DecodeArgs &a, int head_dim, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs &a, const RopeRow &rr, int head_dim, hipStream_t s);
 hipError_t launch_append(const AppendArgs &a, int head_dim, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
 // Key segments the prefill uses for n_tok rows at pos0 (1 = none).

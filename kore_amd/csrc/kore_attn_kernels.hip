@@ -38,6 +38,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
+constexpr size_t kLdsPerCu = 160 * 1024;   // gfx950
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -143,25 +144,31 @@ __device__ __forceinline__ float sum4rows(float x) {
 //           is fed back as the B operand without any data movement; lane
 //           (m, k) gives V[row 4k + s][64j + 4m + e] (16-byte loads) for the
 //           output block 4j + e.
-// Every load is in bounds: rows past the split's end are clamped to its last
-// row and masked.  A wave with more than one block prefetches its next block
-// into a second register set while it works on the current one.
+// Issue order of a wave: its q and the new k/v row, the K rows of its first
+// block, then (once q has returned) the RoPE of q through the wave's own LDS
+// rows, then the V rows, so the score MFMAs run while V streams in.  Every
+// load before the first MFMA is unconditional (rows past the split's end
+// are clamped to its last row and masked): a load under a branch makes the
+// compiler's wait counts for everything after it conservative.  MULTI
+// kernels (splits of more than four blocks) keep the next block of a wave in
+// a second register set while the current one is processed.
 // The new token's row is not read from the cache: the owner workgroup ropes
 // it, appends it, and adds it as one more softmax state (its own score, sum
 // 1, output v).  Slots [0, n_rows) never include it except in a wrapped ring,
-// where its stale slot is masked.  The four wave states (and the new row's)
-// are merged in LDS into one partial per q-head, or into `out` when the
-// kv-head has a single split.
-template <int HD, int NR>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__restrict__ q_in, const float2 *cs_in,
-                                                                float *kc_in, float *vc_in, int n_rows,
-                                                                int rows_per_split, int new_slot, int slots,
-                                                                DecodeArgs a) {
+// where its stale slot is masked.  The four wave states (and the extra and
+// new rows') are merged in LDS into one partial per q-head, or into `out`
+// when the kv-head has a single split.
+template <int HD, int NR, bool MULTI>
+__global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
+                                                                float *vc_in, int n_rows, int rows_per_split,
+                                                                int new_slot, int slots, DecodeArgs a,
+                                                                RopeRow rr) {
     constexpr int NT = HD / 16;    // K float4 per lane per block (MFMA k-steps / 4)
     constexpr int NJ = HD / 64;    // V float4 per lane per row
     constexpr int NMB = HD / 16;   // 16-dim output blocks
     constexpr int HALF = HD / 2;
     constexpr int NST = 2 * kWaves + 1;   // wave states, extra-row states, new row
+    constexpr int NEW_WAVE = kWaves - 1;  // the wave that takes the new row
     static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
 
@@ -191,132 +198,110 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     const float *kg = kc_in + head_base;
     const float *vg = vc_in + head_base;
 
-    // ---- q of the NR heads of kv-head g, roped once per workgroup and
-    // staged through LDS: thread (h, c) < NR * hd/8 loads the float4 pair
-    // (q[h][4c..4c+3], q[h][hd/2 + 4c..]) and its four (cos, sin) pairs.
+    // ---- q of the NR heads of kv-head g, roped and pre-scaled by every wave
+    // for itself and staged through the wave's own LDS rows, so no
+    // workgroup barrier stands between a wave's loads and its first MFMA.
+    // Pair p < NR * hd/8 of the wave is (q[h][4c..4c+3], q[h][hd/2 + 4c..])
+    // with h = p / NC, c = p % NC; lane l takes pairs l and l + 64, which
+    // share c = l % NC and so the four (cos, sin) pairs of dims 4c..4c+3.
     // The MFMA operand layout repeats every q value in 16/NR lanes and every
-    // (cos, sin) pair in 16, so loading the operands directly costs each
-    // wave 16 KB of vector-memory traffic, as much as its cache rows.
+    // (cos, sin) pair in 16, so loading the operands directly would cost each
+    // wave as much vector-memory traffic as its cache rows.
     constexpr int QS = HD + 4;                 // s_q row stride (bank spread)
     constexpr int NC = HALF / 4;               // float4 per half row
-    static_assert(NR * NC <= kThreads, "one staging thread per q float4 pair");
-    __shared__ __align__(16) float s_q[NR * QS];   // roped q * 1/sqrt(hd) * log2(e)
-    __shared__ __align__(16) float s_cs[HD];       // (cos, sin) of dims 0 .. hd/2 - 1
-    const int sh = min(tid / NC, NR - 1), sc = tid % NC;
-    float4 sx0, sx1, scs01, scs23;
-    {
+    constexpr int NP = (NR * NC + 63) / 64;    // pairs per lane
+    static_assert(64 % NC == 0 && NP <= 2, "a lane's pairs share their (cos, sin) values");
+    // per wave NR rows of roped q * 1/sqrt(hd) * log2(e), and one row that
+    // takes the stores of lanes without a pair (so the stores need no branch)
+    __shared__ __align__(16) float s_q[kWaves * (NR + 1) * QS];
+    float *wq = s_q + wave * (NR + 1) * QS;
+    const int sc = lane % NC;
+    float4 sx0[NP], sx1[NP];
+    const float4 scs01 = ld4(&rr.cs[8 * sc]), scs23 = ld4(&rr.cs[8 * sc + 4]);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int sh = min((lane + 64 * i) / NC, NR - 1);
         const float *qh = q_in + (size_t)(g * NR + sh) * HD + 4 * sc;
-        const float *csr = reinterpret_cast<const float *>(cs_in) + 8 * sc;
-        sx0 = ld4(qh);
-        sx1 = ld4(qh + HALF);
-        scs01 = ld4(csr);
-        scs23 = ld4(csr + 4);
+        sx0[i] = ld4(qh);
+        sx1[i] = ld4(qh + HALF);
     }
+    // the new k/v row, pair (i, i + hd/2) in lane i (used at the end by the
+    // owner's NEW_WAVE; loaded by every lane so that no load is conditional)
     const int ni = min(lane, HALF - 1);
+    const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
+    const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
+    const float2 ncs = *reinterpret_cast<const float2 *>(&rr.cs[2 * ni]);
 
-    // RoPE of the staged pairs into LDS, then the B operand: lane (m16, kq)
-    // holds head m16 at dims 16t + 4kq + e (heads past NR are zero columns).
+    float4 kA[NT], vA[4][NJ];
+    float4 kB[MULTI ? NT : 1], vB[MULTI ? 4 : 1][NJ];
+    auto load_k = [&](float4 *kf, int b) {
+        const float *kr = kg + (size_t)min(r0 + 16 * b + m16, last_row) * HD + 4 * kq;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) kf[t] = ld4(kr + 16 * t);
+    };
+    auto load_v = [&](float4 (*vf)[NJ], int b) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float *vr = vg + (size_t)min(r0 + 16 * b + 4 * kq + s, last_row) * HD + 4 * m16;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) vf[s][j] = ld4(vr + 64 * j);
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(kA, wave);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // RoPE of the staged pairs into the wave's LDS rows, then the B operand:
+    // lane (m16, kq) holds head m16 at dims 16t + 4kq + e (heads past NR are
+    // zero columns).
     const float qscale = a.scale * kLog2e;
     const int hq = min(m16, NR - 1);
     float qb[NT][4];
-    auto stage_q = [&]() {
-        if (tid < NR * NC) {
+    {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int p = lane + 64 * i;
+            const int row = p < NR * NC ? p / NC : NR;
             float y0[4], y1[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float4 c4 = e < 2 ? scs01 : scs23;
                 const float2 cs = (e & 1) ? make_float2(c4.z, c4.w) : make_float2(c4.x, c4.y);
-                rope_pair(comp(sx0, e), comp(sx1, e), cs, y0[e], y1[e]);
+                rope_pair(comp(sx0[i], e), comp(sx1[i], e), cs, y0[e], y1[e]);
             }
-            st4(&s_q[sh * QS + 4 * sc], make_float4(y0[0] * qscale, y0[1] * qscale, y0[2] * qscale, y0[3] * qscale));
-            st4(&s_q[sh * QS + HALF + 4 * sc],
+            st4(&wq[row * QS + 4 * sc], make_float4(y0[0] * qscale, y0[1] * qscale, y0[2] * qscale, y0[3] * qscale));
+            st4(&wq[row * QS + HALF + 4 * sc],
                 make_float4(y1[0] * qscale, y1[1] * qscale, y1[2] * qscale, y1[3] * qscale));
-            if (sh == 0) {
-                st4(&s_cs[8 * sc], scs01);
-                st4(&s_cs[8 * sc + 4], scs23);
-            }
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
         float4 qv[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) qv[t] = ld4(&s_q[hq * QS + 16 * t + 4 * kq]);
+        for (int t = 0; t < NT; ++t) qv[t] = ld4(&wq[hq * QS + 16 * t + 4 * kq]);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) qb[t][e] = m16 < NR ? comp(qv[t], e) : 0.f;
-    };
-    float4 kA[NT], vA[4][NJ], kB[NT], vB[4][NJ];
-    auto load_blk = [&](float4 (&kf)[NT], float4 (&vf)[4][NJ], int b) {
-        const int rb = r0 + 16 * b;
-        const float *kr = kg + (size_t)min(rb + m16, last_row) * HD + 4 * kq;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) kf[t] = ld4(kr + 16 * t);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const float *vr = vg + (size_t)min(rb + 4 * kq + s, last_row) * HD + 4 * m16;
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) vf[s][j] = ld4(vr + 64 * j);
-        }
-    };
-    // The first block is loaded unconditionally (a wave without one loads the
-    // split's last rows again and ignores them): a load under a branch makes
-    // the compiler's wait counts for everything after it conservative, so
-    // the score MFMAs would wait for the whole block instead of its first K
-    // registers.
-    load_blk(kA, vA, wave);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(vA, wave);
     // this wave's extra row (clamped: loaded by every wave, used by wave < n_extra)
     const int xrow = min(r0 + (n_own - n_extra) + wave, last_row);
     const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
     const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
-    if (wave + kWaves < n_blk) load_blk(kB, vB, wave + kWaves);
-    // the new k/v row, pair (i, i + hd/2) in lane i (after the cache rows:
-    // its pointers are not among the preloaded kernel arguments)
-    const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
-    const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
-    // q is staged while the cache rows stream in: its loads were issued
-    // first, so they return first, and the rotation runs under the K/V loads.
-    stage_q();
-
-    // ---- the new row (owner workgroup, wave 0, while its K/V loads are in
-    // flight): RoPE, append, and its score for every head (state 2 kWaves:
-    // score, sum 1, output v)
-    if (is_owner && wave == 0) {
-        float y0, y1;
-        rope_pair(nk0, nk1, make_float2(s_cs[2 * ni], s_cs[2 * ni + 1]), y0, y1);
-        if (lane < HALF) {
-            float *kd = kc_in + head_base + (size_t)new_slot * HD;
-            float *vd = vc_in + head_base + (size_t)new_slot * HD;
-            kd[lane] = y0;
-            kd[lane + HALF] = y1;
-            vd[lane] = nv0;
-            vd[lane + HALF] = nv1;
-            s_knew[lane] = y0;
-            s_knew[lane + HALF] = y1;
-            s_vnew[lane] = nv0;
-            s_vnew[lane + HALF] = nv1;
-        }
-        __builtin_amdgcn_wave_barrier();
-        float sn = 0.f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float4 kn = ld4(&s_knew[16 * t + 4 * kq]);
-            sn = fmaf(qb[t][0], kn.x, sn);
-            sn = fmaf(qb[t][1], kn.y, sn);
-            sn = fmaf(qb[t][2], kn.z, sn);
-            sn = fmaf(qb[t][3], kn.w, sn);
-        }
-        sn = sum4rows(sn);
-        if (kq == 0 && m16 < NR) {
-            s_m[2 * kWaves * 8 + m16] = sn;
-            s_l[2 * kWaves * 8 + m16] = 1.f;
+    if constexpr (MULTI) {
+        if (wave + kWaves < n_blk) {
+            load_k(kB, wave + kWaves);
+            load_v(vB, wave + kWaves);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
+
     floatx4 o[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_part = 0.f;
 
-    auto process = [&](const float4 (&kf)[NT], const float4 (&vf)[4][NJ], int b, bool first) {
+    auto process = [&](const float4 *kf, const float4 (*vf)[NJ], int b, bool first) {
         const int rb = r0 + 16 * b;
         floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -350,14 +335,32 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
 #pragma unroll
             for (int sk = 0; sk < 4; ++sk) o[mb] = mfma16(comp(vf[sk][mb / 4], mb % 4), p[sk], o[mb]);
     };
-    for (int b = wave; b < n_blk;) {
-        process(kA, vA, b, b == wave);
-        b += kWaves;
-        if (b >= n_blk) break;
-        if (b + kWaves < n_blk) load_blk(kA, vA, b + kWaves);
-        process(kB, vB, b, false);
-        b += kWaves;
-        if (b + kWaves < n_blk) load_blk(kB, vB, b + kWaves);
+    if constexpr (MULTI) {
+        for (int b = wave; b < n_blk;) {
+            process(kA, vA, b, b == wave);
+            b += kWaves;
+            if (b >= n_blk) break;
+            if (b + kWaves < n_blk) {
+                load_k(kA, b + kWaves);
+                load_v(vA, b + kWaves);
+            }
+            process(kB, vB, b, false);
+            b += kWaves;
+            if (b + kWaves < n_blk) {
+                load_k(kB, b + kWaves);
+                load_v(vB, b + kWaves);
+            }
+        }
+    } else {
+        // at most one block per wave: the first block's loads are exact and
+        // the block runs unconditionally (a wave without one masks it out)
+        process(kA, vA, wave, true);
+        if (wave >= n_blk) {
+            m_run = -INFINITY;
+            l_part = 0.f;
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
     }
 
     // ---- the wave's extra row (state kWaves + wave): its score for every
@@ -383,6 +386,39 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         if (kq == 0 && m16 < NR) {
             s_m[(kWaves + wave) * 8 + m16] = xrow == new_slot ? -INFINITY : sx;
             s_l[(kWaves + wave) * 8 + m16] = 1.f;
+        }
+    }
+    // ---- the new row (owner workgroup): RoPE, append, and its score for
+    // every head (state 2 kWaves: score, sum 1, output v)
+    if (is_owner && wave == NEW_WAVE) {
+        float y0, y1;
+        rope_pair(nk0, nk1, ncs, y0, y1);
+        if (lane < HALF) {
+            float *kd = kc_in + head_base + (size_t)new_slot * HD;
+            float *vd = vc_in + head_base + (size_t)new_slot * HD;
+            kd[lane] = y0;
+            kd[lane + HALF] = y1;
+            vd[lane] = nv0;
+            vd[lane + HALF] = nv1;
+            s_knew[lane] = y0;
+            s_knew[lane + HALF] = y1;
+            s_vnew[lane] = nv0;
+            s_vnew[lane + HALF] = nv1;
+        }
+        __builtin_amdgcn_wave_barrier();
+        float sn = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 kn = ld4(&s_knew[16 * t + 4 * kq]);
+            sn = fmaf(qb[t][0], kn.x, sn);
+            sn = fmaf(qb[t][1], kn.y, sn);
+            sn = fmaf(qb[t][2], kn.z, sn);
+            sn = fmaf(qb[t][3], kn.w, sn);
+        }
+        sn = sum4rows(sn);
+        if (kq == 0 && m16 < NR) {
+            s_m[2 * kWaves * 8 + m16] = sn;
+            s_l[2 * kWaves * 8 + m16] = 1.f;
         }
     }
     // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
@@ -864,12 +900,31 @@ __global__ void synth_kernel(SynthArgs a, uint64_t key, uint64_t okey) {
 // --------------------------------------------------------------- dispatch
 
 template <int HD, int NR>
-hipError_t launch_decode_nr(const DecodeArgs &a, hipStream_t s) {
+hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t s) {
     // The leading scalar arguments are preloaded into SGPRs at wave launch
     // (gfx950 kernel-argument preload), so the first loads do not wait for
     // a kernel-argument fetch (0.24 us measured).
-    hipLaunchKernelGGL((decode_split_kernel<HD, NR>), dim3(a.n_split, a.n_head_kv), dim3(kThreads), 0, s, a.q,
-                       a.cs, a.kc, a.vc, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a);
+    // Splits of at most kWaves blocks plus kWaves extra rows give every wave
+    // one block at most: that kernel has no prefetch registers or branches.
+    // The grid never has more workgroups than CUs.  The single-block kernel
+    // fits two workgroups per CU by registers, so it asks for enough (unused)
+    // dynamic LDS that a CU holds one: two on a CU would leave another idle.
+    const dim3 grid(a.n_split, a.n_head_kv);
+    if (a.rows_per_split > kWaves * kDecodeBlock + kWaves) {
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, true>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc,
+                           a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
+    } else {
+        static const unsigned dyn = [] {
+            hipFuncAttributes fa{};
+            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR, false>)) !=
+                hipSuccess)
+                return 0u;
+            const size_t half_cu = kLdsPerCu / 2 + 256;
+            return fa.sharedSizeBytes < half_cu ? (unsigned)(half_cu - fa.sharedSizeBytes) : 0u;
+        }();
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, false>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc,
+                           a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
+    }
     static_assert(kMaxDecodeSplits <= 8 * 16, "the combine takes at most 16 splits per lane");
     const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 32);
     const float *po = a.part_o, *pml = a.part_ml;
@@ -881,16 +936,16 @@ hipError_t launch_decode_nr(const DecodeArgs &a, hipStream_t s) {
 }
 
 template <int HD>
-hipError_t launch_decode_hd(const DecodeArgs &a, hipStream_t s) {
+hipError_t launch_decode_hd(const DecodeArgs &a, const RopeRow &rr, hipStream_t s) {
     switch (a.n_rep) {
-        case 1: return launch_decode_nr<HD, 1>(a, s);
-        case 2: return launch_decode_nr<HD, 2>(a, s);
-        case 3: return launch_decode_nr<HD, 3>(a, s);
-        case 4: return launch_decode_nr<HD, 4>(a, s);
-        case 5: return launch_decode_nr<HD, 5>(a, s);
-        case 6: return launch_decode_nr<HD, 6>(a, s);
-        case 7: return launch_decode_nr<HD, 7>(a, s);
-        case 8: return launch_decode_nr<HD, 8>(a, s);
+        case 1: return launch_decode_nr<HD, 1>(a, rr, s);
+        case 2: return launch_decode_nr<HD, 2>(a, rr, s);
+        case 3: return launch_decode_nr<HD, 3>(a, rr, s);
+        case 4: return launch_decode_nr<HD, 4>(a, rr, s);
+        case 5: return launch_decode_nr<HD, 5>(a, rr, s);
+        case 6: return launch_decode_nr<HD, 6>(a, rr, s);
+        case 7: return launch_decode_nr<HD, 7>(a, rr, s);
+        case 8: return launch_decode_nr<HD, 8>(a, rr, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -922,9 +977,9 @@ int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu) {
     return rps;
 }
 
-hipError_t launch_decode(const DecodeArgs &a, int head_dim, hipStream_t s) {
-    if (head_dim == 128) return launch_decode_hd<128>(a, s);
-    if (head_dim == 64) return launch_decode_hd<64>(a, s);
+hipError_t launch_decode(const DecodeArgs &a, const RopeRow &rr, int head_dim, hipStream_t s) {
+    if (head_dim == 128) return launch_decode_hd<128>(a, rr, s);
+    if (head_dim == 64) return launch_decode_hd<64>(a, rr, s);
     return hipErrorInvalidValue;
 }
 
