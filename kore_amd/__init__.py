@@ -134,6 +134,12 @@ class KoreAttn:
         self._check(_lib.lib().kore_attn_decode_dev(self._h, layer, pos, self.n_head, self.n_head_kv,
                                                     self.head_dim, q, k, v, out, stream))
 
+    def decode_noalloc_dev(self, layer: int, pos: int, q: int, k: int, v: int, out: int, stream=None) -> None:
+        """decode_dev with the split partials in the library's fixed device array
+        (allocates nothing; overlapping calls on one GPU race)."""
+        self._check(_lib.lib().kore_attn_decode_noalloc_dev(self._h, layer, pos, self.n_head, self.n_head_kv,
+                                                            self.head_dim, q, k, v, out, stream))
+
     def prefill_dev(self, layer: int, pos0: int, n_tok: int, q: int, k: int, v: int, out: int,
                     stream=None) -> None:
         self._check(_lib.lib().kore_attn_prefill_dev(self._h, layer, pos0, n_tok, self.n_head,

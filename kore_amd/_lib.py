@@ -31,6 +31,7 @@ SYMBOLS = [
     ("kore_attn_read_kv", _i, [_vp, _i, _i, _i, _vp, _vp]),
     ("kore_attn_last_error", C.c_char_p, [_vp]),
     ("kore_attn_decode_dev", _i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    ("kore_attn_decode_noalloc_dev", _i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     ("kore_attn_prefill_dev", _i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     ("kore_attn_append_dev", _i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     ("kore_attn_sync", _i, [_vp]),

@@ -32,6 +32,7 @@ struct kore_attn {
     int max_split = 0;
     float *d_pf_part = nullptr;              // prefill key-segment partials
     size_t pf_part_floats = 0;
+    float *d_scratch = nullptr;              // the device's fixed scratch (allocation-free decode)
     float *h_stage = nullptr;                // pinned staging of the host entry points
     size_t h_stage_floats = 0;
     float *d_io = nullptr;                   // device copies of q/k/v/out
@@ -339,7 +340,9 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
     h->pf_part_floats = (size_t)8 * h->num_cu * 32 * ((size_t)head_dim + 2);
     if ((e = hipMalloc(&h->d_pf_part, h->pf_part_floats * sizeof(float))) != hipSuccess)
         return bail(e, "hipMalloc");
-
+    // the device's fixed scratch of kore_attn_decode_noalloc_dev, resolved
+    // once per device with that device current
+    if ((e = static_scratch(h->device, &h->d_scratch)) != hipSuccess) return bail(e, "hipGetSymbolAddress");
     if ((e = hipStreamSynchronize(h->stream)) != hipSuccess) return bail(e, "hipStreamSynchronize");
     *out = h;
     return KORE_ATTN_OK;
@@ -354,6 +357,15 @@ int kore_attn_decode_dev(kore_attn_t h, int layer, int pos, int n_head, int n_he
     HIP_TRY(h, hipSetDevice(h->device));
     return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_part_o,
                           (size_t)h->n_head * h->max_split * ((size_t)h->head_dim + 2));
+}
+
+int kore_attn_decode_noalloc_dev(kore_attn_t h, int layer, int pos, int n_head, int n_head_kv, int head_dim,
+                                 const float *q, const float *k, const float *v, float *out, void *stream) {
+    if (!h) return fail(nullptr, KORE_ATTN_E_INVALID, "null handle");
+    if (int rc = check_decode(h, layer, pos, n_head, n_head_kv, head_dim, q, k, v, out)) return rc;
+    HIP_TRY(h, hipSetDevice(h->device));
+    return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_scratch,
+                          kStaticScratchFloats);
 }
 
 int kore_attn_decode(kore_attn_t h, int layer, int pos, int n_head, int n_head_kv, int head_dim,

@@ -100,6 +100,17 @@ struct SynthArgs {
     float outlier_scale;
 };
 
+// The device's fixed scratch (a file-scope __device__ array of
+// kStaticScratchFloats floats, 1.25 MiB): the split partials of the
+// allocation-free decode entry point.  A decode has at most one split
+// workgroup per CU and at most 8 q-heads per kv-head, so it needs at most
+// 8 x num_cu x (hd + 2) floats: 266,240 on a 256-CU MI355X at head_dim 128.
+// static_scratch() returns the array's address on `device` (made current by
+// the caller), resolved with hipGetSymbolAddress on the first call for that
+// device and remembered.
+constexpr size_t kStaticScratchFloats = (size_t)5 << 16;
+hipError_t static_scratch(int device, float **ptr);
+
 // Rows per split the decode uses for n_rows cache rows (the host sizes the
 // partial buffers from the maximum split count over all lengths).
 int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu);

@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 namespace kore_attn_gpu {
 namespace {
@@ -897,6 +898,15 @@ __global__ void synth_kernel(SynthArgs a, uint64_t key, uint64_t okey) {
     }
 }
 
+// ------------------------------------------------------- fixed scratch
+
+// Split partials of kore_attn_decode_noalloc_dev: every GPU holds its own copy
+// of this array for the life of the process, and every call on that GPU
+// shares it.  Host code never passes the array's name to a kernel (on the
+// host it names a stand-in, not device memory); it passes the address that
+// hipGetSymbolAddress gives for the current device.
+static __device__ __align__(256) float scratch[kStaticScratchFloats];
+
 // --------------------------------------------------------------- dispatch
 
 template <int HD, int NR>
@@ -951,6 +961,22 @@ hipError_t launch_decode_hd(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
 }
 
 }  // namespace
+
+hipError_t static_scratch(int device, float **ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static float *addr[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[device] = static_cast<float *>(p);
+    }
+    *ptr = addr[device];
+    return hipSuccess;
+}
 
 bool decode_supported(int head_dim, int n_rep) {
     return (head_dim == 64 || head_dim == 128) && n_rep >= 1 && n_rep <= 8;

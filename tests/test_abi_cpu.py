@@ -27,7 +27,7 @@ def test_headers_declare_the_abi():
     for fn in ("kore_attn_create", "kore_attn_destroy", "kore_attn_decode", "kore_attn_prefill",
                "kore_attn_read_kv", "kore_attn_last_error", "kore_attn_decode_dev",
                "kore_attn_prefill_dev", "kore_attn_append_dev", "kore_attn_sync", "kore_attn_get_info",
-               "kore_attn_synth_dev"):
+               "kore_attn_synth_dev", "kore_attn_decode_noalloc_dev"):
         assert fn in names
 
 
