@@ -226,12 +226,22 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         sx0[i] = ld4(qh);
         sx1[i] = ld4(qh + HALF);
     }
-    // the new k/v row, pair (i, i + hd/2) in lane i (used at the end by the
-    // owner's NEW_WAVE; loaded by every lane so that no load is conditional)
+    // the new k/v row and this wave's extra row, pair (i, i + hd/2) in lane
+    // i: loaded by every lane of every wave (clamped rows), so that no load
+    // is conditional, and ahead of the K rows, so that their scores are taken
+    // while the cache rows stream in
     const int ni = min(lane, HALF - 1);
     const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
     const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
     const float2 ncs = *reinterpret_cast<const float2 *>(&rr.cs[2 * ni]);
+    const int xrow = min(r0 + (n_own - n_extra) + wave, last_row);
+    const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
+    const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
+    // the arguments the merge needs, read now: a first read after the block
+    // loop would wait for a kernel-argument fetch at the end of the kernel
+    float *const out_p = a.out, *const part_o = a.part_o, *const part_ml = a.part_ml;
+    const int n_split = a.n_split, n_rep = a.n_rep;
+    asm volatile("" ::"s"(out_p), "s"(part_o), "s"(part_ml), "s"(n_split), "s"(n_rep));
 
     float4 kA[NT], vA[4][NJ];
     float4 kB[MULTI ? NT : 1], vB[MULTI ? 4 : 1][NJ];
@@ -283,12 +293,57 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
 #pragma unroll
             for (int e = 0; e < 4; ++e) qb[t][e] = m16 < NR ? comp(qv[t], e) : 0.f;
     }
+    // dot of q (operand layout) with a k row staged in LDS: lane (m16, kq)
+    // sums dims 16t + 4kq + e of head m16, then the four lanes of the head
+    auto row_score = [&](const float *kr) {
+        float sx = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 kx = ld4(&kr[16 * t + 4 * kq]);
+            sx = fmaf(qb[t][0], kx.x, sx);
+            sx = fmaf(qb[t][1], kx.y, sx);
+            sx = fmaf(qb[t][2], kx.z, sx);
+            sx = fmaf(qb[t][3], kx.w, sx);
+        }
+        return sum4rows(sx);
+    };
+    // ---- the wave's extra row (state kWaves + wave; -inf and a zero row
+    // when the wave has none) and, in NEW_WAVE, the new row (state 2 kWaves,
+    // roped here; -inf and a zero row outside the owner workgroup).  Only
+    // LDS and register work: no memory operation under these branches.
+    {
+        const bool x_on = wave < n_extra;
+        if (lane < HALF) {
+            s_kx[wave * HD + lane] = xk0;
+            s_kx[wave * HD + lane + HALF] = xk1;
+            s_vx[wave * HD + lane] = x_on ? xv0 : 0.f;
+            s_vx[wave * HD + lane + HALF] = x_on ? xv1 : 0.f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const float sx = row_score(&s_kx[wave * HD]);
+        if (kq == 0 && m16 < NR) {
+            s_m[(kWaves + wave) * 8 + m16] = (x_on && xrow != new_slot) ? sx : -INFINITY;
+            s_l[(kWaves + wave) * 8 + m16] = x_on ? 1.f : 0.f;
+        }
+    }
+    float nky0, nky1;
+    rope_pair(nk0, nk1, ncs, nky0, nky1);
+    if (wave == NEW_WAVE) {
+        if (lane < HALF) {
+            s_knew[lane] = nky0;
+            s_knew[lane + HALF] = nky1;
+            s_vnew[lane] = is_owner ? nv0 : 0.f;
+            s_vnew[lane + HALF] = is_owner ? nv1 : 0.f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const float sn = row_score(s_knew);
+        if (kq == 0 && m16 < NR) {
+            s_m[2 * kWaves * 8 + m16] = is_owner ? sn : -INFINITY;
+            s_l[2 * kWaves * 8 + m16] = is_owner ? 1.f : 0.f;
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
     load_v(vA, wave);
-    // this wave's extra row (clamped: loaded by every wave, used by wave < n_extra)
-    const int xrow = min(r0 + (n_own - n_extra) + wave, last_row);
-    const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
-    const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
     if constexpr (MULTI) {
         if (wave + kWaves < n_blk) {
             load_k(kB, wave + kWaves);
@@ -364,64 +419,6 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         }
     }
 
-    // ---- the wave's extra row (state kWaves + wave): its score for every
-    // head by VALU (k staged through LDS into the q operand's dim order)
-    if (wave < n_extra) {
-        if (lane < HALF) {
-            s_kx[wave * HD + lane] = xk0;
-            s_kx[wave * HD + lane + HALF] = xk1;
-            s_vx[wave * HD + lane] = xv0;
-            s_vx[wave * HD + lane + HALF] = xv1;
-        }
-        __builtin_amdgcn_wave_barrier();
-        float sx = 0.f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float4 kx = ld4(&s_kx[wave * HD + 16 * t + 4 * kq]);
-            sx = fmaf(qb[t][0], kx.x, sx);
-            sx = fmaf(qb[t][1], kx.y, sx);
-            sx = fmaf(qb[t][2], kx.z, sx);
-            sx = fmaf(qb[t][3], kx.w, sx);
-        }
-        sx = sum4rows(sx);
-        if (kq == 0 && m16 < NR) {
-            s_m[(kWaves + wave) * 8 + m16] = xrow == new_slot ? -INFINITY : sx;
-            s_l[(kWaves + wave) * 8 + m16] = 1.f;
-        }
-    }
-    // ---- the new row (owner workgroup): RoPE, append, and its score for
-    // every head (state 2 kWaves: score, sum 1, output v)
-    if (is_owner && wave == NEW_WAVE) {
-        float y0, y1;
-        rope_pair(nk0, nk1, ncs, y0, y1);
-        if (lane < HALF) {
-            float *kd = kc_in + head_base + (size_t)new_slot * HD;
-            float *vd = vc_in + head_base + (size_t)new_slot * HD;
-            kd[lane] = y0;
-            kd[lane + HALF] = y1;
-            vd[lane] = nv0;
-            vd[lane + HALF] = nv1;
-            s_knew[lane] = y0;
-            s_knew[lane + HALF] = y1;
-            s_vnew[lane] = nv0;
-            s_vnew[lane + HALF] = nv1;
-        }
-        __builtin_amdgcn_wave_barrier();
-        float sn = 0.f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float4 kn = ld4(&s_knew[16 * t + 4 * kq]);
-            sn = fmaf(qb[t][0], kn.x, sn);
-            sn = fmaf(qb[t][1], kn.y, sn);
-            sn = fmaf(qb[t][2], kn.z, sn);
-            sn = fmaf(qb[t][3], kn.w, sn);
-        }
-        sn = sum4rows(sn);
-        if (kq == 0 && m16 < NR) {
-            s_m[2 * kWaves * 8 + m16] = sn;
-            s_l[2 * kWaves * 8 + m16] = 1.f;
-        }
-    }
     // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
     // 64(mb / 4) + 16kq + 4v + mb % 4
     const float l_w = sum4rows(l_part);
@@ -455,20 +452,29 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
         float l = 0.f;
         float4 acc = zero4();
-        // the extra rows' and the new row's states exist only where written
+        // the extra rows' and the new row's states: only those the workgroup
+        // has (uniform branches; the states of the others hold max -inf,
+        // sum 0 and a zero row, so reading them would add nothing)
         float ms[kWaves + 1], ls[kWaves + 1];
         float4 xs[kWaves + 1];
 #pragma unroll
         for (int w = 0; w <= kWaves; ++w) {
             const bool on = w < kWaves ? w < n_extra : is_owner;
-            const int st = kWaves + w;
-            ms[w] = on ? s_m[st * 8 + h] : -INFINITY;
-            ls[w] = on ? s_l[st * 8 + h] : 0.f;
-            xs[w] = on ? ld4(w < kWaves ? &s_vx[w * HD + 4 * d4] : &s_vnew[4 * d4]) : zero4();
-            m = fmaxf(m, ms[w]);
+            ms[w] = -INFINITY;
+            ls[w] = 0.f;
+            xs[w] = zero4();
+            if (on) {
+                const int st = kWaves + w;
+                ms[w] = s_m[st * 8 + h];
+                ls[w] = s_l[st * 8 + h];
+                xs[w] = ld4(w < kWaves ? &s_vx[w * HD + 4 * d4] : &s_vnew[4 * d4]);
+                m = fmaxf(m, ms[w]);
+            }
         }
 #pragma unroll
         for (int w = 0; w < 2 * kWaves + 1; ++w) {
+            const bool on = w < kWaves ? true : (w < 2 * kWaves ? w - kWaves < n_extra : is_owner);
+            if (!on) continue;
             const float mx = w < kWaves ? mw[w] : ms[w - kWaves];
             const float e = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
             const float4 x = w < kWaves ? xw[w] : xs[w - kWaves];
@@ -478,17 +484,27 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             acc.z = fmaf(e, x.z, acc.z);
             acc.w = fmaf(e, x.w, acc.w);
         }
-        const size_t hg = (size_t)g * a.n_rep + h;
-        if (a.n_split == 1) {
+        const size_t hg = (size_t)g * n_rep + h;
+        if (n_split == 1) {
             const float inv = 1.f / l;
-            st4(a.out + hg * HD + 4 * d4, make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
+            st4(out_p + hg * HD + 4 * d4, make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
         } else {
-            st4(a.part_o + (hg * a.n_split + split) * HD + 4 * d4, acc);
+            st4(part_o + (hg * n_split + split) * HD + 4 * d4, acc);
             if (d4 == 0) {
-                a.part_ml[(hg * a.n_split + split) * 2 + 0] = m;
-                a.part_ml[(hg * a.n_split + split) * 2 + 1] = l;
+                part_ml[(hg * n_split + split) * 2 + 0] = m;
+                part_ml[(hg * n_split + split) * 2 + 1] = l;
             }
         }
+    }
+    // ---- append of the new row (owner workgroup), last: no load waits
+    // behind these stores
+    if (is_owner && wave == NEW_WAVE && lane < HALF) {
+        float *kd = kc_in + head_base + (size_t)new_slot * HD;
+        float *vd = vc_in + head_base + (size_t)new_slot * HD;
+        kd[lane] = nky0;
+        kd[lane + HALF] = nky1;
+        vd[lane] = nv0;
+        vd[lane + HALF] = nv1;
     }
 }
 
