@@ -53,6 +53,7 @@ E, KVD = NH * HD, NKV * HD
 ROPE_BASE = 1e6
 DEC_CTX, DEC_POS0 = 8192, 4096
 DEC_SEED, DEC_PER_MILLE, DEC_OUTLIER = 7, 10, 20.0
+DEC_STEPS = 128                # the configured decode steps (positions 4096..4223)
 PF_N, PF_SEED = 2048, 3
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on these
@@ -132,6 +133,8 @@ def _bench_lib():
     L.kab_decode_run.argtypes = [vp, i, i, i, i, vp, vp, vp, i, vp, i, vp, C.POINTER(C.c_float),
                                  C.POINTER(C.c_double)]
     L.kab_prefill_run.argtypes = [vp, i, i, i, i, vp, vp, vp, vp, vp, C.POINTER(C.c_float), C.POINTER(C.c_double)]
+    L.kab_decode_host_run.argtypes = [vp, i, i, i, vp, vp, vp, i, vp, C.POINTER(C.c_double)]
+    L.kab_prefill_host_run.argtypes = [vp, i, i, i, vp, vp, vp, vp, C.POINTER(C.c_double)]
     return L
 
 
@@ -159,7 +162,7 @@ def gpu_decode(steps: int, warmup: int):
     attn.sync()
     for b in (qb, kb, vb, ob):
         b.free()
-    n_in = max(steps, warmup)
+    n_in = max(steps, warmup, DEC_STEPS)
     dq, dk, dv = hip.DeviceBuffer(NL * n_in * E), hip.DeviceBuffer(NL * n_in * KVD), hip.DeviceBuffer(NL * n_in * KVD)
     for l in range(NL):
         synth_dev(dq.at(l * n_in * E), n_in, E, DEC_SEED, q_stream(l), DEC_POS0, 1, DEC_PER_MILLE, DEC_OUTLIER, st)
@@ -176,15 +179,32 @@ def gpu_decode(steps: int, warmup: int):
     # the timed steps: host clock and one HIP event pair around the region
     _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
                             None, C.byref(region), C.byref(wall)), "decode timed")
-    outs = out.download().reshape(steps, NL, E)
     # the same steps again with an event pair around every launch (per-launch
     # spread; re-running a step rewrites the same cache row with the same data)
     launch_ms = np.zeros(steps * NL, np.float32)
     _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
                             launch_ms.ctypes.data, None, C.byref(wall2)), "decode per-launch events")
+    # all 128 configured steps once more, untimed, for the parity check
+    out.free()
+    par = hip.DeviceBuffer(DEC_STEPS * NL * E)
+    _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, DEC_STEPS, dq.ptr, dk.ptr, dv.ptr, n_in, par.ptr,
+                            DEC_STEPS, None, None, C.byref(wall2)), "decode parity pass")
+    outs = par.download().reshape(DEC_STEPS, NL, E)
+    par.free()
+    # the host-pointer entry point kore's forward() would call (kore_attn_decode:
+    # H2D of q/k/v, the kernels, D2H of the output, per layer), on the timed steps
+    hq = dq.download(NL * n_in * E).reshape(NL, n_in, E)
+    hk = dk.download(NL * n_in * KVD).reshape(NL, n_in, KVD)
+    hv = dv.download(NL * n_in * KVD).reshape(NL, n_in, KVD)
+    hout = np.zeros((NL, E), np.float32)
+    host_steps = min(steps, 32)
+    wall_h = C.c_double(0)
+    _check(B.kab_decode_host_run(attn.handle, NL, DEC_POS0, host_steps, hq.ctypes.data, hk.ctypes.data,
+                                 hv.ctypes.data, n_in, hout.ctypes.data, C.byref(wall_h)), "decode host pass")
     info = attn.info()
     return dict(attn=attn, outs=outs, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value,
-                num_cu=info.num_cu, buffers=(dq, dk, dv, out))
+                num_cu=info.num_cu, buffers=(dq, dk, dv), host_us_per_layer=wall_h.value * 1e3 / (host_steps * NL),
+                host_steps=host_steps)
 
 
 def gpu_prefill(steps: int, warmup: int):
@@ -208,11 +228,23 @@ def gpu_prefill(steps: int, warmup: int):
     # per-launch events cost ~1 us against ~450 us launches: one pass gives both
     _check(B.kab_prefill_run(attn.handle, NL, 0, PF_N, steps, dq.ptr, dk.ptr, dv.ptr, out.ptr,
                              launch_ms.ctypes.data, C.byref(region), C.byref(wall)), "prefill timed")
-    outs = out.download(2 * PF_N * E).reshape(2, PF_N, E)   # layers 0 and 1 for the parity check
+    HL = 4   # layers of the host-pointer round trip
+    outs = out.download(HL * PF_N * E).reshape(HL, PF_N, E)   # the first layers for the parity checks
+    # the host-pointer entry point kore's forward_batch() would call
+    # (kore_attn_prefill: H2D of q/k/v, append + attention, D2H of the rows)
+    hq = dq.download(HL * PF_N * E)
+    hk = dk.download(HL * PF_N * KVD)
+    hv = dv.download(HL * PF_N * KVD)
+    hout = np.zeros(HL * PF_N * E, np.float32)
+    wall_h = C.c_double(0)
+    _check(B.kab_prefill_host_run(attn.handle, HL, 0, PF_N, hq.ctypes.data, hk.ctypes.data, hv.ctypes.data,
+                                  hout.ctypes.data, C.byref(wall_h)), "prefill host pass")
+    host_equal = bool(np.array_equal(hout.view(np.uint32), outs.reshape(-1).view(np.uint32)))
     attn.close()
     for b in (dq, dk, dv, out):
         b.free()
-    return dict(outs=outs, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value)
+    return dict(outs=outs, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value,
+                host_us_per_layer=wall_h.value * 1e3 / HL, host_layers=HL, host_equals_device=host_equal)
 
 
 def _decode_bytes_geom(L: int, nh: int, nkv: int, hd: int) -> int:
@@ -630,15 +662,17 @@ def cpu_prompt(seconds: float, threads: int):
     import oracle
     if not os.path.exists(oracle.REF_LAYER_BIN):
         return None
-    r = subprocess.run([oracle.REF_LAYER_BIN, "--time-batch", str(threads), str(seconds)],
+    r = subprocess.run([oracle.REF_LAYER_BIN, "--time-batch", str(threads), str(seconds / CPU_RUNS), str(CPU_RUNS)],
                        capture_output=True, text=True, check=True)
     j = json.loads(r.stdout)
-    return {"value": round(j["tokens"] / j["seconds"], 3), "unit": "tokens/s", "cores": j["threads"],
-            "kind": "reference",
+    st = _runs([64 * c / t for c, t in zip(j["run_chunks"], j["run_seconds"])], "tokens/s")
+    return {"value": round(st["median"], 3), "unit": "tokens/s", "cores": j["threads"], "kind": "reference",
+            "best": round(st["best"], 3), "runs": st["runs"], "threads": j["threads"], "host": _host(),
             "sample": f"kore's own forward_batch() (kore.cpp:1486-1598, matmul_batch_float with AVX2: "
                       f"{bool(j['avx2'])}) built from kore.cpp with kore's flags, {j['threads']} threads, on a "
                       f"synthetic Qwen2.5-7B-shape engine: {j['chunks']} chunks of 64 tokens at positions 0..511 "
-                      f"in {j['seconds']:.1f} s (after one warm-up chunk); host {_cpu_model()}"}
+                      f"in {j['seconds']:.1f} s over {CPU_RUNS} timed runs (after one warm-up chunk; value = median run, "
+                      f"best = fastest run); host {_cpu_model()}"}
 
 
 def token_report(t, mats):
@@ -670,15 +704,17 @@ def cpu_token(seconds: float, threads: int):
     import oracle
     if not os.path.exists(oracle.REF_LAYER_BIN):
         return None
-    r = subprocess.run([oracle.REF_LAYER_BIN, "--time", str(threads), str(seconds), str(DEC_POS0)],
-                       capture_output=True, text=True, check=True)
+    r = subprocess.run([oracle.REF_LAYER_BIN, "--time", str(threads), str(seconds / CPU_RUNS), str(DEC_POS0),
+                        str(CPU_RUNS)], capture_output=True, text=True, check=True)
     j = json.loads(r.stdout)
-    return {"value": round(j["tokens"] / j["seconds"], 3), "unit": "tokens/s", "cores": j["threads"],
-            "kind": "reference",
+    st = _runs([n / t for n, t in zip(j["run_tokens"], j["run_seconds"])], "tokens/s")
+    return {"value": round(st["median"], 3), "unit": "tokens/s", "cores": j["threads"], "kind": "reference",
+            "best": round(st["best"], 3), "runs": st["runs"], "threads": j["threads"], "host": _host(),
             "sample": f"kore's own forward() with logits (kore.cpp:1397-1484, AVX2 matvecs: {bool(j['avx2'])}, "
                       f"attention on one thread as in kore) built from kore.cpp with kore's flags, {j['threads']} "
                       f"threads, on a synthetic Qwen2.5-7B-shape engine at positions {j['pos']}..: {j['tokens']} "
-                      f"tokens in {j['seconds']:.1f} s; host {_cpu_model()}"}
+                      f"tokens in {j['seconds']:.1f} s over {CPU_RUNS} timed runs (value = median run, best = fastest run); "
+                      f"host {_cpu_model()}"}
 
 
 def gemm_report(g, chunks: int):
@@ -791,15 +827,17 @@ def cpu_matvec(seconds: float, threads: int):
                 f.write(struct.pack("<3i", QMV_Q4K, rows, cols))
                 f.write(w.tobytes())
                 f.write(x.tobytes())
-            r = subprocess.run([oracle.REF_QMV_BIN, "--time", str(threads), str(seconds), "16", job],
-                               capture_output=True, text=True, check=True)
+            r = subprocess.run([oracle.REF_QMV_BIN, "--time", str(threads), str(seconds / CPU_RUNS), "16", job,
+                                str(CPU_RUNS)], capture_output=True, text=True, check=True)
         j = json.loads(r.stdout)
-        gbs = j["weight_bytes"] * j["reps"] / j["seconds"] / 1e9
-        return {"value": round(gbs, 2), "unit": "GB/s", "cores": j["threads"], "kind": "reference",
+        st = _runs([j["weight_bytes"] * n / t / 1e9 for n, t in zip(j["run_reps"], j["run_seconds"])], "GB/s")
+        return {"value": round(st["median"], 2), "unit": "GB/s", "cores": j["threads"], "kind": "reference",
+                "best": round(st["best"], 2), "runs": st["runs"], "threads": j["threads"], "host": _host(),
                 "sample": f"kore's own quantize_row_q8_K + matvec_mt (kore.cpp:422-446, 677-682, AVX2 dot "
                           f"products: {bool(j['avx2'])}) built from kore.cpp with kore's flags, {j['threads']} "
                           f"threads, on the 7B ffn_gate shape ({rows} x {cols} Q4_K, 38.2 MB) cycling over 16 "
-                          f"copies: {j['reps']} matvecs in {j['seconds']:.1f} s; host {_cpu_model()}"}
+                          f"copies: {j['reps']} matvecs in {j['seconds']:.1f} s over {CPU_RUNS} timed runs (value = median "
+                          f"run, best = fastest run); host {_cpu_model()}"}
     xq = oracle.quantize_q8K(x)
     t0, n = time.perf_counter(), 0
     while time.perf_counter() - t0 < seconds:
@@ -834,15 +872,17 @@ def cpu_gemm(seconds: float, threads: int):
                 f.write(struct.pack("<4i", QMV_Q4K, rows, cols, GEMM_B))
                 f.write(w.tobytes())
                 f.write(x.tobytes())
-            r = subprocess.run([oracle.REF_QMV_BIN, "--time-batch", str(threads), str(seconds), job],
-                               capture_output=True, text=True, check=True)
+            r = subprocess.run([oracle.REF_QMV_BIN, "--time-batch", str(threads), str(seconds / CPU_RUNS), job,
+                                str(CPU_RUNS)], capture_output=True, text=True, check=True)
         j = json.loads(r.stdout)
-        tf = flop * j["reps"] / j["seconds"] / 1e12
-        return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": j["threads"], "kind": "reference",
+        st = _runs([flop * n / t / 1e12 for n, t in zip(j["run_reps"], j["run_seconds"])], "TFLOP/s")
+        return {"value": round(st["median"], 5), "unit": "TFLOP/s", "cores": j["threads"], "kind": "reference",
+                "best": round(st["best"], 5), "runs": st["runs"], "threads": j["threads"], "host": _host(),
                 "sample": f"kore's own matmul_batch_float (kore.cpp:783-845, AVX2 path: {bool(j['avx2'])}) built "
                           f"from kore.cpp with kore's flags, {j['threads']} threads, on the 7B ffn_gate shape "
                           f"({rows} x {cols} Q4_K) with {GEMM_B} activations: {j['reps']} calls in "
-                          f"{j['seconds']:.1f} s; host {_cpu_model()}"}
+                          f"{j['seconds']:.1f} s over {CPU_RUNS} timed runs (value = median run, best = fastest run); host "
+                          f"{_cpu_model()}"}
     t0, n = time.perf_counter(), 0
     while time.perf_counter() - t0 < seconds:
         oracle.matmul_batch(QMV_Q4K, w.reshape(-1), rows, cols, x[:8], avx2=True)
@@ -897,64 +937,148 @@ def _rel_err(out, ref):
     return float(np.max(np.abs(np.asarray(out, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
-def cpu_decode(budget_s: float, max_steps: int, gpu_outs=None, gpu_attn=None):
-    """The oracle's decode (kore.cpp:1405-1455, scalar, single thread) on the
-    same inputs: cache positions 0..4095 filled as the GPU's were, then steps
-    at 4096.. over all 28 layers until `budget_s` of decode time is spent."""
+CPU_RUNS = 3   # timed runs of every CPU baseline: median and best are reported (kore_kernels.cpp:706-714)
+
+
+def _runs(rates, unit):
+    """Median and best of the per-run rates (higher is better)."""
+    r = [float(x) for x in rates]
+    return {"median": float(np.median(r)), "best": max(r), "runs": [round(x, 6) for x in r], "unit": unit}
+
+
+def _host():
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count()
+    flags = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = line
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": _cpu_model(), "nproc": os.cpu_count(), "cpus_allowed": aff,
+            "avx2": " avx2" in flags, "fma": " fma" in flags}
+
+
+def _pool(fn, items, threads):
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
+        return list(ex.map(fn, items))
+
+
+def decode_parity(gpu_outs, gpu_attn, threads: int, n_layers: int = NL, n_steps: int = DEC_STEPS):
+    """All 128 configured steps x 28 layers of the 7B decode (positions
+    4096..4223, cache rows 0..4095 filled through the append path) against
+    the oracle - kore's scalar decode, bit-identical to kore (kore.cpp:1405-1455)
+    - and against a float64 evaluation of the same attention over the same
+    fp32 roped rows (oracle ko_attn_ref64), which splits the GPU-to-kore
+    difference into the GPU's own error and kore's.  The layers are
+    independent, so they run on `threads` host threads (the oracle's C calls
+    release the GIL).  The GPU's cache rows of every layer are compared bit
+    for bit with the oracle's."""
     import oracle
-    kv = oracle.KV(NL, DEC_POS0 + max_steps, NH, NKV, HD, ROPE_BASE)
+    inv_f = oracle.inv_freq(HD, ROPE_BASE)
+    n_pos = DEC_POS0 + n_steps
+    kv_gpu = [gpu_attn.read_kv(l, 0, n_pos) for l in range(n_layers)]   # one caller per handle
+
+    def layer(l):
+        k_all = oracle.synth(n_pos, KVD, DEC_SEED, k_stream(l), 0, 2, DEC_PER_MILLE, DEC_OUTLIER)
+        v_all = oracle.synth(n_pos, KVD, DEC_SEED, v_stream(l), 0, 3, DEC_PER_MILLE, DEC_OUTLIER)
+        q_all = oracle.synth(n_steps, E, DEC_SEED, q_stream(l), DEC_POS0, 1, DEC_PER_MILLE, DEC_OUTLIER)
+        kc = oracle.rope_rows(k_all, np.arange(n_pos), NKV, HD, inv_f)
+        kv_ok = bool(np.array_equal(kc, kv_gpu[l][0]) and np.array_equal(v_all, kv_gpu[l][1]))
+        qr = oracle.rope_rows(q_all, np.arange(DEC_POS0, n_pos), NH, HD, inv_f)
+        e_gk, e_ge, e_ke = [], [], []
+        for st in range(n_steps):
+            pos = DEC_POS0 + st
+            ref = oracle.attn_decode(qr[st], kc[:pos + 1], v_all[:pos + 1], pos, NH, NKV, HD)
+            ex = oracle.attn_ref64(qr[st], kc, v_all, np.arange(pos + 1), NH, NKV, HD)
+            g = gpu_outs[st, l]
+            e_gk.append(_rel_err(g, ref))
+            e_ge.append(_rel_err(g, ex))
+            e_ke.append(_rel_err(ref, ex))
+        return kv_ok, e_gk, e_ge, e_ke
+
+    t0 = time.perf_counter()
+    res = _pool(layer, range(n_layers), threads)
+    gk = np.array([r[1] for r in res])   # [layer][step]
+    ge = np.array([r[2] for r in res])
+    ke = np.array([r[3] for r in res])
+    worst = np.unravel_index(int(np.argmax(gk)), gk.shape)
+    return {
+        "decode_steps_compared": n_steps, "decode_layers_compared": n_layers,
+        "decode_max_rel_err": float(gk.max()),
+        "decode_max_rel_err_at": {"step": int(worst[1]), "position": DEC_POS0 + int(worst[1]), "layer": int(worst[0])},
+        "decode_step_max_rel_err": [float(f"{x:.3g}") for x in gk.max(axis=0)],
+        "decode_kv_bitwise": all(r[0] for r in res),
+        "decode_error_budget": {
+            "gpu_vs_float64_max": float(ge.max()), "kore_vs_float64_max": float(ke.max()),
+            "gpu_vs_float64_mean": float(ge.mean()), "kore_vs_float64_mean": float(ke.mean()),
+            "note": "max|d|/max|ref| per (step, layer) against a float64 evaluation over the same fp32 roped "
+                    "q and cache rows (oracle ko_attn_ref64)"},
+        "decode_parity_seconds": round(time.perf_counter() - t0, 2), "decode_parity_threads": threads,
+    }
+
+
+def cpu_decode(seconds: float):
+    """The oracle's decode (kore.cpp:1405-1455, scalar, one thread as kore's
+    attention runs) timed on this host: CPU_RUNS runs of at least
+    seconds / CPU_RUNS each, every run decoding position 4096 (4097 rows
+    attended) of the same workload layer after layer (re-decoding a position
+    rewrites the same cache row with the same data, so every call does the
+    same work)."""
+    import oracle
+    kv = oracle.KV(NL, DEC_POS0 + 1, NH, NKV, HD, ROPE_BASE)
     inv_f = oracle.inv_freq(HD, ROPE_BASE)
     kc, vc = kv.kcache(), kv.vcache()
+    ins = []
     for l in range(NL):
         k0 = oracle.synth(DEC_POS0, KVD, DEC_SEED, k_stream(l), 0, 2, DEC_PER_MILLE, DEC_OUTLIER)
         kc[l, :DEC_POS0] = oracle.rope_rows(k0, np.arange(DEC_POS0), NKV, HD, inv_f)
         vc[l, :DEC_POS0] = oracle.synth(DEC_POS0, KVD, DEC_SEED, v_stream(l), 0, 3, DEC_PER_MILLE, DEC_OUTLIER)
-    spent, nbytes, done, err = 0.0, 0, 0, 0.0
-    while done < max_steps and (done == 0 or spent < budget_s):
-        pos = DEC_POS0 + done
-        for l in range(NL):
-            q = oracle.synth(1, E, DEC_SEED, q_stream(l), pos, 1, DEC_PER_MILLE, DEC_OUTLIER)[0]
-            k = oracle.synth(1, KVD, DEC_SEED, k_stream(l), pos, 2, DEC_PER_MILLE, DEC_OUTLIER)[0]
-            v = oracle.synth(1, KVD, DEC_SEED, v_stream(l), pos, 3, DEC_PER_MILLE, DEC_OUTLIER)[0]
-            t0 = time.perf_counter()
-            ref = kv.decode(l, pos, q, k, v)
-            spent += time.perf_counter() - t0
-            nbytes += decode_bytes(pos + 1)
-            if gpu_outs is not None and done < gpu_outs.shape[0]:
-                err = max(err, _rel_err(gpu_outs[done, l], ref))
-        done += 1
-    kv_equal = None
-    if gpu_attn is not None:
-        n = min(done, gpu_outs.shape[0])
-        kv_equal = True
-        for l in range(NL):
-            rows = (0, DEC_POS0 + n) if l in (0, NL - 1) else (DEC_POS0, DEC_POS0 + n)
-            kg, vg = gpu_attn.read_kv(l, rows[0], rows[1] - rows[0])
-            kv_equal &= bool(np.array_equal(kg, kc[l, rows[0]:rows[1]]) and
-                             np.array_equal(vg, vc[l, rows[0]:rows[1]]))
+        ins.append(tuple(oracle.synth(1, d, DEC_SEED, st(l), DEC_POS0, t, DEC_PER_MILLE, DEC_OUTLIER)[0]
+                         for d, st, t in ((E, q_stream, 1), (KVD, k_stream, 2), (KVD, v_stream, 3))))
+    per_call = []
+    for _ in range(CPU_RUNS):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            l = n % NL
+            kv.decode(l, DEC_POS0, *ins[l])
+            n += 1
+            el = time.perf_counter() - t0
+            if n >= NL and el >= seconds / CPU_RUNS:
+                break
+        per_call.append(el / n)
     kv.close()
-    return dict(gbs=nbytes / spent / 1e9, seconds=spent, steps=done, us_per_layer=spent / (done * NL) * 1e6,
-                max_rel_err=err, kv_bitwise=kv_equal)
+    b = decode_bytes(DEC_POS0 + 1)
+    gbs = _runs([b / t / 1e9 for t in per_call], "GB/s")
+    return dict(gbs=gbs, us_per_layer=[t * 1e6 for t in per_call])
 
 
-def cpu_prefill(n_layers: int, gpu_outs=None):
+def cpu_prefill(gpu_outs=None):
     """The oracle's batched causal attention (kore.cpp:1503-1563 with the AVX2
-    hd_dot/hd_fma arithmetic, single thread) for the first `n_layers` layers."""
+    hd_dot/hd_fma arithmetic, one thread) on whole 2048-row layers of the same
+    workload: CPU_RUNS runs of one layer each (layers 0, 1, ..), each compared
+    with the GPU's rows of that layer."""
     import oracle
-    kv = oracle.KV(n_layers, PF_N, NH, NKV, HD, ROPE_BASE)
-    spent, err = 0.0, 0.0
-    for l in range(n_layers):
+    kv = oracle.KV(CPU_RUNS, PF_N, NH, NKV, HD, ROPE_BASE)
+    t, err = [], 0.0
+    for l in range(CPU_RUNS):
         q = oracle.synth(PF_N, E, PF_SEED, q_stream(l), 0, 1)
         k = oracle.synth(PF_N, KVD, PF_SEED, k_stream(l), 0, 2)
         v = oracle.synth(PF_N, KVD, PF_SEED, v_stream(l), 0, 3)
         t0 = time.perf_counter()
         ref = kv.prefill(l, 0, q, k, v, avx2=True)
-        spent += time.perf_counter() - t0
+        t.append(time.perf_counter() - t0)
         if gpu_outs is not None and l < gpu_outs.shape[0]:
             err = max(err, _rel_err(gpu_outs[l], ref))
     kv.close()
-    return dict(tflops=prefill_flops(0, PF_N) * n_layers / spent / 1e12, seconds=spent, layers=n_layers,
-                max_rel_err=err)
+    F = prefill_flops(0, PF_N)
+    return dict(tflops=_runs([F / x / 1e12 for x in t], "TFLOP/s"), seconds=float(sum(t)), max_rel_err=err)
 
 
 def _cpu_model():
@@ -980,7 +1104,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the 0.5B / 3B / 1.5B workloads")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="decode time budget of the CPU sample")
+    ap.add_argument("--cpu-seconds", type=float, default=9.0,
+                    help="time of each CPU baseline, split over its timed runs")
     ap.add_argument("--no-matvec", action="store_true", help="skip the 7B-token matvec leg")
     ap.add_argument("--matvec-only", action="store_true", help="run only the matvec leg (for profiling)")
     ap.add_argument("--matvec-tokens", type=int, default=10, help="timed 7B tokens of the matvec leg")
@@ -997,7 +1122,6 @@ def main(argv=None):
     ap.add_argument("--prompt-chunks", type=int, default=8, help="64-token chunks of the whole-prompt leg")
     ap.add_argument("--cpu-threads", type=int, default=16,
                     help="threads of kore's own matvec in the CPU baseline (the GPU box's CPU share)")
-    ap.add_argument("--cpu-prefill-layers", type=int, default=2)
     ap.add_argument("--read-calibration", action="store_true",
                     help="only time a plain streaming read kernel per launch size (the yardstick of the "
                          "HBM-bound kernels) and an empty launch")
@@ -1094,6 +1218,10 @@ def main(argv=None):
             "us_per_layer_wall": round(dec["wall_ms"] / (K * NL) * 1e3, 3),
             "launch_us_events": {k: round(v * 1e3, 3) for k, v in _stats(lm).items()},
             "bytes_per_launch_mean": int(bytes_per_launch),
+            "host_pointer_us_per_layer": round(dec["host_us_per_layer"], 3),
+            "host_pointer_note": f"kore_attn_decode (the synchronous host-pointer call kore's forward() would make: "
+                                 f"H2D of q/k/v, the kernels, D2H of the output) per layer over {dec['host_steps']} "
+                                 "steps x 28 layers, steady_clock; PCIe-inclusive, not the value",
         },
         "roofline": {
             "bound": "hbm",
@@ -1119,6 +1247,11 @@ def main(argv=None):
             "launch_us_events": {k: round(v * 1e3, 2) for k, v in _stats(plm).items()},
             "flop_per_layer": F,
             "steps": P,
+            "host_pointer_us_per_layer": round(pf["host_us_per_layer"], 2),
+            "host_pointer_equals_device": pf["host_equals_device"],
+            "host_pointer_note": f"kore_attn_prefill (the synchronous host-pointer call kore's forward_batch() would "
+                                 f"make: H2D of q/k/v, append + attention, D2H of the rows) per layer over "
+                                 f"{pf['host_layers']} layers, steady_clock; PCIe-inclusive",
             "roofline": {"bound": "mfma", "achieved": round(p_ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(p_ach / FP32_MFMA_PEAK_TFLOPS, 4),
                          "traffic": TRAFFIC_PREFILL_BYTES},
@@ -1134,21 +1267,29 @@ def main(argv=None):
     if pr is not None:
         res["prompt"] = prompt_report(pr, qt[0])
     if not args.no_cpu:
-        print(f"[bench] cpu baseline: decode sample ({args.cpu_seconds:.0f} s budget)", file=sys.stderr,
-              flush=True)
-        cd = cpu_decode(args.cpu_seconds, K, dec["outs"], dec["attn"])
+        print(f"[bench] parity: {DEC_STEPS} decode steps x {NL} layers against the oracle and float64, "
+              f"{args.cpu_threads} host threads", file=sys.stderr, flush=True)
+        res["parity"] = dict(decode_parity(dec["outs"], dec["attn"], args.cpu_threads), tolerance=1e-4)
+        print(f"[bench] cpu baseline: decode ({CPU_RUNS} runs, {args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
+        cd = cpu_decode(args.cpu_seconds)
+        host = _host()
         res["cpu_baseline"] = {
-            "value": round(cd["gbs"], 4),
+            "value": round(cd["gbs"]["median"], 4),
             "unit": "GB/s",
             "cores": 1,
             "kind": "port",
-            "sample": f"{cd['steps']} decode steps x {NL} layers at positions {DEC_POS0}..{DEC_POS0 + cd['steps'] - 1} "
-                      f"of the same workload, {cd['seconds']:.1f} s, {cd['us_per_layer']:.0f} us/layer; "
-                      f"C restatement of kore.cpp:1405-1455 (bit-identical to kore), gcc -O3, one thread "
-                      f"as kore's attention; host {_cpu_model()}, {os.cpu_count()} cpus",
+            "best": round(cd["gbs"]["best"], 4),
+            "runs": cd["gbs"]["runs"],
+            "threads": 1,
+            "host": host,
+            "sample": f"{CPU_RUNS} timed runs of at least {args.cpu_seconds / CPU_RUNS:.1f} s, each decoding position "
+                      f"{DEC_POS0} ({DEC_POS0 + 1} rows attended) of the same workload over its {NL} layers in turn, "
+                      f"{float(np.median(cd['us_per_layer'])):.0f} us per layer (median run); value = median run, "
+                      "best = fastest run; C restatement of kore.cpp:1405-1455 (bit-identical to kore's own "
+                      "forward()), gcc -O3, one thread: kore's attention runs on the calling thread whatever "
+                      "--threads is (kore.cpp:1432 sits outside parallel_rows); "
+                      f"host {host['cpu_model']}, nproc {host['nproc']}, {host['cpus_allowed']} cpus allowed",
         }
-        res["parity"] = {"decode_max_rel_err": cd["max_rel_err"], "decode_kv_bitwise": cd["kv_bitwise"],
-                         "tolerance": 1e-4}
         if mv is not None:
             import oracle
             print(f"[bench] cpu baseline: kore's matvec, {args.cpu_threads} threads", file=sys.stderr, flush=True)
@@ -1176,15 +1317,19 @@ def main(argv=None):
                   flush=True)
             res["prompt"]["cpu_baseline"] = cpu_prompt(args.cpu_seconds, args.cpu_threads)
         if pf is not None:
-            print(f"[bench] cpu baseline: prefill sample ({args.cpu_prefill_layers} layers)", file=sys.stderr,
+            print(f"[bench] cpu baseline: prefill ({CPU_RUNS} runs of one 2048-row layer)", file=sys.stderr,
                   flush=True)
-            cp = cpu_prefill(args.cpu_prefill_layers, pf["outs"])
+            cp = cpu_prefill(pf["outs"])
             res["prefill"]["cpu_baseline"] = {
-                "value": round(cp["tflops"], 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-                "sample": f"{cp['layers']} layers x {PF_N}-row causal prefill, {cp['seconds']:.1f} s; C restatement "
-                          "of kore.cpp:1503-1563 with kore's AVX2 hd_dot/hd_fma arithmetic, one thread",
+                "value": round(cp["tflops"]["median"], 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                "best": round(cp["tflops"]["best"], 5), "runs": cp["tflops"]["runs"], "threads": 1,
+                "sample": f"{CPU_RUNS} timed runs, each one whole {PF_N}-row causal prefill layer of the same "
+                          f"workload (layers 0..{CPU_RUNS - 1}), {cp['seconds']:.1f} s in all; value = median run, "
+                          "best = fastest run; C restatement of kore.cpp:1503-1563 with kore's AVX2 hd_dot/hd_fma "
+                          "arithmetic (bit-identical to kore's own forward_batch()), one thread as kore's attention",
             }
             res["parity"]["prefill_max_rel_err"] = cp["max_rel_err"]
+            res["parity"]["prefill_layers_compared"] = CPU_RUNS
     dec["attn"].close()
     print(json.dumps(res), flush=True)
     return 0

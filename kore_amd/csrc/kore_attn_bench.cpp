@@ -113,3 +113,53 @@ KAB_API int kab_prefill_run(kore_attn_t h, int n_layer, int pos0, int n_tok, int
                                      nullptr);
     });
 }
+
+// The host-pointer round trip kore's own call sites would make: n_steps decode
+// steps at positions pos_first.. over layers 0..n_layer-1 through
+// kore_attn_decode (H2D of q/k/v, the kernels, D2H of the output, returning
+// when the output is in host memory, like kore's loop at kore.cpp:1432-1455).
+// Host inputs [layer][in_steps][dim]; out [n_layer][n_head*head_dim] (the last
+// step).  wall_ms: steady_clock over the whole loop, after one untimed call
+// (layer 0, first step) that re-decodes that step with the same inputs.
+KAB_API int kab_decode_host_run(kore_attn_t h, int n_layer, int pos_first, int n_steps, const float *q,
+                                const float *k, const float *v, int in_steps, float *out, double *wall_ms) {
+    kore_attn_info inf;
+    if (int rc = kore_attn_get_info(h, &inf)) return rc;
+    if (n_layer <= 0 || n_layer > inf.n_layer || n_steps <= 0 || in_steps < n_steps || !wall_ms)
+        return KORE_ATTN_E_INVALID;
+    const size_t E = (size_t)inf.n_head * inf.head_dim, kvd = (size_t)inf.n_head_kv * inf.head_dim;
+    // one untimed call first: the handle sizes its host staging on its first host-pointer call
+    if (int rc = kore_attn_decode(h, 0, pos_first, inf.n_head, inf.n_head_kv, inf.head_dim, q, k, v, out)) return rc;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int s = 0; s < n_steps; ++s)
+        for (int l = 0; l < n_layer; ++l) {
+            const size_t row = (size_t)l * in_steps + s;
+            if (int rc = kore_attn_decode(h, l, pos_first + s, inf.n_head, inf.n_head_kv, inf.head_dim, q + row * E,
+                                          k + row * kvd, v + row * kvd, out + (size_t)l * E))
+                return rc;
+        }
+    *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return KORE_ATTN_OK;
+}
+
+// The same for a prefill chunk: n_tok rows at pos0 over layers 0..n_layer-1
+// through kore_attn_prefill (kore.cpp:1503-1563).  Host inputs and outputs
+// [layer][n_tok][dim].
+KAB_API int kab_prefill_host_run(kore_attn_t h, int n_layer, int pos0, int n_tok, const float *q, const float *k,
+                                 const float *v, float *out, double *wall_ms) {
+    kore_attn_info inf;
+    if (int rc = kore_attn_get_info(h, &inf)) return rc;
+    if (n_layer <= 0 || n_layer > inf.n_layer || n_tok <= 0 || !wall_ms) return KORE_ATTN_E_INVALID;
+    const size_t E = (size_t)inf.n_head * inf.head_dim, kvd = (size_t)inf.n_head_kv * inf.head_dim;
+    // one untimed call first: the handle sizes its host staging on its first host-pointer call
+    if (int rc = kore_attn_prefill(h, 0, pos0, n_tok, inf.n_head, inf.n_head_kv, inf.head_dim, q, k, v, out)) return rc;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int l = 0; l < n_layer; ++l) {
+        const size_t row = (size_t)l * n_tok;
+        if (int rc = kore_attn_prefill(h, l, pos0, n_tok, inf.n_head, inf.n_head_kv, inf.head_dim, q + row * E,
+                                       k + row * kvd, v + row * kvd, out + row * E))
+            return rc;
+    }
+    *wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return KORE_ATTN_OK;
+}

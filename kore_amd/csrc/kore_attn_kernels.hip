@@ -67,7 +67,6 @@ __device__ __forceinline__ float row16_max(float x) {
     return fmaxf(x, dpp<0x121>(x));
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-constexpr float kLog2e = 1.4426950408889634f;
 
 // NEOX rotation of the pair (x0, x1) = (x[i], x[i + hd/2]) by (c, s)
 // (kore.cpp:1379-1382): products rounded, then difference / sum rounded.
@@ -124,27 +123,60 @@ __device__ __forceinline__ float sum4rows(float x) {
     return a + b;
 }
 
+// v_mfma_f64_16x16x4f64, one block: lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; D register v of lane l is D[4v + l/16][l%16] (checked on the
+// GPU: the f64 output rows are interleaved differently from the f32 ones).
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ doublex4 mfma16d(double a, double b, doublex4 c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+// Sum over the four lanes l % 16 + 16 k of a double (both 32-bit halves go
+// through the permlane swaps).
+__device__ __forceinline__ double sum4rows_d(double x) {
+    auto pair = [](double v, bool p32, double &a, double &b) {
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+        const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+        const auto rl = p32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                            : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto rh = p32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                            : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        const unsigned l0 = rl[0], l1 = rl[1], h0 = rh[0], h1 = rh[1];
+        a = __builtin_bit_cast(double, ((unsigned long long)h0 << 32) | l0);
+        b = __builtin_bit_cast(double, ((unsigned long long)h1 << 32) | l1);
+    };
+    double a, b;
+    pair(x, false, a, b);
+    x = a + b;
+    pair(x, true, a, b);
+    return a + b;
+}
+
 // Workgroup (split, kv-head g): cache slots [r0, r_end) of kv-head g for the
 // NR q-heads of g, so every K/V byte is read once per kv-head (kore's
 // head-outer loop, kore.cpp:1432, reads it once per q-head).  The slots are
 // cut into blocks of 16 rows; wave w takes blocks w, w + 4, ... and keeps its
 // own online softmax (max, sum, output) for all NR heads, so the block loop
-// has no workgroup barrier.  Per block, on fp32 MFMA (v_mfma_f32_16x16x4f32):
-//   scores  S[row][head] = K[16 rows][hd] . q^T: lane (m, k) = (l % 16, l / 16)
-//           gives K[row m][16t + 4k + e] and the roped, pre-scaled q of head m
-//           at the same dim for MFMA k-step (t, e), so both operands come
-//           straight from 16-byte loads (the dims are summed in a different
-//           order, which the dot product allows).  The scores are already
-//           multiplied by 1/sqrt(hd) * log2(e): the softmax runs in base 2
-//           on v_exp_f32.  Lane (m, k) ends up with rows 4k..4k+3 of head m.
-//   softmax the head's running max over the 16 rows is a max over the lane's
-//           four registers and lanes m, m+16, m+32, m+48 (permlane swaps);
-//           the exponentials stay in the score registers.
-//   values  O^T[dim][head] += V^T[dim][16 rows] . P: k-step s takes rows
-//           4k + s, which is exactly score register s of lane (m, k), so P
-//           is fed back as the B operand without any data movement; lane
-//           (m, k) gives V[row 4k + s][64j + 4m + e] (16-byte loads) for the
-//           output block 4j + e.
+// has no workgroup barrier.  Per block:
+//   scores  S[row][head] = K[16 rows][hd] . q^T on fp64 MFMA
+//           (v_mfma_f64_16x16x4f64): lane (m, k) = (l % 16, l / 16) gives
+//           K[row m][16t + 4k + e] (converted to double) and the roped q of
+//           head m at the same dim, times 1/sqrt(hd) * log2(e) in double, for
+//           k-step (t, e), so both operands come straight from 16-byte loads
+//           (the dims are summed in a different order, which the dot product
+//           allows).  The scores reach a few hundred in the log2 domain on
+//           heavy-tailed inputs, where an fp32 accumulation chain loses more
+//           than kore's own rounding; in fp64 the products are exact and the
+//           sum loses nothing that matters.  Lane (m, k) ends up with rows
+//           4v + k (v < 4) of head m.
+//   softmax the head's running max (fp32) over the 16 rows is a max over the
+//           lane's four registers and lanes m, m+16, m+32, m+48 (permlane
+//           swaps); each weight is 2^(score - max) with the difference taken
+//           in fp64, then v_exp_f32; the weights stay in the score registers.
+//   values  O^T[dim][head] += V^T[dim][16 rows] . P on fp32 MFMA: k-step s
+//           takes rows 4s + k, which is exactly score register s of lane
+//           (m, k), so P is fed back as the B operand without any data
+//           movement; lane (m, k) gives V[row 4s + k][64j + 4m + e] (16-byte
+//           loads) for the output block 4j + e.
 // Issue order of a wave: its q and the new k/v row, the K rows of its first
 // block, then (once q has returned) the RoPE of q through the wave's own LDS
 // rows, then the V rows, so the score MFMAs run while V streams in.  Every
@@ -253,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     auto load_v = [&](float4 (*vf)[NJ], int b) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const float *vr = vg + (size_t)min(r0 + 16 * b + 4 * kq + s, last_row) * HD + 4 * m16;
+            const float *vr = vg + (size_t)min(r0 + 16 * b + 4 * s + kq, last_row) * HD + 4 * m16;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) vf[s][j] = ld4(vr + 64 * j);
         }
@@ -263,11 +295,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     __builtin_amdgcn_sched_barrier(0);
 
     // RoPE of the staged pairs into the wave's LDS rows, then the B operand:
-    // lane (m16, kq) holds head m16 at dims 16t + 4kq + e (heads past NR are
-    // zero columns).
-    const float qscale = a.scale * kLog2e;
+    // lane (m16, kq) holds head m16 at dims 16t + 4kq + e, times kore's
+    // 1/sqrt(hd) and log2(e) in double (heads past NR are zero columns).
+    const double qscale = (double)a.scale * 1.4426950408889634;
     const int hq = min(m16, NR - 1);
-    float qb[NT][4];
+    double qb[NT][4];
     {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -280,9 +312,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
                 const float2 cs = (e & 1) ? make_float2(c4.z, c4.w) : make_float2(c4.x, c4.y);
                 rope_pair(comp(sx0[i], e), comp(sx1[i], e), cs, y0[e], y1[e]);
             }
-            st4(&wq[row * QS + 4 * sc], make_float4(y0[0] * qscale, y0[1] * qscale, y0[2] * qscale, y0[3] * qscale));
-            st4(&wq[row * QS + HALF + 4 * sc],
-                make_float4(y1[0] * qscale, y1[1] * qscale, y1[2] * qscale, y1[3] * qscale));
+            st4(&wq[row * QS + 4 * sc], make_float4(y0[0], y0[1], y0[2], y0[3]));
+            st4(&wq[row * QS + HALF + 4 * sc], make_float4(y1[0], y1[1], y1[2], y1[3]));
         }
         __builtin_amdgcn_wave_barrier();
         float4 qv[NT];
@@ -291,26 +322,30 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) qb[t][e] = m16 < NR ? comp(qv[t], e) : 0.f;
+            for (int e = 0; e < 4; ++e) qb[t][e] = m16 < NR ? (double)comp(qv[t], e) * qscale : 0.0;
     }
     // dot of q (operand layout) with a k row staged in LDS: lane (m16, kq)
     // sums dims 16t + 4kq + e of head m16, then the four lanes of the head
     auto row_score = [&](const float *kr) {
-        float sx = 0.f;
+        double sx = 0.0;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const float4 kx = ld4(&kr[16 * t + 4 * kq]);
-            sx = fmaf(qb[t][0], kx.x, sx);
-            sx = fmaf(qb[t][1], kx.y, sx);
-            sx = fmaf(qb[t][2], kx.z, sx);
-            sx = fmaf(qb[t][3], kx.w, sx);
+            sx = fma(qb[t][0], (double)kx.x, sx);
+            sx = fma(qb[t][1], (double)kx.y, sx);
+            sx = fma(qb[t][2], (double)kx.z, sx);
+            sx = fma(qb[t][3], (double)kx.w, sx);
         }
-        return sum4rows(sx);
+        return sum4rows_d(sx);
     };
+    // A single row as a softmax state: max = its score rounded to fp32, sum
+    // = 2^(score - max) with the difference in fp64 (about 1), output = that
+    // sum times the row (the merge applies the sum to the stored v row).
     // ---- the wave's extra row (state kWaves + wave; -inf and a zero row
     // when the wave has none) and, in NEW_WAVE, the new row (state 2 kWaves,
     // roped here; -inf and a zero row outside the owner workgroup).  Only
-    // LDS and register work: no memory operation under these branches.
+    // LDS and register work: no memory operation under these branches.  The
+    // merge weighs each stored v row with the state's sum.
     {
         const bool x_on = wave < n_extra;
         if (lane < HALF) {
@@ -320,10 +355,12 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             s_vx[wave * HD + lane + HALF] = x_on ? xv1 : 0.f;
         }
         __builtin_amdgcn_wave_barrier();
-        const float sx = row_score(&s_kx[wave * HD]);
+        const double sx = row_score(&s_kx[wave * HD]);
         if (kq == 0 && m16 < NR) {
-            s_m[(kWaves + wave) * 8 + m16] = (x_on && xrow != new_slot) ? sx : -INFINITY;
-            s_l[(kWaves + wave) * 8 + m16] = x_on ? 1.f : 0.f;
+            const bool on = x_on && xrow != new_slot;
+            const float mx = (float)sx;
+            s_m[(kWaves + wave) * 8 + m16] = on ? mx : -INFINITY;
+            s_l[(kWaves + wave) * 8 + m16] = on ? fast_exp2((float)(sx - (double)mx)) : 0.f;
         }
     }
     float nky0, nky1;
@@ -336,10 +373,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             s_vnew[lane + HALF] = is_owner ? nv1 : 0.f;
         }
         __builtin_amdgcn_wave_barrier();
-        const float sn = row_score(s_knew);
+        const double sn = row_score(s_knew);
         if (kq == 0 && m16 < NR) {
-            s_m[2 * kWaves * 8 + m16] = is_owner ? sn : -INFINITY;
-            s_l[2 * kWaves * 8 + m16] = is_owner ? 1.f : 0.f;
+            const float mn = (float)sn;
+            s_m[2 * kWaves * 8 + m16] = is_owner ? mn : -INFINITY;
+            s_l[2 * kWaves * 8 + m16] = is_owner ? fast_exp2((float)(sn - (double)mn)) : 0.f;
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -359,17 +397,18 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
 
     auto process = [&](const float4 *kf, const float4 (*vf)[NJ], int b, bool first) {
         const int rb = r0 + 16 * b;
-        floatx4 s = {0.f, 0.f, 0.f, 0.f};
+        doublex4 s = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) s = mfma16(comp(kf[t], e), qb[t][e], s);
-        float x[4], mt = -INFINITY;
+            for (int e = 0; e < 4; ++e) s = mfma16d((double)comp(kf[t], e), qb[t][e], s);
+        bool ok[4];
+        float mt = -INFINITY;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int row = rb + 4 * kq + v;
-            x[v] = (row < r_end && row != new_slot) ? s[v] : -INFINITY;
-            mt = fmaxf(mt, x[v]);
+            const int row = rb + 4 * v + kq;
+            ok[v] = row < r_end && row != new_slot;
+            mt = fmaxf(mt, ok[v] ? (float)s[v] : -INFINITY);
         }
         const float m_new = fmaxf(m_run, max4rows(mt));
         const float m_use = m_new == -INFINITY ? 0.f : m_new;   // a block with every row masked
@@ -377,7 +416,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         float p[4], ps = 0.f;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            p[v] = fast_exp2(x[v] - m_use);
+            p[v] = ok[v] ? fast_exp2((float)(s[v] - (double)m_use)) : 0.f;
             ps += p[v];
         }
         l_part = fmaf(l_part, alpha, ps);
@@ -476,9 +515,12 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             const bool on = w < kWaves ? true : (w < 2 * kWaves ? w - kWaves < n_extra : is_owner);
             if (!on) continue;
             const float mx = w < kWaves ? mw[w] : ms[w - kWaves];
-            const float e = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
+            const float e0 = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
             const float4 x = w < kWaves ? xw[w] : xs[w - kWaves];
-            l = fmaf(e, w < kWaves ? lw[w] : ls[w - kWaves], l);
+            // a wave state holds its weighted output; a single row's state
+            // holds the bare v row, weighed here with the state's sum
+            const float e = w < kWaves ? e0 : e0 * ls[w - kWaves];
+            l = w < kWaves ? fmaf(e, lw[w], l) : l + e;
             acc.x = fmaf(e, x.x, acc.x);
             acc.y = fmaf(e, x.y, acc.y);
             acc.z = fmaf(e, x.z, acc.z);

@@ -24,7 +24,7 @@
 // GGUF mode (pins the loader and the whole token on a real file):
 //   kore_layer_ref --gguf-forward file.gguf CTX_MAX TOKEN...
 //   kore_layer_ref --gguf-forward-batch file.gguf CTX_MAX SPLIT TOKEN...
-//   kore_layer_ref --time-batch THREADS SECONDS   (forward_batch() of 64-token
+//   kore_layer_ref --time-batch THREADS SECONDS [RUNS]  (forward_batch() of 64-token
 //   chunks at positions 0, 64, .., 448 on the synthetic 7B engine of --time)
 // runs kore's load_model + engine_init(ctx_max, 4 threads, quantised path) and
 // forward(token, pos, logits) for the tokens at positions 0, 1, ...; prints one
@@ -32,7 +32,7 @@
 // the hex of their float bits), or {"ok": false} when kore refuses the file.
 //
 // Timing mode (the CPU baseline of the benchmark's whole-token leg):
-//   kore_layer_ref --time THREADS MIN_SECONDS POS
+//   kore_layer_ref --time THREADS MIN_SECONDS POS [RUNS]
 // builds a Qwen2.5-7B-shape engine (28 layers, 3584 / 18944, 28 / 4 heads of
 // 128, 152064-row Q6_K output head; Q4_K weights with attn_v and ffn_down in
 // Q6_K on the layers Q4_K_M files keep them there) from synthetic block bytes,
@@ -100,7 +100,18 @@ void synth(OwnedTensor &o, uint32_t type, uint64_t cols, uint64_t rows, uint64_t
     o.t.data = o.bytes.data();
 }
 
-int time_mode(unsigned nth, double min_s, int pos0, bool batch) {
+// "[a, b, ...]" of per-run values for the timing modes' JSON lines
+std::string json_list(const std::vector<double> &v, const char *fmt) {
+    std::string out = "[";
+    char buf[64];
+    for (size_t i = 0; i < v.size(); ++i) {
+        snprintf(buf, sizeof buf, fmt, v[i]);
+        out += (i ? ", " : "") + std::string(buf);
+    }
+    return out + "]";
+}
+
+int time_mode(unsigned nth, double min_s, int pos0, bool batch, int runs) {
     const int NL = 28, E = 3584, FF = 18944, NH = 28, NKV = 4, HD = 128, VOCAB = 152064;
     const int kvd = NKV * HD, ctx = batch ? 512 : pos0 + 256;
     Engine e;
@@ -160,29 +171,50 @@ int time_mode(unsigned nth, double min_s, int pos0, bool batch) {
         std::vector<int> toks(B, 0);
         if (!forward_batch(e, toks.data(), 64, 0, true)) return 5;   // warm-up
         int chunks = 0;
-        const auto t0 = std::chrono::steady_clock::now();
         double el = 0;
-        do {                                                   // 64-token chunks at 0, 64, .., 448 in turn
-            if (!forward_batch(e, toks.data(), 64, 64 * (chunks % 8), true)) return 5;
-            ++chunks;
-            el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-        } while (el < min_s);
+        std::vector<double> run_chunks, run_s;
+        for (int run = 0; run < runs; ++run) {                 // RUNS timed runs of at least MIN_SECONDS
+            int c = 0;
+            double t = 0;
+            const auto t0 = std::chrono::steady_clock::now();
+            do {                                               // 64-token chunks at 0, 64, .., 448 in turn
+                if (!forward_batch(e, toks.data(), 64, 64 * (c % 8), true)) return 5;
+                ++c;
+                t = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            } while (t < min_s);
+            run_chunks.push_back(c);
+            run_s.push_back(t);
+            chunks += c;
+            el += t;
+        }
         printf("{\"tokens\": %d, \"chunks\": %d, \"seconds\": %.6f, \"threads\": %u, \"avx2\": %d, "
-               "\"checksum\": %.9g}\n", chunks * 64, chunks, el, nth, (int)e.avx2,
-               (double)e.logits[(size_t)VOCAB / 2]);
+               "\"checksum\": %.9g, \"run_chunks\": %s, \"run_seconds\": %s}\n", chunks * 64, chunks, el, nth,
+               (int)e.avx2, (double)e.logits[(size_t)VOCAB / 2], json_list(run_chunks, "%.0f").c_str(),
+               json_list(run_s, "%.6f").c_str());
         return 0;
     }
     if (!forward(e, 0, pos0, true)) return 5;                  // warm-up
     int tokens = 0;
-    const auto t0 = std::chrono::steady_clock::now();
     double el = 0;
-    do {
-        if (!forward(e, 0, pos0 + 1 + tokens % 200, true)) return 5;
-        ++tokens;
-        el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-    } while (el < min_s);
-    printf("{\"tokens\": %d, \"seconds\": %.6f, \"threads\": %u, \"avx2\": %d, \"pos\": %d, \"checksum\": %.9g}\n",
-           tokens, el, nth, (int)e.avx2, pos0, (double)e.logits[(size_t)VOCAB / 2]);
+    std::vector<double> run_tokens, run_s;
+    for (int run = 0; run < runs; ++run) {                     // RUNS timed runs of at least MIN_SECONDS
+        int n = 0;
+        double t = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        do {
+            if (!forward(e, 0, pos0 + 1 + tokens % 200, true)) return 5;
+            ++tokens;
+            ++n;
+            t = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        } while (t < min_s);
+        run_tokens.push_back(n);
+        run_s.push_back(t);
+        el += t;
+    }
+    printf("{\"tokens\": %d, \"seconds\": %.6f, \"threads\": %u, \"avx2\": %d, \"pos\": %d, \"checksum\": %.9g, "
+           "\"run_tokens\": %s, \"run_seconds\": %s}\n",
+           tokens, el, nth, (int)e.avx2, pos0, (double)e.logits[(size_t)VOCAB / 2], json_list(run_tokens, "%.0f").c_str(),
+           json_list(run_s, "%.6f").c_str());
     return 0;
 }
 
@@ -248,10 +280,11 @@ int main(int argc, char **argv) {
         return gguf_forward_batch(argv[2], atoi(argv[3]), atoi(argv[4]), argc - 5, argv + 5);
     if (argc >= 4 && std::string(argv[1]) == "--gguf-forward")
         return gguf_forward(argv[2], atoi(argv[3]), argc - 4, argv + 4);
-    if (argc == 5 && std::string(argv[1]) == "--time")
-        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), false);
-    if (argc == 4 && std::string(argv[1]) == "--time-batch")
-        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), 0, true);
+    if ((argc == 5 || argc == 6) && std::string(argv[1]) == "--time")
+        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), false,
+                         argc == 6 ? std::max(1, atoi(argv[5])) : 1);
+    if ((argc == 4 || argc == 5) && std::string(argv[1]) == "--time-batch")
+        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), 0, true, argc == 5 ? std::max(1, atoi(argv[4])) : 1);
     if (argc != 3) { fprintf(stderr, "usage: kore_layer_ref job.bin result.bin | --time THREADS SECONDS POS\n"); return 2; }
     FILE *in = fopen(argv[1], "rb");
     FILE *out = fopen(argv[2], "wb");

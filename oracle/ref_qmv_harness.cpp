@@ -19,14 +19,15 @@
 // AVX2 one equals the scalar one where the CPU has no AVX2/FMA).
 //
 // Timing mode (the CPU baseline of the benchmark):
-//   kore_qmv_ref --time THREADS MIN_SECONDS COPIES job.bin
+//   kore_qmv_ref --time THREADS MIN_SECONDS COPIES job.bin [RUNS]
 // keeps COPIES copies of the job's matrix (so that the weights streamed exceed
 // the host's caches, as a model's do) and runs kore's own quant() + mv() pair
 // on them in turn - quantize_row_q8_K then matvec_mt over all rows with
 // THREADS threads and the AVX2 dot products where the CPU has them
 // (kore.cpp:1387-1394, 677-682) - until MIN_SECONDS have passed; prints one
 // JSON line {"reps", "seconds", "rows", "cols", "weight_bytes", "avx2",
-// "threads", "copies"}.
+// "threads", "copies", "run_reps", "run_seconds"} (RUNS timed runs of at least
+// MIN_SECONDS each, default 1; the totals sum them).
 //
 //   kore_qmv_ref --gguf file.gguf
 // runs kore's load_model (kore.cpp:188-285) on the file and prints one JSON
@@ -35,11 +36,12 @@
 // by name and fnv the 64-bit FNV-1a hash of the nbytes bytes the tensor points
 // to (kore's stderr messages pass through).
 //
-//   kore_qmv_ref --time-batch THREADS MIN_SECONDS job.bin
+//   kore_qmv_ref --time-batch THREADS MIN_SECONDS job.bin [RUNS]
 // takes a batch-mode job and runs kore's matmul_batch_float on it with
 // THREADS threads and the AVX2 path where the CPU has it (as forward_batch()
 // calls it, kore.cpp:1524) until MIN_SECONDS have passed; prints one JSON line
-// {"reps", "seconds", "rows", "cols", "B", "avx2", "threads"}.
+// {"reps", "seconds", "rows", "cols", "B", "avx2", "threads", "run_reps",
+// "run_seconds"} (RUNS timed runs as in --time).
 
 #define main kore_ref_main
 #include "kore.cpp"
@@ -52,7 +54,18 @@
 #include <string>
 #include <vector>
 
-static int time_mode(unsigned nth, double min_s, int copies, const char *job) {
+// "[a, b, ...]" of per-run values for the timing modes' JSON lines
+static std::string json_list(const std::vector<double> &v, const char *fmt) {
+    std::string out = "[";
+    char buf[64];
+    for (size_t i = 0; i < v.size(); ++i) {
+        snprintf(buf, sizeof buf, fmt, v[i]);
+        out += (i ? ", " : "") + std::string(buf);
+    }
+    return out + "]";
+}
+
+static int time_mode(unsigned nth, double min_s, int copies, const char *job, int runs) {
     FILE *in = fopen(job, "rb");
     if (!in) { perror("open"); return 2; }
     int32_t hdr[3];
@@ -84,18 +97,30 @@ static int time_mode(unsigned nth, double min_s, int copies, const char *job) {
         quantize_row_q8_K(x.data(), xq.data(), cols);
         matvec_mt(t[(size_t)c], xq.data(), out.data(), avx2, nth);
     }
-    int reps = 0;
-    const auto t0 = std::chrono::steady_clock::now();
+    // RUNS timed runs of at least MIN_SECONDS each (kore_kernels times best-of-N)
+    int reps = 0, k = 0;
     double el = 0;
-    do {
-        quantize_row_q8_K(x.data(), xq.data(), cols);
-        matvec_mt(t[(size_t)(reps % copies)], xq.data(), out.data(), avx2, nth);
-        ++reps;
-        el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-    } while (el < min_s);
+    std::vector<double> run_reps, run_s;
+    for (int run = 0; run < runs; ++run) {
+        int r = 0;
+        double e = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        do {
+            quantize_row_q8_K(x.data(), xq.data(), cols);
+            matvec_mt(t[(size_t)(k++ % copies)], xq.data(), out.data(), avx2, nth);
+            ++r;
+            e = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        } while (e < min_s);
+        run_reps.push_back(r);
+        run_s.push_back(e);
+        reps += r;
+        el += e;
+    }
     printf("{\"reps\": %d, \"seconds\": %.6f, \"rows\": %lld, \"cols\": %lld, \"weight_bytes\": %zu, "
-           "\"avx2\": %d, \"threads\": %u, \"copies\": %d, \"checksum\": %.9g}\n",
-           reps, el, (long long)rows, (long long)cols, wb, (int)avx2, nth, copies, (double)out[(size_t)rows / 2]);
+           "\"avx2\": %d, \"threads\": %u, \"copies\": %d, \"checksum\": %.9g, \"run_reps\": %s, "
+           "\"run_seconds\": %s}\n",
+           reps, el, (long long)rows, (long long)cols, wb, (int)avx2, nth, copies, (double)out[(size_t)rows / 2],
+           json_list(run_reps, "%.0f").c_str(), json_list(run_s, "%.6f").c_str());
     return 0;
 }
 
@@ -132,7 +157,7 @@ static int read_batch_job(const char *job, BatchJob &j) {
     return 0;
 }
 
-static int time_batch_mode(unsigned nth, double min_s, const char *job) {
+static int time_batch_mode(unsigned nth, double min_s, const char *job, int runs) {
     BatchJob j;
     if (int rc = read_batch_job(job, j)) return rc;
     const int B8 = (j.B + 7) & ~7;
@@ -140,16 +165,26 @@ static int time_batch_mode(unsigned nth, double min_s, const char *job) {
     const bool avx2 = cpu_has_avx2();
     matmul_batch_float(j.t, j.x.data(), j.B, xT.data(), o.data(), avx2, nth);   // warm-up
     int reps = 0;
-    const auto t0 = std::chrono::steady_clock::now();
     double el = 0;
-    do {
-        matmul_batch_float(j.t, j.x.data(), j.B, xT.data(), o.data(), avx2, nth);
-        ++reps;
-        el = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-    } while (el < min_s);
+    std::vector<double> run_reps, run_s;
+    for (int run = 0; run < runs; ++run) {
+        int r = 0;
+        double e = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        do {
+            matmul_batch_float(j.t, j.x.data(), j.B, xT.data(), o.data(), avx2, nth);
+            ++r;
+            e = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        } while (e < min_s);
+        run_reps.push_back(r);
+        run_s.push_back(e);
+        reps += r;
+        el += e;
+    }
     printf("{\"reps\": %d, \"seconds\": %.6f, \"rows\": %lld, \"cols\": %lld, \"B\": %d, \"avx2\": %d, "
-           "\"threads\": %u, \"checksum\": %.9g}\n",
-           reps, el, (long long)j.rows, (long long)j.cols, j.B, (int)avx2, nth, (double)o[o.size() / 2]);
+           "\"threads\": %u, \"checksum\": %.9g, \"run_reps\": %s, \"run_seconds\": %s}\n",
+           reps, el, (long long)j.rows, (long long)j.cols, j.B, (int)avx2, nth, (double)o[o.size() / 2],
+           json_list(run_reps, "%.0f").c_str(), json_list(run_s, "%.6f").c_str());
     return 0;
 }
 
@@ -203,10 +238,11 @@ static int gguf_mode(const char *path) {
 int main(int argc, char **argv) {
     if (argc == 3 && std::string(argv[1]) == "--gguf") return gguf_mode(argv[2]);
     if (argc == 4 && std::string(argv[1]) == "--batch") return batch_mode(argv[2], argv[3]);
-    if (argc == 5 && std::string(argv[1]) == "--time-batch")
-        return time_batch_mode((unsigned)atoi(argv[2]), atof(argv[3]), argv[4]);
-    if (argc == 6 && std::string(argv[1]) == "--time")
-        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), argv[5]);
+    if ((argc == 5 || argc == 6) && std::string(argv[1]) == "--time-batch")
+        return time_batch_mode((unsigned)atoi(argv[2]), atof(argv[3]), argv[4], argc == 6 ? std::max(1, atoi(argv[5])) : 1);
+    if ((argc == 6 || argc == 7) && std::string(argv[1]) == "--time")
+        return time_mode((unsigned)atoi(argv[2]), atof(argv[3]), atoi(argv[4]), argv[5],
+                         argc == 7 ? std::max(1, atoi(argv[6])) : 1);
     if (argc != 3) {
         fprintf(stderr, "usage: kore_qmv_ref job.bin result.bin | --batch job.bin result.bin | --time THREADS SECONDS COPIES "
                         "job.bin | --time-batch THREADS SECONDS job.bin\n");

@@ -6,7 +6,8 @@ Each case is a sequence of kore calls on one KV store: decode steps
 values of ``oracle.synth``: for step ``st`` and layer ``l`` the q/k/v rows
 are row ``st`` of streams ``(1<<32)|l``, ``(2<<32)|l`` and ``(3<<32)|l``
 (outlier tensors 1, 2, 3).  A prefill chunk uses the same q/k/v for all of
-its rows (in kore those are the layer biases, see oracle/ref_harness.cpp).
+its rows (in kore those are the layer biases, see oracle/ref_harness.cpp);
+the case of one-row prefill steps gives every row its own q/k/v.
 """
 from __future__ import annotations
 
@@ -55,6 +56,13 @@ CASES = [
     dict(name="prefill_1p5b_avx2", mode="prefill", n_layer=1, n_head=12, n_head_kv=2,
          head_dim=128, ctx=128, rope_base=1e6, avx2=1, seed=24, per_mille=0,
          steps=[[0, 64], [64, 64]], sample_steps=[1], keep_kv=False),
+    # Distinct q/k/v on every row of the batched path: forward_batch() with one
+    # row per call (kore's batched attention, AVX2 hd_dot/hd_fma, 1 % outlier
+    # channels x20); row z attends positions 0..z exactly as row z of one
+    # 64-row chunk would, so a GPU chunk of all 64 rows replays it.
+    dict(name="prefill_rows_7b_avx2", mode="prefill", n_layer=1, n_head=14, n_head_kv=2, head_dim=128,
+         ctx=64, rope_base=1e6, avx2=1, seed=27, per_mille=10, steps=[[p, 1] for p in range(64)],
+         sample_steps=list(range(64)), keep_kv=True),
     # head_dim 40: 16-float FMA steps plus an 8-float scalar tail in hd_dot.
     dict(name="prefill_hd40_avx2", mode="prefill", n_layer=1, n_head=32, n_head_kv=8,
          head_dim=40, ctx=80, rope_base=1e6, avx2=1, seed=25, per_mille=0,

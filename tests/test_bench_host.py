@@ -62,3 +62,103 @@ def test_token_and_prompt_report_fields():
     assert p["matmul_flop_per_chunk"] == flops
     assert p["ms_per_chunk_gpu"] == 10.0 and p["tokens_per_s"] == 6400.0
     assert abs(p["matmul_tflops_effective"] - flops / 1e-2 / 1e12) < 0.01
+
+
+def test_runs_summary():
+    r = bench._runs([2.0, 5.0, 3.0], "GB/s")
+    assert r["median"] == 3.0 and r["best"] == 5.0 and r["runs"] == [2.0, 5.0, 3.0]
+
+
+class _OracleCache:
+    """Stands in for the GPU handle in decode_parity: its cache rows are the
+    oracle's own (roped K, V) rows of the decode workload."""
+
+    def __init__(self, n_layers, n_pos):
+        import oracle
+        inv_f = oracle.inv_freq(bench.HD, bench.ROPE_BASE)
+        self.rows = []
+        for l in range(n_layers):
+            k = oracle.synth(n_pos, bench.KVD, bench.DEC_SEED, bench.k_stream(l), 0, 2, bench.DEC_PER_MILLE,
+                             bench.DEC_OUTLIER)
+            v = oracle.synth(n_pos, bench.KVD, bench.DEC_SEED, bench.v_stream(l), 0, 3, bench.DEC_PER_MILLE,
+                             bench.DEC_OUTLIER)
+            self.rows.append((oracle.rope_rows(k, np.arange(n_pos), bench.NKV, bench.HD, inv_f), v))
+
+    def read_kv(self, layer, pos0, n):
+        k, v = self.rows[layer]
+        return k[pos0:pos0 + n], v[pos0:pos0 + n]
+
+
+def _oracle_outputs(n_layers, n_steps):
+    import oracle
+    kv = oracle.KV(n_layers, bench.DEC_POS0 + n_steps, bench.NH, bench.NKV, bench.HD, bench.ROPE_BASE)
+    inv_f = oracle.inv_freq(bench.HD, bench.ROPE_BASE)
+    kc, vc = kv.kcache(), kv.vcache()
+    outs = np.zeros((n_steps, n_layers, bench.E), np.float32)
+    for l in range(n_layers):
+        k0 = oracle.synth(bench.DEC_POS0, bench.KVD, bench.DEC_SEED, bench.k_stream(l), 0, 2, bench.DEC_PER_MILLE,
+                          bench.DEC_OUTLIER)
+        kc[l, :bench.DEC_POS0] = oracle.rope_rows(k0, np.arange(bench.DEC_POS0), bench.NKV, bench.HD, inv_f)
+        vc[l, :bench.DEC_POS0] = oracle.synth(bench.DEC_POS0, bench.KVD, bench.DEC_SEED, bench.v_stream(l), 0, 3,
+                                              bench.DEC_PER_MILLE, bench.DEC_OUTLIER)
+    for st in range(n_steps):
+        pos = bench.DEC_POS0 + st
+        for l in range(n_layers):
+            q, k, v = (oracle.synth(1, d, bench.DEC_SEED, sf(l), pos, t, bench.DEC_PER_MILLE, bench.DEC_OUTLIER)[0]
+                       for d, sf, t in ((bench.E, bench.q_stream, 1), (bench.KVD, bench.k_stream, 2),
+                                        (bench.KVD, bench.v_stream, 3)))
+            outs[st, l] = kv.decode(l, pos, q, k, v)
+    kv.close()
+    return outs
+
+
+def test_decode_parity_finds_a_planted_error():
+    """decode_parity on outputs that are the oracle's own (zero error, cache
+    equal) and with one planted difference, which it must report at the
+    right step and layer; the float64 budget puts kore's own error below the
+    1e-4 bound."""
+    nl, ns = 2, 3
+    outs = _oracle_outputs(nl, ns)
+    cache = _OracleCache(nl, bench.DEC_POS0 + ns)
+    r = bench.decode_parity(outs, cache, 4, n_layers=nl, n_steps=ns)
+    assert r["decode_max_rel_err"] == 0.0 and r["decode_kv_bitwise"]
+    assert len(r["decode_step_max_rel_err"]) == ns
+    assert 0 < r["decode_error_budget"]["kore_vs_float64_max"] < 1e-4
+    bad = outs.copy()
+    scale = float(np.max(np.abs(outs[2, 1])))
+    bad[2, 1, 77] += 3e-4 * scale
+    r = bench.decode_parity(bad, cache, 4, n_layers=nl, n_steps=ns)
+    assert r["decode_max_rel_err"] > 2e-4
+    assert r["decode_max_rel_err_at"] == {"step": 2, "position": bench.DEC_POS0 + 2, "layer": 1}
+    cache.rows[1][0][5, 3] += 1.0                      # one cache bit off
+    assert not bench.decode_parity(outs, cache, 4, n_layers=nl, n_steps=ns)["decode_kv_bitwise"]
+
+
+def test_reference_timing_runs():
+    """kore's own timing harness (built from kore.cpp) reports one entry per
+    timed run, which the CPU baselines take the median and best of."""
+    import json
+    import struct
+    import subprocess
+    import tempfile
+
+    import oracle
+    import pytest
+    if not os.path.exists(oracle.REF_QMV_BIN):
+        pytest.skip("kore's reference harness is not built here")
+    rows, cols = 64, 512
+    rng = np.random.default_rng(1)
+    w = rng.integers(0, 256, size=(rows, cols // 256, 144), dtype=np.uint8)
+    w[:, :, 0:4] = np.frombuffer(np.float16([1e-3, 1e-3]).tobytes(), np.uint8)
+    x = rng.standard_normal(cols).astype(np.float32)
+    with tempfile.TemporaryDirectory() as td:
+        job = os.path.join(td, "job.bin")
+        with open(job, "wb") as f:
+            f.write(struct.pack("<3i", bench.QMV_Q4K, rows, cols))
+            f.write(w.tobytes())
+            f.write(x.tobytes())
+        out = subprocess.run([oracle.REF_QMV_BIN, "--time", "2", "0.02", "2", job, "3"], capture_output=True,
+                             text=True, check=True).stdout
+    j = json.loads(out)
+    assert len(j["run_reps"]) == 3 and len(j["run_seconds"]) == 3
+    assert sum(j["run_reps"]) == j["reps"] and all(t >= 0.02 for t in j["run_seconds"])

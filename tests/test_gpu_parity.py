@@ -77,6 +77,28 @@ def test_golden_replay(name):
     assert C.sha(vc) == man["sha256"]["vcache"], "V cache differs from kore's bits"
 
 
+def test_golden_rows_as_one_chunk():
+    """kore's one-row forward_batch() steps with distinct q/k/v on every row
+    (fixture prefill_rows_7b_avx2) replayed as ONE 64-row causal chunk: row z
+    of the chunk attends positions 0..z like kore's row at step z, so every
+    row must match kore's output to 1e-4 and the cache must hash to kore's."""
+    name = "prefill_rows_7b_avx2"
+    man, data = C.load(name)
+    case = C.case_by_name(name)
+    nh, nkv, hd, ctx = (case[k] for k in ("n_head", "n_head_kv", "head_dim", "ctx"))
+    n = len(case["steps"])
+    _say(f"golden {name} as one {n}-row chunk")
+    rows = [C.step_inputs(case, st, 0) for st in range(n)]
+    Q, K, V = (np.stack([r[i] for r in rows]) for i in range(3))
+    with _attn(1, ctx, nh, nkv, hd, case["rope_base"]) as attn:
+        out = attn.prefill(0, 0, Q, K, V)
+        kc, vc = attn.read_kv(0, 0, n)
+    for st in range(n):
+        _close(out[st:st + 1], data[f"att_{st}"], f"{name} row {st} vs kore")
+    assert C.sha(kc[None]) == man["sha256"]["kcache"], "K cache differs from kore's bits"
+    assert C.sha(vc[None]) == man["sha256"]["vcache"], "V cache differs from kore's bits"
+
+
 def test_unsupported_head_dim_is_refused():
     import kore_amd
     _say("create with head_dim 40")
@@ -115,41 +137,52 @@ def test_decode_lengths(nh, nkv, hd):
 
 
 def test_decode_7b_ctx4096_outliers():
-    """Qwen2.5-7B decode shape at ctx 4096 with 1 % outlier channels x20:
-    cache filled through the prefill append path, then decode steps."""
-    nh, nkv, hd, ctx, n0 = 28, 4, 128, 8192, 4096
-    _say("decode 7b ctx4096 outliers")
-    seed = 7
-    q0 = oracle.synth(n0, nh * hd, seed, 1 << 32, tensor=1, per_mille=10)
-    k0 = oracle.synth(n0, nkv * hd, seed, 2 << 32, tensor=2, per_mille=10)
-    v0 = oracle.synth(n0, nkv * hd, seed, 3 << 32, tensor=3, per_mille=10)
+    """Qwen2.5-7B decode shape at ctx 4096 with 1 % outlier channels x20, the
+    benchmark's workload: layers 0 and 2 of a three-layer cache filled to 4096
+    through the prefill append path, then 32 consecutive decode steps on both
+    (layer-inner, like forward()), every output against kore's scalar decode
+    and every appended row bit for bit; layer 1 stays untouched."""
+    nh, nkv, hd, ctx, n0, steps = 28, 4, 128, 8192, 4096, 32
+    layers = (0, 2)
+    _say(f"decode 7b ctx4096 outliers: {steps} steps on layers {layers}")
+    seed, pm = 7, 10
     inv_f = oracle.inv_freq(hd, 1e6)
-    kexp = oracle.rope_rows(k0, np.arange(n0), nkv, hd, inv_f)
-    with _attn(2, ctx, nh, nkv, hd, 1e6) as attn:
-        attn.prefill(1, 0, q0, k0, v0)
-        kg, vg = attn.read_kv(1, 0, n0)
-        np.testing.assert_array_equal(kg, kexp)
-        np.testing.assert_array_equal(vg, v0)
-        K = np.zeros((ctx, nkv * hd), np.float32)
-        V = np.zeros((ctx, nkv * hd), np.float32)
-        K[:n0], V[:n0] = kexp, v0
-        for step in range(3):
+
+    def rows(t, l, r0, n, dim):
+        return oracle.synth(n, dim, seed, (t << 32) | l, row0=r0, tensor=t, per_mille=pm)
+
+    K, V = {}, {}
+    with _attn(3, ctx, nh, nkv, hd, 1e6) as attn:
+        for l in layers:
+            k0, v0 = rows(2, l, 0, n0, nkv * hd), rows(3, l, 0, n0, nkv * hd)
+            attn.prefill(l, 0, rows(1, l, 0, n0, nh * hd), k0, v0)
+            K[l] = np.zeros((n0 + steps, nkv * hd), np.float32)
+            V[l] = np.zeros((n0 + steps, nkv * hd), np.float32)
+            K[l][:n0], V[l][:n0] = oracle.rope_rows(k0, np.arange(n0), nkv, hd, inv_f), v0
+            kg, vg = attn.read_kv(l, 0, n0)
+            np.testing.assert_array_equal(kg, K[l][:n0])
+            np.testing.assert_array_equal(vg, V[l][:n0])
+        worst = 0.0
+        for step in range(steps):
             pos = n0 + step
-            q = oracle.synth(1, nh * hd, seed, 1 << 32, row0=pos, tensor=1, per_mille=10)[0]
-            k = oracle.synth(1, nkv * hd, seed, 2 << 32, row0=pos, tensor=2, per_mille=10)[0]
-            v = oracle.synth(1, nkv * hd, seed, 3 << 32, row0=pos, tensor=3, per_mille=10)[0]
-            out = attn.decode(1, pos, q, k, v)
-            K[pos] = oracle.rope_rows(k[None], [pos], nkv, hd, inv_f)[0]
-            V[pos] = v
-            qr = oracle.rope_rows(q[None], [pos], nh, hd, inv_f)[0]
-            ref = oracle.attn_decode(qr, K, V, pos, nh, nkv, hd)
-            _close(out, ref, f"7b decode pos {pos}")
-        kg, vg = attn.read_kv(1, n0, 3)
-        np.testing.assert_array_equal(kg, K[n0:n0 + 3])
-        np.testing.assert_array_equal(vg, V[n0:n0 + 3])
-        # layer 0 untouched (zero-initialised like kore.cpp:1344)
-        k_l0, v_l0 = attn.read_kv(0, 0, 16)
-        assert not k_l0.any() and not v_l0.any()
+            for l in layers:
+                q, k, v = rows(1, l, pos, 1, nh * hd)[0], rows(2, l, pos, 1, nkv * hd)[0], rows(3, l, pos, 1, nkv * hd)[0]
+                out = attn.decode(l, pos, q, k, v)
+                K[l][pos] = oracle.rope_rows(k[None], [pos], nkv, hd, inv_f)[0]
+                V[l][pos] = v
+                qr = oracle.rope_rows(q[None], [pos], nh, hd, inv_f)[0]
+                ref = oracle.attn_decode(qr, K[l][:pos + 1], V[l][:pos + 1], pos, nh, nkv, hd)
+                _close(out, ref, f"7b decode layer {l} pos {pos}")
+                ref64 = np.asarray(ref, np.float64)
+                worst = max(worst, float(np.max(np.abs(out - ref64)) / np.max(np.abs(ref64))))
+        _say(f"decode 7b ctx4096 outliers: max rel err {worst:.3e}")
+        for l in layers:
+            kg, vg = attn.read_kv(l, n0, steps)
+            np.testing.assert_array_equal(kg, K[l][n0:])
+            np.testing.assert_array_equal(vg, V[l][n0:])
+        # layer 1 untouched (zero-initialised like kore.cpp:1344)
+        k_l1, v_l1 = attn.read_kv(1, 0, n0 + steps)
+        assert not k_l1.any() and not v_l1.any()
 
 
 def test_decode_3b_long_context():
