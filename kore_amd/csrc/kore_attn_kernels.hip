@@ -123,13 +123,14 @@ __device__ __forceinline__ float sum4rows(float x) {
     return a + b;
 }
 
-// v_mfma_f64_16x16x4f64, one block: lane l supplies A[l%16][l/16] and
-// B[l/16][l%16]; D register v of lane l is D[4v + l/16][l%16] (checked on the
-// GPU: the f64 output rows are interleaved differently from the f32 ones).
-typedef double doublex4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ doublex4 mfma16d(double a, double b, doublex4 c) {
-    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+// v_mfma_f64_4x4x4f64: four 4x4x4 blocks b; lane 16k + 4b + i supplies
+// A_b[i][k], lane 16k + 4b + j supplies B_b[k][j], and lane 16i + 4b + j
+// holds D_b[i][j] (checked on the GPU).  One instruction does a quarter of
+// the products of v_mfma_f64_16x16x4f64 in under a third of its time.
+__device__ __forceinline__ double mfma4d(double a, double b, double c) {
+    return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
 }
+
 // Sum over the four lanes l % 16 + 16 k of a double (both 32-bit halves go
 // through the permlane swaps).
 __device__ __forceinline__ double sum4rows_d(double x) {
@@ -158,25 +159,28 @@ __device__ __forceinline__ double sum4rows_d(double x) {
 // own online softmax (max, sum, output) for all NR heads, so the block loop
 // has no workgroup barrier.  Per block:
 //   scores  S[row][head] = K[16 rows][hd] . q^T on fp64 MFMA
-//           (v_mfma_f64_16x16x4f64): lane (m, k) = (l % 16, l / 16) gives
-//           K[row m][16t + 4k + e] (converted to double) and the roped q of
-//           head m at the same dim, times 1/sqrt(hd) * log2(e) in double, for
-//           k-step (t, e), so both operands come straight from 16-byte loads
-//           (the dims are summed in a different order, which the dot product
-//           allows).  The scores reach a few hundred in the log2 domain on
+//           (v_mfma_f64_4x4x4f64): the four 4x4 blocks are the four groups
+//           of 4 rows, the block columns 4 heads (two chains cover heads
+//           0..3 and 4..7), and the k index picks one of four hd/4-dim
+//           chunks, so lane l gives K[row l % 16][(hd/4)(l / 16) + 4t + e]
+//           (contiguous 16-byte loads) and the roped q of heads l % 4 and
+//           4 + l % 4 at the same dims, all widened to double (their products
+//           are exact); the sums are scaled by kore's 1/sqrt(hd) and log2(e)
+//           in double.  The scores reach a few hundred in the log2 domain on
 //           heavy-tailed inputs, where an fp32 accumulation chain loses more
 //           than kore's own rounding; in fp64 the products are exact and the
-//           sum loses nothing that matters.  Lane (m, k) ends up with rows
-//           4v + k (v < 4) of head m.
-//   softmax the head's running max (fp32) over the 16 rows is a max over the
-//           lane's four registers and lanes m, m+16, m+32, m+48 (permlane
-//           swaps); each weight is 2^(score - max) with the difference taken
-//           in fp64, then v_exp_f32; the weights stay in the score registers.
-//   values  O^T[dim][head] += V^T[dim][16 rows] . P on fp32 MFMA: k-step s
-//           takes rows 4s + k, which is exactly score register s of lane
-//           (m, k), so P is fed back as the B operand without any data
-//           movement; lane (m, k) gives V[row 4s + k][64j + 4m + e] (16-byte
-//           loads) for the output block 4j + e.
+//           sum loses nothing that matters.  Lane l ends up with row
+//           4((l / 4) % 4) + l / 16 of heads l % 4 and 4 + l % 4.
+//   softmax the running max (fp32) and sum of each head over the 16 rows are
+//           reductions over the 16 lanes that hold the head (DPP rotations
+//           inside a 16-lane row, permlane swaps across rows); each weight is
+//           2^(score - max) with the difference taken in fp64, then v_exp_f32.
+//   values  O^T[dim][head] += V^T[dim][16 rows] . P on fp32 MFMA
+//           (v_mfma_f32_16x16x4f32): k-step s takes rows 4s + k for lane
+//           (m, k) = (l % 16, l / 16), which gives V[row 4s + k][64j + 4m + e]
+//           (16-byte loads) for the output block 4j + e and P[row][head m];
+//           the weights and the heads' rescale factors reach that layout
+//           through 0.5 KB of the wave's LDS.
 // Issue order of a wave: its q and the new k/v row, the K rows of its first
 // block, then (once q has returned) the RoPE of q through the wave's own LDS
 // rows, then the V rows, so the score MFMAs run while V streams in.  Every
@@ -201,6 +205,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     constexpr int NMB = HD / 16;   // 16-dim output blocks
     constexpr int HALF = HD / 2;
     constexpr int NST = 2 * kWaves + 1;   // wave states, extra-row states, new row
+    constexpr int CH = HD / 4;            // dims per lane of a K row (one k chunk)
+    constexpr int NHG = NR > 4 ? 2 : 1;   // groups of 4 heads (score chains)
     constexpr int NEW_WAVE = kWaves - 1;  // the wave that takes the new row
     static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
@@ -212,9 +218,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     __shared__ __align__(16) float s_kx[kWaves * HD];       // the extra rows: k
     __shared__ __align__(16) float s_vx[kWaves * HD];       // ... and v
     __shared__ float s_m[NST * 8], s_l[NST * 8];
+    __shared__ __align__(16) float s_p[kWaves * (8 * 16 + 8)];   // per wave: weights, rescale factors
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m16 = lane & 15, kq = lane >> 4;
+    const int jq = lane & 3, bq = (lane >> 2) & 3, iq = lane >> 4;   // score layout: head, row group, row
     const int split = blockIdx.x, g = blockIdx.y;
     const int r0 = split * rows_per_split;
     const int r_end = min(r0 + rows_per_split, n_rows);
@@ -278,9 +286,9 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     float4 kA[NT], vA[4][NJ];
     float4 kB[MULTI ? NT : 1], vB[MULTI ? 4 : 1][NJ];
     auto load_k = [&](float4 *kf, int b) {
-        const float *kr = kg + (size_t)min(r0 + 16 * b + m16, last_row) * HD + 4 * kq;
+        const float *kr = kg + (size_t)min(r0 + 16 * b + m16, last_row) * HD + CH * kq;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) kf[t] = ld4(kr + 16 * t);
+        for (int t = 0; t < NT; ++t) kf[t] = ld4(kr + 4 * t);
     };
     auto load_v = [&](float4 (*vf)[NJ], int b) {
 #pragma unroll
@@ -295,11 +303,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     __builtin_amdgcn_sched_barrier(0);
 
     // RoPE of the staged pairs into the wave's LDS rows, then the B operand:
-    // lane (m16, kq) holds head m16 at dims 16t + 4kq + e, times kore's
-    // 1/sqrt(hd) and log2(e) in double (heads past NR are zero columns).
+    // lane l holds heads jq and jq + 4 (jq = l % 4) at dims CH kq + 4t + e
+    // (heads past NR are zero); the dot products are widened to double and
+    // scaled by kore's 1/sqrt(hd) and log2(e) there.
     const double qscale = (double)a.scale * 1.4426950408889634;
-    const int hq = min(m16, NR - 1);
-    double qb[NT][4];
+    float qb[NHG][NT][4];
     {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -316,27 +324,40 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             st4(&wq[row * QS + HALF + 4 * sc], make_float4(y1[0], y1[1], y1[2], y1[3]));
         }
         __builtin_amdgcn_wave_barrier();
-        float4 qv[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) qv[t] = ld4(&wq[hq * QS + 16 * t + 4 * kq]);
+        for (int hg = 0; hg < NHG; ++hg) {
+            const int h = jq + 4 * hg;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+            for (int t = 0; t < NT; ++t) {
+                const float4 qv = ld4(&wq[min(h, NR - 1) * QS + CH * kq + 4 * t]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) qb[t][e] = m16 < NR ? (double)comp(qv[t], e) * qscale : 0.0;
+                for (int e = 0; e < 4; ++e) qb[hg][t][e] = h < NR ? comp(qv, e) : 0.f;
+            }
+        }
     }
-    // dot of q (operand layout) with a k row staged in LDS: lane (m16, kq)
-    // sums dims 16t + 4kq + e of head m16, then the four lanes of the head
-    auto row_score = [&](const float *kr) {
-        double sx = 0.0;
+
+    // dot of q (operand layout) with a k row staged in LDS, for heads jq + 4hg:
+    // lane l sums its dims CH kq + 4t + e, then the four lanes of its chunk
+    // row (l, l ^ 16, l ^ 32, l ^ 48) add up; every lane ends with the scores
+    // (four independent partial sums per head group: a single chain of
+    // dependent fp64 FMAs would take most of a microsecond)
+    auto row_scores = [&](const float *kr, double (&out)[NHG]) {
+        double sx[NHG][4];
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sx[hg][e] = 0.0;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const float4 kx = ld4(&kr[16 * t + 4 * kq]);
-            sx = fma(qb[t][0], (double)kx.x, sx);
-            sx = fma(qb[t][1], (double)kx.y, sx);
-            sx = fma(qb[t][2], (double)kx.z, sx);
-            sx = fma(qb[t][3], (double)kx.w, sx);
+            const float4 kx = ld4(&kr[CH * kq + 4 * t]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int hg = 0; hg < NHG; ++hg) sx[hg][e] = fma((double)qb[hg][t][e], (double)comp(kx, e), sx[hg][e]);
         }
-        return sum4rows_d(sx);
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg)
+            out[hg] = sum4rows_d((sx[hg][0] + sx[hg][1]) + (sx[hg][2] + sx[hg][3])) * qscale;
     };
     // A single row as a softmax state: max = its score rounded to fp32, sum
     // = 2^(score - max) with the difference in fp64 (about 1), output = that
@@ -355,12 +376,18 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             s_vx[wave * HD + lane + HALF] = x_on ? xv1 : 0.f;
         }
         __builtin_amdgcn_wave_barrier();
-        const double sx = row_score(&s_kx[wave * HD]);
-        if (kq == 0 && m16 < NR) {
-            const bool on = x_on && xrow != new_slot;
-            const float mx = (float)sx;
-            s_m[(kWaves + wave) * 8 + m16] = on ? mx : -INFINITY;
-            s_l[(kWaves + wave) * 8 + m16] = on ? fast_exp2((float)(sx - (double)mx)) : 0.f;
+        const bool on = x_on && xrow != new_slot;
+        double sxs[NHG];
+        row_scores(&s_kx[wave * HD], sxs);
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) {
+            const double sx = sxs[hg];
+            const int h = jq + 4 * hg;
+            if (lane < 4 && h < NR) {
+                const float mx = (float)sx;
+                s_m[(kWaves + wave) * 8 + h] = on ? mx : -INFINITY;
+                s_l[(kWaves + wave) * 8 + h] = on ? fast_exp2((float)(sx - (double)mx)) : 0.f;
+            }
         }
     }
     float nky0, nky1;
@@ -373,11 +400,17 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             s_vnew[lane + HALF] = is_owner ? nv1 : 0.f;
         }
         __builtin_amdgcn_wave_barrier();
-        const double sn = row_score(s_knew);
-        if (kq == 0 && m16 < NR) {
-            const float mn = (float)sn;
-            s_m[2 * kWaves * 8 + m16] = is_owner ? mn : -INFINITY;
-            s_l[2 * kWaves * 8 + m16] = is_owner ? fast_exp2((float)(sn - (double)mn)) : 0.f;
+        double sns[NHG];
+        row_scores(s_knew, sns);
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) {
+            const double sn = sns[hg];
+            const int h = jq + 4 * hg;
+            if (lane < 4 && h < NR) {
+                const float mn = (float)sn;
+                s_m[2 * kWaves * 8 + h] = is_owner ? mn : -INFINITY;
+                s_l[2 * kWaves * 8 + h] = is_owner ? fast_exp2((float)(sn - (double)mn)) : 0.f;
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -393,42 +426,63 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     floatx4 o[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_part = 0.f;
+    // softmax state of heads jq + 4hg (the same in every lane that holds them)
+    float m_run[NHG], l_run[NHG];
+#pragma unroll
+    for (int hg = 0; hg < NHG; ++hg) {
+        m_run[hg] = -INFINITY;
+        l_run[hg] = 0.f;
+    }
+    float *wp = s_p + wave * (8 * 16 + 8);   // the wave's weights [head][k][s], then rescale factors [head]
+    const int rD = 4 * bq + iq;              // this lane's row of the block in the score layout
 
     auto process = [&](const float4 *kf, const float4 (*vf)[NJ], int b, bool first) {
         const int rb = r0 + 16 * b;
-        doublex4 s = {0.0, 0.0, 0.0, 0.0};
+        double acc[NHG];
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) acc[hg] = 0.0;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) s = mfma16d((double)comp(kf[t], e), qb[t][e], s);
-        bool ok[4];
-        float mt = -INFINITY;
+            for (int e = 0; e < 4; ++e) {
+                const double kv = (double)comp(kf[t], e);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int row = rb + 4 * v + kq;
-            ok[v] = row < r_end && row != new_slot;
-            mt = fmaxf(mt, ok[v] ? (float)s[v] : -INFINITY);
-        }
-        const float m_new = fmaxf(m_run, max4rows(mt));
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;   // a block with every row masked
-        const float alpha = fast_exp2(m_run - m_use);
-        float p[4], ps = 0.f;
+                for (int hg = 0; hg < NHG; ++hg) acc[hg] = mfma4d(kv, (double)qb[hg][t][e], acc[hg]);
+            }
+        const int row = rb + rD;
+        const bool ok = row < r_end && row != new_slot;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            p[v] = ok[v] ? fast_exp2((float)(s[v] - (double)m_use)) : 0.f;
-            ps += p[v];
+        for (int hg = 0; hg < NHG; ++hg) {
+            const double sc = acc[hg] * qscale;
+            float mt = ok ? (float)sc : -INFINITY;
+            mt = fmaxf(mt, dpp<0x124>(mt));           // the four row groups of a 16-lane row
+            mt = fmaxf(mt, dpp<0x128>(mt));
+            const float m_new = fmaxf(m_run[hg], max4rows(mt));
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;   // a block with every row masked
+            const float alpha = fast_exp2(m_run[hg] - m_use);
+            const float p = ok ? fast_exp2((float)(sc - (double)m_use)) : 0.f;
+            float ps = p + dpp<0x124>(p);
+            ps += dpp<0x128>(ps);
+            l_run[hg] = fmaf(l_run[hg], alpha, sum4rows(ps));
+            m_run[hg] = m_new;
+            const int h = jq + 4 * hg;
+            wp[h * 16 + iq * 4 + bq] = p;
+            if (lane < 4) wp[8 * 16 + h] = alpha;
         }
-        l_part = fmaf(l_part, alpha, ps);
-        m_run = m_new;
+        __builtin_amdgcn_wave_barrier();
+        // to the value layout: lane (m16, kq) takes rows 4s + kq of head m16
+        const bool hv = m16 < 4 * NHG;
+        const float4 pv = hv ? ld4(&wp[min(m16, 4 * NHG - 1) * 16 + kq * 4]) : zero4();
         if (!first) {
+            const float al = hv ? wp[8 * 16 + min(m16, 4 * NHG - 1)] : 1.f;
 #pragma unroll
-            for (int mb = 0; mb < NMB; ++mb) o[mb] *= alpha;
+            for (int mb = 0; mb < NMB; ++mb) o[mb] *= al;
         }
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
-            for (int sk = 0; sk < 4; ++sk) o[mb] = mfma16(comp(vf[sk][mb / 4], mb % 4), p[sk], o[mb]);
+            for (int sk = 0; sk < 4; ++sk) o[mb] = mfma16(comp(vf[sk][mb / 4], mb % 4), comp(pv, sk), o[mb]);
+        __builtin_amdgcn_wave_barrier();
     };
     if constexpr (MULTI) {
         for (int b = wave; b < n_blk;) {
@@ -451,16 +505,19 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         // the block runs unconditionally (a wave without one masks it out)
         process(kA, vA, wave, true);
         if (wave >= n_blk) {
-            m_run = -INFINITY;
-            l_part = 0.f;
+#pragma unroll
+            for (int hg = 0; hg < NHG; ++hg) {
+                m_run[hg] = -INFINITY;
+                l_run[hg] = 0.f;
+            }
 #pragma unroll
             for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
     }
 
     // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
-    // 64(mb / 4) + 16kq + 4v + mb % 4
-    const float l_w = sum4rows(l_part);
+    // 64(mb / 4) + 16kq + 4v + mb % 4; the max and sum of head jq + 4hg
+    // come from lane jq
     if (m16 < NR) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
@@ -468,9 +525,13 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             for (int v = 0; v < 4; ++v)
                 st4(&s_o[(wave * NR + m16) * OST + 64 * j + 16 * kq + 4 * v],
                     make_float4(o[4 * j][v], o[4 * j + 1][v], o[4 * j + 2][v], o[4 * j + 3][v]));
-        if (kq == 0) {
-            s_m[wave * 8 + m16] = m_run;
-            s_l[wave * 8 + m16] = l_w;
+    }
+#pragma unroll
+    for (int hg = 0; hg < NHG; ++hg) {
+        const int h = jq + 4 * hg;
+        if (lane < 4 && h < NR) {
+            s_m[wave * 8 + h] = m_run[hg];
+            s_l[wave * 8 + h] = l_run[hg];
         }
     }
     __syncthreads();
