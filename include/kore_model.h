@@ -8,7 +8,14 @@
  * consistent, n_embd and n_ff multiples of 256, even head_dim, matrices Q4_K or
  * Q6_K, norms and biases F32, token_embd and output with the same vocabulary)
  * and its context: min(qwen2.context_length, ctx_max), or ctx_max when the file
- * has none.  Part of libkore_layer.so. */
+ * has none.  Beyond kore, it refuses (KORE_MODEL_E_LOAD, before anything reaches
+ * the device) a file whose tensors do not have the shapes the forward pass
+ * reads: matrices [n_embd x n_embd], [kv_dim x n_embd], [n_ff x n_embd],
+ * [n_embd x n_ff], token_embd and output.weight n_embd wide and 2-D, every norm
+ * and attn_q.bias n_embd floats, attn_k.bias and attn_v.bias kv_dim floats.
+ * The matvecs always sum in kore's AVX2 order (kore's forward() uses its scalar
+ * order only on a CPU without AVX2, kore.cpp:1293; on such a host the logits
+ * of kore and of this engine differ in the last bits).  Part of libkore_layer.so. */
 #ifndef KORE_MODEL_H
 #define KORE_MODEL_H
 

@@ -65,6 +65,46 @@ int build(kore_model *m, kore_gguf_t g, int ctx_max) {
     if (ctx_max <= 0) return fail(m, KORE_MODEL_E_LOAD, "ctx_max must be positive");
     m->ctx = h.n_ctx ? (int)std::min<uint32_t>(h.n_ctx, (uint32_t)ctx_max) : ctx_max;
 
+    // The shape of every tensor the forward pass reads, checked before any of
+    // them reaches the device: a parseable file with a short norm or bias, or
+    // a head of the wrong width, would otherwise send the kernels past the
+    // ends of their buffers (kore would read past its host arrays there).
+    {
+        const uint64_t E = h.n_embd, FF = h.n_ff, KVD = (uint64_t)m->kv_dim;
+        std::string bad;
+        auto shape = [&](const std::string &n, uint64_t cols, uint64_t rows) {   // 2-D matrix [rows][cols]
+            kore_gguf_tensor t{};
+            if (!bad.empty() || kore_gguf_find(g, n.c_str(), &t) != KORE_GGUF_OK) return;   // missing: reported below
+            if (t.n_dims > 2 || t.dims[0] != cols || (rows && t.dims[1] != rows) || t.dims[1] == 0)
+                bad = n + " has the wrong shape";
+        };
+        auto vec = [&](const std::string &n, uint64_t len) {                      // F32 array of len floats
+            kore_gguf_tensor t{};
+            if (!bad.empty() || kore_gguf_find(g, n.c_str(), &t) != KORE_GGUF_OK) return;
+            if (t.type == 0 && (t.n_dims != 1 || t.dims[0] != len || t.nbytes != 4 * len))
+                bad = n + " does not hold " + std::to_string(len) + " floats";
+        };
+        shape("token_embd.weight", E, 0);
+        shape("output.weight", E, 0);
+        vec("output_norm.weight", E);
+        for (uint32_t l = 0; l < h.n_layer && bad.empty(); ++l) {
+            const std::string p = "blk." + std::to_string(l) + ".";
+            shape(p + "attn_q.weight", E, E);
+            shape(p + "attn_k.weight", E, KVD);
+            shape(p + "attn_v.weight", E, KVD);
+            shape(p + "attn_output.weight", E, E);
+            shape(p + "ffn_gate.weight", E, FF);
+            shape(p + "ffn_up.weight", E, FF);
+            shape(p + "ffn_down.weight", FF, E);
+            vec(p + "attn_q.bias", E);
+            vec(p + "attn_k.bias", KVD);
+            vec(p + "attn_v.bias", KVD);
+            vec(p + "attn_norm.weight", E);
+            vec(p + "ffn_norm.weight", E);
+        }
+        if (!bad.empty()) return fail(m, KORE_MODEL_E_LOAD, bad);
+    }
+
     std::string missing;
     auto mat = [&](const std::string &n) -> kore_qmv_tensor_t {      // matvec weights: Q4_K or Q6_K
         kore_gguf_tensor t{};

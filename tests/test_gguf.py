@@ -199,3 +199,45 @@ def test_oracle_forward_batch_matches_kore():
     _, dec, _ = oracle_engine_logits(os.path.join(GOLD, man["file"]), man["tokens"], man["ctx_max"])
     assert not np.array_equal(dec[-1].astype(np.float32), logits.astype(np.float32))
 
+
+
+@pytest.mark.parametrize("change,fragment", [
+    ({"output.weight": [128, 12]}, "output.weight has the wrong shape"),
+    ({"output.weight": [256, 12, 2]}, "output.weight has the wrong shape"),
+    ({"blk.0.attn_norm.weight": [128]}, "blk.0.attn_norm.weight does not hold 256 floats"),
+    ({"output_norm.weight": [255]}, "output_norm.weight does not hold 256 floats"),
+    ({"blk.0.attn_k.bias": [256]}, "blk.0.attn_k.bias does not hold 128 floats"),
+    ({"blk.0.attn_q.bias": [128]}, "blk.0.attn_q.bias does not hold 256 floats"),
+    ({"blk.0.ffn_down.weight": [256, 512]}, "blk.0.ffn_down.weight has the wrong shape"),
+])
+def test_model_refuses_malformed_shapes_before_the_device(tmp_path, change, fragment):
+    """kore_model_load checks the shape of every tensor the forward pass reads
+    and refuses a parseable file with a short norm or bias, or a head of the
+    wrong width, with KORE_MODEL_E_LOAD before anything is copied to a GPU
+    (runs on a host without one)."""
+    import sys
+    sys.path.insert(0, os.path.join(GOLD))
+    import make_golden_gguf as mg
+    from kore_amd.model import KORE_MODEL_E_LOAD, Model, ModelError
+    rng = np.random.default_rng(3)
+    E, FF, V = 256, 256, 12
+    meta = [("general.architecture", mg.STR, "qwen2"), ("qwen2.block_count", mg.U32, 1),
+            ("qwen2.context_length", mg.U32, 64), ("qwen2.embedding_length", mg.U32, E),
+            ("qwen2.feed_forward_length", mg.U32, FF), ("qwen2.attention.head_count", mg.U32, 2),
+            ("qwen2.attention.head_count_kv", mg.U32, 1), ("qwen2.rope.freq_base", mg.F32, 1e6),
+            ("qwen2.attention.layer_norm_rms_epsilon", mg.F32, 1e-6)]
+    shapes = {"token_embd.weight": ([E, V], 12), "blk.0.attn_q.weight": ([E, E], 12),
+              "blk.0.attn_k.weight": ([E, 128], 12), "blk.0.attn_v.weight": ([E, 128], 14),
+              "blk.0.attn_q.bias": ([E], 0), "blk.0.attn_k.bias": ([128], 0), "blk.0.attn_v.bias": ([128], 0),
+              "blk.0.attn_output.weight": ([E, E], 12), "blk.0.ffn_gate.weight": ([E, FF], 12),
+              "blk.0.ffn_up.weight": ([E, FF], 12), "blk.0.ffn_down.weight": ([FF, E], 14),
+              "blk.0.attn_norm.weight": ([E], 0), "blk.0.ffn_norm.weight": ([E], 0),
+              "output_norm.weight": ([E], 0), "output.weight": ([E, V], 14)}
+    for name, dims in change.items():
+        shapes[name] = (dims, shapes[name][1])
+    tensors = [(n, d, t, mg.tensor_bytes(t, d, rng)) for n, (d, t) in shapes.items()]
+    path = tmp_path / "bad.gguf"
+    path.write_bytes(mg.gguf(meta, tensors))
+    with pytest.raises(ModelError) as e:
+        Model(str(path), 64)
+    assert e.value.code == KORE_MODEL_E_LOAD and fragment in str(e.value)

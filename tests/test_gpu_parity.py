@@ -350,8 +350,9 @@ def test_prefill_chunks(nh, nkv, hd, chunks):
 
 
 def test_prefill_7b_2048_rows_vs_brute_force():
-    """The 2048-token 7B prefill: sampled rows against the double brute force
-    (the full CPU restatement takes too long for a test)."""
+    """The 2048-token 7B prefill: sampled rows against the double brute
+    force, every row against the oracle (kore's AVX2 batched attention), the
+    cache rows bit for bit."""
     nh, nkv, hd, n = 28, 4, 128, 2048
     _say("prefill 7b 2048")
     seed = 3
@@ -369,6 +370,14 @@ def test_prefill_7b_2048_rows_vs_brute_force():
     for z in (0, 1, 31, 32, 500, 1023, 1024, 2047):
         ref = oracle.attn_ref64(qr[z], K, v, np.arange(z + 1), nh, nkv, hd)
         _close(out[z], ref, f"row {z}")
+    # every row against kore's own arithmetic (the oracle's AVX2 batched
+    # attention, kore.cpp:1542-1563): kore's 64-row chunks give each row the
+    # same result as one 2048-row call
+    kv = oracle.KV(1, n, nh, nkv, hd, 1e6)
+    ref_all = kv.prefill(0, 0, q, k, v, avx2=True)
+    kv.close()
+    for z0 in range(0, n, 64):
+        _close(out[z0:z0 + 64], ref_all[z0:z0 + 64], f"rows {z0}..{z0 + 63}")
 
 
 def test_prefill_chunk_then_window_decode_1p5b():
@@ -493,3 +502,65 @@ def test_append_dev_matches_prefill_cache_rows():
         # a decode over appended rows equals a decode over prefilled rows
         np.testing.assert_array_equal(a.decode(1, ctx - 1, q[-1], k[-1], v[-1]),
                                       b.decode(1, ctx - 1, q[-1], k[-1], v[-1]))
+
+
+def test_condense_reprefill_over_a_filled_cache():
+    """kore's condense (kore.cpp:1786-1796) re-prefills a shorter sequence
+    from position 0 over a cache that holds a longer one; attention reads only
+    positions <= pos (kore.cpp:1437, 1549), so the stale rows past the new end
+    must never be read.  The stale rows are overwritten with NaN (through the
+    append path) before the decode and the next chunk: outputs must match the
+    oracle's fresh run of the condensed sequence, hold no NaN, and the rows up
+    to the new end must be bit-identical."""
+    from kore_amd import hip
+    nh, nkv, hd, ctx, nl = 28, 4, 128, 512, 2
+    old_n, new_n, dec, tail = 400, 150, 20, 64
+    E, kvd = nh * hd, nkv * hd
+    _say(f"condense: {old_n} rows, re-prefill {new_n} from 0, NaN rows {new_n}..{old_n - 1}, decode and a chunk")
+    rng = np.random.default_rng(77)
+
+    def rows(n, d):
+        return rng.standard_normal((n, d)).astype(np.float32)
+
+    kv = oracle.KV(nl, ctx, nh, nkv, hd, 1e6)
+    with _attn(nl, ctx, nh, nkv, hd, 1e6) as attn:
+        for l in range(nl):   # the old conversation, in kore's 64-row chunks
+            qo, ko, vo = rows(old_n, E), rows(old_n, kvd), rows(old_n, kvd)
+            for z0 in range(0, old_n, 64):
+                attn.prefill(l, z0, qo[z0:z0 + 64], ko[z0:z0 + 64], vo[z0:z0 + 64])
+        # condense: a new, shorter sequence from position 0
+        new = [(rows(new_n, E), rows(new_n, kvd), rows(new_n, kvd)) for _ in range(nl)]
+        for l in range(nl):
+            qn, kn, vn = new[l]
+            for z0 in range(0, new_n, 64):
+                out = attn.prefill(l, z0, qn[z0:z0 + 64], kn[z0:z0 + 64], vn[z0:z0 + 64])
+                ref = kv.prefill(l, z0, qn[z0:z0 + 64], kn[z0:z0 + 64], vn[z0:z0 + 64], avx2=True)
+                _close(out, ref, f"re-prefill layer {l} rows {z0}..")
+        # poison the stale rows of the old conversation
+        nan = np.full((old_n - new_n, kvd), np.nan, np.float32)
+        dn = hip.DeviceBuffer.from_array(nan)
+        for l in range(nl):
+            attn.append_dev(l, new_n, old_n - new_n, dn.ptr, dn.ptr)
+        attn.sync()
+        dn.free()
+        for st in range(dec):
+            pos = new_n + st
+            for l in range(nl):
+                q, k, v = rows(1, E)[0], rows(1, kvd)[0], rows(1, kvd)[0]
+                out = attn.decode(l, pos, q, k, v)
+                assert np.all(np.isfinite(out)), f"stale row read at decode pos {pos} layer {l}"
+                _close(out, kv.decode(l, pos, q, k, v), f"decode layer {l} pos {pos}")
+        p0 = new_n + dec
+        for l in range(nl):
+            qc, kc_, vc_ = rows(tail, E), rows(tail, kvd), rows(tail, kvd)
+            out = attn.prefill(l, p0, qc, kc_, vc_)
+            assert np.all(np.isfinite(out)), f"stale row read by the chunk at {p0} layer {l}"
+            _close(out, kv.prefill(l, p0, qc, kc_, vc_, avx2=True), f"chunk layer {l}")
+        end = p0 + tail
+        for l in range(nl):
+            kg, vg = attn.read_kv(l, 0, end)
+            np.testing.assert_array_equal(kg, kv.kcache()[l, :end])
+            np.testing.assert_array_equal(vg, kv.vcache()[l, :end])
+            ks, _ = attn.read_kv(l, end, old_n - end)   # rows past the new end stay stale
+            assert np.isnan(ks).all()
+    kv.close()

@@ -37,10 +37,13 @@ def _up(a):
     return hip.DeviceBuffer.from_array(np.ascontiguousarray(a, np.float32).reshape(-1))
 
 
-def test_rmsnorm_rows_bitwise():
-    """Rows of the 7B width, random and the midpoint case that needs kore's own loop."""
+@pytest.mark.parametrize("E", [3584, 4096, 4097, 5120, 7, 17])
+def test_rmsnorm_rows_bitwise(E):
+    """Rows of the 7B width, random and the midpoint case that needs kore's own
+    loop; also the widths around the kernel's register path (up to 4096
+    values) and its two-pass path for wider rows (a width that is not a
+    multiple of its load batch), and short odd rows, in place and not."""
     from kore_amd import qmv
-    E = 3584
     _say(f"rmsnorm rows, E {E}")
     rng = np.random.default_rng(21)
     x = np.stack([_x(E, rng) for _ in range(6)] + [np.full(E, 1 + 2.0 ** -12, np.float32)])
