@@ -60,8 +60,8 @@ PF_N, PF_SEED = 2048, 3
 # kernels and workloads, each counter scaled by what it reads for a 256 MiB device copy
 # (fetch x 2.0, write x 1.0): decode layer = split + combine kernel, prefill layer =
 # append + prefill kernel.  Re-measure when a kernel changes.
-TRAFFIC_DECODE_BYTES = 19_078_000
-TRAFFIC_PREFILL_BYTES = 109_052_000
+TRAFFIC_DECODE_BYTES = 19_115_000
+TRAFFIC_PREFILL_BYTES = 109_106_000
 # the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
 # of weights, activations and outputs algorithmic)
 TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_416_000}
@@ -146,7 +146,7 @@ def _check(rc, what):
 
 # ------------------------------------------------------------------ GPU legs
 
-def gpu_decode(steps: int, warmup: int):
+def gpu_decode(steps: int, warmup: int, extras: bool = True):
     from kore_amd import KoreAttn, hip, synth_dev
     B = _bench_lib()
     attn = KoreAttn(NL, DEC_CTX, NH, NKV, HD, ROPE_BASE)
@@ -184,6 +184,10 @@ def gpu_decode(steps: int, warmup: int):
     launch_ms = np.zeros(steps * NL, np.float32)
     _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
                             launch_ms.ctypes.data, None, C.byref(wall2)), "decode per-launch events")
+    if not extras:
+        out.free()
+        return dict(attn=attn, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value,
+                    buffers=(dq, dk, dv))
     # all 128 configured steps once more, untimed, for the parity check
     out.free()
     par = hip.DeviceBuffer(DEC_STEPS * NL * E)
@@ -911,7 +915,9 @@ def read_calibration():
     us = C.c_float(0)
     for mb in (8, 17, 38, 76, 150, 447, 1024, 4096):
         nbytes = mb << 20
-        rot = max(1, min(total // nbytes, 8))
+        # enough copies that one rotation covers 1 GiB, four times the 256 MB MALL:
+        # no launch finds its bytes in the memory-side cache
+        rot = max(1, min(total // nbytes, max(8, -(-(1 << 30) // nbytes))))
         row = {"mbytes": mb}
         for grid in (1024, 2048, 4096):
             reps = 10 if mb >= 1024 else 100
@@ -1103,6 +1109,10 @@ def main(argv=None):
     ap.add_argument("--prefill-warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the 7B 2048-row prefill leg (for profiling its kernels on their own)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the 7B decode leg, without the parity pass or any CPU work (for profiling)")
     ap.add_argument("--no-other", action="store_true", help="skip the 0.5B / 3B / 1.5B workloads")
     ap.add_argument("--cpu-seconds", type=float, default=9.0,
                     help="time of each CPU baseline, split over its timed runs")
@@ -1168,6 +1178,22 @@ def main(argv=None):
         for m in qt[1]:
             m.close()
         print(json.dumps(out), flush=True)
+        return 0
+    if args.prefill_only:
+        pf = gpu_prefill(args.prefill_steps, args.prefill_warmup)
+        F = prefill_flops(0, PF_N)
+        per = pf["region_ms"] / 1e3 / (args.prefill_steps * NL)
+        print(json.dumps({"prefill": {"us_per_layer_gpu": round(per * 1e6, 2), "flop_per_layer": F,
+                                      "tflops": round(F / per / 1e12, 3),
+                                      "frac": round(F / per / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}}), flush=True)
+        return 0
+    if args.decode_only:
+        dec = gpu_decode(args.steps, args.warmup, extras=False)
+        per = dec["region_ms"] / 1e3 / (args.steps * NL)
+        nbytes = sum(decode_bytes(DEC_POS0 + s + 1) for s in range(args.steps)) / args.steps
+        dec["attn"].close()
+        print(json.dumps({"decode": {"us_per_layer_gpu": round(per * 1e6, 3), "bytes_per_layer": int(nbytes),
+                                     "gbs": round(nbytes / per / 1e9, 1)}}), flush=True)
         return 0
     pf = None
     if not args.no_prefill:
