@@ -62,7 +62,10 @@ enum {
 /* Create a KV-cache handle on the current HIP device.
  * Replaces Engine's cache/RoPE set-up in engine_init (kore.cpp:1287-1291,
  * 1337-1345): head_dim is even, n_head % n_head_kv == 0, rope_base > 0
- * (kore.cpp:1278-1288).  ctx is the number of positions per layer.
+ * (kore.cpp:1278-1288).  Every such geometry with head_dim <= 256 runs on the
+ * GPU (head_dim 64 or 128 with at most 8 q-heads per kv-head on the MFMA
+ * kernels, the rest on generic tiled kernels); a larger head_dim fails with
+ * KORE_ATTN_E_UNSUPPORTED.  ctx is the number of positions per layer.
  * window = 0 keeps kore's semantics (a position must be < ctx).  window > 0
  * (must equal ctx) makes each layer a ring of `window` slots: position p is
  * stored in slot p % window and a decode at p >= window attends the last
@@ -121,9 +124,9 @@ KORE_ATTN_API int kore_attn_prefill_dev(kore_attn_t h, int layer, int pos0, int 
  * allocates nothing, synchronises nothing and calls no allocating routine.
  * No counterpart in kore; it is for callers that cannot allocate (HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  A decode
- * needs n_head x splits x (head_dim + 2) floats, at most 8 x CUs x 130
- * (266,240 on a 256-CU MI355X); a larger need fails with
- * KORE_ATTN_E_UNSUPPORTED.  Every call on one GPU shares the array (each call
+ * needs n_head x splits x (head_dim + 2) floats, on the MFMA kernels at most
+ * 8 x CUs x 130 (266,240 on a 256-CU MI355X), on the generic kernels
+ * n_head x head_dim more; a larger need fails with KORE_ATTN_E_UNSUPPORTED.  Every call on one GPU shares the array (each call
  * writes every partial it reads, so nothing carries over): calls that overlap
  * on one GPU (other streams, other handles) race. */
 KORE_ATTN_API int kore_attn_decode_noalloc_dev(kore_attn_t h, int layer, int pos, int n_head, int n_head_kv,

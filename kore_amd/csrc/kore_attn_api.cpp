@@ -28,8 +28,11 @@ struct kore_attn {
     std::vector<float> inv_freq;
     RopeRow dec_cs{};                        // (cos, sin) of the last decode position
     int dec_cs_pos = -1;
-    float *d_part_o = nullptr;               // decode split partials (o, then max/sum)
+    float *d_part_o = nullptr;               // decode split partials (o, then max/sum), then
+                                             // the roped q of the generic decode
     int max_split = 0;
+    size_t part_floats = 0;
+    bool fast_decode = false, fast_prefill = false;   // MFMA kernels for this geometry
     float *d_pf_part = nullptr;              // prefill key-segment partials
     size_t pf_part_floats = 0;
     float *d_scratch = nullptr;              // the device's fixed scratch (allocation-free decode)
@@ -162,8 +165,43 @@ hipStream_t pick_stream(kore_attn *h, void *stream) {
     return stream ? (hipStream_t)stream : h->stream;
 }
 
+// The decode of a geometry without an MFMA kernel: a prep launch ropes q
+// (into part, after the partials) and appends the new row, then the split
+// attention reads every row up to and including it.
+int generic_decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float *k, const float *v,
+                           float *out, hipStream_t s, float *part, size_t part_floats) {
+    const bool wrapped = h->window && pos >= h->window;
+    GenericArgs a{};
+    a.kc = h->d_k + (size_t)layer * h->layer_floats();
+    a.vc = h->d_v + (size_t)layer * h->layer_floats();
+    a.out = out;
+    a.slots = h->ctx;
+    a.hd = h->head_dim;
+    a.n_head_kv = h->n_head_kv;
+    a.n_rep = h->n_head / h->n_head_kv;
+    generic_shape(a.hd, a.n_rep, &a.tile, &a.chunk, &a.n_chunks);
+    a.n_rows = wrapped ? h->window : pos + 1;
+    a.rows_per_split = generic_rows_per_split(a.hd, a.n_rep, a.n_rows, a.n_head_kv, h->num_cu);
+    a.n_split = (a.n_rows + a.rows_per_split - 1) / a.rows_per_split;
+    a.scale = 1.0f / std::sqrt((float)h->head_dim);   // kore.cpp:1411
+    const size_t np = (size_t)h->n_head * a.n_split, hd = (size_t)h->head_dim;
+    const size_t need = np * (hd + 2) + (size_t)h->n_head * hd;
+    if (need > part_floats)
+        return fail(h, KORE_ATTN_E_UNSUPPORTED, "decode partials need %zu floats, the scratch holds %zu", need,
+                    part_floats);
+    a.part_o = part;
+    a.part_ml = part + np * hd;
+    float *q_roped = part + np * (hd + 2);
+    a.q = q_roped;
+    float *kc = h->d_k + (size_t)layer * h->layer_floats(), *vc = h->d_v + (size_t)layer * h->layer_floats();
+    HIP_TRY(h, launch_generic_decode(a, q, k, v, q_roped, kc, vc, h->n_head, h->window ? pos % h->window : pos,
+                                     decode_row(h, pos), s));
+    return KORE_ATTN_OK;
+}
+
 // Enqueues a decode with its split partials in part (part_floats floats; a
-// decode needs n_head * splits * (head_dim + 2)).
+// decode needs n_head * splits * (head_dim + 2), the generic one n_head *
+// head_dim more).
 int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float *k, const float *v,
                    float *out, hipStream_t s, float *part, size_t part_floats) {
     // Cache rows read besides the new one: positions 0..pos-1 (kore.cpp:1437),
@@ -172,6 +210,7 @@ int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float
     const bool wrapped = h->window && pos >= h->window;
     const int n_rows = wrapped ? h->window : pos;
     const int slot = h->window ? pos % h->window : pos;
+    if (!h->fast_decode) return generic_decode_enqueue(h, layer, pos, q, k, v, out, s, part, part_floats);
     DecodeArgs a{};
     a.q = q;
     a.k = k;
@@ -213,6 +252,24 @@ int prefill_enqueue(kore_attn *h, int layer, int pos0, int n_tok, const float *q
     ap.n_tok = n_tok;
     ap.n_head_kv = h->n_head_kv;
     HIP_TRY(h, launch_append(ap, h->head_dim, s));
+    if (!h->fast_prefill) {
+        GenericArgs ga{};
+        ga.q = q;
+        ga.cs = h->d_cs;
+        ga.kc = ap.kc;
+        ga.vc = ap.vc;
+        ga.out = out;
+        ga.slots = h->ctx;
+        ga.hd = h->head_dim;
+        ga.n_head_kv = h->n_head_kv;
+        ga.n_rep = h->n_head / h->n_head_kv;
+        generic_shape(ga.hd, ga.n_rep, &ga.tile, &ga.chunk, &ga.n_chunks);
+        ga.pos0 = pos0;
+        ga.n_split = 1;
+        ga.scale = 1.0f / std::sqrt((float)h->head_dim);   // kore.cpp:1411
+        HIP_TRY(h, launch_generic_prefill(ga, n_tok, s));
+        return KORE_ATTN_OK;
+    }
     PrefillArgs pa{};
     pa.q = q;
     pa.cs = h->d_cs;
@@ -283,11 +340,9 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
     if (window < 0 || (window > 0 && window != ctx))
         return fail(nullptr, KORE_ATTN_E_INVALID, "window must be 0 or equal to ctx");
     const int n_rep = n_head / n_head_kv;
-    if (!decode_supported(head_dim, n_rep) || !prefill_supported(head_dim, n_rep))
-        return fail(nullptr, KORE_ATTN_E_UNSUPPORTED,
-                    "no gfx950 kernel for head_dim %d with %d q-heads per kv-head (supported: "
-                    "head_dim 64 or 128, 1..8 q-heads per kv-head)",
-                    head_dim, n_rep);
+    if (!generic_supported(head_dim))
+        return fail(nullptr, KORE_ATTN_E_UNSUPPORTED, "no gfx950 kernel for head_dim %d (supported: even, up to %d)",
+                    head_dim, kMaxGenericHeadDim);
     const double kv_bytes = 2.0 * n_layer * (double)n_head_kv * ctx * head_dim * 4.0;
     if (kv_bytes > 1e15) return fail(nullptr, KORE_ATTN_E_INVALID, "cache size overflows");
 
@@ -300,6 +355,8 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
     h->head_dim = head_dim;
     h->window = window;
     h->rope_base = rope_base;
+    h->fast_decode = decode_supported(head_dim, n_rep);
+    h->fast_prefill = prefill_supported(head_dim, n_rep);
     auto bail = [&](hipError_t e, const char *what) {
         g_create_error = std::string(what) + ": " + hipGetErrorString(e);
         release(h);
@@ -328,18 +385,23 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
         release(h);
         return KORE_ATTN_E_HIP;
     }
-    // Decode split partials: n_head * max_split * (hd + 2) floats.
-    h->max_split = decode_max_split(head_dim, window ? window : ctx, n_head_kv, h->num_cu);
+    // Decode split partials: n_head * max_split * (hd + 2) floats, and the
+    // roped q of the generic decode.
+    h->max_split = h->fast_decode ? decode_max_split(head_dim, window ? window : ctx, n_head_kv, h->num_cu)
+                                  : generic_max_split(head_dim, n_rep, n_head_kv, h->num_cu);
     const size_t np = (size_t)n_head * h->max_split;
-    if ((e = hipMalloc(&h->d_part_o, np * ((size_t)head_dim + 2) * sizeof(float))) != hipSuccess)
+    h->part_floats = np * ((size_t)head_dim + 2) + (h->fast_decode ? 0 : (size_t)n_head * head_dim);
+    if ((e = hipMalloc(&h->d_part_o, h->part_floats * sizeof(float))) != hipSuccess)
         return bail(e, "hipMalloc");
     // Prefill key-segment partials, sized for the largest split any chunk
     // gets: segments are only used while a chunk has fewer workgroups than
     // CUs, which bounds (heads x strips x segments) by 8 x num_cu
     // (prefill_key_segments), i.e. 8 x num_cu x 32 rows of (hd + 2) floats.
-    h->pf_part_floats = (size_t)8 * h->num_cu * 32 * ((size_t)head_dim + 2);
-    if ((e = hipMalloc(&h->d_pf_part, h->pf_part_floats * sizeof(float))) != hipSuccess)
-        return bail(e, "hipMalloc");
+    if (h->fast_prefill) {
+        h->pf_part_floats = (size_t)8 * h->num_cu * 32 * ((size_t)head_dim + 2);
+        if ((e = hipMalloc(&h->d_pf_part, h->pf_part_floats * sizeof(float))) != hipSuccess)
+            return bail(e, "hipMalloc");
+    }
     // the device's fixed scratch of kore_attn_decode_noalloc_dev, resolved
     // once per device with that device current
     if ((e = static_scratch(h->device, &h->d_scratch)) != hipSuccess) return bail(e, "hipGetSymbolAddress");
@@ -355,8 +417,7 @@ int kore_attn_decode_dev(kore_attn_t h, int layer, int pos, int n_head, int n_he
     if (!h) return fail(nullptr, KORE_ATTN_E_INVALID, "null handle");
     if (int rc = check_decode(h, layer, pos, n_head, n_head_kv, head_dim, q, k, v, out)) return rc;
     HIP_TRY(h, hipSetDevice(h->device));
-    return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_part_o,
-                          (size_t)h->n_head * h->max_split * ((size_t)h->head_dim + 2));
+    return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_part_o, h->part_floats);
 }
 
 int kore_attn_decode_noalloc_dev(kore_attn_t h, int layer, int pos, int n_head, int n_head_kv, int head_dim,
@@ -381,7 +442,7 @@ int kore_attn_decode(kore_attn_t h, int layer, int pos, int n_head, int n_head_k
     std::memcpy(hs + E + kvd, v, kvd * sizeof(float));
     HIP_TRY(h, hipMemcpyAsync(ds, hs, (E + 2 * kvd) * sizeof(float), hipMemcpyHostToDevice, h->stream));
     if (int rc = decode_enqueue(h, layer, pos, ds, ds + E, ds + E + kvd, ds + E + 2 * kvd, h->stream,
-                                h->d_part_o, (size_t)h->n_head * h->max_split * ((size_t)h->head_dim + 2)))
+                                h->d_part_o, h->part_floats))
         return rc;
     HIP_TRY(h, hipMemcpyAsync(hs + E + 2 * kvd, ds + E + 2 * kvd, E * sizeof(float), hipMemcpyDeviceToHost,
                               h->stream));

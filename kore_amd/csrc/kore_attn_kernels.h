@@ -45,7 +45,7 @@ struct DecodeArgs {
 // built on the host (kore.cpp:1405-1410) and passed by value with the launch:
 // a decode needs one row, so no device table has to cover its position (a
 // ring decodes past ctx without bound).
-constexpr int kMaxRopeHalf = 64;
+constexpr int kMaxRopeHalf = 128;
 struct RopeRow {
     float cs[2 * kMaxRopeHalf];
 };
@@ -90,6 +90,42 @@ struct PrefillArgs {
     int fold;
 };
 
+// Any even head_dim up to kMaxGenericHeadDim and any n_rep (the geometries
+// kore accepts, kore.cpp:1278-1290, that the MFMA kernels above do not
+// cover): tiled attention on VALU with fp64 scores.  A workgroup takes `chunk`
+// q-heads of one kv-head and one key range: a decode split of the cache rows
+// (after a prep launch has roped q and appended the new row), or all keys
+// 0..pos of one prefill row.
+constexpr int kMaxGenericHeadDim = 2 * kMaxRopeHalf;
+struct GenericArgs {
+    const float *q;       // decode: roped q [n_head][hd]; prefill: pre-RoPE q [n_tok][n_head][hd]
+    const float2 *cs;     // prefill: RoPE table (row p = position p); decode: null
+    const float *kc, *vc; // layer base
+    float *out;           // [n_tok][n_head][hd]
+    float *part_o;        // decode with n_split > 1: [n_head][n_split][hd]
+    float *part_ml;       //                          [n_head][n_split][2]
+    int slots, hd, n_head_kv, n_rep;
+    int chunk, n_chunks;  // q-heads per workgroup, workgroups per kv-head
+    int tile;             // keys per LDS tile
+    int pos0;             // prefill: position of row 0
+    int n_rows;           // decode: cache rows attended, [0, n_rows), the new row included
+    int rows_per_split, n_split;
+    float scale;          // kore's 1/sqrt(hd) (kore.cpp:1411)
+};
+bool generic_supported(int head_dim);
+// Launch shape of the generic kernels: tile, chunk and the split bound.
+void generic_shape(int head_dim, int n_rep, int *tile, int *chunk, int *n_chunks);
+int generic_max_split(int head_dim, int n_rep, int n_head_kv, int num_cu);
+int generic_rows_per_split(int head_dim, int n_rep, int n_rows, int n_head_kv, int num_cu);
+size_t generic_lds_bytes(int head_dim, int tile, int chunk);
+// Decode: RoPE of q into q_out and of the new k row, append of k and v at
+// new_slot, then the split attention and (n_split > 1) the merge.
+hipError_t launch_generic_decode(const GenericArgs &a, const float *q, const float *k, const float *v,
+                                 float *q_out, float *kc, float *vc, int n_head, int new_slot, const RopeRow &rr,
+                                 hipStream_t s);
+// Prefill rows after their append: grid (n_tok, n_head_kv * n_chunks).
+hipError_t launch_generic_prefill(const GenericArgs &a, int n_tok, hipStream_t s);
+
 // Counter-based synthetic inputs (identical bits to the CPU oracle's
 // generator): dst[r*dim + c] for r < rows.
 struct SynthArgs {
@@ -114,6 +150,8 @@ hipError_t static_scratch(int device, float **ptr);
 // Rows per split the decode uses for n_rows cache rows (the host sizes the
 // partial buffers from the maximum split count over all lengths).
 int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu);
+// Geometries of the MFMA decode / prefill kernels; the others take the
+// generic kernels.
 bool decode_supported(int head_dim, int n_rep);
 bool prefill_supported(int head_dim, int n_rep);
 

@@ -20,6 +20,11 @@
 //                   on fp32 MFMA (v_mfma_f32_32x32x2_f32) with LDS-staged K and
 //                   transposed V tiles shared by the four waves of a
 //                   workgroup, which all belong to one kv-head (GQA sharing).
+//   generic_*       every other geometry kore accepts (any even head_dim up
+//                   to 256, any q-heads per kv-head): a decode prep launch
+//                   (RoPE of q, RoPE + append of the new row), LDS-tiled
+//                   attention on VALU with fp64 scores for decode splits and
+//                   prefill rows, and the merge of the decode's split partials.
 //   synth_kernel    counter-based synthetic inputs for benchmarks and tests.
 //
 // RoPE is bit-exact with kore: cos/sin come from the host-built table (the
@@ -686,6 +691,187 @@ __global__ void append_kernel(AppendArgs a, int hd) {
     for (int i = threadIdx.x; i < hd; i += blockDim.x) vd[i] = vin[i];
 }
 
+// ------------------------------------------------------------ any geometry
+
+// Block i < n_head: RoPE of q row i at the decode position into q_out; block
+// n_head + g: RoPE of the new k row of kv-head g and the append of k and v at
+// new_slot (kore.cpp:1424-1430).
+__global__ void generic_decode_prep_kernel(const float *q, const float *k, const float *v, float *q_out,
+                                           float *kc, float *vc, int n_head, int hd, int slots, int new_slot,
+                                           RopeRow rr) {
+    const int i = blockIdx.x, half = hd / 2;
+    const bool is_q = i < n_head;
+    const int g = i - n_head;
+    const float *src = is_q ? q + (size_t)i * hd : k + (size_t)g * hd;
+    float *dst = is_q ? q_out + (size_t)i * hd : kc + ((size_t)g * slots + new_slot) * hd;
+    for (int d = threadIdx.x; d < half; d += blockDim.x) {
+        float y0, y1;
+        rope_pair(src[d], src[d + half], make_float2(rr.cs[2 * d], rr.cs[2 * d + 1]), y0, y1);
+        dst[d] = y0;
+        dst[d + half] = y1;
+    }
+    if (!is_q) {
+        float *vd = vc + ((size_t)g * slots + new_slot) * hd;
+        for (int d = threadIdx.x; d < hd; d += blockDim.x) vd[d] = v[(size_t)g * hd + d];
+    }
+}
+
+__device__ __forceinline__ double wave_max_d(double x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmax(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+// Workgroup (key range, kv-head g x head chunk c): q-heads g * n_rep + c *
+// chunk + i (i < nh) attend keys [r_begin, r_end) of kv-head g in LDS tiles
+// of `tile` rows (rows past r_end read as zeros, never from memory).  Per
+// tile: scores as fp64 dots of the fp32 roped q and k (each product exact in
+// fp64), times kore's 1/sqrt(hd) and log2(e); one wave per head takes the
+// tile's max and the weights 2^(score - max) with the difference in fp64;
+// then every thread advances its outputs (head, dim) by the weighted V rows
+// in fp32.  Prefill workgroups take row z = blockIdx.x with keys 0..pos0+z
+// and rope their q rows from the table; decode workgroups take split
+// blockIdx.x of the rows [0, n_rows) with q already roped.
+__global__ __launch_bounds__(kThreads) void generic_attend_kernel(GenericArgs a) {
+    extern __shared__ __align__(16) unsigned char g_lds[];
+    const int hd = a.hd, T = a.tile, CH = a.chunk, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = blockIdx.y / a.n_chunks, c = blockIdx.y % a.n_chunks;
+    const int h0 = c * CH, nh = min(CH, a.n_rep - h0);
+    const int n_head = a.n_head_kv * a.n_rep, hq0 = g * a.n_rep + h0;
+    const bool prefill = a.cs != nullptr;
+    const int z = prefill ? (int)blockIdx.x : 0;
+    const int r_begin = prefill ? 0 : (int)blockIdx.x * a.rows_per_split;
+    const int r_end = prefill ? a.pos0 + z + 1 : min(r_begin + a.rows_per_split, a.n_rows);
+
+    double *s_sc = reinterpret_cast<double *>(g_lds);   // [CH][T] scores
+    float *s_p = reinterpret_cast<float *>(s_sc + CH * T);   // [CH][T] weights
+    float *s_al = s_p + CH * T;                              // [CH] rescale of the tile
+    float *s_m = s_al + CH, *s_l = s_m + CH;                 // [CH] running max, sum
+    float *s_q = s_l + CH;                                   // [CH][hd]
+    float *s_k = s_q + CH * hd;                              // [T][hd + 1]
+    float *s_v = s_k + T * (hd + 1);                         // [T][hd]
+
+    const float *qb = a.q + ((size_t)z * n_head + hq0) * hd;
+    for (int e = tid; e < nh * hd; e += kThreads) {
+        if (prefill) {
+            const int i = e / hd, d = e % hd, half = hd / 2, d0 = d < half ? d : d - half;
+            const float *qr = qb + (size_t)i * hd;
+            float y0, y1;
+            rope_pair(qr[d0], qr[d0 + half], a.cs[(size_t)(a.pos0 + z) * half + d0], y0, y1);
+            s_q[e] = d < half ? y0 : y1;
+        } else {
+            s_q[e] = qb[e];
+        }
+    }
+    if (tid < nh) {
+        s_m[tid] = -INFINITY;
+        s_l[tid] = 0.f;
+    }
+    const double sscale = (double)a.scale * 1.4426950408889634;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const float *kg = a.kc + (size_t)g * a.slots * hd;
+    const float *vg = a.vc + (size_t)g * a.slots * hd;
+    for (int t0 = r_begin; t0 < r_end; t0 += T) {
+        const int nr = min(T, r_end - t0);
+        __syncthreads();   // the previous tile's readers are done (and s_q, s_m, s_l are set)
+        const float *kt = kg + (size_t)t0 * hd, *vt = vg + (size_t)t0 * hd;
+        for (int e = tid; e < T * hd; e += kThreads) {
+            const int r = e / hd, d = e % hd;
+            const bool ok = r < nr;
+            s_k[r * (hd + 1) + d] = ok ? kt[e] : 0.f;
+            s_v[e] = ok ? vt[e] : 0.f;
+        }
+        __syncthreads();
+        for (int e = tid; e < nh * T; e += kThreads) {
+            const int i = e / T, r = e % T;
+            double s = -INFINITY;
+            if (r < nr) {
+                const float *qi = s_q + i * hd, *kr = s_k + r * (hd + 1);
+                double d0 = 0.0, d1 = 0.0;
+                for (int d = 0; d < hd; d += 2) {
+                    d0 = fma((double)qi[d], (double)kr[d], d0);
+                    d1 = fma((double)qi[d + 1], (double)kr[d + 1], d1);
+                }
+                s = (d0 + d1) * sscale;
+            }
+            s_sc[e] = s;
+        }
+        __syncthreads();
+        for (int i = wave; i < nh; i += kWaves) {
+            const double sv = lane < T ? s_sc[i * T + lane] : -INFINITY;
+            const float m_old = s_m[i];
+            const float m_new = fmaxf(m_old, (float)wave_max_d(sv));
+            const float p = sv != -INFINITY ? fast_exp2((float)(sv - (double)m_new)) : 0.f;
+            const float sum = wave_sum(p);
+            if (lane < T) s_p[i * T + lane] = p;
+            if (lane == 0) {
+                const float al = m_old == -INFINITY ? 0.f : fast_exp2(m_old - m_new);
+                s_al[i] = al;
+                s_m[i] = m_new;
+                s_l[i] = s_l[i] * al + sum;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int o = tid + j * kThreads;
+            if (o < nh * hd) {
+                const int i = o / hd, d = o % hd;
+                const float *pi = s_p + i * T;
+                float x = acc[j] * s_al[i];
+                for (int r = 0; r < nr; ++r) x = fmaf(pi[r], s_v[r * hd + d], x);
+                acc[j] = x;
+            }
+        }
+    }
+    __syncthreads();
+    if (prefill || a.n_split == 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int o = tid + j * kThreads;
+            if (o < nh * hd) a.out[((size_t)z * n_head + hq0) * hd + o] = acc[j] / s_l[o / hd];
+        }
+    } else {
+        const int sp = blockIdx.x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int o = tid + j * kThreads;
+            if (o < nh * hd) {
+                const int i = o / hd, d = o % hd;
+                a.part_o[((size_t)(hq0 + i) * a.n_split + sp) * hd + d] = acc[j];
+            }
+        }
+        if (tid < nh)
+            reinterpret_cast<float2 *>(a.part_ml)[(size_t)(hq0 + tid) * a.n_split + sp] =
+                make_float2(s_m[tid], s_l[tid]);
+    }
+}
+
+// Block h: log-sum-exp merge of q-head h's split partials (max and sum in
+// the base-2 domain of generic_attend_kernel), one thread per dim.
+__global__ void generic_combine_kernel(const float *part_o, const float *part_ml, float *out, int n_split, int hd) {
+    const int h = blockIdx.x;
+    const float2 *ml = reinterpret_cast<const float2 *>(part_ml) + (size_t)h * n_split;
+    float m = -INFINITY;
+    for (int s = 0; s < n_split; ++s) m = fmaxf(m, ml[s].x);
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float acc = 0.f, den = 0.f;
+        for (int s = 0; s < n_split; ++s) {
+            const float2 st = ml[s];
+            const float w = fast_exp2(st.x - m);
+            den = fmaf(w, st.y, den);
+            acc = fmaf(w, part_o[((size_t)h * n_split + s) * hd + d], acc);
+        }
+        out[(size_t)h * hd + d] = acc / den;
+    }
+}
+
 // ----------------------------------------------------------------- prefill
 
 // v_mfma_f32_32x32x2_f32, one block: lane l supplies A[l%32][l/32] and
@@ -1160,6 +1346,60 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
         if (head_dim == 128) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL(prefill_combine_kernel<64>, cgrid, dim3(256), 0, s, a);
     }
+    return hipGetLastError();
+}
+
+bool generic_supported(int head_dim) {
+    return head_dim >= 2 && head_dim <= kMaxGenericHeadDim && head_dim % 2 == 0;
+}
+
+void generic_shape(int head_dim, int n_rep, int *tile, int *chunk, int *n_chunks) {
+    // K and V tiles within 40 KB; a tile's rows fit one wave (softmax); at
+    // most 1024 (head, dim) outputs (4 per thread) and 1024 (head, row) scores.
+    int T = 64;
+    while (T > 8 && (size_t)T * (2 * head_dim + 1) * sizeof(float) > 40 * 1024) T /= 2;
+    const int ch = std::max(1, std::min({n_rep, 1024 / head_dim, 1024 / T}));
+    *tile = T;
+    *chunk = ch;
+    *n_chunks = (n_rep + ch - 1) / ch;
+}
+
+size_t generic_lds_bytes(int head_dim, int tile, int chunk) {
+    const size_t T = tile, C = chunk, hd = head_dim;
+    return C * T * sizeof(double) + (C * T + 3 * C + C * hd + T * (hd + 1) + T * hd) * sizeof(float);
+}
+
+int generic_max_split(int head_dim, int n_rep, int n_head_kv, int num_cu) {
+    int T, ch, nc;
+    generic_shape(head_dim, n_rep, &T, &ch, &nc);
+    return std::max(1, std::min(kMaxDecodeSplits, num_cu / std::max(1, n_head_kv * nc)));
+}
+
+int generic_rows_per_split(int head_dim, int n_rep, int n_rows, int n_head_kv, int num_cu) {
+    // at most generic_max_split splits, each whole tiles (the last one shorter)
+    int T, ch, nc;
+    generic_shape(head_dim, n_rep, &T, &ch, &nc);
+    const int S = std::max(1, std::min(generic_max_split(head_dim, n_rep, n_head_kv, num_cu), (n_rows + T - 1) / T));
+    const int rps = std::max(1, (n_rows + S - 1) / S);
+    return (rps + T - 1) / T * T;
+}
+
+hipError_t launch_generic_decode(const GenericArgs &a, const float *q, const float *k, const float *v,
+                                 float *q_out, float *kc, float *vc, int n_head, int new_slot, const RopeRow &rr,
+                                 hipStream_t s) {
+    hipLaunchKernelGGL(generic_decode_prep_kernel, dim3(n_head + a.n_head_kv), dim3(64), 0, s, q, k, v, q_out, kc,
+                       vc, n_head, a.hd, a.slots, new_slot, rr);
+    const size_t lds = generic_lds_bytes(a.hd, a.tile, a.chunk);
+    hipLaunchKernelGGL(generic_attend_kernel, dim3(a.n_split, a.n_head_kv * a.n_chunks), dim3(kThreads), lds, s, a);
+    if (a.n_split > 1)
+        hipLaunchKernelGGL(generic_combine_kernel, dim3(n_head), dim3(std::min(256, (a.hd + 63) / 64 * 64)), 0, s,
+                           a.part_o, a.part_ml, a.out, a.n_split, a.hd);
+    return hipGetLastError();
+}
+
+hipError_t launch_generic_prefill(const GenericArgs &a, int n_tok, hipStream_t s) {
+    const size_t lds = generic_lds_bytes(a.hd, a.tile, a.chunk);
+    hipLaunchKernelGGL(generic_attend_kernel, dim3(n_tok, a.n_head_kv * a.n_chunks), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
 

@@ -77,9 +77,11 @@ def test_create_rejects_bad_geometry(args, fragment):
 
 
 def test_create_reports_unsupported_geometry():
+    """Every even head_dim up to 256 has a kernel; a larger one is refused
+    before anything touches the device."""
     import kore_amd
-    rc, h, msg = _create(1, 80, 32, 8, 40, 1e6, 0)
-    assert rc == kore_amd.KORE_ATTN_E_UNSUPPORTED and "head_dim 40" in msg
+    rc, h, msg = _create(1, 80, 4, 2, 258, 1e6, 0)
+    assert rc == kore_amd.KORE_ATTN_E_UNSUPPORTED and "head_dim 258" in msg and not h.value
 
 
 def test_null_handle_calls_fail_cleanly():

@@ -21,6 +21,8 @@ def _say(msg):
     (28, 4, 128, 3000, (3000, 77)),     # Qwen2.5-7B geometry: 64 splits, then 4
     (16, 2, 128, 4200, (4200, 1500)),   # 3B geometry: 128 splits of 33 rows, then 93 splits
     (14, 2, 64, 600, (600, 16)),        # 0.5B geometry, head_dim 64
+    (32, 8, 40, 2000, (2000, 50)),      # head_dim 40: the generic kernels (roped q in the array too)
+    (24, 2, 128, 3000, (3000, 100)),    # 12 q-heads per kv-head: generic decode
 ])
 def test_noalloc_decode_equals_decode_dev(nh, nkv, hd, fill, positions):
     from kore_amd import KoreAttn, hip
