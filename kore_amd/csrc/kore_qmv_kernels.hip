@@ -16,17 +16,13 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstdlib>
 #include <type_traits>
 
 namespace kore_qmv_gpu {
 namespace {
 
 constexpr int kThreads = 256;
-
-// Steps of weight loads in flight per thread.
-#ifndef KQMV_DEPTH
-#define KQMV_DEPTH 2
-#endif
 
 __device__ __forceinline__ float f16_bits(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -163,6 +159,8 @@ __device__ __forceinline__ float kore_swiglu(float g, float u) {
     return q * u;
 }
 
+__device__ __forceinline__ Q8Lane quantize16(const float (&v)[16], int m);
+
 // kore's quantisation of one 256-value block (kore.cpp:422-446) by the 16
 // lanes of a DPP row: lane m owns values 16m .. 16m+15 (x 16-byte aligned),
 // after the pre-op (rmsnorm with `scale`, or SwiGLU) of the values at xb[i] =
@@ -197,6 +195,12 @@ __device__ __forceinline__ Q8Lane quantize_lane(const float *xb, int m, const Pr
             v[4 * k + 3] = kore_swiglu(v[4 * k + 3], u.w);
         }
     }
+    return quantize16(v, m);
+}
+
+// The quantisation proper of quantize_lane: lane m of a DPP row holds values
+// 16m .. 16m+15 of the block (after any pre-op) in v.
+__device__ __forceinline__ Q8Lane quantize16(const float (&v)[16], int m) {
     // kore keeps the first value of largest magnitude, starting from amax = 0
     // with a strict comparison (kore.cpp:424-428): the largest |x| wins, ties
     // go to the lowest index, NaN and zeros are never chosen.
@@ -291,6 +295,45 @@ __global__ __launch_bounds__(kThreads) void quantize_q8k_kernel(const float *__r
     qw[3] = q.qs.w;
     *(int16_t *)(rec + 260 + 2 * m) = (int16_t)q.bsum;
     if (m == 0) *(float *)rec = q.d;
+}
+
+// kore's SwiGLU (kore.cpp:1465-1468) then quantize_row_q8_K of the product:
+// one block per workgroup, one value per thread (its exp and division in
+// double are the long part, so they are spread over 256 lanes), then the 16
+// lanes of the first DPP row quantise the block from LDS.  Bit-identical to
+// quantize_q8k_kernel with the SwiGLU pre-op.
+template <bool IMAGE>
+__global__ __launch_bounds__(kThreads) void swiglu_quantize_kernel(const float *__restrict__ g,
+                                                                   const float *__restrict__ u,
+                                                                   uint8_t *__restrict__ xq, int64_t nblocks) {
+    __shared__ __align__(16) float sv[256];
+    const int64_t blk = blockIdx.x;
+    const int t = threadIdx.x;
+    sv[t] = kore_swiglu(g[blk * 256 + t], u[blk * 256 + t]);
+    __syncthreads();
+    if (t >= 16) return;
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 f = *(const float4 *)&sv[16 * t + 4 * k];
+        v[4 * k] = f.x;
+        v[4 * k + 1] = f.y;
+        v[4 * k + 2] = f.z;
+        v[4 * k + 3] = f.w;
+    }
+    const Q8Lane q = quantize16(v, t);
+    if constexpr (IMAGE) {
+        xs_store(xq, (int)nblocks, (int)blk, t, q);
+        return;
+    }
+    uint8_t *rec = xq + blk * kQ8Bytes;
+    uint32_t *qw = (uint32_t *)(rec + 4 + 16 * t);
+    qw[0] = q.qs.x;
+    qw[1] = q.qs.y;
+    qw[2] = q.qs.z;
+    qw[3] = q.qs.w;
+    *(int16_t *)(rec + 260 + 2 * t) = (int16_t)q.bsum;
+    if (t == 0) *(float *)rec = q.d;
 }
 
 // ------------------------------------------------------------------ units
@@ -456,7 +499,7 @@ __device__ __forceinline__ Rec part_q6(const Q6Raw &r, const Q8View &x, int i, i
 // lanes of phase 0, which advance the chains block by block.  The weight
 // loads of the next D steps are in flight while a step is computed, across
 // the tiles of the workgroup's run [tile_begin, tile_end).
-template <int TYPE, bool AVX2, int RW, bool FUSED, int D>
+template <int TYPE, bool AVX2, int RW, bool FUSED, int D, int PIPE>
 __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, int tile_end, const GroupArgs &a,
                                             uint8_t *smem) {
     constexpr int P = 16 / RW;
@@ -494,13 +537,71 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
         return r;
     };
 
-    // the activations
-    if constexpr (FUSED) {
+    // the activations; the first D steps' weights are requested as soon as
+    // the activations' own loads are issued, so their latency runs under the
+    // quantisation (loads complete in order: requested earlier, the
+    // activations are waited for without waiting for the weights)
+    Raw buf[D];
+    if (FUSED && nblk > kThreads / 16) {
+        // more blocks than one pass of 16-lane quantisers covers (the host
+        // fuses such inputs only when asked to): the scale over the whole
+        // vector first, then pass after pass, then the weights
         const PreOp pre{a.norm_w, a.norm_eps, a.up};
-        // rmsnorm's scale: the records area is free until the blocks start
         const float scale = a.norm_w ? block_rms_scale(a.x, nblk * 256, a.norm_eps, (double *)smem) : 1.f;
         for (int b = t >> 4; b < nblk; b += kThreads / 16)
             xs_store(xs, nblk, b, t & 15, quantize_lane(a.x + (int64_t)b * 256, t & 15, pre, scale, (int64_t)b * 256));
+#pragma unroll
+        for (int d = 0; d < D; ++d) buf[d] = load_next();
+    } else if constexpr (FUSED) {
+        // one pass: thread t quantises values
+        // 16 m .. 16 m + 15 of block b as lane m of a DPP row, from one round
+        // of loads of x and of the pre-op's operand (rmsnorm weights or up;
+        // x again when there is none); threads past the last block take a
+        // clamped copy, add nothing to the sum of squares and store nothing
+        const int b = t >> 4, m = t & 15;
+        const bool on = b < nblk;
+        const int64_t off = (int64_t)min(b, nblk - 1) * 256 + 16 * m;
+        const float *opnd = a.norm_w ? a.norm_w : a.up ? a.up : a.x;
+        float v[16], w[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 f = *(const float4 *)(a.x + off + 4 * k);
+            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 f = *(const float4 *)(opnd + off + 4 * k);
+            w[4 * k] = f.x; w[4 * k + 1] = f.y; w[4 * k + 2] = f.z; w[4 * k + 3] = f.w;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < D; ++d) buf[d] = load_next();
+        __builtin_amdgcn_sched_barrier(0);
+        if (a.norm_w) {
+            // kore's rmsnorm (kore.cpp:1367-1372): the certified scale of
+            // block_rms_scale_from from this thread's double-double partial
+            // sum (in two chains), then x * scale * w with kore's roundings;
+            // the records area is free until the blocks start
+            double hi0 = 0.0, lo0 = 0.0, hi1 = 0.0, lo1 = 0.0;
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+                double s0, e0, s1, e1;
+                two_sum(hi0, on ? (double)v[e] * (double)v[e] : 0.0, s0, e0);
+                two_sum(hi1, on ? (double)v[e + 1] * (double)v[e + 1] : 0.0, s1, e1);
+                hi0 = s0; lo0 += e0;
+                hi1 = s1; lo1 += e1;
+            }
+            double hi, e01;
+            two_sum(hi0, hi1, hi, e01);
+            const float scale = block_rms_scale_from(hi, (lo0 + lo1) + e01, a.x, nblk * 256, a.norm_eps, (double *)smem);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = (v[e] * scale) * w[e];
+        } else if (a.up) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = kore_swiglu(v[e], w[e]);
+        }
+        const Q8Lane q = quantize16(v, m);
+        if (on) xs_store(xs, nblk, b, m, q);
     } else if (a.xq_image) {
         // already in the LDS layout (xs_bytes(nblk) is a multiple of 4 bytes)
         const int n16 = (int)(xs_bytes(nblk) >> 4);
@@ -517,6 +618,10 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
             if (l < 8) *(uint32_t *)(xs + nblk * kXsQs + 32 * b + 4 * l) = src[65 + l];
             else if (l == 8) *(float *)(xs + nblk * 304 + 4 * b) = __uint_as_float(src[0]);
         }
+    }
+    if constexpr (!FUSED) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) buf[d] = load_next();
     }
     __syncthreads();
     const Q8View x{xs, nblk};
@@ -549,78 +654,113 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
         }
     };
 
-    for (int k0 = 0; k0 < total; k0 += D) {
-        // the loads of D steps first (a step past the end repeats the last
-        // one's clamped addresses and is discarded); nothing loaded is carried
-        // from one iteration to the next, so no register copy has to wait for
-        // loads in flight
-        Raw buf[D];
-#pragma unroll
-        for (int d = 0; d < D; ++d) buf[d] = load_next();
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int k = k0 + d;
-            const int i = min(cs * P + ph, nblk - 1);
-            Rec r;
-            if constexpr (TYPE == kQ4K) r = part_q4<AVX2>(buf[d], x, i, j);
-            else r = part_q6<AVX2>(buf[d], x, i, j);
-            if (k < total) {
-                if constexpr (P == 1) {
-                    // the unit's four parts are this lane's quad: d / dmin from parts 0 / 1
-                    Rec q0 = r, q1 = r;
-                    if constexpr (TYPE == kQ4K && AVX2) {
-                        // part j holds d (j even) or dmin (j odd): take both from the quad
-                        const float other = quad_xor1f(r.x);
-                        q0.x = (j & 1) ? other : r.x;
-                        q1.x = (j & 1) ? r.x : other;
-                    }
-                    advance(r, q0, q1);
-                } else {
-                    Rec *rb = recs + (k & 1) * 64;
-                    rb[l] = r;
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                    if (chain) {
-                        const int nb = min(P, nblk - cs * P);
-                        for (int b = 0; b < nb; ++b) {
-                            const int base = (b * RW + rho) * 4;
-                            advance(rb[base + j], rb[base], rb[base + 1]);
-                        }
-                    }
+    // one step k of the compute cursor over the loaded parts `raw`
+    auto step = [&](const Raw &raw, int k) {
+        const int i = min(cs * P + ph, nblk - 1);
+        Rec r;
+        if constexpr (TYPE == kQ4K) r = part_q4<AVX2>(raw, x, i, j);
+        else r = part_q6<AVX2>(raw, x, i, j);
+        if (k < total) {
+            if constexpr (P == 1) {
+                // the unit's four parts are this lane's quad: d / dmin from parts 0 / 1
+                Rec q0 = r, q1 = r;
+                if constexpr (TYPE == kQ4K && AVX2) {
+                    // part j holds d (j even) or dmin (j odd): take both from the quad
+                    const float other = quad_xor1f(r.x);
+                    q0.x = (j & 1) ? other : r.x;
+                    q1.x = (j & 1) ? r.x : other;
                 }
-                if (++cs == nsteps) {
-                    // the tile's rows are complete
-                    if (chain) {
-                        float res;
-                        if constexpr (AVX2) {
-                            // kore's hsum256 (kore.cpp:521-528): lanes k and k+4 first,
-                            // then (l0 + l2) + (l1 + l3); parts 0..3 hold lanes {0,1},
-                            // {4,5}, {2,3}, {6,7}
-                            const float u = acc0 + quad_xor1f(acc0);     // part 0: l0, part 2: l2
-                            const float v = acc1 + quad_xor1f(acc1);     // part 0: l1, part 2: l3
-                            const float h8 = (u + quad_xor2f(u)) + (v + quad_xor2f(v));
-                            if constexpr (TYPE == kQ4K) {
-                                const float m = accm + quad_xor2f(accm); // hsum128 (kore.cpp:537-541)
-                                res = h8 + (m + quad_xor1f(m));
-                            } else {
-                                res = h8 + accm;
-                            }
-                        } else {
-                            res = acc0;
+                advance(r, q0, q1);
+            } else {
+                Rec *rb = recs + (k & 1) * 64;
+                rb[l] = r;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (chain) {
+                    // the records of four blocks at a time are read before
+                    // their chain steps, so the LDS latency is paid per group
+                    const int nb = min(P, nblk - cs * P);
+#pragma unroll
+                    for (int b0 = 0; b0 < P; b0 += 4) {
+                        if (b0 >= nb) break;
+                        constexpr int G = P < 4 ? P : 4;
+                        Rec qs[G], q0s[G], q1s[G];
+#pragma unroll
+                        for (int u = 0; u < G; ++u) {
+                            const int base = ((b0 + u) * RW + rho) * 4;
+                            qs[u] = rb[base + j];
+                            q0s[u] = rb[base];
+                            q1s[u] = rb[base + 1];
                         }
-                        const int orow = (ct * 4 + wave) * RW + rho;
-                        if (j == 0 && orow < rows) {
-                            // kore's q += bq (kore.cpp:1422-1423), x += o (kore.cpp:1458, 1471)
-                            const float v = md.bias ? res + md.bias[orow] : res;
-                            md.out[orow] = md.accumulate ? md.out[orow] + v : v;
-                        }
-                        acc0 = acc1 = accm = 0.f;
+#pragma unroll
+                        for (int u = 0; u < G; ++u)
+                            if (b0 + u < nb) advance(qs[u], q0s[u], q1s[u]);
                     }
-                    cs = 0;
-                    ++ct;
                 }
             }
+            if (++cs == nsteps) {
+                // the tile's rows are complete
+                if (chain) {
+                    float res;
+                    if constexpr (AVX2) {
+                        // kore's hsum256 (kore.cpp:521-528): lanes k and k+4 first,
+                        // then (l0 + l2) + (l1 + l3); parts 0..3 hold lanes {0,1},
+                        // {4,5}, {2,3}, {6,7}
+                        const float u = acc0 + quad_xor1f(acc0);     // part 0: l0, part 2: l2
+                        const float v = acc1 + quad_xor1f(acc1);     // part 0: l1, part 2: l3
+                        const float h8 = (u + quad_xor2f(u)) + (v + quad_xor2f(v));
+                        if constexpr (TYPE == kQ4K) {
+                            const float m = accm + quad_xor2f(accm); // hsum128 (kore.cpp:537-541)
+                            res = h8 + (m + quad_xor1f(m));
+                        } else {
+                            res = h8 + accm;
+                        }
+                    } else {
+                        res = acc0;
+                    }
+                    const int orow = (ct * 4 + wave) * RW + rho;
+                    if (j == 0 && orow < rows) {
+                        // kore's q += bq (kore.cpp:1422-1423), x += o (kore.cpp:1458, 1471)
+                        const float v = md.bias ? res + md.bias[orow] : res;
+                        md.out[orow] = md.accumulate ? md.out[orow] + v : v;
+                    }
+                    acc0 = acc1 = accm = 0.f;
+                }
+                cs = 0;
+                ++ct;
+            }
+        }
+    };
+
+    if constexpr (PIPE == 0) {
+        // D steps are computed, then the next D requested (a step past the
+        // end repeats the last one's clamped addresses and is discarded); buf
+        // keeps its registers across the back-edge, so no copy waits for its
+        // loads.
+        for (int k0 = 0;;) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) step(buf[d], k0 + d);
+            k0 += D;
+            if (k0 >= total) break;
+#pragma unroll
+            for (int d = 0; d < D; ++d) buf[d] = load_next();
+        }
+    } else {
+        // the next D steps are requested before the current D are computed
+        // (two register sets, unrolled so that neither is copied)
+        for (int k0 = 0;; k0 += 2 * D) {
+            Raw nb[D];
+#pragma unroll
+            for (int d = 0; d < D; ++d) nb[d] = load_next();
+#pragma unroll
+            for (int d = 0; d < D; ++d) step(buf[d], k0 + d);
+            if (k0 + D >= total) break;
+#pragma unroll
+            for (int d = 0; d < D; ++d) buf[d] = load_next();
+#pragma unroll
+            for (int d = 0; d < D; ++d) step(nb[d], k0 + D + d);
+            if (k0 + 2 * D >= total) break;
         }
     }
 }
@@ -628,10 +768,9 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
 // One launch over up to kMaxGroup matrices that read the same activations:
 // workgroups [m.wg_begin, m.wg_begin + m.wg_count) belong to matrix m and
 // split its tiles of 4 RW rows evenly in contiguous runs.
-template <bool AVX2, int RW, bool FUSED>
+template <bool AVX2, int RW, bool FUSED, int D, int PIPE>
 __global__ __launch_bounds__(kThreads) void matvec_group_kernel(GroupArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int D = KQMV_DEPTH;
     const int g = blockIdx.x;
     MatDesc md = a.m[0];
 #pragma unroll
@@ -641,8 +780,8 @@ __global__ __launch_bounds__(kThreads) void matvec_group_kernel(GroupArgs a) {
     const int64_t tiles = (md.rows + 4 * RW - 1) / (4 * RW);
     const int tb = (int)(tiles * w / md.wg_count), te = (int)(tiles * (w + 1) / md.wg_count);
     if (tb >= te) return;
-    if (md.type == kQ4K) matvec_body<kQ4K, AVX2, RW, FUSED, D>(md, tb, te, a, smem);
-    else matvec_body<kQ6K, AVX2, RW, FUSED, D>(md, tb, te, a, smem);
+    if (md.type == kQ4K) matvec_body<kQ4K, AVX2, RW, FUSED, D, PIPE>(md, tb, te, a, smem);
+    else matvec_body<kQ6K, AVX2, RW, FUSED, D, PIPE>(md, tb, te, a, smem);
 }
 
 // Q6_K upload: thread per output dword (52 body dwords + the scale per block).
@@ -683,7 +822,14 @@ __global__ __launch_bounds__(kThreads) void synth_blocks_kernel(uint16_t *__rest
 template <bool AVX2, int RW, bool FUSED>
 hipError_t launch_group_r(const GroupArgs &a, int grid, hipStream_t s) {
     const size_t lds = 2 * kThreads * sizeof(Rec) + xs_bytes(a.nblk);
-    hipLaunchKernelGGL((matvec_group_kernel<AVX2, RW, FUSED>), dim3(grid), dim3(kThreads), lds, s, a);
+    // KORE_QMV_PIPE=0: batches of two steps, each requested after the one
+    // before is computed (the measured default is one step requested ahead)
+    static const int pipe = [] {
+        const char *e = getenv("KORE_QMV_PIPE");
+        return e ? atoi(e) : 1;
+    }();
+    if (pipe == 0) hipLaunchKernelGGL((matvec_group_kernel<AVX2, RW, FUSED, 2, 0>), dim3(grid), dim3(kThreads), lds, s, a);
+    else hipLaunchKernelGGL((matvec_group_kernel<AVX2, RW, FUSED, 1, 1>), dim3(grid), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -751,6 +897,12 @@ hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool imag
     if (image && nb > kMaxBlocks) return hipErrorInvalidValue;
     if (pre.norm_w && pre.up) return hipErrorInvalidValue;
     if (pre.norm_w && n > INT32_MAX) return hipErrorInvalidValue;
+    if (pre.up) {
+        if (nb > INT32_MAX) return hipErrorInvalidValue;
+        if (image) hipLaunchKernelGGL(swiglu_quantize_kernel<true>, dim3((unsigned)nb), dim3(kThreads), 0, s, x, pre.up, xq, nb);
+        else hipLaunchKernelGGL(swiglu_quantize_kernel<false>, dim3((unsigned)nb), dim3(kThreads), 0, s, x, pre.up, xq, nb);
+        return hipGetLastError();
+    }
     const int64_t grid = (nb + kThreads / 16 - 1) / (kThreads / 16);
     if (image) hipLaunchKernelGGL(quantize_q8k_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb, pre);
     else hipLaunchKernelGGL(quantize_q8k_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, s, x, xq, nb, pre);
