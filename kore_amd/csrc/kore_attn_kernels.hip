@@ -202,9 +202,10 @@ __device__ __forceinline__ double sum4rows_d(double x) {
 // when the kv-head has a single split.
 template <int HD, int NR, bool MULTI>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
-                                                                float *vc_in, int n_rows, int rows_per_split,
-                                                                int new_slot, int slots, DecodeArgs a,
-                                                                RopeRow rr) {
+                                                                float *vc_in, const float *__restrict__ k_in,
+                                                                const float *__restrict__ v_in, int n_rows,
+                                                                int rows_per_split, int new_slot, int slots,
+                                                                DecodeArgs a, RopeRow rr) {
     constexpr int NT = HD / 16;    // K float4 per lane per block (MFMA k-steps / 4)
     constexpr int NJ = HD / 64;    // V float4 per lane per row
     constexpr int NMB = HD / 16;   // 16-dim output blocks
@@ -276,17 +277,16 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     // is conditional, and ahead of the K rows, so that their scores are taken
     // while the cache rows stream in
     const int ni = min(lane, HALF - 1);
-    const float nk0 = a.k[(size_t)g * HD + ni], nk1 = a.k[(size_t)g * HD + ni + HALF];
-    const float nv0 = a.v[(size_t)g * HD + ni], nv1 = a.v[(size_t)g * HD + ni + HALF];
+    const float nk0 = k_in[(size_t)g * HD + ni], nk1 = k_in[(size_t)g * HD + ni + HALF];
+    const float nv0 = v_in[(size_t)g * HD + ni], nv1 = v_in[(size_t)g * HD + ni + HALF];
     const float2 ncs = *reinterpret_cast<const float2 *>(&rr.cs[2 * ni]);
     const int xrow = min(r0 + (n_own - n_extra) + wave, last_row);
     const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
     const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
-    // the arguments the merge needs, read now: a first read after the block
-    // loop would wait for a kernel-argument fetch at the end of the kernel
+    // the arguments the merge needs (read from the kernel-argument segment,
+    // not preloaded)
     float *const out_p = a.out, *const part_o = a.part_o, *const part_ml = a.part_ml;
     const int n_split = a.n_split, n_rep = a.n_rep;
-    asm volatile("" ::"s"(out_p), "s"(part_o), "s"(part_ml), "s"(n_split), "s"(n_rep));
 
     float4 kA[NT], vA[4][NJ];
     float4 kB[MULTI ? NT : 1], vB[MULTI ? 4 : 1][NJ];
@@ -306,6 +306,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     __builtin_amdgcn_sched_barrier(0);
     load_k(kA, wave);
     __builtin_amdgcn_sched_barrier(0);
+    // the merge arguments are waited for here, behind the K rows' requests: a
+    // first read after the block loop would wait for a kernel-argument fetch
+    // at the end of the kernel
+    asm volatile("" ::"s"(out_p), "s"(part_o), "s"(part_ml), "s"(n_split), "s"(n_rep));
 
     // RoPE of the staged pairs into the wave's LDS rows, then the B operand:
     // lane l holds heads jq and jq + 4 (jq = l % 4) at dims CH kq + 4t + e
@@ -1216,9 +1220,11 @@ static __device__ __align__(256) float scratch[kStaticScratchFloats];
 
 template <int HD, int NR>
 hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t s) {
-    // The leading scalar arguments are preloaded into SGPRs at wave launch
-    // (gfx950 kernel-argument preload), so the first loads do not wait for
-    // a kernel-argument fetch (0.24 us measured).
+    // The leading scalar arguments (everything before the first aggregate:
+    // the pointers and sizes the first loads need, the new row's included)
+    // are preloaded into SGPRs at wave launch (gfx950 kernel-argument
+    // preload, at most 16 dwords), so no load is issued behind a
+    // kernel-argument fetch.
     // Splits of at most kWaves blocks plus kWaves extra rows give every wave
     // one block at most: that kernel has no prefetch registers or branches.
     // The grid never has more workgroups than CUs.  The single-block kernel
@@ -1226,7 +1232,7 @@ hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
     // dynamic LDS that a CU holds one: two on a CU would leave another idle.
     const dim3 grid(a.n_split, a.n_head_kv);
     if (a.rows_per_split > kWaves * kDecodeBlock + kWaves) {
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR, true>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc,
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, true>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     } else {
         static const unsigned dyn = [] {
@@ -1237,7 +1243,7 @@ hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
             const size_t half_cu = kLdsPerCu / 2 + 256;
             return fa.sharedSizeBytes < half_cu ? (unsigned)(half_cu - fa.sharedSizeBytes) : 0u;
         }();
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR, false>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc,
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, false>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     }
     static_assert(kMaxDecodeSplits <= 8 * 16, "the combine takes at most 16 splits per lane");
