@@ -273,7 +273,7 @@ static int launch_group(int n, kore_qmv_tensor *const *ts, const void *xq, const
         a.up = opts->up;
     }
     const int r = n == 1 ? ts[0]->rows_per_wave : pick_rows_per_wave(rows, ts[0]->num_cu);
-    hipError_t e = launch_matvec_group(avx2 != 0, a, r, max_workgroups(ts[0]->num_cu), s);
+    hipError_t e = launch_matvec_group(avx2 != 0, a, r, max_workgroups(ts[0]->num_cu), ts[0]->num_cu, s);
     if (e != hipSuccess) return hip_fail(ts[0], e, "matvec launch");
     return KORE_QMV_OK;
 }

@@ -73,8 +73,9 @@ struct PreOp {
 // dot_q*_K_q8_K_ref (kore.cpp:450-506).  Bit-identical to kore's results in
 // both orders, with or without the fused quantisation.  Tiles are 4 x
 // rows_per_wave rows; about max_wgs workgroups (0: one per tile) share them,
-// each a contiguous run.
-hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int max_wgs, hipStream_t s);
+// each a contiguous run.  num_cu (0 if unknown) selects the load pipelining:
+// a grid that does not fit on the device at once takes batches of two steps.
+hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int max_wgs, int num_cu, hipStream_t s);
 
 // kore's quantize_row_q8_K (kore.cpp:422-446): x[n] -> n/256 BlockQ8K records,
 // or (image) the same values in the matvec's own layout (n/256 * 308 bytes,

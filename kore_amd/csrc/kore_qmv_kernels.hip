@@ -819,28 +819,32 @@ __global__ __launch_bounds__(kThreads) void synth_blocks_kernel(uint16_t *__rest
     dst[g] = v;
 }
 
+// Load pipelining (measured on 7B shapes): one step requested ahead of the
+// step computed, except for grids of more workgroups than the device holds
+// at once (the 152064-row output head: 2376), where batches of two steps,
+// each requested after the one before is computed, leave more room for
+// other workgroups' loads.  KORE_QMV_PIPE=0 / 1 forces either form.
 template <bool AVX2, int RW, bool FUSED>
-hipError_t launch_group_r(const GroupArgs &a, int grid, hipStream_t s) {
+hipError_t launch_group_r(const GroupArgs &a, int grid, int num_cu, hipStream_t s) {
     const size_t lds = 2 * kThreads * sizeof(Rec) + xs_bytes(a.nblk);
-    // KORE_QMV_PIPE=0: batches of two steps, each requested after the one
-    // before is computed (the measured default is one step requested ahead)
-    static const int pipe = [] {
+    static const int forced = [] {
         const char *e = getenv("KORE_QMV_PIPE");
-        return e ? atoi(e) : 1;
+        return e ? atoi(e) : -1;
     }();
+    const int pipe = forced >= 0 ? forced : (num_cu > 0 && grid > 4 * num_cu ? 0 : 1);
     if (pipe == 0) hipLaunchKernelGGL((matvec_group_kernel<AVX2, RW, FUSED, 2, 0>), dim3(grid), dim3(kThreads), lds, s, a);
     else hipLaunchKernelGGL((matvec_group_kernel<AVX2, RW, FUSED, 1, 1>), dim3(grid), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
 
 template <bool AVX2, bool FUSED>
-hipError_t launch_group_f(const GroupArgs &a, int rw, int grid, hipStream_t s) {
+hipError_t launch_group_f(const GroupArgs &a, int rw, int grid, int num_cu, hipStream_t s) {
     switch (rw) {
-        case 1: return launch_group_r<AVX2, 1, FUSED>(a, grid, s);
-        case 2: return launch_group_r<AVX2, 2, FUSED>(a, grid, s);
-        case 4: return launch_group_r<AVX2, 4, FUSED>(a, grid, s);
-        case 8: return launch_group_r<AVX2, 8, FUSED>(a, grid, s);
-        default: return launch_group_r<AVX2, 16, FUSED>(a, grid, s);
+        case 1: return launch_group_r<AVX2, 1, FUSED>(a, grid, num_cu, s);
+        case 2: return launch_group_r<AVX2, 2, FUSED>(a, grid, num_cu, s);
+        case 4: return launch_group_r<AVX2, 4, FUSED>(a, grid, num_cu, s);
+        case 8: return launch_group_r<AVX2, 8, FUSED>(a, grid, num_cu, s);
+        default: return launch_group_r<AVX2, 16, FUSED>(a, grid, num_cu, s);
     }
 }
 
@@ -853,7 +857,7 @@ uint64_t splitmix64_host(uint64_t z) {
 
 }  // namespace
 
-hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int max_wgs, hipStream_t s) {
+hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int max_wgs, int num_cu, hipStream_t s) {
     if (a.n_mat < 1 || a.n_mat > kMaxGroup || a.nblk <= 0 || a.nblk > kMaxBlocks) return hipErrorInvalidValue;
     const int rw = rows_per_wave;
     if (rw != 1 && rw != 2 && rw != 4 && rw != 8 && rw != 16) return hipErrorInvalidValue;
@@ -887,8 +891,9 @@ hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int ma
     for (int k = a.n_mat; k < kMaxGroup; ++k) a.m[k] = a.m[a.n_mat - 1];
     if (wg > INT32_MAX) return hipErrorInvalidValue;
     const int grid = (int)wg;
-    if (avx2) return fused ? launch_group_f<true, true>(a, rw, grid, s) : launch_group_f<true, false>(a, rw, grid, s);
-    return fused ? launch_group_f<false, true>(a, rw, grid, s) : launch_group_f<false, false>(a, rw, grid, s);
+    if (avx2)
+        return fused ? launch_group_f<true, true>(a, rw, grid, num_cu, s) : launch_group_f<true, false>(a, rw, grid, num_cu, s);
+    return fused ? launch_group_f<false, true>(a, rw, grid, num_cu, s) : launch_group_f<false, false>(a, rw, grid, num_cu, s);
 }
 
 hipError_t launch_quantize_q8k(const float *x, int64_t n, uint8_t *xq, bool image, hipStream_t s, PreOp pre) {
