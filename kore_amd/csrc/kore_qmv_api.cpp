@@ -97,15 +97,19 @@ hipError_t host_path(int dev, size_t need, HostPath **out) {
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Rows per wave: as many as still give every SIMD of the device (four per
-// CU) two waves or more; with fewer rows each wave spreads a row's blocks
-// over more lanes.
-int pick_rows_per_wave(int64_t rows, int num_cu) {
+// Rows per wave: as many as still give the device about three waves per CU
+// (six for long rows, more than 16 blocks, whose waves each take several
+// load round trips); with fewer rows each wave spreads a row's blocks over
+// more lanes, and every step's chain advances then run on fewer lanes.
+// Measured on the 7B shapes (us per launch, rows per wave 1 / 2 / 4 / 8):
+// attn_output 8.2 / 7.0 / 6.4 / 7.2, q+k+v 14.7 / 11.1 / 10.4 / 12.3,
+// ffn_down (Q4_K) 18.4 / 17.0 / 19.7 / 29.1.
+int pick_rows_per_wave(int64_t rows, int nblk, int num_cu) {
     if (const char *env = getenv("KORE_QMV_ROWS_PER_WAVE")) {
         const int r = atoi(env);
         if (r == 1 || r == 2 || r == 4 || r == 8 || r == 16) return r;
     }
-    const int64_t want = 8LL * std::max(num_cu, 1);
+    const int64_t want = (nblk > 16 ? 6LL : 3LL) * std::max(num_cu, 1);
     for (int r = 16; r > 1; r /= 2)
         if (rows / r >= want) return r;
     return 1;
@@ -173,7 +177,7 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
     e = hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, t->device);
     if (e != hipSuccess) return bail(hip_fail(t, e, "hipDeviceGetAttribute"));
     t->num_cu = num_cu;
-    t->rows_per_wave = pick_rows_per_wave(rows, num_cu);
+    t->rows_per_wave = pick_rows_per_wave(rows, t->nblk, num_cu);
     if ((e = hipMalloc(&t->xq, (size_t)t->nblk * 308)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
     if (t->device < 0 || t->device >= 64) return bail(fail(t, KORE_QMV_E_UNSUPPORTED, "device ordinal above 63"));
     if ((e = gemm_scratch_reserve(t->device, num_cu)) != hipSuccess)
@@ -272,7 +276,7 @@ static int launch_group(int n, kore_qmv_tensor *const *ts, const void *xq, const
         a.norm_eps = opts->norm_eps;
         a.up = opts->up;
     }
-    const int r = n == 1 ? ts[0]->rows_per_wave : pick_rows_per_wave(rows, ts[0]->num_cu);
+    const int r = n == 1 ? ts[0]->rows_per_wave : pick_rows_per_wave(rows, ts[0]->nblk, ts[0]->num_cu);
     hipError_t e = launch_matvec_group(avx2 != 0, a, r, max_workgroups(ts[0]->num_cu), ts[0]->num_cu, s);
     if (e != hipSuccess) return hip_fail(ts[0], e, "matvec launch");
     return KORE_QMV_OK;
@@ -306,7 +310,7 @@ KORE_QMV_API int kore_qmv_mv_group_ex_dev(int n, const kore_qmv_tensor_t *ts, co
     }
     int64_t rows = 0;
     for (int k = 0; k < n; ++k) rows += ts[k]->rows;
-    const int r = n == 1 ? t0->rows_per_wave : pick_rows_per_wave(rows, t0->num_cu);
+    const int r = n == 1 ? t0->rows_per_wave : pick_rows_per_wave(rows, t0->nblk, t0->num_cu);
     int64_t wgs = 0;
     for (int k = 0; k < n; ++k) wgs += (ts[k]->rows + 4 * r - 1) / (4 * r);
     if (const int cap = max_workgroups(t0->num_cu)) wgs = std::min<int64_t>(wgs, cap);
