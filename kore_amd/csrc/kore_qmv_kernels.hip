@@ -126,6 +126,63 @@ __device__ float block_rms_scale_from(double hi, double lo, const float *x, int 
     return sc;
 }
 
+// The same scale from each thread's plain double sum ss of its squares (each
+// (double)x * x is exact): sums in registers and across the wave by DPP and
+// lane swaps, the four waves' sums through LDS in a fixed order, so every
+// thread holds the same S.  Any order's double sum of n nonnegative exact
+// terms lies within gamma(n-1) * S of the exact sum, this one and kore's
+// alike, so kore's sum lies within 2 gamma(n-1) / (1 - gamma(n-1)) of S_gpu;
+// the float scale is certified at both ends of twice that interval, and
+// otherwise one thread runs kore's loop.  red: kThreads / 64 doubles.
+__device__ __forceinline__ double dpp_d(double x, int which) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, x);
+    int lo = (int)(unsigned)u, hi = (int)(unsigned)(u >> 32);
+    switch (which) {
+        case 0: lo = dpp<0xB1>(lo); hi = dpp<0xB1>(hi); break;     // lane ^ 1
+        case 1: lo = dpp<0x4E>(lo); hi = dpp<0x4E>(hi); break;     // lane ^ 2
+        case 2: lo = dpp<0x124>(lo); hi = dpp<0x124>(hi); break;   // rotate the 16-lane row by 4
+        default: lo = dpp<0x128>(lo); hi = dpp<0x128>(hi); break;  // ... by 8
+    }
+    return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+__device__ float block_rms_scale_sum(double ss, const float *x, int n, float eps, double *red) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ss += dpp_d(ss, k);
+    // the four 16-lane rows: lane l and l ^ 16, then l and l ^ 32
+#pragma unroll
+    for (int p32 = 0; p32 < 2; ++p32) {
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, ss);
+        const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+        const auto rl = p32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                            : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto rh = p32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                            : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        const unsigned l0 = rl[0], l1 = rl[1], h0 = rh[0], h1 = rh[1];
+        ss = __builtin_bit_cast(double, ((unsigned long long)h0 << 32) | l0) +
+             __builtin_bit_cast(double, ((unsigned long long)h1 << 32) | l1);
+    }
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    double S = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) S += red[w];
+    const double g = (double)(n - 1) * 0x1p-53 / (1.0 - (double)(n - 1) * 0x1p-53);
+    const double m = 4.0 * g + 0x1p-50;
+    const float lo_s = kore_rms_scale(S * (1.0 - m), n, eps), hi_s = kore_rms_scale(S * (1.0 + m), n, eps);
+    __syncthreads();                       // red is reused below and by the caller
+    if (__float_as_uint(lo_s) == __float_as_uint(hi_s)) return lo_s;
+    if (t == 0) {                          // kore's own loop
+        double sk = 0.0;
+        for (int i = 0; i < n; ++i) sk += (double)x[i] * x[i];
+        red[0] = sk;
+    }
+    __syncthreads();
+    const float sc = kore_rms_scale(red[0], n, eps);
+    __syncthreads();
+    return sc;
+}
+
 __device__ float block_rms_scale(const float *x, int n, float eps, double *red) {
     // 8 loads at a time issued ahead of the dependent sum chain (clamped
     // indexes: no load waits on a branch); a slot past n adds 0.0, which leaves
@@ -579,21 +636,14 @@ __device__ __forceinline__ void matvec_body(const MatDesc &md, int tile_begin, i
         __builtin_amdgcn_sched_barrier(0);
         if (a.norm_w) {
             // kore's rmsnorm (kore.cpp:1367-1372): the certified scale of
-            // block_rms_scale_from from this thread's double-double partial
-            // sum (in two chains), then x * scale * w with kore's roundings;
-            // the records area is free until the blocks start
-            double hi0 = 0.0, lo0 = 0.0, hi1 = 0.0, lo1 = 0.0;
+            // block_rms_scale_sum from this thread's sum of squares (four
+            // chains), then x * scale * w with kore's roundings; the records
+            // area is free until the blocks start
+            double sq[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-            for (int e = 0; e < 16; e += 2) {
-                double s0, e0, s1, e1;
-                two_sum(hi0, on ? (double)v[e] * (double)v[e] : 0.0, s0, e0);
-                two_sum(hi1, on ? (double)v[e + 1] * (double)v[e + 1] : 0.0, s1, e1);
-                hi0 = s0; lo0 += e0;
-                hi1 = s1; lo1 += e1;
-            }
-            double hi, e01;
-            two_sum(hi0, hi1, hi, e01);
-            const float scale = block_rms_scale_from(hi, (lo0 + lo1) + e01, a.x, nblk * 256, a.norm_eps, (double *)smem);
+            for (int e = 0; e < 16; ++e) sq[e & 3] += on ? (double)v[e] * (double)v[e] : 0.0;
+            const float scale = block_rms_scale_sum((sq[0] + sq[1]) + (sq[2] + sq[3]), a.x, nblk * 256, a.norm_eps,
+                                                    (double *)smem);
 #pragma unroll
             for (int e = 0; e < 16; ++e) v[e] = (v[e] * scale) * w[e];
         } else if (a.up) {
