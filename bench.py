@@ -721,6 +721,30 @@ def cpu_token(seconds: float, threads: int):
                       f"host {_cpu_model()}"}
 
 
+def kore_token_dropin(seconds: float, threads: int):
+    """kore's own forward() with logits with the attention drop-in linked in
+    (oracle/_ref/kore_layer_gpu --time: kore.cpp with INTEGRATION.md's binding
+    applied, kore_attn_decode per layer through the host-pointer entry point,
+    kore's matvecs on the host threads) on the same synthetic 7B engine."""
+    import subprocess
+
+    import oracle
+    if not os.path.exists(oracle.REF_LAYER_GPU_BIN):
+        return None
+    r = subprocess.run([oracle.REF_LAYER_GPU_BIN, "--time", str(threads), str(seconds / CPU_RUNS), str(DEC_POS0),
+                        str(CPU_RUNS)], capture_output=True, text=True, check=True)
+    j = json.loads(r.stdout)
+    st = _runs([n / t for n, t in zip(j["run_tokens"], j["run_seconds"])], "tokens/s")
+    return {"value": round(st["median"], 3), "unit": "tokens/s", "threads": j["threads"], "best": round(st["best"], 3),
+            "runs": st["runs"],
+            "sample": f"kore's own forward() with logits, built from kore.cpp with the attention binding of "
+                      f"INTEGRATION.md applied (RoPE, KV cache and attention through kore_attn_decode, host "
+                      f"buffers in and out per layer) and linked to libkore_attn.so; matvecs on {j['threads']} host "
+                      f"threads (AVX2: {bool(j['avx2'])}); same synthetic Qwen2.5-7B-shape engine at positions "
+                      f"{j['pos']}..: {j['tokens']} tokens in {j['seconds']:.1f} s over {CPU_RUNS} timed runs "
+                      f"(value = median run)"}
+
+
 def gemm_report(g, chunks: int):
     mats, op_mats = g["mats"], g["op_mats"]
     flops = sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] for ts in op_mats for ti in ts)
@@ -1338,6 +1362,9 @@ def main(argv=None):
         if tk is not None:
             print(f"[bench] cpu baseline: kore's forward(), {args.cpu_threads} threads", file=sys.stderr, flush=True)
             res["token"]["cpu_baseline"] = cpu_token(args.cpu_seconds, args.cpu_threads)
+            print(f"[bench] kore's forward() with the attention drop-in, {args.cpu_threads} threads", file=sys.stderr,
+                  flush=True)
+            res["token"]["kore_with_attention_dropin"] = kore_token_dropin(args.cpu_seconds, args.cpu_threads)
         if pr is not None:
             print(f"[bench] cpu baseline: kore's forward_batch(), {args.cpu_threads} threads", file=sys.stderr,
                   flush=True)

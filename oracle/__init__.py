@@ -23,6 +23,8 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_BIN = os.path.join(HERE, "_ref", "kore_ref")
 REF_QMV_BIN = os.path.join(HERE, "_ref", "kore_qmv_ref")
 REF_LAYER_BIN = os.path.join(HERE, "_ref", "kore_layer_ref")
+# kore.cpp with the attention binding of INTEGRATION.md applied, linked to the GPU library
+REF_LAYER_GPU_BIN = os.path.join(HERE, "_ref", "kore_layer_gpu")
 
 # kore's BlockQ8K (kore.cpp:415-420): d, 256 int8 values, 16 int16 sums of 16
 Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
@@ -45,10 +47,14 @@ class _KV(C.Structure):
 
 def build() -> None:
     """Compile liboracle.so (gcc) and, when the kore sources are present,
-    oracle/_ref/kore_ref."""
+    kore's own harnesses under oracle/_ref/ (kore_ref, kore_qmv_ref,
+    kore_layer_ref) and kore with the attention binding linked to the GPU
+    library (kore_layer_gpu, once kore_amd/libkore_attn.so is built)."""
     subprocess.run(["make", "-s", "-C", HERE, "-B", "all"], check=True)
     if os.path.exists(os.path.join(os.environ.get("KORE_SRC", "/root/reference"), "kore.cpp")):
         subprocess.run(["make", "-s", "-C", HERE, "-B", "ref"], check=True)
+        if os.path.exists(os.path.join(os.path.dirname(HERE.rstrip("/")), "kore_amd", "libkore_attn.so")):
+            subprocess.run(["make", "-s", "-C", HERE, "-B", "ref-gpu"], check=True)
 
 
 _lib = None

@@ -31,6 +31,14 @@
 // JSON line {"ok", "ctx", "n_vocab", "avx2", "logits": [[...], ...]} (logits as
 // the hex of their float bits), or {"ok": false} when kore refuses the file.
 //
+// Built with -DKORE_GPU_ATTN against the kore.cpp that oracle/make_kore_gpu.py
+// writes (INTEGRATION.md's binding applied: RoPE, the KV cache and attention
+// through libkore_attn.so), as oracle/_ref/kore_layer_gpu: the same modes then
+// run kore's own forward() / forward_batch() with the attention on the GPU;
+// the engines built here by hand get their attention handle from attach_gpu
+// (engine_init does it for the GGUF modes), and the job mode reads the K/V
+// rows back from the handle.
+//
 // Timing mode (the CPU baseline of the benchmark's whole-token leg):
 //   kore_layer_ref --time THREADS MIN_SECONDS POS [RUNS]
 // builds a Qwen2.5-7B-shape engine (28 layers, 3584 / 18944, 28 / 4 heads of
@@ -100,6 +108,20 @@ void synth(OwnedTensor &o, uint32_t type, uint64_t cols, uint64_t rows, uint64_t
     o.t.data = o.bytes.data();
 }
 
+#ifdef KORE_GPU_ATTN
+// The attention handle engine_init creates in the patched kore, for the
+// engines built here without engine_init.
+bool attach_gpu(Engine &e) {
+    const Hparams &h = e.hp;
+    if (kore_attn_create(&e.attn.h, (int)h.n_layer, e.ctx, (int)h.n_head, (int)h.n_head_kv, e.head_dim, h.rope_base,
+                         0) != KORE_ATTN_OK) {
+        fprintf(stderr, "attention: %s\n", kore_attn_last_error(nullptr));
+        return false;
+    }
+    return true;
+}
+#endif
+
 // "[a, b, ...]" of per-run values for the timing modes' JSON lines
 std::string json_list(const std::vector<double> &v, const char *fmt) {
     std::string out = "[";
@@ -120,6 +142,9 @@ int time_mode(unsigned nth, double min_s, int pos0, bool batch, int runs) {
     e.head_dim = HD; e.kv_dim = kvd; e.n_rep = NH / NKV; e.ctx = ctx; e.n_vocab = VOCAB;
     e.nth = nth; e.use_float = false;
     e.avx2 = KORE_HAVE_AVX2 && cpu_has_avx2();
+#ifdef KORE_GPU_ATTN
+    if (!attach_gpu(e)) return 5;
+#endif
     std::vector<OwnedTensor> mats((size_t)NL * 7);
     std::vector<float> ones((size_t)E, 1.0f), zeros((size_t)E, 0.0f);
     for (int l = 0; l < NL; l++) {
@@ -304,6 +329,9 @@ int main(int argc, char **argv) {
     e.head_dim = hd; e.kv_dim = kvd; e.n_rep = nh / nkv; e.ctx = ctx; e.n_vocab = n_steps;
     e.nth = 4; e.use_float = false;
     e.avx2 = KORE_HAVE_AVX2 && cpu_has_avx2() && avx2;
+#ifdef KORE_GPU_ATTN
+    if (!attach_gpu(e)) return 5;
+#endif
 
     std::vector<std::vector<float>> vecs((size_t)n_layer * 5);
     std::vector<OwnedTensor> mats((size_t)n_layer * 7);
@@ -365,6 +393,12 @@ int main(int argc, char **argv) {
         if (!forward(e, st, pos[(size_t)st], false)) { fprintf(stderr, "forward failed at step %d\n", st); return 5; }
         if (!wr(out, e.x.data(), sizeof(float) * E)) return 6;
     }
+#ifdef KORE_GPU_ATTN
+    for (int l = 0; l < n_layer; l++)   // the cache lives on the GPU: kore's layout back
+        if (kore_attn_read_kv(e.attn.h, l, 0, ctx, e.kcache.data() + (size_t)l * ctx * kvd,
+                              e.vcache.data() + (size_t)l * ctx * kvd) != KORE_ATTN_OK)
+            return 6;
+#endif
     if (!wr(out, e.kcache.data(), sizeof(float) * e.kcache.size()) ||
         !wr(out, e.vcache.data(), sizeof(float) * e.vcache.size())) return 6;
     fclose(out);
