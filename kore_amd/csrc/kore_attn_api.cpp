@@ -293,6 +293,18 @@ int prefill_enqueue(kore_attn *h, int layer, int pos0, int n_tok, const float *q
                         h->pf_part_floats);
         pa.part_o = h->d_pf_part;
         pa.part_ml = h->d_pf_part + entries * h->head_dim;
+    } else {
+        prefill_split_plan(pa, h->num_cu);
+        if (pa.n_split > 0) {
+            // n_head_kv * n_split < num_cu items, 4 waves x 2 halves x 32 rows each
+            const size_t entries = (size_t)h->n_head_kv * pa.n_split * 8 * 32;
+            const size_t need = entries * ((size_t)h->head_dim + 2);
+            if (need > h->pf_part_floats)   // cannot happen: sized at create for 8 x num_cu x 32 rows
+                return fail(h, KORE_ATTN_E_UNSUPPORTED, "prefill partials need %zu floats, scratch holds %zu",
+                            need, h->pf_part_floats);
+            pa.part_o = h->d_pf_part;
+            pa.part_ml = h->d_pf_part + entries * h->head_dim;
+        }
     }
     HIP_TRY(h, launch_prefill(pa, h->head_dim, s));
     return KORE_ATTN_OK;
@@ -396,7 +408,9 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
     // Prefill key-segment partials, sized for the largest split any chunk
     // gets: segments are only used while a chunk has fewer workgroups than
     // CUs, which bounds (heads x strips x segments) by 8 x num_cu
-    // (prefill_key_segments), i.e. 8 x num_cu x 32 rows of (hd + 2) floats.
+    // (prefill_key_segments), i.e. 8 x num_cu x 32 rows of (hd + 2) floats;
+    // a split plan (prefill_split_plan) halves fewer than num_cu items of 4
+    // entries: under 8 x num_cu entries as well.
     if (h->fast_prefill) {
         h->pf_part_floats = (size_t)8 * h->num_cu * 32 * ((size_t)head_dim + 2);
         if ((e = hipMalloc(&h->d_pf_part, h->pf_part_floats * sizeof(float))) != hipSuccess)

@@ -65,6 +65,7 @@ struct AppendArgs {
 
 // Batched causal attention of n_tok query rows at positions pos0.. against
 // cache rows [0, pos0 + n_tok) (kore.cpp:1542-1563).  q is pre-RoPE.
+constexpr int kMaxPrefillUnits = 512;   // work units per kv-head of a split plan
 struct PrefillArgs {
     const float *q;       // [n_tok][n_head][hd]
     const float2 *cs;     // table base
@@ -88,6 +89,18 @@ struct PrefillArgs {
     // grid index is folded so that the second one runs the work list from
     // its short end (work index grid - 1 - (b - fold) for b >= fold).
     int fold;
+    // Split plan (n_kseg == 1, between one and two workgroups per CU): items
+    // 0 .. n_split - 1 of every kv-head (the longest) run as two workgroups
+    // over the first and second half of their key tiles and write partials
+    // [n_head_kv][n_split][4 waves][2 halves][32] (o, then max / sum), merged
+    // by the prefill combine kernel; the other items run whole.  unit[r] is
+    // the r-th longest of a kv-head's n_units work units, item << 2 | part
+    // (part 0 whole, 1 first half, 2 second half); work index w runs unit
+    // w / n_head_kv of kv-head w % n_head_kv, so the folded pairs of a CU
+    // add up to about the same number of tiles.
+    int n_split;
+    int n_units;
+    uint16_t unit[kMaxPrefillUnits];
 };
 
 // Any even head_dim up to kMaxGenericHeadDim and any n_rep (the geometries
@@ -160,6 +173,9 @@ hipError_t launch_append(const AppendArgs &a, int head_dim, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s);
 // Key segments the prefill uses for n_tok rows at pos0 (1 = none).
 int prefill_key_segments(int n_tok, int pos0, int n_head_kv, int n_rep, int num_cu, int *seg_tiles);
+// Fills a.n_split / a.n_units / a.unit for a chunk without key segments (its
+// other fields set); n_split stays 0 where the plan does not apply.
+void prefill_split_plan(PrefillArgs &a, int num_cu);
 hipError_t launch_synth(const SynthArgs &a, hipStream_t s);
 
 }  // namespace kore_attn_gpu

@@ -38,6 +38,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <vector>
 
 namespace kore_attn_gpu {
 namespace {
@@ -925,8 +926,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     const int bx = blockIdx.x;
     const int wi = bx < a.fold ? bx : (int)gridDim.x - 1 - (bx - a.fold);
     const int g = wi % nkv;
-    const int seg = (wi / nkv) % a.n_kseg;
-    const int item = wi / nkv / a.n_kseg;
+    // split plan: unit = item << 2 | part (0 whole, 1 / 2 first / second half)
+    const int unit = a.n_split > 0 ? (int)a.unit[wi / nkv] : 0;
+    const int part = unit & 3;
+    const int seg = a.n_split > 0 ? 0 : (wi / nkv) % a.n_kseg;
+    const int item = a.n_split > 0 ? unit >> 2 : wi / nkv / a.n_kseg;
     const int total = a.n_rep * a.n_strips;
     const int e = item * 4 + wave;
     const bool active = e < total;
@@ -1088,8 +1092,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
             }
     };
 
-    const int t_begin = seg * a.seg_tiles;
-    const int t_end = a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles);
+    // key tiles of this workgroup: a key segment, a half of a split item
+    // (the plan splits only items of at least two tiles), or all of them
+    const int t_half = n_tiles / 2;
+    const int t_begin = part == 2 ? t_half : seg * a.seg_tiles;
+    const int t_end = part == 1 ? t_half : (a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles));
     if (t_begin < t_end) issue_tile(sK0, sV0, t_begin);
     for (int t = t_begin; t < t_end; t += 2) {
         // this wave's loads of tile t have landed; after the barrier every
@@ -1117,9 +1124,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
                 *reinterpret_cast<float2 *>(dst + 2 * i) = make_float2(acc[0][r] * sc, acc[1][r] * sc);
         }
     };
-    if (a.n_kseg > 1) {
+    if (a.n_kseg > 1 || part != 0) {
         if (!active) return;
-        const size_t pe = ((size_t)g * total + ee) * a.n_kseg + seg;
+        const size_t pe = part != 0 ? (((size_t)g * a.n_split + item) * 4 + wave) * 2 + (part - 1)
+                                    : ((size_t)g * total + ee) * a.n_kseg + seg;
         store_row(a.part_o + (pe * 32 + qi) * HD, 1.f);
         if (qg == 0) {
             a.part_ml[(pe * 32 + qi) * 2 + 0] = m_run;
@@ -1131,21 +1139,34 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 // Block = one (kv-head, strip, q-head) entry of the prefill: the log-sum-exp
-// merge of its key segments for 32 query rows; thread (row r, chunk c) owns
-// 16 dims of one row.
+// merge of its key segments (or of the two halves of a split item) for 32
+// query rows; thread (row r, chunk c) owns HD / 8 dims of one row.
 template <int HD>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
     constexpr int CH = HD / 8;                          // dims per thread
-    const int entry = blockIdx.x;
     const int total = a.n_rep * a.n_strips;
-    const int g = entry / total, e = entry - g * total;
+    int g, e, S;
+    size_t base;
+    if (a.n_split > 0) {
+        // block = (kv-head, split item, wave) of the split plan
+        const int id = blockIdx.x, gi = id >> 2;
+        g = gi / a.n_split;
+        e = (gi - g * a.n_split) * 4 + (id & 3);
+        if (e >= total) return;
+        S = 2;
+        base = (size_t)id * 2;
+    } else {
+        const int entry = blockIdx.x;
+        g = entry / total;
+        e = entry - g * total;
+        S = a.n_kseg;
+        base = (size_t)entry * S;
+    }
     const int strip = a.n_strips - 1 - e / a.n_rep;
     const int h = g * a.n_rep + e % a.n_rep;
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
     const int qrow = 32 * strip + r;
     if (qrow >= a.n_tok) return;
-    const int S = a.n_kseg;
-    const size_t base = (size_t)entry * S;
     float m = -INFINITY;
     for (int s = 0; s < S; ++s) m = fmaxf(m, a.part_ml[((base + s) * 32 + r) * 2]);
     float den = 0.f;
@@ -1341,13 +1362,55 @@ int prefill_key_segments(int n_tok, int pos0, int n_head_kv, int n_rep, int num_
     return n_kseg;
 }
 
+void prefill_split_plan(PrefillArgs &a, int num_cu) {
+    // Two workgroups fit per CU and the grid is folded so that each CU's pair
+    // adds up to about the mean work; with between one and two workgroups per
+    // CU some CUs hold one item only, while the pairs' sums run up to about
+    // the longest item plus the shortest.  Splitting the longest items into
+    // two halves of their key tiles fills the grid to two per CU and lets the
+    // pairs (r-th longest unit with the r-th shortest) even out.
+    a.n_split = 0;
+    a.n_units = 0;
+    const int items = (a.n_rep * a.n_strips + 3) / 4;
+    const int n_wg = items * a.n_head_kv;
+    if (a.n_kseg != 1 || n_wg < num_cu || n_wg >= 2 * num_cu) return;
+    const int n_keys = a.pos0 + a.n_tok;
+    auto tiles = [&](int i) {   // key tiles of item i (its first entry's strip)
+        const int strip0 = a.n_strips - 1 - (4 * i) / a.n_rep;
+        return std::min(a.pos0 + 32 * strip0 + 31, n_keys - 1) / 32 + 1;
+    };
+    int split = std::min(items, (2 * num_cu - n_wg) / a.n_head_kv);
+    while (split > 0 && tiles(split - 1) < 4) --split;   // halves of at least two tiles
+    if (split == 0 || items + split > kMaxPrefillUnits) return;
+    struct Unit { int tiles, code; };
+    std::vector<Unit> u;
+    u.reserve(items + split);
+    for (int i = 0; i < items; ++i) {
+        const int t = tiles(i);
+        if (i < split) {
+            u.push_back({t / 2, i << 2 | 1});
+            u.push_back({t - t / 2, i << 2 | 2});
+        } else {
+            u.push_back({t, i << 2});
+        }
+    }
+    std::stable_sort(u.begin(), u.end(), [](const Unit &x, const Unit &y) { return x.tiles > y.tiles; });
+    for (size_t r = 0; r < u.size(); ++r) a.unit[r] = (uint16_t)u[r].code;
+    a.n_split = split;
+    a.n_units = (int)u.size();
+}
+
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, hipStream_t s) {
     const int items = (a.n_rep * a.n_strips + 3) / 4;
-    const dim3 grid(items * a.n_head_kv * a.n_kseg);
+    const dim3 grid(a.n_split > 0 ? a.n_units * a.n_head_kv : items * a.n_head_kv * a.n_kseg);
     if (head_dim == 128) hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, s, a);
     else if (head_dim == 64) hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kThreads), 0, s, a);
     else return hipErrorInvalidValue;
-    if (a.n_kseg > 1) {
+    if (a.n_split > 0) {
+        const dim3 cgrid(a.n_head_kv * a.n_split * 4);
+        if (head_dim == 128) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL(prefill_combine_kernel<64>, cgrid, dim3(256), 0, s, a);
+    } else if (a.n_kseg > 1) {
         const dim3 cgrid(a.n_head_kv * a.n_rep * a.n_strips);
         if (head_dim == 128) hipLaunchKernelGGL(prefill_combine_kernel<128>, cgrid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL(prefill_combine_kernel<64>, cgrid, dim3(256), 0, s, a);

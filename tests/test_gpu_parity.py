@@ -326,6 +326,11 @@ PREFILL_CASES = [
     # short chunks over a longer cache: the key range is split into segments
     (28, 4, 128, [(0, 700), (700, 45)]),
     (14, 2, 64, [(0, 900), (900, 40)]),
+    # between one and two workgroups per CU (256 CUs): the longest items run
+    # as two key halves merged afterwards; 33 items per kv-head with the last
+    # one half empty, and a chunk at an offset on head_dim 64
+    (40, 8, 128, [(0, 830)]),
+    (32, 8, 64, [(0, 300), (300, 1000)]),
 ]
 
 
