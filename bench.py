@@ -59,9 +59,9 @@ PF_N, PF_SEED = 2048, 3
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on these
 # kernels and workloads, each counter scaled by what it reads for a 256 MiB device copy
 # (fetch x 2.0, write x 1.0): decode layer = split + combine kernel, prefill layer =
-# append + prefill kernel.  Re-measure when a kernel changes.
+# append + prefill + prefill combine kernel.  Re-measure when a kernel changes.
 TRAFFIC_DECODE_BYTES = 19_115_000
-TRAFFIC_PREFILL_BYTES = 109_106_000
+TRAFFIC_PREFILL_BYTES = 138_660_000
 # the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
 # of weights, activations and outputs algorithmic)
 TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_478_000}
