@@ -30,6 +30,8 @@
 #include "kore_qmv_kernels.h"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 namespace kore_qmv_gpu {
@@ -329,6 +331,450 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {   // tw
     }
 }
 
+// ------------------------------------------------------------- fp16 path
+//
+// out[b][r] = sum over blocks of d_r * P[b][r] - dmin_r * M[b][r], with
+//   P = sum_c A_c x_c, A_c = sc_j q_c (Q4_K, an integer <= 945, exact in fp16)
+//   or sc_j (q_c - 32) (Q6_K, |A| <= 4096: an fp16 high part and an exact
+//   integer low part), and M = sum_j m_j Sx_j (Q4_K minimums times the
+//   activations' sub-block sums): kore's value d*sc*q - dmin*m regrouped, so
+//   the results agree with kore's to rounding (kore's tolerance), not bit for
+//   bit.  Each activation block is scaled by a power of two s (max |x s| <
+//   2^10) and split into fp16 hi + lo (|x s - hi - lo| <= 2^-22 |x s|); the
+//   products of an integer weight and an fp16 part are exact in the MFMA's
+//   fp32 accumulator, and 1 / s is applied with d.
+//
+// MFMA v_mfma_f32_32x32x16_f16 (lane layout checked on the GPU): A = the
+// activations (32 of them x 16 k), lane l holds activation l % 32 at k 8 (l /
+// 32) + e; B = the weights (16 k x 32 rows), lane l holds row l % 32 at the
+// same k; D lane l register r = activation 8 (r / 4) + 4 (l / 32) + r % 4 of
+// row l % 32.  Within a block, k-step s (16 columns) and half h take the
+// nibble dword q = 16 h + s of a Q4_K row (group g = q / 8, dword t = q % 8):
+// slots e < 4 are columns 64 g + 4 t + e (low nibbles), e >= 4 columns 64 g +
+// 32 + 4 t + e - 4 (high nibbles); the split activations are stored in that
+// order, as chunk c = 2 s + h of 8 fp16 per activation, chunk position c ^ (b
+// & 15) so that the 16-byte reads of 16 activations hit different banks.  The
+// same order gives a Q6_K lane contiguous bytes too (its half h of ql, qh and
+// the scales).
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// One workgroup per activation row b: the split of x[min(b, B - 1)] with one
+// power-of-two scale s for the whole row (max |x s| < 2^10), so that 1 / s is
+// applied once per tile instead of once per block; the blocks' 1 / s slots
+// all hold it.  Pass 1 finds the row's maximum, pass 2 (the row again, from
+// L2) splits four blocks at a time, wave w taking block 4 k + w.
+__global__ __launch_bounds__(256) void gemm16_prep_kernel(const float *__restrict__ x, uint8_t *__restrict__ x16,
+                                                          int B, int nblk) {
+    __shared__ float red[4];
+    const int b = blockIdx.x, t = threadIdx.x, i = t & 63, w = t >> 6;
+    const float4 *row = (const float4 *)(x + (int64_t)min(b, B - 1) * nblk * 256);
+    const int n4 = nblk * 64;
+    float amax = 0.f;
+    for (int k0 = t; k0 < n4; k0 += 8 * 256) {     // eight loads in flight
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = row[min(k0 + 256 * u, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if (i == 0) red[w] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e;
+    (void)frexpf(amax, &e);                 // amax < 2^e (0 for amax = 0)
+    e = max(e, -100);
+    const float s = ldexpf(1.f, 10 - e), inv = ldexpf(1.f, e - 10);
+    // columns 4i .. 4i + 3 of a block: group g = i / 16, dword t and nibble half from i % 16
+    const int iw = i & 15, low = iw < 8, tq = low ? iw : iw - 8;
+    const int q = 8 * (i >> 4) + tq, c = 2 * (q & 15) + (q >> 4);
+    const int off = b * 512 + ((c ^ (b & 15)) * 16) + (low ? 0 : 8);
+    for (int b0 = w; b0 < nblk; b0 += 4 * 8) {      // eight blocks' loads in flight
+        float4 vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) vv[u] = row[min(b0 + 4 * u, nblk - 1) * 64 + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int blk = b0 + 4 * u;
+        if (blk >= nblk) break;
+        const float4 v = vv[u];
+        const float y[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            hi[k] = (_Float16)y[k];
+            lo[k] = (_Float16)(y[k] - (float)hi[k]);
+        }
+        uint8_t *blkp = x16 + (int64_t)blk * kG16BlockBytes;
+        *(uint2 *)(blkp + off) = __builtin_bit_cast(uint2, (_Float16 __attribute__((ext_vector_type(4)))){hi[0], hi[1], hi[2], hi[3]});
+        *(uint2 *)(blkp + kG16Lo + off) = __builtin_bit_cast(uint2, (_Float16 __attribute__((ext_vector_type(4)))){lo[0], lo[1], lo[2], lo[3]});
+        // sub-block j = i / 8: the sum of its 32 scaled values, in a fixed order
+        float S = (y[0] + y[1]) + (y[2] + y[3]);
+        S += __shfl_xor(S, 1);
+        S += __shfl_xor(S, 2);
+        S += __shfl_xor(S, 4);
+        if ((i & 7) == 0) {
+            const _Float16 sh = (_Float16)S, sl = (_Float16)(S - (float)sh);
+            _Float16 *sx = (_Float16 *)(blkp + kG16Sx + b * 32);
+            sx[i >> 3] = sh;
+            sx[8 + (i >> 3)] = sl;
+        }
+        if (i == 0) *(float *)(blkp + kG16Inv + b * 4) = inv;
+    }
+    }
+}
+
+// One lane's weights of one block: Q4_K the header and nibble bytes 64 h ..
+// 64 h + 63; Q6_K ql bytes 64 h .., qh bytes 32 h .., the half's 8 scales, d.
+template <bool Q6>
+struct W16 {
+    uint4 v[Q6 ? 6 : 5];
+    uint2 sc;
+    uint32_t d;
+};
+
+template <bool Q6>
+__device__ __forceinline__ void load_w16(W16<Q6> &g, const GemmMat &m, int row, int blk, int nblk, int h) {
+    if (!Q6 || m.type == kQ4K) {
+        const uint8_t *b = m.w + ((int64_t)row * nblk + blk) * kQ4Bytes;
+        g.v[0] = *(const uint4 *)b;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) g.v[1 + k] = *(const uint4 *)(b + 16 + 64 * h + 16 * k);
+    } else if constexpr (Q6) {
+        const uint8_t *b = m.w + ((int64_t)row * nblk + blk) * kQ6Body;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) g.v[k] = *(const uint4 *)(b + 64 * h + 16 * k);
+        g.v[4] = *(const uint4 *)(b + 128 + 32 * h);
+        g.v[5] = *(const uint4 *)(b + 128 + 32 * h + 16);
+        g.sc = *(const uint2 *)(b + 192 + 8 * h);
+        g.d = m.wd[(int64_t)row * nblk + blk];
+    }
+}
+
+__device__ __forceinline__ uint32_t dword_of(const uint4 *v, int k) {   // dword k of v[0..]
+    const uint4 &u = v[k >> 2];
+    const int m = k & 3;
+    return m == 0 ? u.x : m == 1 ? u.y : m == 2 ? u.z : u.w;
+}
+
+// (1024 + byte i, 1024 + byte j) of u as fp16 (0x64 high bytes)
+__device__ __forceinline__ half2v magic2(uint32_t u, uint32_t sel) {
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, sel));
+}
+
+// The activations' A operand of k-step s for tile tt, hi and lo parts.
+__device__ __forceinline__ void read_a(const uint8_t *ls, int m, int c, half8 &ahi, half8 &alo) {
+    const int off = m * 512 + ((c ^ (m & 15)) * 16);
+    ahi = *(const half8 *)(ls + off);
+    alo = *(const half8 *)(ls + kG16Lo + off);
+}
+
+__device__ __forceinline__ floatx16 mfma16(half8 a, half8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// The A operands (hi, lo) of k-step s for the NT tiles of activations.
+template <int NT>
+__device__ __forceinline__ void read_step(const uint8_t *ls, int l, int s, half8 (*A)[2]) {
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) read_a(ls, 32 * tt + (l & 31), 2 * s + (l >> 5), A[tt][0], A[tt][1]);
+}
+
+// One Q4_K block: P[tt] = sum_k A x (hi and lo parts); the tiles' MFMA
+// chains alternate.
+template <int NT, bool Q6>
+__device__ __forceinline__ void block16_q4(const W16<Q6> &g, const uint8_t *ls, int l, floatx16 *P) {
+    const int h = l >> 5;
+    const uint4 &hdr = g.v[0];
+    // scales of sub-blocks 4h .. 4h + 3 as fp16 pairs (sc, sc) and (-1024 sc, -1024 sc)
+    half2v scp[4], scn[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const _Float16 sc = (_Float16)(float)q4s(hdr, 4 * h + k);
+        scp[k] = half2v{sc, sc};
+        scn[k] = half2v{(_Float16)(-1024.f) * sc, (_Float16)(-1024.f) * sc};
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) P[tt] = floatx16{};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        half8 A[NT][2];
+        read_step<NT>(ls, l, s, A);
+        const uint32_t D = dword_of(&g.v[1], s);
+        const uint32_t L = D & 0x0F0F0F0Fu, H = (D >> 4) & 0x0F0F0F0Fu;
+        const int a = s >> 3;                                   // sub-blocks 4h + 2a (low), + 1 (high)
+        half2v w0 = __builtin_elementwise_fma(magic2(L, 0x04010400u), scp[2 * a], scn[2 * a]);
+        half2v w1 = __builtin_elementwise_fma(magic2(L, 0x04030402u), scp[2 * a], scn[2 * a]);
+        half2v w2 = __builtin_elementwise_fma(magic2(H, 0x04010400u), scp[2 * a + 1], scn[2 * a + 1]);
+        half2v w3 = __builtin_elementwise_fma(magic2(H, 0x04030402u), scp[2 * a + 1], scn[2 * a + 1]);
+        const half8 bw = {w0[0], w0[1], w1[0], w1[1], w2[0], w2[1], w3[0], w3[1]};
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) P[tt] = mfma16(A[tt][pp], bw, P[tt]);
+    }
+}
+
+// Q4_K minimums of one block: M[tt] = sum_j m_j Sx_j, k 0..7 the hi parts of
+// Sx_0..7 times m_0..7, k 8..15 the lo parts times the same.
+template <int NT, bool Q6>
+__device__ __forceinline__ void block16_q4_mins(const W16<Q6> &g, const uint8_t *ls, int l, floatx16 *M) {
+    const uint4 &hdr = g.v[0];
+    half8 bm;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bm[j] = (_Float16)(float)q4m(hdr, j);
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        const half8 am = *(const half8 *)(ls + kG16Sx + (32 * tt + (l & 31)) * 32 + 16 * (l >> 5));
+        M[tt] = mfma16(am, bm, floatx16{});
+    }
+}
+
+// One Q6_K block: P[tt] = sum_k (A_hi + A_lo) (x_hi + x_lo) without the lo x lo term.
+template <int NT>
+__device__ __forceinline__ void block16_q6(const W16<true> &g, const uint8_t *ls, int l, floatx16 *P) {
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) P[tt] = floatx16{};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        half8 A[NT][2];
+        read_step<NT>(ls, l, s, A);
+        const int a = s >> 3, t = s & 7, sh = 4 * a;
+        const uint32_t D1 = dword_of(g.v, t), D2 = dword_of(g.v, 8 + t), Q = dword_of(&g.v[4], t);
+        const uint32_t q1 = ((D1 >> sh) & 0x0F0F0F0Fu) | (((Q >> sh) & 0x03030303u) << 4);
+        const uint32_t q2 = ((D2 >> sh) & 0x0F0F0F0Fu) | (((Q >> (sh + 2)) & 0x03030303u) << 4);
+        // scales of the four values of each half: bytes 4a + (t >= 4) and 4a + 2 + (t >= 4)
+        const int si1 = 4 * a + (t >> 2), si2 = si1 + 2;
+        const uint32_t scw1 = si1 < 4 ? g.sc.x : g.sc.y, scw2 = si2 < 4 ? g.sc.x : g.sc.y;
+        const _Float16 s1 = (_Float16)(float)(int)(int8_t)(scw1 >> (8 * (si1 & 3)));
+        const _Float16 s2 = (_Float16)(float)(int)(int8_t)(scw2 >> (8 * (si2 & 3)));
+        const half2v m1056 = {(_Float16)(-1056.f), (_Float16)(-1056.f)};
+        const half2v v0 = magic2(q1, 0x04010400u) + m1056, v1 = magic2(q1, 0x04030402u) + m1056;
+        const half2v v2 = magic2(q2, 0x04010400u) + m1056, v3 = magic2(q2, 0x04030402u) + m1056;
+        const half2v c1 = {s1, s1}, c2 = {s2, s2};
+        const half2v h0 = v0 * c1, h1 = v1 * c1, h2 = v2 * c2, h3 = v3 * c2;        // fp16(A)
+        const half2v l0 = __builtin_elementwise_fma(v0, c1, -h0), l1 = __builtin_elementwise_fma(v1, c1, -h1);
+        const half2v l2 = __builtin_elementwise_fma(v2, c2, -h2), l3 = __builtin_elementwise_fma(v3, c2, -h3);
+        const half8 bh = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+        const half8 bl = {l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) P[tt] = mfma16(A[tt][0], bh, P[tt]);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) P[tt] = mfma16(A[tt][1], bh, P[tt]);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) P[tt] = mfma16(A[tt][0], bl, P[tt]);
+    }
+}
+
+// D lane l register r of tile tt: activation 32 tt + 8 (r / 4) + 4 (l / 32) + r % 4, row l % 32
+template <int NT>
+__device__ __forceinline__ void store16(const GemmArgs &a, const GemmMat &mt, int tile, int wave, int l,
+                                        const floatx16 *acc) {
+    const int row = (tile - mt.tile0) * kG16Rows + 32 * wave + (l & 31);
+    if (row >= mt.rows) return;
+    const float bias = mt.bias ? mt.bias[row] : 0.f;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int b = 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+            if (b >= a.B) continue;
+            float *o = mt.out + (int64_t)b * mt.rows + row;
+            // kore's q += bq (kore.cpp:1530-1532) and x += o (kore.cpp:1567-1570, 1586-1589)
+            float f = acc[tt][r];
+            if (mt.bias) f = f + bias;
+            *o = mt.accumulate ? *o + f : f;
+        }
+}
+
+// One workgroup of 8 waves per CU (tiles of 256 rows: each activation block's
+// split is staged once for 256 rows), two LDS buffers: the next block's split
+// activations are copied in (global_load_lds, a linear copy) while the
+// current block's MFMAs run.  The two buffers are separate LDS objects and the
+// loop is unrolled by two, so the compiler sees that reading one does not
+// depend on the copy into the other.
+constexpr int kG16Threads = 512;
+
+template <int NT, bool Q6>
+__global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
+    __shared__ __align__(16) uint8_t ls0[kG16BlockBytes];
+    __shared__ __align__(16) uint8_t ls1[kG16BlockBytes];
+    const int t = threadIdx.x, l = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int h = l >> 5;
+    const int nblk = a.nblk, P = a.workers;
+    const int64_t T = (int64_t)a.tiles * nblk;
+    const int p = (P % 8 == 0) ? (int)(blockIdx.x % 8) * (P / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int64_t it0 = run_first(T, P, p), it1 = run_first(T, P, p + 1);
+    if (it0 >= it1) return;
+    auto row_of = [&](int tile, int m) {
+        return min((tile - a.m[m].tile0) * kG16Rows + 32 * wave + (l & 31), a.m[m].rows - 1);
+    };
+    // a block's split activations: 4240 chunks of 16 bytes, copied linearly:
+    // eight rounds of 64 chunks per wave, then the last 144 by waves 0..2
+    constexpr int kChunks = kG16BlockBytes / 16;
+    constexpr int kRounds = kChunks / (8 * 64);
+    static_assert(kG16BlockBytes % 16 == 0 && kChunks - 8 * 64 * kRounds <= 8 * 64, "whole chunks");
+    auto stage = [&](uint8_t *dst, int blk) {
+        const uint8_t *src = a.x16 + (int64_t)blk * kG16BlockBytes + 16 * l;
+#pragma unroll
+        for (int k = 0; k < kRounds; ++k) {
+            const int c0 = (k * 8 + wave) * 64;
+            __builtin_amdgcn_global_load_lds(src + 16 * c0, (void __attribute__((address_space(3))) *)(dst + 16 * c0), 16, 0, 0);
+        }
+        const int c0 = (kRounds * 8 + wave) * 64;
+        if (c0 < kChunks && c0 + l < kChunks)
+            __builtin_amdgcn_global_load_lds(src + 16 * c0, (void __attribute__((address_space(3))) *)(dst + 16 * c0), 16, 0, 0);
+    };
+    // acc += d P - dmin M per block, in the rows' scaled units; times 1 / s of
+    // each activation when the tile is stored or left as a partial
+    floatx16 acc[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) acc[tt] = floatx16{};
+    auto unscale = [&](const uint8_t *ls) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const float4 f = *(const float4 *)(ls + kG16Inv + 4 * (32 * tt + 8 * qd + 4 * h));
+                acc[tt][4 * qd + 0] *= f.x;
+                acc[tt][4 * qd + 1] *= f.y;
+                acc[tt][4 * qd + 2] *= f.z;
+                acc[tt][4 * qd + 3] *= f.w;
+            }
+    };
+    auto compute = [&](const uint8_t *ls, const W16<Q6> &gc, int cm) {
+        if (Q6 && a.m[cm].type == kQ6K) {
+            floatx16 Pb[NT];
+            if constexpr (Q6) block16_q6<NT>(gc, ls, l, Pb);
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)gc.d);
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[tt][r] = fmaf(d, Pb[tt][r], acc[tt][r]);
+        } else {
+            // d P first, then the minimums in the same registers
+            floatx16 Pb[NT];
+            block16_q4<NT, Q6>(gc, ls, l, Pb);
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(gc.v[0].x & 0xFFFFu));
+            const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(gc.v[0].x >> 16));
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[tt][r] = fmaf(d, Pb[tt][r], acc[tt][r]);
+            block16_q4_mins<NT, Q6>(gc, ls, l, Pb);
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[tt][r] = fmaf(-dmin, Pb[tt][r], acc[tt][r]);
+        }
+    };
+
+    int tile = (int)(it0 / nblk), blk = (int)(it0 % nblk), seg0 = blk;
+    int m = mat_of_tile(a, tile);
+    W16<Q6> g;
+    load_w16<Q6>(g, a.m[m], row_of(tile, m), blk, nblk, h);
+    stage(ls0, blk);
+    __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0)
+    __syncthreads();
+
+    // one iteration: block `blk` of `tile` from `cur`, the next block's split into `nxt`
+    auto step = [&](int64_t it, const uint8_t *cur, uint8_t *nxt) {
+        int ntile = tile, nb = blk + 1;
+        if (nb == nblk) { nb = 0; ++ntile; }
+        const W16<Q6> gc = g;
+        const int cm = m;
+        if (it + 1 < it1) {                            // the next block's activations and weights
+            stage(nxt, nb);
+            m = ntile == tile ? m : mat_of_tile(a, ntile);
+            load_w16<Q6>(g, a.m[m], row_of(ntile, m), nb, nblk, h);
+        }
+        compute(cur, gc, cm);
+        if (it + 1 == it1 || nb == 0) {                // end of this worker's part of the tile
+            unscale(cur);
+            if (seg0 != 0 || blk + 1 != nblk) {        // split tile: partial sums for the fix-up launch
+                const int slot = 2 * p + (it0 / nblk == tile ? 0 : 1);
+                float *mine = a.partials + (int64_t)slot * kG16SlotFloats;
+#pragma unroll
+                for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mine[((wave * 2 + tt) * 16 + r) * 64 + l] = acc[tt][r];
+            } else {
+                store16<NT>(a, a.m[cm], tile, wave, l, acc);
+            }
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) acc[tt] = floatx16{};
+            seg0 = 0;
+        }
+        tile = ntile;
+        blk = nb;
+        __builtin_amdgcn_s_waitcnt(0x0F70);            // vmcnt(0): the next block's copies have landed
+        __syncthreads();                               // ... for every wave, and `cur` is free
+    };
+    for (int64_t it = it0; it < it1; it += 2) {
+        step(it, ls0, ls1);
+        if (it + 1 >= it1) break;
+        step(it + 1, ls1, ls0);
+    }
+}
+
+// Fix-up of the fp16 path: blockIdx.x = tile, blockIdx.y = a slice of 1024 of
+// its kG16SlotFloats partial floats (slot float ((wave 2 + tt) 16 + r) 64 + l
+// is register r of tile tt of lane l of wave `wave`, 8 waves); thread t adds
+// float4 t of the slice over the tile's workers in worker order, eight
+// workers' loads in flight at a time, and stores four consecutive rows of one
+// activation.
+__global__ __launch_bounds__(kThreads) void gemm16_fixup_kernel(GemmArgs a) {
+    const int tile = blockIdx.x, nblk = a.nblk, P = a.workers;
+    const int64_t T = (int64_t)a.tiles * nblk, tfirst = (int64_t)tile * nblk;
+    const int pf = run_of(T, P, tfirst), pl = run_of(T, P, tfirst + nblk - 1);
+    if (pf == pl) return;                        // one worker ran the whole tile and stored it
+    const int f = blockIdx.y * 1024 + 4 * threadIdx.x;   // first of the thread's four floats
+    const int l = f & 63, r = (f >> 6) & 15, tt = (f >> 10) & 1, wave = f >> 11;
+    const int b = 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    if (b >= a.B) return;
+    constexpr int kBatch = 8;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q0 = pf; q0 <= pl; q0 += kBatch) {
+        float4 v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int q = min(q0 + u, pl);
+            const int slot = 2 * q + (run_first(T, P, q) / nblk == tile ? 0 : 1);
+            v[u] = *(const float4 *)(a.partials + (int64_t)slot * kG16SlotFloats + f);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (q0 + u <= pl) {
+                if (q0 + u == pf) acc = v[u];
+                else {
+                    acc.x += v[u].x;
+                    acc.y += v[u].y;
+                    acc.z += v[u].z;
+                    acc.w += v[u].w;
+                }
+            }
+    }
+    const GemmMat &mt = a.m[mat_of_tile(a, tile)];
+    const int row0 = (tile - mt.tile0) * kG16Rows + 32 * wave + (l & 31);
+    const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int row = row0 + k;
+        if (row >= mt.rows) break;
+        float *o = mt.out + (int64_t)b * mt.rows + row;
+        // kore's q += bq (kore.cpp:1530-1532) and x += o (kore.cpp:1567-1570, 1586-1589)
+        float v = vals[k];
+        if (mt.bias) v = v + mt.bias[row];
+        *o = mt.accumulate ? *o + v : v;
+    }
+}
+
 constexpr size_t lds_bytes(int nbk) { return (size_t)16 * nbk * kXStride * sizeof(float); }
 
 // Dynamic LDS above 64 KiB (64 activations: 66,560 bytes) needs the kernel's
@@ -387,29 +833,66 @@ hipError_t launch_t(const GemmArgs &a, hipStream_t s) {
 
 int gemm_max_workers(int num_cu) { return 4 * num_cu; }
 
+bool gemm_fp16() {
+    static const bool fp16 = [] {
+        const char *e = std::getenv("KORE_GEMM");
+        return !(e && std::strcmp(e, "fp32") == 0);
+    }();
+    return fp16;
+}
+
+int gemm_rows_per_tile() { return gemm_fp16() ? kG16Rows : kGemmRowsPerTile; }
+
 int gemm_workers(int tiles, int nblk, int B, bool has_q6k, int num_cu) {
-    int occ = 1;
-    if ((has_q6k ? prepare_t<true>(B, &occ) : prepare_t<false>(B, &occ)) != hipSuccess) occ = 1;
+    int occ = 1;                               // fp16 path: one workgroup per CU (LDS)
+    if (!gemm_fp16() && (has_q6k ? prepare_t<true>(B, &occ) : prepare_t<false>(B, &occ)) != hipSuccess) occ = 1;
     const int64_t T = (int64_t)tiles * nblk;
     int64_t p = std::min<int64_t>((int64_t)occ * num_cu, std::max<int64_t>(1, T / 2));
     if (p >= 8) p -= p % 8;
     return (int)p;
 }
 
+namespace {
+
+template <int NT, bool Q6>
+hipError_t launch16_nt(const GemmArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(gemm16_prep_kernel, dim3(32 * NT), dim3(256), 0, s, a.x, a.x16, a.B, a.nblk);
+    if (hipError_t e = hipGetLastError()) return e;
+    hipLaunchKernelGGL((gemm16_kernel<NT, Q6>), dim3(a.workers), dim3(kG16Threads), 0, s, a);
+    if (hipError_t e = hipGetLastError()) return e;
+    const int64_t T = (int64_t)a.tiles * a.nblk;
+    if (T % a.workers == 0 && (T / a.workers) % a.nblk == 0) return hipSuccess;
+    // 8 slices of 1024 partial floats (the slices of a second tile of
+    // activations return at once when NT = 1)
+    hipLaunchKernelGGL(gemm16_fixup_kernel, dim3(a.tiles, kG16SlotFloats / 1024), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+template <bool Q6>
+hipError_t launch16(const GemmArgs &a, hipStream_t s) {
+    return a.B > 32 ? launch16_nt<2, Q6>(a, s) : launch16_nt<1, Q6>(a, s);
+}
+
+}  // namespace
+
 hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
     if (a.n_mat < 1 || a.n_mat > kMaxGroup || a.nblk <= 0 || a.B <= 0 || a.B > kGemmMaxB) return hipErrorInvalidValue;
     if (a.workers < 1 || !a.partials) return hipErrorInvalidValue;
+    const bool fp16 = gemm_fp16();
+    if (fp16 && !a.x16) return hipErrorInvalidValue;
+    const int rpt = gemm_rows_per_tile();
     int tiles = 0;
     for (int k = 0; k < a.n_mat; ++k) {
         const GemmMat &m = a.m[k];
         if (m.rows <= 0 || !m.w || !m.out || (m.type != kQ4K && m.type != kQ6K) || (m.type == kQ6K && !m.wd))
             return hipErrorInvalidValue;
         a.m[k].tile0 = tiles;
-        tiles += (m.rows + kGemmRowsPerTile - 1) / kGemmRowsPerTile;
+        tiles += (m.rows + rpt - 1) / rpt;
     }
     if (tiles != a.tiles || (int64_t)tiles * a.nblk < a.workers) return hipErrorInvalidValue;
     bool q6 = false;
     for (int k = 0; k < a.n_mat; ++k) q6 |= a.m[k].type == kQ6K;
+    if (fp16) return q6 ? launch16<true>(a, s) : launch16<false>(a, s);
     return q6 ? launch_t<true>(a, s) : launch_t<false>(a, s);
 }
 

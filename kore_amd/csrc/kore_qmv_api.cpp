@@ -50,21 +50,42 @@ int hip_fail(kore_qmv_tensor *t, hipError_t e, const char *what) {
     } while (0)
 
 // Per-device workspace of the batched matmul: the partial sums of split tiles,
-// sized for the largest grid at the first tensor creation, never inside a call.
+// sized for the largest grid at the first tensor creation, and the fp16 split
+// of the activations, sized for the widest tensor created so far (grown at a
+// tensor creation, after the device has finished its work, never inside a
+// call).  Calls on one device share it: they must not overlap.
 struct GemmScratch {
     std::mutex mu;
     float *partials = nullptr;
+    uint8_t *x16 = nullptr;
+    int x16_nblk = 0;
 };
 GemmScratch g_gemm[64];
 
-int row_tiles(int64_t rows) { return (int)((rows + kGemmRowsPerTile - 1) / kGemmRowsPerTile); }
+int row_tiles(int64_t rows) { return (int)((rows + gemm_rows_per_tile() - 1) / gemm_rows_per_tile()); }
 
-hipError_t gemm_scratch_reserve(int dev, int num_cu) {
+hipError_t gemm_scratch_reserve(int dev, int num_cu, int nblk) {
     GemmScratch &g = g_gemm[dev];
     std::lock_guard<std::mutex> lock(g.mu);
-    if (g.partials) return hipSuccess;
-    const size_t bytes = (size_t)2 * gemm_max_workers(num_cu) * kGemmSlotFloats * sizeof(float);
-    return hipMalloc((void **)&g.partials, bytes);
+    hipError_t e = hipSuccess;
+    if (!g.partials) {
+        // 2 slots per worker: the fp32 path's 64-row slots at up to 4 workgroups
+        // per CU, the same bytes as the fp16 path's 256-row slots at 1 per CU
+        static_assert(4 * kGemmSlotFloats == kG16SlotFloats, "slot sizes");
+        const size_t bytes = (size_t)2 * gemm_max_workers(num_cu) * kGemmSlotFloats * sizeof(float);
+        if ((e = hipMalloc((void **)&g.partials, bytes)) != hipSuccess) return e;
+    }
+    if (nblk > g.x16_nblk) {
+        if (g.x16) {
+            if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+            (void)hipFree(g.x16);
+            g.x16 = nullptr;
+            g.x16_nblk = 0;
+        }
+        if ((e = hipMalloc((void **)&g.x16, (size_t)nblk * kG16BlockBytes)) != hipSuccess) return e;
+        g.x16_nblk = nblk;
+    }
+    return hipSuccess;
 }
 
 // Per-device staging buffers and stream of the synchronous host-pointer calls.
@@ -180,7 +201,7 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
     t->rows_per_wave = pick_rows_per_wave(rows, t->nblk, num_cu);
     if ((e = hipMalloc(&t->xq, (size_t)t->nblk * 308)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
     if (t->device < 0 || t->device >= 64) return bail(fail(t, KORE_QMV_E_UNSUPPORTED, "device ordinal above 63"));
-    if ((e = gemm_scratch_reserve(t->device, num_cu)) != hipSuccess)
+    if ((e = gemm_scratch_reserve(t->device, num_cu, t->nblk)) != hipSuccess)
         return bail(hip_fail(t, e, "matmul workspace"));
 
     const int64_t nblocks = rows * t->nblk;
@@ -404,6 +425,8 @@ KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor
     for (int k = 0; k < n; ++k) q6 |= t[k]->type == KORE_QMV_Q6_K;
     a.workers = gemm_workers(a.tiles, a.nblk, nb, q6, t0->num_cu);
     a.partials = g.partials;
+    a.x16 = g.x16;
+    if (g.x16_nblk < a.nblk) return fail(t0, KORE_QMV_E_INVALID, "matmul workspace narrower than the tensor");
     hipError_t e = launch_gemm(a, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(t0, e, "matmul launch");
     return KORE_QMV_OK;

@@ -130,7 +130,26 @@ struct GemmArgs {
     int tiles;               // all matrices' tiles
     int workers;             // grid size (gemm_workers)
     float *partials;         // 2 * workers * kGemmSlotFloats floats
+    uint8_t *x16;            // nblk * kG16BlockBytes: the fp16 split of x (fp16 path)
 };
+
+// fp16 path of the batched matmul (the default): the weights enter the MFMA
+// as small exact integers (Q4_K sc*q, Q6_K sc*(q-32) split in two fp16
+// parts), the activations as two fp16 parts per value with a power-of-two
+// scale per (activation, 256-column block); d, dmin and the Q4_K minimums
+// are applied per block in fp32.  Tiles of 256 rows; per block the split
+// activations take kG16BlockBytes: hi [64][32 chunks of 8 fp16], lo (same),
+// the sub-block sums (8 hi, 8 lo fp16 per activation) and 1 / scale.
+constexpr int kG16Rows = 256;
+constexpr int kG16Lo = 64 * 512;
+constexpr int kG16Sx = 2 * 64 * 512;
+constexpr int kG16Inv = kG16Sx + 64 * 32;
+constexpr int kG16BlockBytes = kG16Inv + 64 * 4;
+constexpr int kG16SlotFloats = kG16Rows * kGemmMaxB;   // one partial tile
+// Tiles of the fp16 path, or of the fp32 one (KORE_GEMM=fp32 in the
+// environment selects it, for comparisons).
+bool gemm_fp16();
+int gemm_rows_per_tile();
 // Workers of one launch: as many as fit on the CUs at once (by the LDS and
 // registers of the kernel that B activations and the weight types select), at
 // least two iterations each.
