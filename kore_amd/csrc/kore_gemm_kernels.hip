@@ -1,30 +1,35 @@
-// kore_gemm_kernels.hip - gfx950 kernel of kore's batched prefill matmul
+// kore_gemm_kernels.hip - gfx950 kernels of kore's batched prefill matmul
 // (matmul_batch_float, kore.cpp:783-845): out[b][r] = row r of the
 // dequantised Q4_K / Q6_K weights . x[b] for B <= 64 activations at once, for
-// up to four matrices that share x in one launch.
+// up to four matrices that share x in one launch.  Two paths:
 //
-// fp32 MFMA (v_mfma_f32_16x16x4f32) on weights dequantised in registers: a
-// wave owns 16 rows of a 64-row tile and up to 64 activations (NB blocks of
-// 16); lane l supplies row l % 16 and, of every 256-column block, the 64
-// columns of group l / 16 (the order of the K sum inside a block is permuted
-// so that each lane dequantises contiguous bytes; the sum is the same up to
-// fp32 rounding).  The activations of a block are staged in LDS, each of them
-// a 260-float row so the 16-byte reads of 16 consecutive activations hit
-// different banks.  The next block's activations and weights are loaded into
-// registers while the current block's MFMAs run.
+// fp16 (the default; described with its kernels below): the weights enter
+// v_mfma_f32_32x32x16_f16 as exact small integers and the activations as fp16
+// hi + lo parts, with kore's block scales applied per block in fp32.
 //
-// Work split: stream-K.  The iteration space (tile, block) of all matrices is
-// cut into `workers` contiguous runs of equal length, one per workgroup, so
-// every CU gets the same number of block iterations whatever the shapes.  A
-// tile split between workers leaves one partial sum per worker in a slot of
-// the workspace (slot 2p for worker p's first tile, 2p + 1 for its last), and
-// a second launch adds each split tile's slots in worker order.  (Finishing
-// split tiles inside the first launch would need device-scope fences, which
-// write back and invalidate the XCD's L2 each time and cost far more than the
-// second launch.)
+// fp32 (KORE_GEMM=fp32, kept for comparisons): v_mfma_f32_16x16x4f32 on
+// weights dequantised in registers: a wave owns 16 rows of a 64-row tile and
+// up to 64 activations (NB blocks of 16); lane l supplies row l % 16 and, of
+// every 256-column block, the 64 columns of group l / 16 (the order of the K
+// sum inside a block is permuted so that each lane dequantises contiguous
+// bytes; the sum is the same up to fp32 rounding).  The activations of a
+// block are staged in LDS, each of them a 260-float row so the 16-byte reads
+// of 16 consecutive activations hit different banks.  The next block's
+// activations and weights are loaded into registers while the current
+// block's MFMAs run.
 //
-// kore sums each output in one fused multiply-add chain over the columns; this
-// sums in MFMA blocks, so results agree with kore's to fp32 rounding (kore's
+// Work split (both paths): stream-K.  The iteration space (tile, block) of all
+// matrices is cut into `workers` contiguous runs of equal length, one per
+// workgroup, so every CU gets the same number of block iterations whatever
+// the shapes.  A tile split between workers leaves one partial sum per worker
+// in a slot of the workspace (slot 2p for worker p's first tile, 2p + 1 for
+// its last), and a second launch adds each split tile's slots in worker order.
+// (Finishing split tiles inside the first launch would need device-scope
+// fences, which write back and invalidate the XCD's L2 each time and cost far
+// more than the second launch.)
+//
+// kore sums each output in one fused multiply-add chain over the columns; both
+// paths sum in MFMA blocks, so results agree with kore's to rounding (kore's
 // own tolerance, max|d| <= 1e-4 max|ref| + 1e-6, kore_kernels.cpp:742), not
 // bit for bit.  For one device, shape and B the result is deterministic.
 #include "kore_qmv_kernels.h"

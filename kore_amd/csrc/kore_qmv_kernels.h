@@ -102,11 +102,12 @@ hipError_t launch_get_row(int type, const uint8_t *data, int64_t row, int64_t n,
 hipError_t launch_synth_blocks(int type, int64_t nblocks, uint64_t seed, uint8_t *dst, hipStream_t s);
 
 // Batched prefill matmul (kore's matmul_batch_float, kore.cpp:783-845):
-// out[b * rows + r] = dequantised row r . x[b], b < B <= kGemmMaxB; fp32 MFMA,
-// equal to kore's results to fp32 rounding.  One launch covers up to
-// kMaxGroup matrices that share x (same cols), each with its own output.
+// out[b * rows + r] = dequantised row r . x[b], b < B <= kGemmMaxB; fp16 MFMA
+// on exact integer weights and split activations (below), or fp32 MFMA;
+// equal to kore's results to rounding.  One launch covers up to kMaxGroup
+// matrices that share x (same cols), each with its own output.
 //
-// Work split (stream-K): the iteration space (64-row tile, 256-column block)
+// Work split (stream-K): the iteration space (row tile, 256-column block)
 // of all the matrices is cut into `workers` equal contiguous runs, one per
 // workgroup.  A tile whose blocks fall to several workers is finished by a
 // second launch that adds their partial sums in worker order.
