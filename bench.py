@@ -66,8 +66,13 @@ TRAFFIC_PREFILL_BYTES = 138_660_000
 # of weights, activations and outputs algorithmic)
 TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_478_000}
 # the same for the batched matmul leg's dominant launch, ffn_gate + ffn_up of one layer on 64
-# activations (87.17 MB algorithmic); the main kernel only (its fix-up launch adds 23.08 MB)
-TRAFFIC_GEMM_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 105_975_000}
+# activations (87.17 MB algorithmic), fp16 path: split pre-pass 3.98 MB, main kernel 124.4 MB
+# (the partials of split tiles included), fix-up 35.1 MB
+TRAFFIC_GEMM_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 163_500_000}
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix, published
+# MFMA passes per product of the fp16 batched matmul: Q4_K hi and lo parts of the
+# activations (the minimums' MFMA adds 1/32), Q6_K also the weights' integer remainder
+GEMM16_PASSES = {12: 2 + 1 / 32, 14: 3}
 
 # Qwen2.5-7B matrix shapes of the matvec leg
 QMV_FF, QMV_VOCAB = 18944, 152064
@@ -757,12 +762,21 @@ def gemm_report(g, chunks: int):
                                  "weight_bytes": sum(qmv_weight_bytes(*mats[ti][1:]) for ti in ts)})
         d["launches_per_chunk"] += 1
         d["ms"].extend(g["op_ms"][:, i].tolist())
+    # the fp16 path (default) is bound by the fp16 MFMA rate on its MFMA work (the algorithmic
+    # flops times the passes); the fp32 path (KORE_GEMM=fp32) by the fp32 MFMA rate
+    fp16 = os.environ.get("KORE_GEMM", "") != "fp32"
     table = {}
+    for i, ts in enumerate(op_mats):
+        key = "+".join(mats[ti][0].split(".")[-1] + ("_q6k" if mats[ti][1] == QMV_Q6K else "_q4k") for ti in ts)
+        per[key]["mfma_flop"] = sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] * (GEMM16_PASSES[mats[ti][1]] if fp16 else 1)
+                                    for ti in ts)
+    peak = FP16_MFMA_PEAK_TFLOPS if fp16 else FP32_MFMA_PEAK_TFLOPS
     for key, d in per.items():
         us = float(np.mean(d["ms"])) * 1e3
         tf = d["flop"] / (us / 1e6) / 1e12
+        mtf = d["mfma_flop"] / (us / 1e6) / 1e12
         table[key] = {"launches_per_chunk": d["launches_per_chunk"], "us_mean": round(us, 2), "flop": d["flop"],
-                      "tflops": round(tf, 2), "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                      "tflops": round(tf, 2), "mfma_tflops": round(mtf, 2), "frac": round(mtf / peak, 4),
                       "weight_gbs": round(d["weight_bytes"] / (us / 1e6) / 1e9, 1),
                       "us_per_chunk": round(us * d["launches_per_chunk"], 1)}
     dom = max(table, key=lambda k: table[k]["us_per_chunk"])
@@ -781,9 +795,10 @@ def gemm_report(g, chunks: int):
         "prefill_tokens_per_s_matmuls": round(GEMM_B / chunk_s, 1),
         "chunks": chunks,
         "per_matrix": table,
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": table[dom]["tflops"],
-                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": table[dom]["frac"],
-                     "traffic": TRAFFIC_GEMM_BYTES.get(dom)},
+        "path": "fp16 MFMA (exact integer weights, split activations)" if fp16 else "fp32 MFMA",
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": table[dom]["mfma_tflops"],
+                     "peak": peak, "unit": "TFLOP/s", "frac": table[dom]["frac"],
+                     "traffic": TRAFFIC_GEMM_BYTES.get(dom) if fp16 else None},
     }
 
 

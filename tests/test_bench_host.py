@@ -47,8 +47,12 @@ def test_gemm_report_fields():
     flop = sum(2 * bench.GEMM_B * mats[i][2] * mats[i][3] for i in range(7 * bench.NL))
     assert r["flop_per_chunk"] == flop
     assert abs(r["tflops"] - flop / 0.01 / 1e12) < 0.01
-    assert r["roofline"]["bound"] == "mfma" and r["roofline"]["peak"] == bench.FP32_MFMA_PEAK_TFLOPS
+    # the fp16 path (the default): fp16 MFMA peak, MFMA work = flops x passes
+    assert r["roofline"]["bound"] == "mfma" and r["roofline"]["peak"] == bench.FP16_MFMA_PEAK_TFLOPS
     assert r["roofline"]["kernel"] == "ffn_gate_q4k+ffn_up_q4k"
+    gu = r["per_matrix"]["ffn_gate_q4k+ffn_up_q4k"]
+    assert abs(gu["mfma_tflops"] - gu["tflops"] * bench.GEMM16_PASSES[bench.QMV_Q4K]) < 0.02
+    assert abs(r["roofline"]["frac"] - gu["mfma_tflops"] / bench.FP16_MFMA_PEAK_TFLOPS) < 1e-4
 
 
 def test_token_and_prompt_report_fields():
