@@ -342,6 +342,32 @@ def test_matmul_batch_vs_oracle(wtype, rows, nblk, B):
     _close_kore(out, oracle.matmul_batch(wtype, w, rows, nblk * 256, x, avx2=True), "vs oracle")
 
 
+@pytest.mark.parametrize("wtype,B", [(oracle.TYPE_Q4K, 40), (oracle.TYPE_Q6K, 20)])
+def test_matmul_batch_activation_ranges(wtype, B):
+    """Activations of very different magnitudes per row (10^-20 .. 10^20, an
+    all-zero row, a row whose values span 16 orders of magnitude): the
+    batched matmul scales each activation by its own power of two, so every
+    row is held to kore's tolerance against its own maximum."""
+    from kore_amd import qmv
+    rows, nblk = 300, 14
+    _say(f"qmm activation ranges type {wtype}, B {B}")
+    rng = np.random.default_rng(97 + B)
+    w = _weights(wtype, rows, nblk, rng)
+    x = np.stack([_x(nblk * 256, rng) for _ in range(B)])
+    x *= (10.0 ** rng.integers(-20, 21, size=B)).astype(np.float32)[:, None]
+    x[1] = 0.0
+    x[2, ::2] *= 1e-16
+    x = x.astype(np.float32)
+    with qmv.QMat(wtype, rows, nblk * 256, w) as m:
+        out = m.matmul_batch(x)
+    ref = oracle.matmul_batch(wtype, w, rows, nblk * 256, x, avx2=True)
+    assert np.all(out[1] == 0.0)
+    for b in range(B):
+        if b != 1:
+            _close_kore(out[b] / np.float64(np.max(np.abs(ref[b]))), ref[b] / np.float64(np.max(np.abs(ref[b]))),
+                        f"activation {b} (scale {np.max(np.abs(x[b])):.1e})")
+
+
 def test_matmul_batch_device_api_and_rejections():
     from kore_amd import hip, qmv
     _say("qmm device API, Q4_K 600 x 2048, B 40")
