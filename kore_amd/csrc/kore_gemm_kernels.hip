@@ -378,10 +378,17 @@ __global__ __launch_bounds__(256) void gemm16_prep_kernel(const float *__restric
     const float4 *row = (const float4 *)(x + (int64_t)min(b, B - 1) * nblk * 256);
     const int n4 = nblk * 64;
     float amax = 0.f;
-    for (int k0 = t; k0 < n4; k0 += 8 * 256) {     // eight loads in flight
+    // eight loads in flight; float4 t + 256 u is lane i of block 4 u + w, so the
+    // first eight (blocks w, w + 4, ..) are kept for the second pass
+    float4 keep[8];
+    for (int k0 = t; k0 < n4; k0 += 8 * 256) {
         float4 v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) v[u] = row[min(k0 + 256 * u, n4 - 1)];
+        if (k0 == t) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) keep[u] = v[u];
+        }
 #pragma unroll
         for (int u = 0; u < 8; ++u)
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
@@ -402,7 +409,7 @@ __global__ __launch_bounds__(256) void gemm16_prep_kernel(const float *__restric
     for (int b0 = w; b0 < nblk; b0 += 4 * 8) {      // eight blocks' loads in flight
         float4 vv[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) vv[u] = row[min(b0 + 4 * u, nblk - 1) * 64 + i];
+        for (int u = 0; u < 8; ++u) vv[u] = b0 == w ? keep[u] : row[min(b0 + 4 * u, nblk - 1) * 64 + i];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int blk = b0 + 4 * u;
