@@ -169,6 +169,27 @@ KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor
 KORE_QMV_API int kore_qmv_rmsnorm_rows_dev(const float *x, const float *w, int64_t n, int rows, float eps, float *out,
                                            void *stream);
 
+/* The batched matmul's fp16 activation split, for callers that produce the
+ * activations with kore_qmv_rmsnorm_rows_split_dev (forward_batch()'s
+ * attn_norm -> q/k/v and ffn_norm -> gate/up, kore.cpp:1521-1526, 1572-1576):
+ * one pre-pass launch less per matmul.  kore_qmv_split_bytes(cols) is the
+ * size of the split of up to 64 activations of cols values, or 0 when the
+ * split is not available (cols not a multiple of 256 up to 4096, or the fp32
+ * matmul path selected by KORE_GEMM=fp32); then use the plain calls. */
+KORE_QMV_API size_t kore_qmv_split_bytes(int64_t cols);
+
+/* kore_qmv_rmsnorm_rows_dev that also writes the normalised rows' split into
+ * x16 (device, kore_qmv_split_bytes(n) bytes); rows <= 64; x, w, out and x16
+ * 16-byte aligned. */
+KORE_QMV_API int kore_qmv_rmsnorm_rows_split_dev(const float *x, const float *w, int64_t n, int rows, float eps,
+                                                 float *out, void *x16, void *stream);
+
+/* kore_qmv_matmul_batch_group_ex_dev on the split x16 of nb activations
+ * (written by kore_qmv_rmsnorm_rows_split_dev, kept unchanged since) instead
+ * of x: the same results, bit for bit. */
+KORE_QMV_API int kore_qmv_matmul_batch_group_split_dev(int n, const kore_qmv_tensor_t *t, const void *x16, int nb,
+                                                       const kore_qmv_mv_opts *opts, float *const *out, void *stream);
+
 /* kore's batched SwiGLU in place (kore.cpp:1577-1583): g[i] = g[i] / (1 +
  * exp(-g[i])) * u[i] over n floats, exp rounded from double as in
  * kore_qmv_mv_group_ex_dev.  Device buffers, enqueued on `stream`. */

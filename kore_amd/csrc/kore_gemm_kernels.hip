@@ -868,8 +868,10 @@ namespace {
 
 template <int NT, bool Q6>
 hipError_t launch16_nt(const GemmArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(gemm16_prep_kernel, dim3(32 * NT), dim3(256), 0, s, a.x, a.x16, a.B, a.nblk);
-    if (hipError_t e = hipGetLastError()) return e;
+    if (!a.presplit) {
+        hipLaunchKernelGGL(gemm16_prep_kernel, dim3(32 * NT), dim3(256), 0, s, a.x, a.x16, a.B, a.nblk);
+        if (hipError_t e = hipGetLastError()) return e;
+    }
     hipLaunchKernelGGL((gemm16_kernel<NT, Q6>), dim3(a.workers), dim3(kG16Threads), 0, s, a);
     if (hipError_t e = hipGetLastError()) return e;
     const int64_t T = (int64_t)a.tiles * a.nblk;
@@ -892,6 +894,7 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
     if (a.workers < 1 || !a.partials) return hipErrorInvalidValue;
     const bool fp16 = gemm_fp16();
     if (fp16 && !a.x16) return hipErrorInvalidValue;
+    if (a.presplit && !fp16) return hipErrorInvalidValue;
     const int rpt = gemm_rows_per_tile();
     int tiles = 0;
     for (int k = 0; k < a.n_mat; ++k) {

@@ -17,6 +17,9 @@ struct kore_layer {
     // forward_batch() rows (kore's e.bxb, bq, bk, bv, batt, bgate, bup), kMaxBatch each
     float *bxb = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *batt = nullptr, *bgate = nullptr,
           *bup = nullptr;
+    // the normalised rows' fp16 split for the batched matmuls (nullptr when
+    // the split is not available: then the matmuls split bxb themselves)
+    void *bx16 = nullptr;
     std::string error;
 };
 
@@ -34,6 +37,7 @@ void release(kore_layer *L) {
     for (float *p : {L->q, L->k, L->v, L->att, L->gate, L->up, L->bxb, L->bq, L->bk, L->bv, L->batt, L->bgate,
                      L->bup})
         if (p) (void)hipFree(p);
+    if (L->bx16) (void)hipFree(L->bx16);
     if (L->stream) (void)hipStreamDestroy(L->stream);
     delete L;
 }
@@ -73,6 +77,7 @@ KORE_LAYER_API int kore_layer_create(kore_layer_t *out, int n_embd, int n_ff, in
     float **bufs[13] = {&L->q,   &L->k,  &L->v,  &L->att,  &L->gate,  &L->up, &L->bxb,
                         &L->bq,  &L->bk, &L->bv, &L->batt, &L->bgate, &L->bup};
     for (int i = 0; i < 13 && e == hipSuccess; ++i) e = hipMalloc((void **)bufs[i], sizes[i] * sizeof(float));
+    if (const size_t sb = kore_qmv_split_bytes(L->E); sb && e == hipSuccess) e = hipMalloc(&L->bx16, sb);
     if (e != hipSuccess) {
         g_error = std::string("kore_layer_create: ") + hipGetErrorString(e);
         release(L);
@@ -157,17 +162,32 @@ KORE_LAYER_API int kore_layer_prefill_dev(kore_layer_t L, const kore_layer_weigh
     auto qmv_err = [&](kore_qmv_tensor_t t, const char *what) {
         return fail(L, KORE_LAYER_E_STEP, std::string(what) + ": " + kore_qmv_last_error(t));
     };
+    // rmsnorm of every row, then a batched matmul on the normalised rows: with
+    // the split available the rmsnorm writes it and the matmul skips its own
+    // split pre-pass (the same results, bit for bit)
+    auto norm_matmul = [&](const float *norm_w, int nm, const kore_qmv_tensor_t *mats, const kore_qmv_mv_opts *o,
+                           float *const *outs, const char *what) -> int {
+        if (L->bx16) {
+            if (kore_qmv_rmsnorm_rows_split_dev(x, norm_w, E, n_tok, L->eps, L->bxb, L->bx16, s) != KORE_QMV_OK)
+                return qmv_err(nullptr, what);
+            if (kore_qmv_matmul_batch_group_split_dev(nm, mats, L->bx16, n_tok, o, outs, s) != KORE_QMV_OK)
+                return qmv_err(mats[0], what);
+            return KORE_LAYER_OK;
+        }
+        if (kore_qmv_rmsnorm_rows_dev(x, norm_w, E, n_tok, L->eps, L->bxb, s) != KORE_QMV_OK)
+            return qmv_err(nullptr, what);
+        if (kore_qmv_matmul_batch_group_ex_dev(nm, mats, L->bxb, n_tok, o, outs, s) != KORE_QMV_OK)
+            return qmv_err(mats[0], what);
+        return KORE_LAYER_OK;
+    };
     // 1. rmsnorm of every row, then q/k/v + biases (kore.cpp:1521-1532)
-    if (kore_qmv_rmsnorm_rows_dev(x, w->attn_norm, E, n_tok, L->eps, L->bxb, s) != KORE_QMV_OK)
-        return qmv_err(nullptr, "attn_norm");
     kore_qmv_mv_opts o1{};
     o1.bias[0] = w->bq;
     o1.bias[1] = w->bk;
     o1.bias[2] = w->bv;
     kore_qmv_tensor_t qkv[3] = {w->wq, w->wk, w->wv};
     float *qkv_out[3] = {L->bq, L->bk, L->bv};
-    if (kore_qmv_matmul_batch_group_ex_dev(3, qkv, L->bxb, n_tok, &o1, qkv_out, s) != KORE_QMV_OK)
-        return qmv_err(w->wq, "q/k/v");
+    if (int rc = norm_matmul(w->attn_norm, 3, qkv, &o1, qkv_out, "attn_norm, q/k/v")) return rc;
     // 2. RoPE + append + causal attention of the rows (kore.cpp:1533-1563)
     if (kore_attn_prefill_dev(attn, layer, pos0, n_tok, L->n_head, L->n_head_kv, L->head_dim, L->bq, L->bk, L->bv,
                               L->batt, s) != KORE_ATTN_OK)
@@ -178,12 +198,9 @@ KORE_LAYER_API int kore_layer_prefill_dev(kore_layer_t L, const kore_layer_weigh
     if (kore_qmv_matmul_batch_group_ex_dev(1, &w->wo, L->batt, n_tok, &acc, &x, s) != KORE_QMV_OK)
         return qmv_err(w->wo, "wo");
     // 4. rmsnorm, gate/up, SwiGLU (kore.cpp:1572-1583)
-    if (kore_qmv_rmsnorm_rows_dev(x, w->ffn_norm, E, n_tok, L->eps, L->bxb, s) != KORE_QMV_OK)
-        return qmv_err(nullptr, "ffn_norm");
     kore_qmv_tensor_t gu[2] = {w->w_gate, w->w_up};
     float *gu_out[2] = {L->bgate, L->bup};
-    if (kore_qmv_matmul_batch_group_ex_dev(2, gu, L->bxb, n_tok, nullptr, gu_out, s) != KORE_QMV_OK)
-        return qmv_err(w->w_gate, "gate/up");
+    if (int rc = norm_matmul(w->ffn_norm, 2, gu, nullptr, gu_out, "ffn_norm, gate/up")) return rc;
     if (kore_qmv_swiglu_dev(L->bgate, L->bup, (int64_t)n_tok * FF, s) != KORE_QMV_OK) return qmv_err(nullptr, "swiglu");
     // 5. down, x += o (kore.cpp:1585-1589)
     if (kore_qmv_matmul_batch_group_ex_dev(1, &w->w_down, L->bgate, n_tok, &acc, &x, s) != KORE_QMV_OK)

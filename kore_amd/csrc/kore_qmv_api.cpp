@@ -393,8 +393,12 @@ KORE_QMV_API int kore_qmv_mv(kore_qmv_tensor_t t, const float *x, float *out, in
     return rc;
 }
 
-KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
-                                                    const kore_qmv_mv_opts *opts, float *const *out, void *stream) {
+namespace {
+
+// The batched matmul of kore_qmv_matmul_batch_group_ex_dev, on x or (x16 set)
+// on activations already split by kore_qmv_rmsnorm_rows_split_dev.
+int matmul_group(int n, const kore_qmv_tensor_t *t, const float *x, const void *x16, int nb,
+                 const kore_qmv_mv_opts *opts, float *const *out, void *stream) {
     if (n < 1 || n > kMaxGroup || !t || !out) return fail(nullptr, KORE_QMV_E_INVALID, "n must be 1..4, t and out set");
     for (int k = 0; k < n; ++k)
         if (!t[k]) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
@@ -405,7 +409,12 @@ KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor
     for (int k = 0; opts && k < n; ++k)
         if (opts->bias[k])
             if (int rc = check_dev_ptr(t0, opts->bias[k], 4, "bias")) return rc;
-    if (int rc = check_dev_ptr(t0, x, 16, "x")) return rc;
+    if (x16) {
+        if (!gemm_fp16()) return fail(t0, KORE_QMV_E_UNSUPPORTED, "split activations need the fp16 matmul path");
+        if (int rc = check_dev_ptr(t0, x16, 16, "x16")) return rc;
+    } else if (int rc = check_dev_ptr(t0, x, 16, "x")) {
+        return rc;
+    }
     GemmArgs a{};
     a.n_mat = n;
     a.x = x;
@@ -425,11 +434,43 @@ KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor
     for (int k = 0; k < n; ++k) q6 |= t[k]->type == KORE_QMV_Q6_K;
     a.workers = gemm_workers(a.tiles, a.nblk, nb, q6, t0->num_cu);
     a.partials = g.partials;
-    a.x16 = g.x16;
-    if (g.x16_nblk < a.nblk) return fail(t0, KORE_QMV_E_INVALID, "matmul workspace narrower than the tensor");
+    a.x16 = x16 ? (uint8_t *)x16 : g.x16;
+    a.presplit = x16 ? 1 : 0;
+    if (!x16 && g.x16_nblk < a.nblk) return fail(t0, KORE_QMV_E_INVALID, "matmul workspace narrower than the tensor");
     hipError_t e = launch_gemm(a, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(t0, e, "matmul launch");
     return KORE_QMV_OK;
+}
+
+}  // namespace
+
+KORE_QMV_API int kore_qmv_matmul_batch_group_ex_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,
+                                                    const kore_qmv_mv_opts *opts, float *const *out, void *stream) {
+    return matmul_group(n, t, x, nullptr, nb, opts, out, stream);
+}
+
+KORE_QMV_API int kore_qmv_matmul_batch_group_split_dev(int n, const kore_qmv_tensor_t *t, const void *x16, int nb,
+                                                       const kore_qmv_mv_opts *opts, float *const *out, void *stream) {
+    if (!x16) return fail(nullptr, KORE_QMV_E_INVALID, "x16 is NULL");
+    return matmul_group(n, t, nullptr, x16, nb, opts, out, stream);
+}
+
+KORE_QMV_API size_t kore_qmv_split_bytes(int64_t cols) {
+    if (!gemm_fp16() || cols < 256 || cols % 256 || cols > 16 * 256) return 0;
+    return (size_t)(cols / 256) * kG16BlockBytes;
+}
+
+KORE_QMV_API int kore_qmv_rmsnorm_rows_split_dev(const float *x, const float *w, int64_t n, int rows, float eps,
+                                                 float *out, void *x16, void *stream) {
+    if (!x || !w || !out || !x16 || n < 1 || rows < 1)
+        return fail(nullptr, KORE_QMV_E_INVALID, "x, w, out, x16 set, n >= 1 and rows >= 1 required");
+    if (kore_qmv_split_bytes(n) == 0 || rows > kGemmMaxB)
+        return fail(nullptr, KORE_QMV_E_UNSUPPORTED,
+                    "split rows need the fp16 matmul path, n a multiple of 256 up to 4096 and rows <= 64");
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)x16) & 15)
+        return fail(nullptr, KORE_QMV_E_INVALID, "x, w, out and x16 must be 16-byte aligned");
+    const hipError_t e = launch_rmsnorm_rows(x, w, (int)n, rows, eps, out, (hipStream_t)stream, (uint8_t *)x16);
+    return e == hipSuccess ? KORE_QMV_OK : hip_fail(nullptr, e, "rmsnorm launch");
 }
 
 KORE_QMV_API int kore_qmv_matmul_batch_group_dev(int n, const kore_qmv_tensor_t *t, const float *x, int nb,

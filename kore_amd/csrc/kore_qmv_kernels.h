@@ -90,7 +90,11 @@ hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, 
 // kore's rmsnorm (kore.cpp:1367-1372) of each of n_rows rows of n values
 // (out may be x), bit-identical to kore's sequential double sum; and kore's
 // SwiGLU in place over n values (kore.cpp:1577-1581, exp rounded from double).
-hipError_t launch_rmsnorm_rows(const float *x, const float *w, int n, int n_rows, float eps, float *out, hipStream_t s);
+// With x16 (n a multiple of 256 up to 4096, n_rows <= 64) the normalised rows
+// are also written as the fp16 batched matmul's split activations (the layout
+// and values its own pre-pass would produce, bit for bit).
+hipError_t launch_rmsnorm_rows(const float *x, const float *w, int n, int n_rows, float eps, float *out, hipStream_t s,
+                               uint8_t *x16 = nullptr);
 hipError_t launch_swiglu(float *g, const float *u, int64_t n, hipStream_t s);
 
 // kore's get_row (kore.cpp:384-407): row `row` of a table of rows of n values
@@ -132,6 +136,7 @@ struct GemmArgs {
     int workers;             // grid size (gemm_workers)
     float *partials;         // 2 * workers * kGemmSlotFloats floats
     uint8_t *x16;            // nblk * kG16BlockBytes: the fp16 split of x (fp16 path)
+    int presplit;            // x16 already holds the split (x unused): no pre-pass
 };
 
 // fp16 path of the batched matmul (the default): the weights enter the MFMA

@@ -989,14 +989,105 @@ hipError_t launch_q6k_split(const uint8_t *raw, int64_t nblocks, uint8_t *body, 
 namespace kore_qmv_gpu {
 namespace {
 
+// kore's rmsnorm of one row of n values (n a multiple of 256 up to 4096, every
+// pointer 16-byte aligned) that also writes the row as the fp16 batched
+// matmul's split activations: gemm16_prep_kernel's layout and arithmetic, so
+// the bytes are the pre-pass's own.  Thread t takes float4 groups t + 256 j
+// (lane t % 64 of block 4 j + t / 64), which is the pre-pass's column order:
+// one power-of-two scale s for the row (max |y s| < 2^10), the hi and lo
+// fp16 parts of four columns in one 8-byte store each, the sub-block sums
+// (four columns, then lanes ^1, ^2, ^4) and 1 / s per block.
+__device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, int n, float eps, float *orow,
+                                  uint8_t *__restrict__ x16, double *red) {
+    const int t = threadIdx.x, lane = t & 63, b = blockIdx.x, n4 = n / 4;
+    const float4 *x4 = (const float4 *)xr, *w4 = (const float4 *)w;
+    float4 v[4], wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = min(t + j * kThreads, n4 - 1);
+        v[j] = x4[f];
+        wv[j] = w4[f];
+    }
+    double hi = 0.0, lo = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool in = t + j * kThreads < n4;
+        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float xv = in ? e[k] : 0.0f;
+            double s, er;
+            two_sum(hi, (double)xv * (double)xv, s, er);
+            hi = s;
+            lo += er;
+        }
+    }
+    const float scale = block_rms_scale_from(hi, lo, xr, n, eps, red);
+    float4 y[4];
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        y[j] = make_float4((v[j].x * scale) * wv[j].x, (v[j].y * scale) * wv[j].y, (v[j].z * scale) * wv[j].z,
+                           (v[j].w * scale) * wv[j].w);
+        if (t + j * kThreads < n4) {
+            ((float4 *)orow)[t + j * kThreads] = y[j];
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y[j].x), fabsf(y[j].y)), fmaxf(fabsf(y[j].z), fabsf(y[j].w))));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    float *fred = (float *)red;                        // free again past block_rms_scale_from's last barrier
+    if (lane == 0) fred[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    int e;
+    (void)frexpf(amax, &e);                            // amax < 2^e (0 for amax = 0)
+    e = max(e, -100);
+    const float s = ldexpf(1.f, 10 - e), inv = ldexpf(1.f, e - 10);
+    // columns 4 lane .. + 3 of a block: group lane / 16, dword and nibble half from lane % 16
+    const int iw = lane & 15, low = iw < 8, tq = low ? iw : iw - 8;
+    const int q = 8 * (lane >> 4) + tq, c = 2 * (q & 15) + (q >> 4);
+    const int off = b * 512 + ((c ^ (b & 15)) * 16) + (low ? 0 : 8);
+    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (t + j * kThreads >= n4) break;             // whole waves: n4 is a multiple of 64
+        const float ys[4] = {y[j].x * s, y[j].y * s, y[j].z * s, y[j].w * s};
+        half4v h, l;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            h[k] = (_Float16)ys[k];
+            l[k] = (_Float16)(ys[k] - (float)h[k]);
+        }
+        uint8_t *blkp = x16 + (int64_t)((t + j * kThreads) >> 6) * kG16BlockBytes;
+        *(uint2 *)(blkp + off) = __builtin_bit_cast(uint2, h);
+        *(uint2 *)(blkp + kG16Lo + off) = __builtin_bit_cast(uint2, l);
+        float S = (ys[0] + ys[1]) + (ys[2] + ys[3]);
+        S += __shfl_xor(S, 1);
+        S += __shfl_xor(S, 2);
+        S += __shfl_xor(S, 4);
+        if ((lane & 7) == 0) {
+            const _Float16 sh = (_Float16)S, sl = (_Float16)(S - (float)sh);
+            _Float16 *sx = (_Float16 *)(blkp + kG16Sx + b * 32);
+            sx[lane >> 3] = sh;
+            sx[8 + (lane >> 3)] = sl;
+        }
+        if (lane == 0) *(float *)(blkp + kG16Inv + b * 4) = inv;
+    }
+}
+
 // kore's rmsnorm of row blockIdx.x (kore.cpp:1367-1372, 1522, 1573): the
 // certified scale of block_rms_scale, then x * scale * w with kore's roundings.
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, const float *__restrict__ w, int n,
-                                                                float eps, float *out) {
+                                                                float eps, float *out, uint8_t *__restrict__ x16) {
     __shared__ double red[2 * kThreads / 64];
     const float *xr = x + (int64_t)blockIdx.x * n;
     float *orow = out + (int64_t)blockIdx.x * n;
     constexpr int kPer = 16;
+    if (x16) {
+        rmsnorm_split_row(xr, w, n, eps, orow, x16, red);
+        return;
+    }
     if (n > kPer * kThreads) {
         const float scale = block_rms_scale(xr, n, eps, red);
         for (int i = threadIdx.x; i < n; i += kThreads) orow[i] = (xr[i] * scale) * w[i];
@@ -1036,9 +1127,13 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(float *__restrict__ g,
 
 }  // namespace
 
-hipError_t launch_rmsnorm_rows(const float *x, const float *w, int n, int n_rows, float eps, float *out, hipStream_t s) {
+hipError_t launch_rmsnorm_rows(const float *x, const float *w, int n, int n_rows, float eps, float *out, hipStream_t s,
+                               uint8_t *x16) {
     if (n <= 0 || n_rows <= 0 || !x || !w || !out) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n_rows), dim3(kThreads), 0, s, x, w, n, eps, out);
+    if (x16 && (n % 256 || n > 16 * kThreads || n_rows > kGemmMaxB ||
+                (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)x16) & 15)))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n_rows), dim3(kThreads), 0, s, x, w, n, eps, out, x16);
     return hipGetLastError();
 }
 

@@ -57,6 +57,9 @@ SYMBOLS = [
     ("kore_qmv_get_row_dev", _i, [_i, _vp, _i64, _i64, _vp, _vp]),
     ("kore_qmv_matmul_batch_group_ex_dev", _i, [_i, _vp, _vp, _i, _vp, _vp, _vp]),
     ("kore_qmv_rmsnorm_rows_dev", _i, [_vp, _vp, _i64, _i, C.c_float, _vp, _vp]),
+    ("kore_qmv_split_bytes", C.c_size_t, [_i64]),
+    ("kore_qmv_rmsnorm_rows_split_dev", _i, [_vp, _vp, _i64, _i, C.c_float, _vp, _vp, _vp]),
+    ("kore_qmv_matmul_batch_group_split_dev", _i, [_i, _vp, _vp, _i, _vp, _vp, _vp]),
     ("kore_qmv_swiglu_dev", _i, [_vp, _vp, _i64, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
@@ -248,6 +251,33 @@ def matmul_batch_group_ex_dev(mats, x_ptr: int, nb: int, out_ptrs, bias=None, ac
 def rmsnorm_rows_dev(x_ptr: int, w_ptr: int, n: int, rows: int, eps: float, out_ptr: int, stream=None) -> None:
     """kore's rmsnorm of `rows` rows of n floats (device pointers)."""
     _check(lib().kore_qmv_rmsnorm_rows_dev(x_ptr, w_ptr, n, rows, eps, out_ptr, stream))
+
+
+def split_bytes(cols: int) -> int:
+    """kore_qmv_split_bytes: bytes of the fp16 activation split of up to 64
+    rows of cols values (0: not available, use the plain calls)."""
+    return int(lib().kore_qmv_split_bytes(cols))
+
+
+def rmsnorm_rows_split_dev(x_ptr: int, w_ptr: int, n: int, rows: int, eps: float, out_ptr: int, x16_ptr: int,
+                           stream=None) -> None:
+    """kore_qmv_rmsnorm_rows_split_dev: rmsnorm_rows_dev, also writing the
+    rows' fp16 split into x16 (device, split_bytes(n) bytes)."""
+    _check(lib().kore_qmv_rmsnorm_rows_split_dev(x_ptr, w_ptr, n, rows, eps, out_ptr, x16_ptr, stream))
+
+
+def matmul_batch_group_split_dev(mats, x16_ptr: int, nb: int, out_ptrs, bias=None, accumulate: bool = False,
+                                 stream=None) -> None:
+    """kore_qmv_matmul_batch_group_split_dev: matmul_batch_group_ex_dev on the
+    split written by rmsnorm_rows_split_dev."""
+    n = len(mats)
+    o = MvOpts()
+    o.accumulate = int(accumulate)
+    for k, b in enumerate(bias or ()):
+        o.bias[k] = b
+    hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
+    outs = (C.c_void_p * n)(*out_ptrs)
+    _check(lib().kore_qmv_matmul_batch_group_split_dev(n, hs, x16_ptr, nb, C.byref(o), outs, stream))
 
 
 def swiglu_dev(g_ptr: int, u_ptr: int, n: int, stream=None) -> None:

@@ -76,6 +76,48 @@ def test_swiglu_rows():
     du.free()
 
 
+@pytest.mark.parametrize("B,E", [(1, 3584), (33, 3584), (64, 3584), (7, 512), (64, 4096)])
+def test_rmsnorm_split_then_matmul_is_bitwise_the_plain_pair(B, E):
+    """kore_qmv_rmsnorm_rows_split_dev + kore_qmv_matmul_batch_group_split_dev
+    (the rmsnorm writes the matmul's fp16 split, no pre-pass) against
+    kore_qmv_rmsnorm_rows_dev + kore_qmv_matmul_batch_group_ex_dev: the
+    normalised rows and every output bit for bit, biases included."""
+    from kore_amd import hip, qmv
+    KVD = 512
+    if qmv.split_bytes(E) == 0:
+        pytest.skip("the split needs the fp16 matmul path")
+    _say(f"rmsnorm split + matmul, B {B}, width {E}")
+    rng = np.random.default_rng(41 + B)
+    mats = [_synth(t, r, E, 900 + k)[0] for k, (t, r) in
+            enumerate([(oracle.TYPE_Q4K, E), (oracle.TYPE_Q4K, KVD), (oracle.TYPE_Q6K, KVD)])]
+    x = np.stack([_x(E, rng) for _ in range(B)])
+    x[0] *= 1e-3
+    nw = (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32)
+    biases = [(0.5 * rng.standard_normal(m.rows)).astype(np.float32) for m in mats]
+    dx, dw = _up(x), _up(nw)
+    xn_a, xn_b = _up(np.zeros((B, E))), _up(np.zeros((B, E)))
+    x16 = hip.DeviceBuffer(qmv.split_bytes(E) // 4)
+    out_a = [_up(np.zeros((B, m.rows))) for m in mats]
+    out_b = [_up(np.zeros((B, m.rows))) for m in mats]
+    db = [_up(b) for b in biases]
+    try:
+        qmv.rmsnorm_rows_dev(dx.ptr, dw.ptr, E, B, 1e-6, xn_a.ptr)
+        qmv.matmul_batch_group_ex_dev(mats, xn_a.ptr, B, [o.ptr for o in out_a], bias=[b.ptr for b in db])
+        qmv.rmsnorm_rows_split_dev(dx.ptr, dw.ptr, E, B, 1e-6, xn_b.ptr, x16.ptr)
+        qmv.matmul_batch_group_split_dev(mats, x16.ptr, B, [o.ptr for o in out_b], bias=[b.ptr for b in db])
+        hip.synchronize()
+        assert np.array_equal(_bits(xn_a.download()), _bits(xn_b.download())), "normalised rows"
+        for k in range(3):
+            assert np.array_equal(_bits(out_a[k].download()), _bits(out_b[k].download())), f"matrix {k}"
+        with pytest.raises(qmv.QmvError):       # widths above 4096 have no split
+            qmv.rmsnorm_rows_split_dev(dx.ptr, dw.ptr, 4352, 1, 1e-6, xn_b.ptr, x16.ptr)
+    finally:
+        for b in [dx, dw, xn_a, xn_b, x16] + out_a + out_b + db:
+            b.free()
+        for m in mats:
+            m.close()
+
+
 @pytest.mark.parametrize("B", [1, 13, 64])
 def test_matmul_epilogues(B):
     """bias and accumulate: the stores of the same launch without them, then
