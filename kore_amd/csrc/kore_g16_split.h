@@ -1,0 +1,59 @@
+// kore_g16_split.h - writing the fp16 batched matmul's split activations
+// (device code shared by gemm16_prep_kernel and the rmsnorm that writes the
+// split itself).  Internal to libkore_qmv.so.
+//
+// Per 256-column block the split of up to 64 activations takes kG16BlockBytes:
+// hi [64][32 chunks of 8 fp16] (chunk c of activation b at position c ^ (b &
+// 15), so that 16 activations' 16-byte reads hit different banks), lo (same
+// layout), the eight sub-block sums (hi, lo fp16) and 1 / s per activation.
+// Column 4 i .. 4 i + 3 of a block (float4 group i) is in chunk c = 2 (q & 15)
+// + (q >> 4), q = 8 (i / 16) + i % 8, its first (i % 16 < 8) or second half:
+// the MFMA's k order over the Q4_K nibble dwords.
+#pragma once
+
+#include "kore_qmv_kernels.h"
+
+namespace kore_qmv_gpu {
+
+// The row's power of two s (max |y s| < 2^10 for amax = max |y|) and 1 / s.
+__device__ __forceinline__ void g16_split_scale(float amax, float &s, float &inv) {
+    int e;
+    (void)frexpf(amax, &e);                            // amax < 2^e (0 for amax = 0)
+    e = max(e, -100);
+    s = ldexpf(1.f, 10 - e);
+    inv = ldexpf(1.f, e - 10);
+}
+
+// Float4 group `lane` of block `blk` of activation b: ys = its four values
+// times s.  The hi and lo fp16 parts in one 8-byte store each, the sub-block
+// sum (the four values, then lanes ^1, ^2, ^4: 32 columns) and 1 / s.  Every
+// lane of the wave takes part (lane sums); lane = the wave's lane index.
+__device__ __forceinline__ void g16_split_group(uint8_t *__restrict__ x16, int b, int blk, int lane,
+                                                const float ys[4], float inv) {
+    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+    const int iw = lane & 15, low = iw < 8, tq = low ? iw : iw - 8;
+    const int q = 8 * (lane >> 4) + tq, c = 2 * (q & 15) + (q >> 4);
+    const int off = b * 512 + ((c ^ (b & 15)) * 16) + (low ? 0 : 8);
+    half4v h, l;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        h[k] = (_Float16)ys[k];
+        l[k] = (_Float16)(ys[k] - (float)h[k]);
+    }
+    uint8_t *blkp = x16 + (int64_t)blk * kG16BlockBytes;
+    *(uint2 *)(blkp + off) = __builtin_bit_cast(uint2, h);
+    *(uint2 *)(blkp + kG16Lo + off) = __builtin_bit_cast(uint2, l);
+    float S = (ys[0] + ys[1]) + (ys[2] + ys[3]);
+    S += __shfl_xor(S, 1);
+    S += __shfl_xor(S, 2);
+    S += __shfl_xor(S, 4);
+    if ((lane & 7) == 0) {
+        const _Float16 sh = (_Float16)S, sl = (_Float16)(S - (float)sh);
+        _Float16 *sx = (_Float16 *)(blkp + kG16Sx + b * 32);
+        sx[lane >> 3] = sh;
+        sx[8 + (lane >> 3)] = sl;
+    }
+    if (lane == 0) *(float *)(blkp + kG16Inv + b * 4) = inv;
+}
+
+}  // namespace kore_qmv_gpu

@@ -33,6 +33,7 @@
 // own tolerance, max|d| <= 1e-4 max|ref| + 1e-6, kore_kernels.cpp:742), not
 // bit for bit.  For one device, shape and B the result is deterministic.
 #include "kore_qmv_kernels.h"
+#include "kore_g16_split.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -366,78 +367,41 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-// One workgroup per activation row b: the split of x[min(b, B - 1)] with one
-// power-of-two scale s for the whole row (max |x s| < 2^10), so that 1 / s is
-// applied once per tile instead of once per block; the blocks' 1 / s slots
-// all hold it.  Pass 1 finds the row's maximum, pass 2 (the row again, from
-// L2) splits four blocks at a time, wave w taking block 4 k + w.
-__global__ __launch_bounds__(256) void gemm16_prep_kernel(const float *__restrict__ x, uint8_t *__restrict__ x16,
-                                                          int B, int nblk) {
-    __shared__ float red[4];
-    const int b = blockIdx.x, t = threadIdx.x, i = t & 63, w = t >> 6;
+// One workgroup of 1024 threads per activation row b: the split of x[min(b,
+// B - 1)] with one power-of-two scale s for the whole row (max |x s| < 2^10),
+// so that 1 / s is applied once per tile instead of once per block; the
+// blocks' 1 / s slots all hold it.  The row (up to 32768 values) is read once
+// into registers: thread t holds float4 groups t + 1024 j, lane t % 64 of block
+// 16 j + t / 64, for the row maximum and then the split (g16_split_group).
+constexpr int kPrepThreads = 1024, kPrepPer = 8;
+static_assert(kPrepThreads * kPrepPer * 4 >= 32768, "rows of up to 32768 values (kore's 128 blocks)");
+__global__ __launch_bounds__(kPrepThreads) void gemm16_prep_kernel(const float *__restrict__ x,
+                                                                    uint8_t *__restrict__ x16, int B, int nblk) {
+    __shared__ float red[kPrepThreads / 64];
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const float4 *row = (const float4 *)(x + (int64_t)min(b, B - 1) * nblk * 256);
     const int n4 = nblk * 64;
+    float4 v[kPrepPer];
+#pragma unroll
+    for (int j = 0; j < kPrepPer; ++j) v[j] = row[min(t + j * kPrepThreads, n4 - 1)];
     float amax = 0.f;
-    // eight loads in flight; float4 t + 256 u is lane i of block 4 u + w, so the
-    // first eight (blocks w, w + 4, ..) are kept for the second pass
-    float4 keep[8];
-    for (int k0 = t; k0 < n4; k0 += 8 * 256) {
-        float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = row[min(k0 + 256 * u, n4 - 1)];
-        if (k0 == t) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) keep[u] = v[u];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
-    }
+    for (int j = 0; j < kPrepPer; ++j)
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    if (i == 0) red[w] = amax;
+    if (lane == 0) red[t >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int e;
-    (void)frexpf(amax, &e);                 // amax < 2^e (0 for amax = 0)
-    e = max(e, -100);
-    const float s = ldexpf(1.f, 10 - e), inv = ldexpf(1.f, e - 10);
-    // columns 4i .. 4i + 3 of a block: group g = i / 16, dword t and nibble half from i % 16
-    const int iw = i & 15, low = iw < 8, tq = low ? iw : iw - 8;
-    const int q = 8 * (i >> 4) + tq, c = 2 * (q & 15) + (q >> 4);
-    const int off = b * 512 + ((c ^ (b & 15)) * 16) + (low ? 0 : 8);
-    for (int b0 = w; b0 < nblk; b0 += 4 * 8) {      // eight blocks' loads in flight
-        float4 vv[8];
+    amax = red[0];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) vv[u] = b0 == w ? keep[u] : row[min(b0 + 4 * u, nblk - 1) * 64 + i];
+    for (int k = 1; k < kPrepThreads / 64; ++k) amax = fmaxf(amax, red[k]);
+    float s, inv;
+    g16_split_scale(amax, s, inv);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int blk = b0 + 4 * u;
-        if (blk >= nblk) break;
-        const float4 v = vv[u];
-        const float y[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
-        _Float16 hi[4], lo[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            hi[k] = (_Float16)y[k];
-            lo[k] = (_Float16)(y[k] - (float)hi[k]);
-        }
-        uint8_t *blkp = x16 + (int64_t)blk * kG16BlockBytes;
-        *(uint2 *)(blkp + off) = __builtin_bit_cast(uint2, (_Float16 __attribute__((ext_vector_type(4)))){hi[0], hi[1], hi[2], hi[3]});
-        *(uint2 *)(blkp + kG16Lo + off) = __builtin_bit_cast(uint2, (_Float16 __attribute__((ext_vector_type(4)))){lo[0], lo[1], lo[2], lo[3]});
-        // sub-block j = i / 8: the sum of its 32 scaled values, in a fixed order
-        float S = (y[0] + y[1]) + (y[2] + y[3]);
-        S += __shfl_xor(S, 1);
-        S += __shfl_xor(S, 2);
-        S += __shfl_xor(S, 4);
-        if ((i & 7) == 0) {
-            const _Float16 sh = (_Float16)S, sl = (_Float16)(S - (float)sh);
-            _Float16 *sx = (_Float16 *)(blkp + kG16Sx + b * 32);
-            sx[i >> 3] = sh;
-            sx[8 + (i >> 3)] = sl;
-        }
-        if (i == 0) *(float *)(blkp + kG16Inv + b * 4) = inv;
-    }
+    for (int j = 0; j < kPrepPer; ++j) {
+        if (t + j * kPrepThreads >= n4) break;         // whole waves: n4 is a multiple of 64
+        const float ys[4] = {v[j].x * s, v[j].y * s, v[j].z * s, v[j].w * s};
+        g16_split_group(x16, b, (t + j * kPrepThreads) >> 6, lane, ys, inv);
     }
 }
 
@@ -869,7 +833,7 @@ namespace {
 template <int NT, bool Q6>
 hipError_t launch16_nt(const GemmArgs &a, hipStream_t s) {
     if (!a.presplit) {
-        hipLaunchKernelGGL(gemm16_prep_kernel, dim3(32 * NT), dim3(256), 0, s, a.x, a.x16, a.B, a.nblk);
+        hipLaunchKernelGGL(gemm16_prep_kernel, dim3(32 * NT), dim3(kPrepThreads), 0, s, a.x, a.x16, a.B, a.nblk);
         if (hipError_t e = hipGetLastError()) return e;
     }
     hipLaunchKernelGGL((gemm16_kernel<NT, Q6>), dim3(a.workers), dim3(kG16Threads), 0, s, a);
@@ -893,7 +857,7 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
     if (a.n_mat < 1 || a.n_mat > kMaxGroup || a.nblk <= 0 || a.B <= 0 || a.B > kGemmMaxB) return hipErrorInvalidValue;
     if (a.workers < 1 || !a.partials) return hipErrorInvalidValue;
     const bool fp16 = gemm_fp16();
-    if (fp16 && !a.x16) return hipErrorInvalidValue;
+    if (fp16 && (!a.x16 || a.nblk > kMaxBlocks)) return hipErrorInvalidValue;   // the pre-pass holds 128 blocks
     if (a.presplit && !fp16) return hipErrorInvalidValue;
     const int rpt = gemm_rows_per_tile();
     int tiles = 0;

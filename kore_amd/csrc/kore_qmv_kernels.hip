@@ -13,6 +13,7 @@
 // units go through LDS to one wave that advances the chains, so blocks can
 // be spread over all lanes without changing a single rounding.
 #include "kore_qmv_kernels.h"
+#include "kore_g16_split.h"
 
 #include <algorithm>
 #include <climits>
@@ -991,12 +992,9 @@ namespace {
 
 // kore's rmsnorm of one row of n values (n a multiple of 256 up to 4096, every
 // pointer 16-byte aligned) that also writes the row as the fp16 batched
-// matmul's split activations: gemm16_prep_kernel's layout and arithmetic, so
-// the bytes are the pre-pass's own.  Thread t takes float4 groups t + 256 j
-// (lane t % 64 of block 4 j + t / 64), which is the pre-pass's column order:
-// one power-of-two scale s for the row (max |y s| < 2^10), the hi and lo
-// fp16 parts of four columns in one 8-byte store each, the sub-block sums
-// (four columns, then lanes ^1, ^2, ^4) and 1 / s per block.
+// matmul's split activations (g16_split_group, as gemm16_prep_kernel writes
+// them, so the bytes are the pre-pass's own).  Thread t takes float4 groups
+// t + 256 j: lane t % 64 of block 4 j + t / 64.
 __device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, int n, float eps, float *orow,
                                   uint8_t *__restrict__ x16, double *red) {
     const int t = threadIdx.x, lane = t & 63, b = blockIdx.x, n4 = n / 4;
@@ -1040,39 +1038,13 @@ __device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, 
     if (lane == 0) fred[t >> 6] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
-    int e;
-    (void)frexpf(amax, &e);                            // amax < 2^e (0 for amax = 0)
-    e = max(e, -100);
-    const float s = ldexpf(1.f, 10 - e), inv = ldexpf(1.f, e - 10);
-    // columns 4 lane .. + 3 of a block: group lane / 16, dword and nibble half from lane % 16
-    const int iw = lane & 15, low = iw < 8, tq = low ? iw : iw - 8;
-    const int q = 8 * (lane >> 4) + tq, c = 2 * (q & 15) + (q >> 4);
-    const int off = b * 512 + ((c ^ (b & 15)) * 16) + (low ? 0 : 8);
-    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+    float s, inv;
+    g16_split_scale(amax, s, inv);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         if (t + j * kThreads >= n4) break;             // whole waves: n4 is a multiple of 64
         const float ys[4] = {y[j].x * s, y[j].y * s, y[j].z * s, y[j].w * s};
-        half4v h, l;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            h[k] = (_Float16)ys[k];
-            l[k] = (_Float16)(ys[k] - (float)h[k]);
-        }
-        uint8_t *blkp = x16 + (int64_t)((t + j * kThreads) >> 6) * kG16BlockBytes;
-        *(uint2 *)(blkp + off) = __builtin_bit_cast(uint2, h);
-        *(uint2 *)(blkp + kG16Lo + off) = __builtin_bit_cast(uint2, l);
-        float S = (ys[0] + ys[1]) + (ys[2] + ys[3]);
-        S += __shfl_xor(S, 1);
-        S += __shfl_xor(S, 2);
-        S += __shfl_xor(S, 4);
-        if ((lane & 7) == 0) {
-            const _Float16 sh = (_Float16)S, sl = (_Float16)(S - (float)sh);
-            _Float16 *sx = (_Float16 *)(blkp + kG16Sx + b * 32);
-            sx[lane >> 3] = sh;
-            sx[8 + (lane >> 3)] = sl;
-        }
-        if (lane == 0) *(float *)(blkp + kG16Inv + b * 4) = inv;
+        g16_split_group(x16, b, (t + j * kThreads) >> 6, lane, ys, inv);
     }
 }
 
