@@ -454,17 +454,18 @@ __device__ __forceinline__ floatx16 mfma16(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// The A operands (hi, lo) of k-step s for the NT tiles of activations.
+// The A operands (hi, lo) of k-step s for the NT tiles of activations from
+// activation am on (am = 32 for the second half of a halves-mode unit).
 template <int NT>
-__device__ __forceinline__ void read_step(const uint8_t *ls, int l, int s, half8 (*A)[2]) {
+__device__ __forceinline__ void read_step(const uint8_t *ls, int l, int s, int am, half8 (*A)[2]) {
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt) read_a(ls, 32 * tt + (l & 31), 2 * s + (l >> 5), A[tt][0], A[tt][1]);
+    for (int tt = 0; tt < NT; ++tt) read_a(ls, am + 32 * tt + (l & 31), 2 * s + (l >> 5), A[tt][0], A[tt][1]);
 }
 
 // One Q4_K block: P[tt] = sum_k A x (hi and lo parts); the tiles' MFMA
 // chains alternate.
 template <int NT, bool Q6>
-__device__ __forceinline__ void block16_q4(const W16<Q6> &g, const uint8_t *ls, int l, floatx16 *P) {
+__device__ __forceinline__ void block16_q4(const W16<Q6> &g, const uint8_t *ls, int l, int am, floatx16 *P) {
     const int h = l >> 5;
     const uint4 &hdr = g.v[0];
     // scales of sub-blocks 4h .. 4h + 3 as fp16 pairs (sc, sc) and (-1024 sc, -1024 sc)
@@ -480,7 +481,7 @@ __device__ __forceinline__ void block16_q4(const W16<Q6> &g, const uint8_t *ls, 
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
         half8 A[NT][2];
-        read_step<NT>(ls, l, s, A);
+        read_step<NT>(ls, l, s, am, A);
         const uint32_t D = dword_of(&g.v[1], s);
         const uint32_t L = D & 0x0F0F0F0Fu, H = (D >> 4) & 0x0F0F0F0Fu;
         const int a = s >> 3;                                   // sub-blocks 4h + 2a (low), + 1 (high)
@@ -499,27 +500,27 @@ __device__ __forceinline__ void block16_q4(const W16<Q6> &g, const uint8_t *ls, 
 // Q4_K minimums of one block: M[tt] = sum_j m_j Sx_j, k 0..7 the hi parts of
 // Sx_0..7 times m_0..7, k 8..15 the lo parts times the same.
 template <int NT, bool Q6>
-__device__ __forceinline__ void block16_q4_mins(const W16<Q6> &g, const uint8_t *ls, int l, floatx16 *M) {
+__device__ __forceinline__ void block16_q4_mins(const W16<Q6> &g, const uint8_t *ls, int l, int am, floatx16 *M) {
     const uint4 &hdr = g.v[0];
     half8 bm;
 #pragma unroll
     for (int j = 0; j < 8; ++j) bm[j] = (_Float16)(float)q4m(hdr, j);
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
-        const half8 am = *(const half8 *)(ls + kG16Sx + (32 * tt + (l & 31)) * 32 + 16 * (l >> 5));
-        M[tt] = mfma16(am, bm, floatx16{});
+        const half8 sx = *(const half8 *)(ls + kG16Sx + (am + 32 * tt + (l & 31)) * 32 + 16 * (l >> 5));
+        M[tt] = mfma16(sx, bm, floatx16{});
     }
 }
 
 // One Q6_K block: P[tt] = sum_k (A_hi + A_lo) (x_hi + x_lo) without the lo x lo term.
 template <int NT>
-__device__ __forceinline__ void block16_q6(const W16<true> &g, const uint8_t *ls, int l, floatx16 *P) {
+__device__ __forceinline__ void block16_q6(const W16<true> &g, const uint8_t *ls, int l, int am, floatx16 *P) {
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) P[tt] = floatx16{};
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
         half8 A[NT][2];
-        read_step<NT>(ls, l, s, A);
+        read_step<NT>(ls, l, s, am, A);
         const int a = s >> 3, t = s & 7, sh = 4 * a;
         const uint32_t D1 = dword_of(g.v, t), D2 = dword_of(g.v, 8 + t), Q = dword_of(&g.v[4], t);
         const uint32_t q1 = ((D1 >> sh) & 0x0F0F0F0Fu) | (((Q >> sh) & 0x03030303u) << 4);
@@ -547,9 +548,9 @@ __device__ __forceinline__ void block16_q6(const W16<true> &g, const uint8_t *ls
     }
 }
 
-// D lane l register r of tile tt: activation 32 tt + 8 (r / 4) + 4 (l / 32) + r % 4, row l % 32
+// D lane l register r of tile tt: activation am + 32 tt + 8 (r / 4) + 4 (l / 32) + r % 4, row l % 32
 template <int NT>
-__device__ __forceinline__ void store16(const GemmArgs &a, const GemmMat &mt, int tile, int wave, int l,
+__device__ __forceinline__ void store16(const GemmArgs &a, const GemmMat &mt, int tile, int wave, int l, int am,
                                         const floatx16 *acc) {
     const int row = (tile - mt.tile0) * kG16Rows + 32 * wave + (l & 31);
     if (row >= mt.rows) return;
@@ -558,7 +559,7 @@ __device__ __forceinline__ void store16(const GemmArgs &a, const GemmMat &mt, in
     for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int b = 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+            const int b = am + 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
             if (b >= a.B) continue;
             float *o = mt.out + (int64_t)b * mt.rows + row;
             // kore's q += bq (kore.cpp:1530-1532) and x += o (kore.cpp:1567-1570, 1586-1589)
@@ -573,7 +574,10 @@ __device__ __forceinline__ void store16(const GemmArgs &a, const GemmMat &mt, in
 // activations are copied in (global_load_lds, a linear copy) while the
 // current block's MFMAs run.  The two buffers are separate LDS objects and the
 // loop is unrolled by two, so the compiler sees that reading one does not
-// depend on the copy into the other.
+// depend on the copy into the other.  Work units are the tiles, or with
+// a.halves = 2 (NT = 1) each tile's two halves of 32 activations (unit 2 tile
+// + half): twice the units for launches with few tiles, each staging and
+// multiplying half the activations.
 constexpr int kG16Threads = 512;
 
 template <int NT, bool Q6>
@@ -583,8 +587,8 @@ __global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
     const int t = threadIdx.x, l = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int h = l >> 5;
-    const int nblk = a.nblk, P = a.workers;
-    const int64_t T = (int64_t)a.tiles * nblk;
+    const int nblk = a.nblk, P = a.workers, hv = a.halves;
+    const int64_t T = (int64_t)a.tiles * hv * nblk;
     const int p = (P % 8 == 0) ? (int)(blockIdx.x % 8) * (P / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const int64_t it0 = run_first(T, P, p), it1 = run_first(T, P, p + 1);
     if (it0 >= it1) return;
@@ -607,27 +611,47 @@ __global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
         if (c0 < kChunks && c0 + l < kChunks)
             __builtin_amdgcn_global_load_lds(src + 16 * c0, (void __attribute__((address_space(3))) *)(dst + 16 * c0), 16, 0, 0);
     };
+    // the 32 activations am .. am + 31 of a block (halves mode), at their own
+    // offsets: hi and lo (1024 chunks each, four rounds of 64 per wave), the
+    // sub-block sums (64 chunks, wave 0) and 1 / s (8 chunks, wave 1)
+    auto stage_half = [&](uint8_t *dst, int blk, int am) {
+        const uint8_t *src = a.x16 + (int64_t)blk * kG16BlockBytes + 16 * l;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int c0 = (r < 2 ? 0 : kG16Lo / 16) + am * 32 + 64 * (wave + 8 * (r & 1));
+            __builtin_amdgcn_global_load_lds(src + 16 * c0, (void __attribute__((address_space(3))) *)(dst + 16 * c0), 16, 0, 0);
+        }
+        const int cs = kG16Sx / 16 + am * 2, ci = kG16Inv / 16 + am / 4;
+        if (wave == 0)
+            __builtin_amdgcn_global_load_lds(src + 16 * cs, (void __attribute__((address_space(3))) *)(dst + 16 * cs), 16, 0, 0);
+        if (wave == 1 && l < 8)
+            __builtin_amdgcn_global_load_lds(src + 16 * ci, (void __attribute__((address_space(3))) *)(dst + 16 * ci), 16, 0, 0);
+    };
+    auto stage_unit = [&](uint8_t *dst, int blk, int am) {
+        if (hv == 1) stage(dst, blk);
+        else stage_half(dst, blk, am);
+    };
     // acc += d P - dmin M per block, in the rows' scaled units; times 1 / s of
     // each activation when the tile is stored or left as a partial
     floatx16 acc[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) acc[tt] = floatx16{};
-    auto unscale = [&](const uint8_t *ls) {
+    auto unscale = [&](const uint8_t *ls, int am) {
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
-                const float4 f = *(const float4 *)(ls + kG16Inv + 4 * (32 * tt + 8 * qd + 4 * h));
+                const float4 f = *(const float4 *)(ls + kG16Inv + 4 * (am + 32 * tt + 8 * qd + 4 * h));
                 acc[tt][4 * qd + 0] *= f.x;
                 acc[tt][4 * qd + 1] *= f.y;
                 acc[tt][4 * qd + 2] *= f.z;
                 acc[tt][4 * qd + 3] *= f.w;
             }
     };
-    auto compute = [&](const uint8_t *ls, const W16<Q6> &gc, int cm) {
+    auto compute = [&](const uint8_t *ls, const W16<Q6> &gc, int cm, int am) {
         if (Q6 && a.m[cm].type == kQ6K) {
             floatx16 Pb[NT];
-            if constexpr (Q6) block16_q6<NT>(gc, ls, l, Pb);
+            if constexpr (Q6) block16_q6<NT>(gc, ls, l, am, Pb);
             const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)gc.d);
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt)
@@ -636,14 +660,14 @@ __global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
         } else {
             // d P first, then the minimums in the same registers
             floatx16 Pb[NT];
-            block16_q4<NT, Q6>(gc, ls, l, Pb);
+            block16_q4<NT, Q6>(gc, ls, l, am, Pb);
             const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(gc.v[0].x & 0xFFFFu));
             const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(gc.v[0].x >> 16));
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[tt][r] = fmaf(d, Pb[tt][r], acc[tt][r]);
-            block16_q4_mins<NT, Q6>(gc, ls, l, Pb);
+            block16_q4_mins<NT, Q6>(gc, ls, l, am, Pb);
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -651,43 +675,47 @@ __global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
         }
     };
 
-    int tile = (int)(it0 / nblk), blk = (int)(it0 % nblk), seg0 = blk;
+    int unit = (int)(it0 / nblk), blk = (int)(it0 % nblk), seg0 = blk;
+    int tile = unit / hv, am = (unit % hv) * 32;
     int m = mat_of_tile(a, tile);
     W16<Q6> g;
     load_w16<Q6>(g, a.m[m], row_of(tile, m), blk, nblk, h);
-    stage(ls0, blk);
+    stage_unit(ls0, blk, am);
     __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0)
     __syncthreads();
 
-    // one iteration: block `blk` of `tile` from `cur`, the next block's split into `nxt`
+    // one iteration: block `blk` of `unit` from `cur`, the next block's split into `nxt`
     auto step = [&](int64_t it, const uint8_t *cur, uint8_t *nxt) {
-        int ntile = tile, nb = blk + 1;
-        if (nb == nblk) { nb = 0; ++ntile; }
+        int nunit = unit, nb = blk + 1;
+        if (nb == nblk) { nb = 0; ++nunit; }
+        const int ntile = nunit / hv, nam = (nunit % hv) * 32;
         const W16<Q6> gc = g;
         const int cm = m;
         if (it + 1 < it1) {                            // the next block's activations and weights
-            stage(nxt, nb);
+            stage_unit(nxt, nb, nam);
             m = ntile == tile ? m : mat_of_tile(a, ntile);
             load_w16<Q6>(g, a.m[m], row_of(ntile, m), nb, nblk, h);
         }
-        compute(cur, gc, cm);
-        if (it + 1 == it1 || nb == 0) {                // end of this worker's part of the tile
-            unscale(cur);
-            if (seg0 != 0 || blk + 1 != nblk) {        // split tile: partial sums for the fix-up launch
-                const int slot = 2 * p + (it0 / nblk == tile ? 0 : 1);
+        compute(cur, gc, cm, am);
+        if (it + 1 == it1 || nb == 0) {                // end of this worker's part of the unit
+            unscale(cur, am);
+            if (seg0 != 0 || blk + 1 != nblk) {        // split unit: partial sums for the fix-up launch
+                const int slot = 2 * p + (it0 / nblk == unit ? 0 : 1);
                 float *mine = a.partials + (int64_t)slot * kG16SlotFloats;
 #pragma unroll
                 for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) mine[((wave * 2 + tt) * 16 + r) * 64 + l] = acc[tt][r];
             } else {
-                store16<NT>(a, a.m[cm], tile, wave, l, acc);
+                store16<NT>(a, a.m[cm], tile, wave, l, am, acc);
             }
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) acc[tt] = floatx16{};
             seg0 = 0;
         }
+        unit = nunit;
         tile = ntile;
+        am = nam;
         blk = nb;
         __builtin_amdgcn_s_waitcnt(0x0F70);            // vmcnt(0): the next block's copies have landed
         __syncthreads();                               // ... for every wave, and `cur` is free
@@ -699,20 +727,23 @@ __global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
     }
 }
 
-// Fix-up of the fp16 path: blockIdx.x = tile, blockIdx.y = a slice of 1024 of
-// its kG16SlotFloats partial floats (slot float ((wave 2 + tt) 16 + r) 64 + l
-// is register r of tile tt of lane l of wave `wave`, 8 waves); thread t adds
-// float4 t of the slice over the tile's workers in worker order, eight
+// Fix-up of the fp16 path: blockIdx.x = unit (tile, or tile and half),
+// blockIdx.y = a slice of 1024 of its kG16SlotFloats partial floats (slot
+// float ((wave 2 + tt) 16 + r) 64 + l is register r of activation tile tt of
+// lane l of wave `wave`, 8 waves; a halves-mode unit has tile 0 only); thread
+// t adds float4 t of the slice over the unit's workers in worker order, eight
 // workers' loads in flight at a time, and stores four consecutive rows of one
 // activation.
 __global__ __launch_bounds__(kThreads) void gemm16_fixup_kernel(GemmArgs a) {
-    const int tile = blockIdx.x, nblk = a.nblk, P = a.workers;
-    const int64_t T = (int64_t)a.tiles * nblk, tfirst = (int64_t)tile * nblk;
+    const int unit = blockIdx.x, nblk = a.nblk, P = a.workers, hv = a.halves;
+    const int tile = unit / hv, am = (unit % hv) * 32;
+    const int64_t T = (int64_t)a.tiles * hv * nblk, tfirst = (int64_t)unit * nblk;
     const int pf = run_of(T, P, tfirst), pl = run_of(T, P, tfirst + nblk - 1);
-    if (pf == pl) return;                        // one worker ran the whole tile and stored it
+    if (pf == pl) return;                        // one worker ran the whole unit and stored it
     const int f = blockIdx.y * 1024 + 4 * threadIdx.x;   // first of the thread's four floats
     const int l = f & 63, r = (f >> 6) & 15, tt = (f >> 10) & 1, wave = f >> 11;
-    const int b = 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    if (hv == 2 && tt) return;
+    const int b = am + 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
     if (b >= a.B) return;
     constexpr int kBatch = 8;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -721,7 +752,7 @@ __global__ __launch_bounds__(kThreads) void gemm16_fixup_kernel(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int q = min(q0 + u, pl);
-            const int slot = 2 * q + (run_first(T, P, q) / nblk == tile ? 0 : 1);
+            const int slot = 2 * q + (run_first(T, P, q) / nblk == unit ? 0 : 1);
             v[u] = *(const float4 *)(a.partials + (int64_t)slot * kG16SlotFloats + f);
         }
 #pragma unroll
@@ -819,6 +850,10 @@ bool gemm_fp16() {
 
 int gemm_rows_per_tile() { return gemm_fp16() ? kG16Rows : kGemmRowsPerTile; }
 
+int gemm_halves(int tiles, int nblk, int B, int num_cu) {
+    return gemm_fp16() && B > 32 && (int64_t)tiles * nblk < 2LL * std::max(num_cu, 1) ? 2 : 1;
+}
+
 int gemm_workers(int tiles, int nblk, int B, bool has_q6k, int num_cu) {
     int occ = 1;                               // fp16 path: one workgroup per CU (LDS)
     if (!gemm_fp16() && (has_q6k ? prepare_t<true>(B, &occ) : prepare_t<false>(B, &occ)) != hipSuccess) occ = 1;
@@ -833,22 +868,24 @@ namespace {
 template <int NT, bool Q6>
 hipError_t launch16_nt(const GemmArgs &a, hipStream_t s) {
     if (!a.presplit) {
-        hipLaunchKernelGGL(gemm16_prep_kernel, dim3(32 * NT), dim3(kPrepThreads), 0, s, a.x, a.x16, a.B, a.nblk);
+        // every activation the units read: 32 per tile of activations, both halves in halves mode
+        hipLaunchKernelGGL(gemm16_prep_kernel, dim3(32 * NT * a.halves), dim3(kPrepThreads), 0, s, a.x, a.x16, a.B,
+                           a.nblk);
         if (hipError_t e = hipGetLastError()) return e;
     }
     hipLaunchKernelGGL((gemm16_kernel<NT, Q6>), dim3(a.workers), dim3(kG16Threads), 0, s, a);
     if (hipError_t e = hipGetLastError()) return e;
-    const int64_t T = (int64_t)a.tiles * a.nblk;
+    const int64_t T = (int64_t)a.tiles * a.halves * a.nblk;
     if (T % a.workers == 0 && (T / a.workers) % a.nblk == 0) return hipSuccess;
-    // 8 slices of 1024 partial floats (the slices of a second tile of
+    // 16 slices of 1024 partial floats (the slices of a second tile of
     // activations return at once when NT = 1)
-    hipLaunchKernelGGL(gemm16_fixup_kernel, dim3(a.tiles, kG16SlotFloats / 1024), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(gemm16_fixup_kernel, dim3(a.tiles * a.halves, kG16SlotFloats / 1024), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
 template <bool Q6>
 hipError_t launch16(const GemmArgs &a, hipStream_t s) {
-    return a.B > 32 ? launch16_nt<2, Q6>(a, s) : launch16_nt<1, Q6>(a, s);
+    return a.B > 32 && a.halves == 1 ? launch16_nt<2, Q6>(a, s) : launch16_nt<1, Q6>(a, s);
 }
 
 }  // namespace
@@ -868,7 +905,8 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
         a.m[k].tile0 = tiles;
         tiles += (m.rows + rpt - 1) / rpt;
     }
-    if (tiles != a.tiles || (int64_t)tiles * a.nblk < a.workers) return hipErrorInvalidValue;
+    if (a.halves != 1 && !(a.halves == 2 && fp16)) return hipErrorInvalidValue;
+    if (tiles != a.tiles || (int64_t)tiles * a.halves * a.nblk < a.workers) return hipErrorInvalidValue;
     bool q6 = false;
     for (int k = 0; k < a.n_mat; ++k) q6 |= a.m[k].type == kQ6K;
     if (fp16) return q6 ? launch16<true>(a, s) : launch16<false>(a, s);

@@ -432,7 +432,8 @@ int matmul_group(int n, const kore_qmv_tensor_t *t, const float *x, const void *
     GemmScratch &g = g_gemm[t0->device & 63];
     bool q6 = false;
     for (int k = 0; k < n; ++k) q6 |= t[k]->type == KORE_QMV_Q6_K;
-    a.workers = gemm_workers(a.tiles, a.nblk, nb, q6, t0->num_cu);
+    a.halves = gemm_halves(a.tiles, a.nblk, nb, t0->num_cu);
+    a.workers = gemm_workers(a.tiles * a.halves, a.nblk, nb, q6, t0->num_cu);
     a.partials = g.partials;
     a.x16 = x16 ? (uint8_t *)x16 : g.x16;
     a.presplit = x16 ? 1 : 0;

@@ -137,6 +137,7 @@ struct GemmArgs {
     float *partials;         // 2 * workers * kGemmSlotFloats floats
     uint8_t *x16;            // nblk * kG16BlockBytes: the fp16 split of x (fp16 path)
     int presplit;            // x16 already holds the split (x unused): no pre-pass
+    int halves;              // 1, or 2 (fp16 path): work units of 32 activations per tile
 };
 
 // fp16 path of the batched matmul (the default): the weights enter the MFMA
@@ -156,6 +157,11 @@ constexpr int kG16SlotFloats = kG16Rows * kGemmMaxB;   // one partial tile
 // environment selects it, for comparisons).
 bool gemm_fp16();
 int gemm_rows_per_tile();
+// 2 when the fp16 path splits each tile's activations into two units of 32
+// (B > 32 and fewer than two (tile, block) iterations per CU: the workers then
+// cover all CUs with units half the size), else 1.  The workers and the
+// partials are counted in units (tiles x halves).
+int gemm_halves(int tiles, int nblk, int B, int num_cu);
 // Workers of one launch: as many as fit on the CUs at once (by the LDS and
 // registers of the kernel that B activations and the weight types select), at
 // least two iterations each.
