@@ -745,16 +745,19 @@ __global__ __launch_bounds__(kThreads) void gemm16_fixup_kernel(GemmArgs a) {
     if (hv == 2 && tt) return;
     const int b = am + 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
     if (b >= a.B) return;
+    // up to eight contributors' loads in flight, only those the unit has
+    // (pf and pl are the same for the whole workgroup: uniform branches)
     constexpr int kBatch = 8;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int q0 = pf; q0 <= pl; q0 += kBatch) {
         float4 v[kBatch];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int q = min(q0 + u, pl);
-            const int slot = 2 * q + (run_first(T, P, q) / nblk == unit ? 0 : 1);
-            v[u] = *(const float4 *)(a.partials + (int64_t)slot * kG16SlotFloats + f);
-        }
+        for (int u = 0; u < kBatch; ++u)
+            if (q0 + u <= pl) {
+                const int q = q0 + u;
+                const int slot = 2 * q + (run_first(T, P, q) / nblk == unit ? 0 : 1);
+                v[u] = *(const float4 *)(a.partials + (int64_t)slot * kG16SlotFloats + f);
+            }
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
             if (q0 + u <= pl) {
@@ -769,18 +772,32 @@ __global__ __launch_bounds__(kThreads) void gemm16_fixup_kernel(GemmArgs a) {
     }
     const GemmMat &mt = a.m[mat_of_tile(a, tile)];
     const int row0 = (tile - mt.tile0) * kG16Rows + 32 * wave + (l & 31);
+    float *o = mt.out + (int64_t)b * mt.rows + row0;
+    // kore's q += bq (kore.cpp:1530-1532) and x += o (kore.cpp:1567-1570, 1586-1589)
+    if (row0 + 3 < mt.rows && !(((uintptr_t)o | (uintptr_t)(mt.bias ? mt.bias + row0 : nullptr)) & 15)) {
+        float4 v = acc;                                // four whole rows, 16-byte aligned
+        if (mt.bias) {
+            const float4 bb = *(const float4 *)(mt.bias + row0);
+            v = make_float4(v.x + bb.x, v.y + bb.y, v.z + bb.z, v.w + bb.w);
+        }
+        if (mt.accumulate) {
+            const float4 ov = *(const float4 *)o;
+            v = make_float4(ov.x + v.x, ov.y + v.y, ov.z + v.z, ov.w + v.w);
+        }
+        *(float4 *)o = v;
+        return;
+    }
     const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int row = row0 + k;
         if (row >= mt.rows) break;
-        float *o = mt.out + (int64_t)b * mt.rows + row;
-        // kore's q += bq (kore.cpp:1530-1532) and x += o (kore.cpp:1567-1570, 1586-1589)
         float v = vals[k];
         if (mt.bias) v = v + mt.bias[row];
-        *o = mt.accumulate ? *o + v : v;
+        o[k] = mt.accumulate ? o[k] + v : v;
     }
 }
+
 
 constexpr size_t lds_bytes(int nbk) { return (size_t)16 * nbk * kXStride * sizeof(float); }
 
