@@ -1351,13 +1351,14 @@ hipError_t launch_append(const AppendArgs &a, int head_dim, hipStream_t s) {
 int prefill_key_segments(int n_tok, int pos0, int n_head_kv, int n_rep, int num_cu, int *seg_tiles) {
     // Split the key range when the workgroups of a chunk do not fill every
     // CU (two fit per CU): as many segments as keep all of them in one wave
-    // of two per CU, each of at least 8 key tiles.
+    // of two per CU, each of at least 2 key tiles.  A 64-row chunk has 16
+    // workgroups (7B): unsplit, each walks all its key tiles alone.
     const int n_strips = (n_tok + 31) / 32;
     const int n_wg = (n_rep * n_strips + 3) / 4 * n_head_kv;
     const int n_tiles = (pos0 + n_tok - 1) / 32 + 1;
     int n_kseg = 1;
     if (n_wg < num_cu)
-        n_kseg = std::max(1, std::min(2 * num_cu / n_wg, n_tiles / 8));
+        n_kseg = std::max(1, std::min(2 * num_cu / n_wg, n_tiles / 2));
     *seg_tiles = (n_tiles + n_kseg - 1) / n_kseg;
     return n_kseg;
 }
