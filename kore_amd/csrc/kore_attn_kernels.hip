@@ -1167,25 +1167,46 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
     const int qrow = 32 * strip + r;
     if (qrow >= a.n_tok) return;
+    // segments in batches of four, every load of a batch issued before its
+    // arithmetic (one memory round trip per batch); the sums in segment order
+    constexpr int kSeg = 4;
+    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml);
     float m = -INFINITY;
-    for (int s = 0; s < S; ++s) m = fmaxf(m, a.part_ml[((base + s) * 32 + r) * 2]);
+    for (int s0 = 0; s0 < S; s0 += 2 * kSeg) {
+        float mv[2 * kSeg];
+#pragma unroll
+        for (int u = 0; u < 2 * kSeg; ++u) mv[u] = s0 + u < S ? ml[(base + s0 + u) * 32 + r].x : -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2 * kSeg; ++u) m = fmaxf(m, mv[u]);
+    }
     float den = 0.f;
     float4 acc[CH / 4];
 #pragma unroll
     for (int j = 0; j < CH / 4; ++j) acc[j] = zero4();
-    for (int s = 0; s < S; ++s) {
-        const float ms = a.part_ml[((base + s) * 32 + r) * 2];
-        const float w = ms == -INFINITY ? 0.f : exp2f(ms - m);
-        den = fmaf(w, a.part_ml[((base + s) * 32 + r) * 2 + 1], den);
-        const float *po = a.part_o + ((base + s) * 32 + r) * HD + c * CH;
+    for (int s0 = 0; s0 < S; s0 += kSeg) {
+        float2 st[kSeg];
+        float4 x[kSeg][CH / 4];
 #pragma unroll
-        for (int j = 0; j < CH / 4; ++j) {
-            const float4 x = ld4(po + 4 * j);
-            acc[j].x = fmaf(w, x.x, acc[j].x);
-            acc[j].y = fmaf(w, x.y, acc[j].y);
-            acc[j].z = fmaf(w, x.z, acc[j].z);
-            acc[j].w = fmaf(w, x.w, acc[j].w);
-        }
+        for (int u = 0; u < kSeg; ++u)
+            if (s0 + u < S) {
+                st[u] = ml[(base + s0 + u) * 32 + r];
+                const float *po = a.part_o + ((base + s0 + u) * 32 + r) * HD + c * CH;
+#pragma unroll
+                for (int j = 0; j < CH / 4; ++j) x[u][j] = ld4(po + 4 * j);
+            }
+#pragma unroll
+        for (int u = 0; u < kSeg; ++u)
+            if (s0 + u < S) {
+                const float w = st[u].x == -INFINITY ? 0.f : exp2f(st[u].x - m);
+                den = fmaf(w, st[u].y, den);
+#pragma unroll
+                for (int j = 0; j < CH / 4; ++j) {
+                    acc[j].x = fmaf(w, x[u][j].x, acc[j].x);
+                    acc[j].y = fmaf(w, x[u][j].y, acc[j].y);
+                    acc[j].z = fmaf(w, x[u][j].z, acc[j].z);
+                    acc[j].w = fmaf(w, x[u][j].w, acc[j].w);
+                }
+            }
     }
     const float inv = 1.f / den;
     float *op = a.out + ((size_t)qrow * a.n_head_kv * a.n_rep + h) * HD + c * CH;
