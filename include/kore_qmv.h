@@ -184,6 +184,15 @@ KORE_QMV_API size_t kore_qmv_split_bytes(int64_t cols);
 KORE_QMV_API int kore_qmv_rmsnorm_rows_split_dev(const float *x, const float *w, int64_t n, int rows, float eps,
                                                  float *out, void *x16, void *stream);
 
+/* forward_batch()'s gate/up matmuls and SwiGLU (kore.cpp:1575-1581) in one call
+ * on the split x16 of nb activations: out[b * rows + r] = SwiGLU(gate row r .
+ * x_b, up row r . x_b), bit for bit kore_qmv_matmul_batch_group_split_dev of
+ * {gate, up} followed by kore_qmv_swiglu_dev; the SwiGLU is applied where the
+ * matmul adds its split tiles' partial sums (no launch of its own).  tmp
+ * (device, nb * rows floats) is scratch; gate and up share rows and cols. */
+KORE_QMV_API int kore_qmv_matmul_batch_glu_split_dev(const kore_qmv_tensor_t *gate_up, const void *x16, int nb,
+                                                     float *out, float *tmp, void *stream);
+
 /* kore_qmv_matmul_batch_group_ex_dev on the split x16 of nb activations
  * (written by kore_qmv_rmsnorm_rows_split_dev, kept unchanged since) instead
  * of x: the same results, bit for bit. */

@@ -34,6 +34,7 @@
 // bit for bit.  For one device, shape and B the result is deterministic.
 #include "kore_qmv_kernels.h"
 #include "kore_g16_split.h"
+#include "kore_swiglu.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -799,6 +800,102 @@ __global__ __launch_bounds__(kThreads) void gemm16_fixup_kernel(GemmArgs a) {
 }
 
 
+// Fix-up of a gate/up pair (GemmArgs::glu): blockIdx.x = gate unit u (tile, or
+// tile and half), whose rows and activations up unit u + m[1].tile0 x halves
+// shares; blockIdx.y and the thread's float4 as in gemm16_fixup_kernel.  Each
+// of the two values comes from its unit's partial sums (added in worker order,
+// as the fix-up adds them) when the unit was split, else from the output the
+// main kernel stored; m[0].out receives kore's SwiGLU of the pair
+// (kore.cpp:1577-1581), bit for bit what the plain fix-up followed by the
+// SwiGLU kernel gives.
+__global__ __launch_bounds__(kThreads) void gemm16_glu_fixup_kernel(GemmArgs a) {
+    const int ug = blockIdx.x, nblk = a.nblk, P = a.workers, hv = a.halves;
+    const int tile = ug / hv, am = (ug % hv) * 32;
+    const int64_t T = (int64_t)a.tiles * hv * nblk;
+    const int f = blockIdx.y * 1024 + 4 * threadIdx.x;   // first of the thread's four floats
+    const int l = f & 63, r = (f >> 6) & 15, tt = (f >> 10) & 1, wave = f >> 11;
+    if (hv == 2 && tt) return;
+    const int b = am + 32 * tt + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    const int rows = a.m[0].rows, row0 = tile * kG16Rows + 32 * wave + (l & 31);
+    if (b >= a.B || row0 >= rows) return;
+    const bool whole = row0 + 3 < rows;
+    // both units' loads of a batch issued before either is summed (a unit
+    // stored whole is read from its output instead); sums in worker order
+    constexpr int kBatch = 8;
+    auto range = [&](int unit, int &pf, int &pl) {
+        pf = run_of(T, P, (int64_t)unit * nblk);
+        pl = run_of(T, P, (int64_t)unit * nblk + nblk - 1);
+    };
+    auto issue = [&](int unit, int pf, int pl, int q0, const float *out, float4 *v) {
+        if (pf == pl) {
+            const float *o = out + (int64_t)b * rows + row0;
+            if (whole && !((uintptr_t)o & 15)) {
+                v[0] = *(const float4 *)o;
+            } else {
+                v[0] = make_float4(o[0], 0.f, 0.f, 0.f);
+                if (row0 + 1 < rows) v[0].y = o[1];
+                if (row0 + 2 < rows) v[0].z = o[2];
+                if (row0 + 3 < rows) v[0].w = o[3];
+            }
+            return;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (q0 + u <= pl) {
+                const int q = q0 + u;
+                const int slot = 2 * q + (run_first(T, P, q) / nblk == unit ? 0 : 1);
+                v[u] = *(const float4 *)(a.partials + (int64_t)slot * kG16SlotFloats + f);
+            }
+    };
+    auto add = [&](int pf, int pl, int q0, const float4 *v, float4 &acc) {
+        if (pf == pl) {
+            acc = v[0];
+            return;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (q0 + u <= pl) {
+                if (q0 + u == pf) acc = v[u];
+                else {
+                    acc.x += v[u].x;
+                    acc.y += v[u].y;
+                    acc.z += v[u].z;
+                    acc.w += v[u].w;
+                }
+            }
+    };
+    const int uu = ug + a.m[1].tile0 * hv;
+    int pfg, plg, pfu, plu;
+    range(ug, pfg, plg);
+    range(uu, pfu, plu);
+    float4 vg[kBatch], vu[kBatch], g, u;
+    issue(ug, pfg, plg, pfg, a.m[0].out, vg);
+    issue(uu, pfu, plu, pfu, a.m[1].out, vu);
+    add(pfg, plg, pfg, vg, g);
+    add(pfu, plu, pfu, vu, u);
+    if (pfg != plg)
+        for (int q0 = pfg + kBatch; q0 <= plg; q0 += kBatch) {
+            issue(ug, pfg, plg, q0, a.m[0].out, vg);
+            add(pfg, plg, q0, vg, g);
+        }
+    if (pfu != plu)
+        for (int q0 = pfu + kBatch; q0 <= plu; q0 += kBatch) {
+            issue(uu, pfu, plu, q0, a.m[1].out, vu);
+            add(pfu, plu, q0, vu, u);
+        }
+    float *o = a.m[0].out + (int64_t)b * rows + row0;
+    const float4 y = make_float4(kore_swiglu(g.x, u.x), kore_swiglu(g.y, u.y), kore_swiglu(g.z, u.z),
+                                 kore_swiglu(g.w, u.w));
+    if (whole && !((uintptr_t)o & 15)) {
+        *(float4 *)o = y;
+        return;
+    }
+    const float ys[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (row0 + k < rows) o[k] = ys[k];
+}
+
 constexpr size_t lds_bytes(int nbk) { return (size_t)16 * nbk * kXStride * sizeof(float); }
 
 // Dynamic LDS above 64 KiB (64 activations: 66,560 bytes) needs the kernel's
@@ -892,6 +989,11 @@ hipError_t launch16_nt(const GemmArgs &a, hipStream_t s) {
     }
     hipLaunchKernelGGL((gemm16_kernel<NT, Q6>), dim3(a.workers), dim3(kG16Threads), 0, s, a);
     if (hipError_t e = hipGetLastError()) return e;
+    if (a.glu) {   // every gate tile: its SwiGLU is written by the pair's fix-up
+        hipLaunchKernelGGL(gemm16_glu_fixup_kernel, dim3(a.m[1].tile0 * a.halves, kG16SlotFloats / 1024),
+                           dim3(kThreads), 0, s, a);
+        return hipGetLastError();
+    }
     const int64_t T = (int64_t)a.tiles * a.halves * a.nblk;
     if (T % a.workers == 0 && (T / a.workers) % a.nblk == 0) return hipSuccess;
     // 16 slices of 1024 partial floats (the slices of a second tile of
@@ -923,6 +1025,9 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
         tiles += (m.rows + rpt - 1) / rpt;
     }
     if (a.halves != 1 && !(a.halves == 2 && fp16)) return hipErrorInvalidValue;
+    if (a.glu && (!fp16 || a.n_mat != 2 || a.m[0].rows != a.m[1].rows || a.m[0].bias ||
+                  a.m[1].bias || a.m[0].accumulate || a.m[1].accumulate))
+        return hipErrorInvalidValue;
     if (tiles != a.tiles || (int64_t)tiles * a.halves * a.nblk < a.workers) return hipErrorInvalidValue;
     bool q6 = false;
     for (int k = 0; k < a.n_mat; ++k) q6 |= a.m[k].type == kQ6K;

@@ -200,8 +200,16 @@ KORE_LAYER_API int kore_layer_prefill_dev(kore_layer_t L, const kore_layer_weigh
     // 4. rmsnorm, gate/up, SwiGLU (kore.cpp:1572-1583)
     kore_qmv_tensor_t gu[2] = {w->w_gate, w->w_up};
     float *gu_out[2] = {L->bgate, L->bup};
-    if (int rc = norm_matmul(w->ffn_norm, 2, gu, nullptr, gu_out, "ffn_norm, gate/up")) return rc;
-    if (kore_qmv_swiglu_dev(L->bgate, L->bup, (int64_t)n_tok * FF, s) != KORE_QMV_OK) return qmv_err(nullptr, "swiglu");
+    if (L->bx16) {   // the SwiGLU where gate/up's split tiles are summed (bup is scratch)
+        if (kore_qmv_rmsnorm_rows_split_dev(x, w->ffn_norm, E, n_tok, L->eps, L->bxb, L->bx16, s) != KORE_QMV_OK)
+            return qmv_err(nullptr, "ffn_norm");
+        if (kore_qmv_matmul_batch_glu_split_dev(gu, L->bx16, n_tok, L->bgate, L->bup, s) != KORE_QMV_OK)
+            return qmv_err(w->w_gate, "gate/up, swiglu");
+    } else {
+        if (int rc = norm_matmul(w->ffn_norm, 2, gu, nullptr, gu_out, "ffn_norm, gate/up")) return rc;
+        if (kore_qmv_swiglu_dev(L->bgate, L->bup, (int64_t)n_tok * FF, s) != KORE_QMV_OK)
+            return qmv_err(nullptr, "swiglu");
+    }
     // 5. down, x += o (kore.cpp:1585-1589)
     if (kore_qmv_matmul_batch_group_ex_dev(1, &w->w_down, L->bgate, n_tok, &acc, &x, s) != KORE_QMV_OK)
         return qmv_err(w->w_down, "down");

@@ -398,7 +398,7 @@ namespace {
 // The batched matmul of kore_qmv_matmul_batch_group_ex_dev, on x or (x16 set)
 // on activations already split by kore_qmv_rmsnorm_rows_split_dev.
 int matmul_group(int n, const kore_qmv_tensor_t *t, const float *x, const void *x16, int nb,
-                 const kore_qmv_mv_opts *opts, float *const *out, void *stream) {
+                 const kore_qmv_mv_opts *opts, float *const *out, void *stream, bool glu = false) {
     if (n < 1 || n > kMaxGroup || !t || !out) return fail(nullptr, KORE_QMV_E_INVALID, "n must be 1..4, t and out set");
     for (int k = 0; k < n; ++k)
         if (!t[k]) return fail(nullptr, KORE_QMV_E_INVALID, "tensor is NULL");
@@ -432,6 +432,7 @@ int matmul_group(int n, const kore_qmv_tensor_t *t, const float *x, const void *
     GemmScratch &g = g_gemm[t0->device & 63];
     bool q6 = false;
     for (int k = 0; k < n; ++k) q6 |= t[k]->type == KORE_QMV_Q6_K;
+    a.glu = glu ? 1 : 0;
     a.halves = gemm_halves(a.tiles, a.nblk, nb, t0->num_cu);
     a.workers = gemm_workers(a.tiles * a.halves, a.nblk, nb, q6, t0->num_cu);
     a.partials = g.partials;
@@ -454,6 +455,16 @@ KORE_QMV_API int kore_qmv_matmul_batch_group_split_dev(int n, const kore_qmv_ten
                                                        const kore_qmv_mv_opts *opts, float *const *out, void *stream) {
     if (!x16) return fail(nullptr, KORE_QMV_E_INVALID, "x16 is NULL");
     return matmul_group(n, t, nullptr, x16, nb, opts, out, stream);
+}
+
+KORE_QMV_API int kore_qmv_matmul_batch_glu_split_dev(const kore_qmv_tensor_t *gate_up, const void *x16, int nb,
+                                                     float *out, float *tmp, void *stream) {
+    if (!gate_up || !gate_up[0] || !gate_up[1] || !x16 || !out || !tmp)
+        return fail(nullptr, KORE_QMV_E_INVALID, "gate_up[0..1], x16, out and tmp must be set");
+    if (gate_up[0]->rows != gate_up[1]->rows)
+        return fail(gate_up[0], KORE_QMV_E_INVALID, "gate and up must have the same rows");
+    float *outs[2] = {out, tmp};
+    return matmul_group(2, gate_up, nullptr, x16, nb, nullptr, outs, stream, true);
 }
 
 KORE_QMV_API size_t kore_qmv_split_bytes(int64_t cols) {

@@ -138,6 +138,9 @@ struct GemmArgs {
     uint8_t *x16;            // nblk * kG16BlockBytes: the fp16 split of x (fp16 path)
     int presplit;            // x16 already holds the split (x unused): no pre-pass
     int halves;              // 1, or 2 (fp16 path): work units of 32 activations per tile
+    int glu;                 // fp16 path, m[0] = gate, m[1] = up (equal rows, no bias or
+                             // accumulate): m[0].out = kore's SwiGLU of the two products,
+                             // m[1].out scratch
 };
 
 // fp16 path of the batched matmul (the default): the weights enter the MFMA

@@ -14,6 +14,7 @@
 // be spread over all lanes without changing a single rounding.
 #include "kore_qmv_kernels.h"
 #include "kore_g16_split.h"
+#include "kore_swiglu.h"
 
 #include <algorithm>
 #include <climits>
@@ -204,17 +205,6 @@ __device__ float block_rms_scale(const float *x, int n, float eps, double *red) 
         }
     }
     return block_rms_scale_from(hi, lo, x, n, eps, red);
-}
-
-// kore's SwiGLU of one value (kore.cpp:1466-1467): g / (1.0f + std::exp(-g)) * u.
-// exp is taken in double and rounded to float (glibc's expf agrees with that
-// correctly rounded value except in rare hard cases); the division is rounded
-// once from double like kore's float division.
-__device__ __forceinline__ float kore_swiglu(float g, float u) {
-    const float ex = (float)exp(-(double)g);
-    const float den = 1.0f + ex;
-    const float q = (float)((double)g / (double)den);
-    return q * u;
 }
 
 __device__ __forceinline__ Q8Lane quantize16(const float (&v)[16], int m);

@@ -61,6 +61,7 @@ SYMBOLS = [
     ("kore_qmv_rmsnorm_rows_split_dev", _i, [_vp, _vp, _i64, _i, C.c_float, _vp, _vp, _vp]),
     ("kore_qmv_matmul_batch_group_split_dev", _i, [_i, _vp, _vp, _i, _vp, _vp, _vp]),
     ("kore_qmv_swiglu_dev", _i, [_vp, _vp, _i64, _vp]),
+    ("kore_qmv_matmul_batch_glu_split_dev", _i, [_vp, _vp, _i, _vp, _vp, _vp]),
     ("kore_qmv_last_error", C.c_char_p, [_vp]),
     ("kore_qmv_get_info", _i, [_vp, C.POINTER(QmvInfo)]),
     ("kore_qmv_synth_dev", _i, [_i, _i64, _i64, C.c_uint64, _vp, _vp]),
@@ -278,6 +279,13 @@ def matmul_batch_group_split_dev(mats, x16_ptr: int, nb: int, out_ptrs, bias=Non
     hs = (C.c_void_p * n)(*[m.handle.value for m in mats])
     outs = (C.c_void_p * n)(*out_ptrs)
     _check(lib().kore_qmv_matmul_batch_group_split_dev(n, hs, x16_ptr, nb, C.byref(o), outs, stream))
+
+
+def matmul_batch_glu_split_dev(gate, up, x16_ptr: int, nb: int, out_ptr: int, tmp_ptr: int, stream=None) -> None:
+    """kore_qmv_matmul_batch_glu_split_dev: SwiGLU(gate . x, up . x) of the nb
+    activations split in x16 into out (tmp: nb * rows floats of scratch)."""
+    hs = (C.c_void_p * 2)(gate.handle.value, up.handle.value)
+    _check(lib().kore_qmv_matmul_batch_glu_split_dev(hs, x16_ptr, nb, out_ptr, tmp_ptr, stream))
 
 
 def swiglu_dev(g_ptr: int, u_ptr: int, n: int, stream=None) -> None:

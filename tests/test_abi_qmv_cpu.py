@@ -37,7 +37,7 @@ def test_headers_declare_the_abi():
                            "kore_qmv_matmul_batch_dev", "kore_qmv_matmul_batch_group_dev",
                            "kore_qmv_matmul_batch_group_ex_dev", "kore_qmv_rmsnorm_rows_dev", "kore_qmv_swiglu_dev",
                            "kore_qmv_split_bytes", "kore_qmv_rmsnorm_rows_split_dev",
-                           "kore_qmv_matmul_batch_group_split_dev",
+                           "kore_qmv_matmul_batch_group_split_dev", "kore_qmv_matmul_batch_glu_split_dev",
                            "kore_qmv_last_error", "kore_qmv_get_info", "kore_qmv_synth_dev"}
 
 
@@ -95,6 +95,7 @@ def test_calls_without_a_tensor_fail_cleanly():
     assert L.kore_qmv_matmul_batch_group_dev(5, None, None, 1, None, None) == qmv.KORE_QMV_E_INVALID
     assert L.kore_qmv_rmsnorm_rows_split_dev(None, None, 256, 1, 1e-6, None, None, None) == qmv.KORE_QMV_E_INVALID
     assert L.kore_qmv_matmul_batch_group_split_dev(1, None, None, 1, None, None, None) == qmv.KORE_QMV_E_INVALID
+    assert L.kore_qmv_matmul_batch_glu_split_dev(None, None, 1, None, None, None) == qmv.KORE_QMV_E_INVALID
     # the fp16 split: 256-column blocks of 67,840 bytes (64 activations: hi and lo fp16,
     # the sub-block sums and 1 / scale), widths up to 4096 only
     assert L.kore_qmv_split_bytes(3584) == 14 * 67840

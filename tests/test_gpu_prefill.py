@@ -118,6 +118,39 @@ def test_rmsnorm_split_then_matmul_is_bitwise_the_plain_pair(B, E):
             m.close()
 
 
+@pytest.mark.parametrize("B,rows,E", [(64, 18944, 3584), (1, 18944, 3584), (37, 700, 2048), (5, 512, 512)])
+def test_glu_matmul_is_bitwise_matmul_then_swiglu(B, rows, E):
+    """kore_qmv_matmul_batch_glu_split_dev (gate/up with the SwiGLU applied where
+    the split tiles are summed) against kore_qmv_matmul_batch_group_split_dev +
+    kore_qmv_swiglu_dev: every output bit for bit.  Shapes: the 7B gate/up, a
+    ragged last tile, and tiles that one worker runs whole (no partials)."""
+    from kore_amd import hip, qmv
+    if qmv.split_bytes(E) == 0:
+        pytest.skip("the split needs the fp16 matmul path")
+    _say(f"glu matmul, B {B}, {rows} x {E}")
+    rng = np.random.default_rng(71 + B)
+    gate, up = (_synth(oracle.TYPE_Q4K, rows, E, 1300 + k)[0] for k in range(2))
+    x = np.stack([_x(E, rng) for _ in range(B)])
+    nw = (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32)
+    dx, dw, xn = _up(x), _up(nw), _up(np.zeros((B, E)))
+    x16 = hip.DeviceBuffer(qmv.split_bytes(E) // 4)
+    g_a, u_a, g_b, tmp = (_up(np.zeros((B, rows))) for _ in range(4))
+    try:
+        qmv.rmsnorm_rows_split_dev(dx.ptr, dw.ptr, E, B, 1e-6, xn.ptr, x16.ptr)
+        qmv.matmul_batch_group_split_dev([gate, up], x16.ptr, B, [g_a.ptr, u_a.ptr])
+        qmv.swiglu_dev(g_a.ptr, u_a.ptr, B * rows)
+        qmv.matmul_batch_glu_split_dev(gate, up, x16.ptr, B, g_b.ptr, tmp.ptr)
+        hip.synchronize()
+        a, b = g_a.download(), g_b.download()
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(_bits(a), _bits(b)), f"{int(np.sum(_bits(a) != _bits(b)))} values differ"
+    finally:
+        for buf in [dx, dw, xn, x16, g_a, u_a, g_b, tmp]:
+            buf.free()
+        gate.close()
+        up.close()
+
+
 @pytest.mark.parametrize("B", [1, 13, 64])
 def test_matmul_epilogues(B):
     """bias and accumulate: the stores of the same launch without them, then
