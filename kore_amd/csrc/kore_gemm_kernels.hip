@@ -415,20 +415,33 @@ struct W16 {
     uint32_t d;
 };
 
+// Weight loads, non-temporal when nothing reads the same weights again (one
+// unit per tile): the streamed weights then leave the split activations in L2.
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_w4(const uint8_t *p, bool nt) {
+    const u32x4v v = nt ? __builtin_nontemporal_load((const u32x4v *)p) : *(const u32x4v *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_w2(const uint8_t *p, bool nt) {
+    const u32x2v v = nt ? __builtin_nontemporal_load((const u32x2v *)p) : *(const u32x2v *)p;
+    return make_uint2(v.x, v.y);
+}
+
 template <bool Q6>
-__device__ __forceinline__ void load_w16(W16<Q6> &g, const GemmMat &m, int row, int blk, int nblk, int h) {
+__device__ __forceinline__ void load_w16(W16<Q6> &g, const GemmMat &m, int row, int blk, int nblk, int h, bool nt) {
     if (!Q6 || m.type == kQ4K) {
         const uint8_t *b = m.w + ((int64_t)row * nblk + blk) * kQ4Bytes;
-        g.v[0] = *(const uint4 *)b;
+        g.v[0] = ld_w4(b, nt);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) g.v[1 + k] = *(const uint4 *)(b + 16 + 64 * h + 16 * k);
+        for (int k = 0; k < 4; ++k) g.v[1 + k] = ld_w4(b + 16 + 64 * h + 16 * k, nt);
     } else if constexpr (Q6) {
         const uint8_t *b = m.w + ((int64_t)row * nblk + blk) * kQ6Body;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) g.v[k] = *(const uint4 *)(b + 64 * h + 16 * k);
-        g.v[4] = *(const uint4 *)(b + 128 + 32 * h);
-        g.v[5] = *(const uint4 *)(b + 128 + 32 * h + 16);
-        g.sc = *(const uint2 *)(b + 192 + 8 * h);
+        for (int k = 0; k < 4; ++k) g.v[k] = ld_w4(b + 64 * h + 16 * k, nt);
+        g.v[4] = ld_w4(b + 128 + 32 * h, nt);
+        g.v[5] = ld_w4(b + 128 + 32 * h + 16, nt);
+        g.sc = ld_w2(b + 192 + 8 * h, nt);
         g.d = m.wd[(int64_t)row * nblk + blk];
     }
 }
@@ -680,7 +693,7 @@ __global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
     int tile = unit / hv, am = (unit % hv) * 32;
     int m = mat_of_tile(a, tile);
     W16<Q6> g;
-    load_w16<Q6>(g, a.m[m], row_of(tile, m), blk, nblk, h);
+    load_w16<Q6>(g, a.m[m], row_of(tile, m), blk, nblk, h, hv == 1);
     stage_unit(ls0, blk, am);
     __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0)
     __syncthreads();
@@ -695,7 +708,7 @@ __global__ __launch_bounds__(kG16Threads, 1) void gemm16_kernel(GemmArgs a) {
         if (it + 1 < it1) {                            // the next block's activations and weights
             stage_unit(nxt, nb, nam);
             m = ntile == tile ? m : mat_of_tile(a, ntile);
-            load_w16<Q6>(g, a.m[m], row_of(ntile, m), nb, nblk, h);
+            load_w16<Q6>(g, a.m[m], row_of(ntile, m), nb, nblk, h, hv == 1);
         }
         compute(cur, gc, cm, am);
         if (it + 1 == it1 || nb == 0) {                // end of this worker's part of the unit
