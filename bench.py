@@ -611,7 +611,9 @@ def gpu_prompt(qt, chunks: int, warmup: int):
     in 64-token chunks at positions 0, 64, ..: per chunk 28 layers through
     kore_layer_prefill_dev (rmsnorm rows, q/k/v matmul + bias, RoPE + append +
     causal attention, Wo + residual, rmsnorm rows, gate/up matmul, SwiGLU, down
-    + residual) and the last row's logits, driven from C++."""
+    + residual), and after the prompt's last chunk its last row's logits (kore's
+    prompt loop asks for logits on the last chunk only, kore.cpp:1727-1733),
+    driven from C++."""
     from kore_amd import KoreAttn, hip
     from kore_amd.layer import Layer
     from kore_amd.layer import lib as layer_lib
@@ -654,7 +656,8 @@ def prompt_report(p, mats):
         "workload": f"Qwen2.5-7B-shape prompt prefill as kore's forward_batch() runs it: {p['tokens']} tokens in "
                     f"{p['chunks']} chunks of 64 at positions 0, 64, .. (28 layers: rmsnorm rows, q/k/v batched "
                     "matmul + bias, RoPE + append + causal attention, Wo + residual, rmsnorm rows, gate/up matmul, "
-                    "SwiGLU, down + residual; then the last row's logits), synthetic Q4_K/Q6_K weights",
+                    "SwiGLU, down + residual; after the prompt's last chunk its last row's logits, as kore's "
+                    "prompt loop asks for them), synthetic Q4_K/Q6_K weights",
         "ms_per_chunk_gpu": round(s_chunk * 1e3, 3),
         "ms_per_chunk_wall": round(p["wall_ms"] / p["chunks"], 3),
         "tokens_per_s": round(PROMPT_NB / s_chunk, 1),
@@ -680,6 +683,7 @@ def cpu_prompt(seconds: float, threads: int):
             "sample": f"kore's own forward_batch() (kore.cpp:1486-1598, matmul_batch_float with AVX2: "
                       f"{bool(j['avx2'])}) built from kore.cpp with kore's flags, {j['threads']} threads, on a "
                       f"synthetic Qwen2.5-7B-shape engine: {j['chunks']} chunks of 64 tokens at positions 0..511 "
+                      f"in turn (logits after the 8-chunk prompt's last chunk, as kore's prompt loop asks for them) "
                       f"in {j['seconds']:.1f} s over {CPU_RUNS} timed runs (after one warm-up chunk; value = median run, "
                       f"best = fastest run); host {_cpu_model()}"}
 

@@ -54,11 +54,11 @@ KLB_API int klb_tokens(kore_layer_t L, const kore_layer_weights *w, int n_layer,
 }
 
 // kore's prompt prefill (forward_batch(), kore.cpp:1486-1598, as kore's prompt
-// loop calls it in 64-token chunks): chunk c's embedding rows emb[c * nb ..]
-// into x [nb][E], every layer through kore_layer_prefill_dev at positions
-// c * nb .., then the logits of the chunk's last row; `chunks` chunks, `reps`
-// times over the same positions.  Same timing outputs and return codes as
-// klb_tokens.
+// loop calls it in 64-token chunks, kore.cpp:1727-1733): chunk c's embedding
+// rows emb[c * nb ..] into x [nb][E], every layer through kore_layer_prefill_dev
+// at positions c * nb .., and after the prompt's last chunk the logits of its
+// last row (kore's want_logits = last); `chunks` chunks, `reps` times over the
+// same positions.  Same timing outputs and return codes as klb_tokens.
 KLB_API int klb_prefill(kore_layer_t L, const kore_layer_weights *w, int n_layer, kore_attn_t attn,
                         kore_qmv_tensor_t head, const float *out_norm, float eps, const float *emb, int E, int nb,
                         int chunks, float *x, float *logits, int reps, float *region_ms, double *wall_ms) {
@@ -83,7 +83,7 @@ KLB_API int klb_prefill(kore_layer_t L, const kore_layer_weights *w, int n_layer
             }
             for (int l = 0; l < n_layer && !rc; ++l) rc = kore_layer_prefill_dev(L, &w[l], attn, l, c * nb, nb, x, s);
             float *last = x + (size_t)(nb - 1) * E;
-            if (!rc) rc = kore_qmv_mv_group_ex_dev(1, &head, last, &ho, &logits, 1, s);
+            if (!rc && c == chunks - 1) rc = kore_qmv_mv_group_ex_dev(1, &head, last, &ho, &logits, 1, s);
         }
     }
     if (!rc) (void)hipEventRecord(ev[1], s);

@@ -202,8 +202,9 @@ int time_mode(unsigned nth, double min_s, int pos0, bool batch, int runs) {
             int c = 0;
             double t = 0;
             const auto t0 = std::chrono::steady_clock::now();
-            do {                                               // 64-token chunks at 0, 64, .., 448 in turn
-                if (!forward_batch(e, toks.data(), 64, 64 * (c % 8), true)) return 5;
+            do {                                               // 64-token chunks at 0, 64, .., 448 in turn;
+                // logits after the 8-chunk prompt's last chunk (kore's prefill loop, kore.cpp:1729-1730)
+                if (!forward_batch(e, toks.data(), 64, 64 * (c % 8), c % 8 == 7)) return 5;
                 ++c;
                 t = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
             } while (t < min_s);
