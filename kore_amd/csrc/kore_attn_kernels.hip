@@ -950,9 +950,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     const int qrow_c = min(qrow, a.n_tok - 1);
     const int qpos = a.pos0 + qrow_c;
 
-    // Q^T operand: qreg[4j+e] = roped q[qrow][8j + 4qg + e] * 1/sqrt(hd) * log2(e)
+    // Q^T operand: qreg[4j+e] = roped q[qrow][8j + 4qg + e] * 1/sqrt(hd) * log2(e),
+    // filled after the first key tile is requested (its loads then overlap q's)
     float qreg[HD / 2];
-    {
+    auto load_q = [&] {
         const float *qp = a.q + ((size_t)qrow_c * n_head + h) * HD;
         const float2 *cs = a.cs + (size_t)qpos * HALF;
 #pragma unroll
@@ -968,7 +969,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
                 qreg[4 * (j + HD / 16) + e2] = y1 * a.scale_log2;
             }
         }
-    }
+    };
 
     floatx16 acc[NT];
 #pragma unroll
@@ -1098,6 +1099,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     const int t_begin = part == 2 ? t_half : seg * a.seg_tiles;
     const int t_end = part == 1 ? t_half : (a.n_kseg == 1 ? n_tiles : min(n_tiles, t_begin + a.seg_tiles));
     if (t_begin < t_end) issue_tile(sK0, sV0, t_begin);
+    load_q();
     for (int t = t_begin; t < t_end; t += 2) {
         // this wave's loads of tile t have landed; after the barrier every
         // wave's have, and every wave is done with the other buffer
