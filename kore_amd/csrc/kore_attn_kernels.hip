@@ -680,7 +680,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const float *part_o,
 // Block (token z, kv-head g): k row rotated at position pos0+z and stored,
 // v row copied (kore.cpp:1536-1538).  Slot = position (a prefill never wraps).
 __global__ void append_kernel(AppendArgs a, int hd) {
-    const int z = blockIdx.x, g = blockIdx.y, half = hd / 2;
+    const int z = blockIdx.x * blockDim.y + threadIdx.y, g = blockIdx.y, half = hd / 2;
+    if (z >= a.n_tok) return;
     const int pos = a.pos0 + z;
     const float *kin = a.k + ((size_t)z * a.n_head_kv + g) * hd;
     const float *vin = a.v + ((size_t)z * a.n_head_kv + g) * hd;
@@ -1365,9 +1366,11 @@ hipError_t launch_decode(const DecodeArgs &a, const RopeRow &rr, int head_dim, h
 }
 
 hipError_t launch_append(const AppendArgs &a, int head_dim, hipStream_t s) {
-    const dim3 grid(a.n_tok, a.n_head_kv);
+    // four tokens per workgroup (threadIdx.y), a kv-head per blockIdx.y
+    constexpr int kTok = 4;
+    const dim3 grid((a.n_tok + kTok - 1) / kTok, a.n_head_kv);
     const int threads = head_dim / 2 >= 64 ? 64 : (head_dim / 2 > 0 ? head_dim / 2 : 1);
-    hipLaunchKernelGGL(append_kernel, grid, dim3(threads), 0, s, a, head_dim);
+    hipLaunchKernelGGL(append_kernel, grid, dim3(threads, kTok), 0, s, a, head_dim);
     return hipGetLastError();
 }
 
