@@ -66,9 +66,9 @@ TRAFFIC_PREFILL_BYTES = 138_660_000
 # of weights, activations and outputs algorithmic)
 TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_478_000}
 # the same for the batched matmul leg's dominant launch, ffn_gate + ffn_up of one layer on 64
-# activations (87.17 MB algorithmic), fp16 path: split pre-pass 3.98 MB, main kernel 124.4 MB
+# activations (87.17 MB algorithmic), fp16 path: split pre-pass 1.93 MB, main kernel 124.3 MB
 # (the partials of split tiles included), fix-up 35.1 MB
-TRAFFIC_GEMM_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 163_500_000}
+TRAFFIC_GEMM_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 161_290_000}
 FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix, published
 # MFMA passes per product of the fp16 batched matmul: Q4_K hi and lo parts of the
 # activations (the minimums' MFMA adds 1/32), Q6_K also the weights' integer remainder
