@@ -61,7 +61,7 @@ PF_N, PF_SEED = 2048, 3
 # (fetch x 2.0, write x 1.0): decode layer = split + combine kernel, prefill layer =
 # append + prefill + prefill combine kernel.  Re-measure when a kernel changes.
 TRAFFIC_DECODE_BYTES = 19_115_000
-TRAFFIC_PREFILL_BYTES = 138_660_000
+TRAFFIC_PREFILL_BYTES = 141_000_000
 # the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
 # of weights, activations and outputs algorithmic)
 TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_478_000}
