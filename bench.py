@@ -55,6 +55,7 @@ DEC_CTX, DEC_POS0 = 8192, 4096
 DEC_SEED, DEC_PER_MILLE, DEC_OUTLIER = 7, 10, 20.0
 DEC_STEPS = 128                # the configured decode steps (positions 4096..4223)
 PF_N, PF_SEED = 2048, 3
+WARM_SECONDS = 0.5             # least decode work ahead of the timed region (steady clocks)
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on these
 # kernels and workloads, each counter scaled by what it reads for a 256 MiB device copy
@@ -176,11 +177,17 @@ def gpu_decode(steps: int, warmup: int, extras: bool = True):
     attn.sync()
     out = hip.DeviceBuffer(steps * NL * E)
     wall, wall2, region = C.c_double(0), C.c_double(0), C.c_float(0)
-    if warmup:
-        _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, warmup, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr,
+    # warm-up: the requested steps, then more of them until WARM_SECONDS of decode work have run, so
+    # the timed region starts at the device's steady clocks whatever --warmup is
+    t_warm, warm_steps = time.perf_counter(), 0
+    while warm_steps < warmup or time.perf_counter() - t_warm < WARM_SECONDS:
+        n_w = max(1, min(warmup, steps)) if warmup else min(8, steps)
+        _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, n_w, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr,
                                 steps, None, None, C.byref(wall)), "decode warmup")
-    print(f"[bench] decode: {steps} timed steps x {NL} layers at positions {DEC_POS0}..", file=sys.stderr,
-          flush=True)
+        warm_steps += n_w
+    warm_s = time.perf_counter() - t_warm
+    print(f"[bench] decode: {steps} timed steps x {NL} layers at positions {DEC_POS0}.. (after {warm_steps} "
+          f"warm-up steps, {warm_s:.2f} s)", file=sys.stderr, flush=True)
     # the timed steps: host clock and one HIP event pair around the region
     _check(B.kab_decode_run(attn.handle, NL, DEC_POS0, 1, steps, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, steps,
                             None, C.byref(region), C.byref(wall)), "decode timed")
@@ -192,7 +199,7 @@ def gpu_decode(steps: int, warmup: int, extras: bool = True):
     if not extras:
         out.free()
         return dict(attn=attn, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value,
-                    buffers=(dq, dk, dv))
+                    buffers=(dq, dk, dv), warm_steps=warm_steps, warm_s=warm_s)
     # all 128 configured steps once more, untimed, for the parity check
     out.free()
     par = hip.DeviceBuffer(DEC_STEPS * NL * E)
@@ -213,7 +220,7 @@ def gpu_decode(steps: int, warmup: int, extras: bool = True):
     info = attn.info()
     return dict(attn=attn, outs=outs, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value,
                 num_cu=info.num_cu, buffers=(dq, dk, dv), host_us_per_layer=wall_h.value * 1e3 / (host_steps * NL),
-                host_steps=host_steps)
+                host_steps=host_steps, warm_steps=warm_steps, warm_s=warm_s)
 
 
 def gpu_prefill(steps: int, warmup: int):
@@ -277,9 +284,12 @@ def _fill_cache(attn, n_layer, rows, kvd, seed, stream):
     vb.free()
 
 
-def _decode_leg(attn, n_layer, pos_first, pos_step, steps, warmup, nh, nkv, hd, seed, attended):
+def _decode_leg(attn, n_layer, pos_first, pos_step, steps, warmup, nh, nkv, hd, seed, attended, keep_outs=False):
     """Timed decode steps (one kore_attn_decode_dev per layer and step);
-    `attended(s)` is the number of positions step s attends."""
+    `attended(s)` is the number of positions step s attends.  keep_outs: the
+    outputs of the steps in order from the cache as it is on entry ([steps][layer][E];
+    one untimed pass ahead of the warm-up when the steps move, the timed
+    region's last outputs when they repeat one position)."""
     from kore_amd import hip, synth_dev
     B = _bench_lib()
     st = attn.stream
@@ -294,11 +304,23 @@ def _decode_leg(attn, n_layer, pos_first, pos_step, steps, warmup, nh, nkv, hd, 
     attn.sync()
     out = hip.DeviceBuffer(n_layer * E_)
     wall, wall2, region = C.c_double(0), C.c_double(0), C.c_float(0)
-    if warmup:
-        _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, warmup, dq.ptr, dk.ptr, dv.ptr, n_in,
-                                out.ptr, 1, None, None, C.byref(wall)), "decode warmup")
+    outs = None
+    if keep_outs and pos_step:
+        par = hip.DeviceBuffer(steps * n_layer * E_)
+        _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, steps, dq.ptr, dk.ptr, dv.ptr, n_in,
+                                par.ptr, steps, None, None, C.byref(wall)), "decode parity pass")
+        outs = par.download().reshape(steps, n_layer, E_)
+        par.free()
+    t_warm = time.perf_counter()
+    while True:
+        _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, max(warmup, 1), dq.ptr, dk.ptr, dv.ptr,
+                                n_in, out.ptr, 1, None, None, C.byref(wall)), "decode warmup")
+        if time.perf_counter() - t_warm >= WARM_SECONDS / 2:
+            break
     _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, steps, dq.ptr, dk.ptr, dv.ptr, n_in,
                             out.ptr, 1, None, C.byref(region), C.byref(wall)), "decode timed")
+    if keep_outs and not pos_step:
+        outs = out.download().reshape(1, n_layer, E_)
     lm = np.zeros(steps * n_layer, np.float32)
     _check(B.kab_decode_run(attn.handle, n_layer, pos_first, pos_step, steps, dq.ptr, dk.ptr, dv.ptr, n_in,
                             out.ptr, 1, lm.ctypes.data, None, C.byref(wall2)), "decode per-launch events")
@@ -307,33 +329,86 @@ def _decode_leg(attn, n_layer, pos_first, pos_step, steps, warmup, nh, nkv, hd, 
     nbytes = sum(_decode_bytes_geom(attended(s), nh, nkv, hd) for s in range(steps)) * n_layer
     mean_s = region.value / 1e3 / (steps * n_layer)
     ach = nbytes / (steps * n_layer) / mean_s / 1e9
-    return {"us_per_layer_gpu": round(mean_s * 1e6, 3), "launch_us_median": round(float(np.median(lm)) * 1e3, 3),
-            "gbs_wall": round(nbytes / (wall.value / 1e3) / 1e9, 2),
-            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ach / HBM_PEAK_GBS, 4)}}
+    res = {"us_per_layer_gpu": round(mean_s * 1e6, 3), "launch_us_median": round(float(np.median(lm)) * 1e3, 3),
+           "gbs_wall": round(nbytes / (wall.value / 1e3) / 1e9, 2),
+           "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4)}}
+    return res, outs
 
 
-def gpu_other_workloads(quick: bool):
+def _parity_decode_layers(n_layer, rows, nh, nkv, hd, seed, pos_first, outs, threads, window=0, kv_rows=None):
+    """The oracle's decode (kore.cpp:1405-1455; with `window`, the last
+    `window` positions of a ring) for every layer of a workload whose cache
+    rows 0..rows-1 were filled through the append path from synth(seed) and
+    whose steps s decode position pos_first + s with synth(seed) inputs:
+    max|d|/max|ref| over outs [steps][layer][E].  kv_rows(l) (optional) returns
+    the GPU's K and V rows 0..rows (the decoded row included) of layer l, held
+    bit for bit to the oracle's."""
+    import oracle
+    n_steps = outs.shape[0]
+    E_, kvd = nh * hd, nkv * hd
+    inv_f = oracle.inv_freq(hd, ROPE_BASE)
+    ctx = window if window else rows + n_steps
+
+    def layer(l):
+        kv = oracle.KV(1, ctx, nh, nkv, hd, ROPE_BASE, window=window)
+        k0 = oracle.synth(rows, kvd, seed, k_stream(l), 0, 2)
+        kv.kcache()[0, :rows] = oracle.rope_rows(k0, np.arange(rows), nkv, hd, inv_f)
+        kv.vcache()[0, :rows] = oracle.synth(rows, kvd, seed, v_stream(l), 0, 3)
+        q = oracle.synth(n_steps, E_, seed, q_stream(l), pos_first, 1)
+        k = oracle.synth(n_steps, kvd, seed, k_stream(l), pos_first, 2)
+        v = oracle.synth(n_steps, kvd, seed, v_stream(l), pos_first, 3)
+        errs = [_rel_err(outs[s, l], kv.decode(0, pos_first + s, q[s], k[s], v[s])) for s in range(n_steps)]
+        digest = _kv_digest(kv.kcache()[0], kv.vcache()[0]) if kv_rows is not None else None
+        kv.close()
+        return errs, digest
+
+    res = _pool(layer, range(n_layer), threads)
+    e = np.array([r[0] for r in res])
+    out = {"max_rel_err": float(e.max()), "layers": n_layer, "steps": n_steps}
+    if kv_rows is not None:   # one caller per handle: the GPU rows are read on this thread
+        out["kv_bitwise"] = all(_kv_digest(*kv_rows(l)) == r[1] for l, r in enumerate(res))
+    return out
+
+
+def _kv_digest(k, v):
+    import hashlib
+    return hashlib.sha256(np.ascontiguousarray(k).tobytes()).hexdigest() + \
+        hashlib.sha256(np.ascontiguousarray(v).tobytes()).hexdigest()
+
+
+def gpu_other_workloads(quick: bool, parity_threads: int = 0):
     """The other attention workloads of the path, each on its own handle:
     0.5B single-layer decode at 511, 3B decode at 32767 over 36 layers, 1.5B
-    1024-row chunk at 7168 then sliding-window decode at ctx 8192."""
+    1024-row chunk at 7168 then sliding-window decode at ctx 8192.  With
+    parity_threads > 0 each is also compared with the oracle on that many host
+    threads (every layer, every step; the 1.5B chunk's every row on four
+    layers), returned as the second value."""
+    import oracle
     from kore_amd import KoreAttn, hip, synth_dev
     B = _bench_lib()
-    res = {}
+    res, par = {}, {}
     reps = 20 if quick else 50
     # 0.5B: 14/2/64, one layer, cache 0..510, decode at 511
     with KoreAttn(1, 512, 14, 2, 64, ROPE_BASE) as a:
         _fill_cache(a, 1, 511, 128, 11, a.stream)
-        r = _decode_leg(a, 1, 511, 0, reps * 10, 10, 14, 2, 64, 11, lambda s: 512)
+        r, outs = _decode_leg(a, 1, 511, 0, reps * 10, 10, 14, 2, 64, 11, lambda s: 512, keep_outs=True)
         r["workload"] = "Qwen2.5-0.5B-shape decode, 1 layer, 14/2/64, position 511 (cache 0..510)"
         res["decode_0p5b_pos511"] = r
+        if parity_threads:
+            par["c1_decode_0p5b"] = _parity_decode_layers(1, 511, 14, 2, 64, 11, 511, outs, 1,
+                                                          kv_rows=lambda l: a.read_kv(l, 0, 512))
     print("[bench] 0.5B decode done", file=sys.stderr, flush=True)
     # 3B: 16/2/128, 36 layers, ctx 32768, decode at 32767
     with KoreAttn(36, 32768, 16, 2, 128, ROPE_BASE) as a:
         _fill_cache(a, 36, 32767, 256, 9, a.stream)
-        r = _decode_leg(a, 36, 32767, 0, reps, 2, 16, 2, 128, 9, lambda s: 32768)
+        r, outs = _decode_leg(a, 36, 32767, 0, reps, 2, 16, 2, 128, 9, lambda s: 32768, keep_outs=True)
         r["workload"] = "Qwen2.5-3B-shape decode, 36 layers, 16/2/128, position 32767 (cache 0..32766)"
         res["decode_3b_pos32767"] = r
+        if parity_threads:
+            par["c4_decode_3b"] = _parity_decode_layers(36, 32767, 16, 2, 128, 9, 32767, outs,
+                                                        min(parity_threads, 8),
+                                                        kv_rows=lambda l: a.read_kv(l, 0, 32768))
     print("[bench] 3B decode done", file=sys.stderr, flush=True)
     # 1.5B: 12/2/128, 28 layers, ring of 8192 slots
     nl, nh, nkv, hd, W, c0, cn = 28, 12, 2, 128, 8192, 7168, 1024
@@ -355,6 +430,9 @@ def gpu_other_workloads(quick: bool):
         lm = np.zeros(P * nl, np.float32)
         _check(B.kab_prefill_run(a.handle, nl, c0, cn, P, dq.ptr, dk.ptr, dv.ptr, out.ptr, lm.ctypes.data,
                                  C.byref(region), C.byref(wall)), "chunk timed")
+        chunk_layers = (0, 9, 18, 27)
+        chunk_outs = {l: out.download(cn * E_, offset=l * cn * E_).reshape(cn, E_) for l in chunk_layers} \
+            if parity_threads else None
         for b in (dq, dk, dv, out):
             b.free()
         F = _prefill_flops_geom(c0, cn, nh, hd)
@@ -363,13 +441,34 @@ def gpu_other_workloads(quick: bool):
         chunk = {"us_per_layer_gpu": round(per_s * 1e6, 2), "flop_per_layer": F,
                  "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
                               "unit": "TFLOP/s", "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4)}}
-        dec = _decode_leg(a, nl, W, 1, 256, 8, nh, nkv, hd, 5, lambda s: W)
+        dec, outs = _decode_leg(a, nl, W, 1, 256, 8, nh, nkv, hd, 5, lambda s: W, keep_outs=bool(parity_threads))
         res["chunk_1p5b_1024_at_7168"] = dict(chunk, workload="Qwen2.5-1.5B-shape causal prefill chunk, 28 layers, "
                                                               "12/2/128, 1024 rows at 7168 onto 7168 cached rows")
         res["decode_1p5b_sliding_8192"] = dict(dec, workload="Qwen2.5-1.5B-shape decode, 28 layers, ring of 8192 "
                                                              "slots, 256 steps at positions 8192..8447")
+    if parity_threads:
+        # the chunk: every row of four layers against the oracle's batched attention
+        # (kore's AVX2 hd_dot / hd_fma arithmetic), 64-row pieces on the host threads
+        inv_f = oracle.inv_freq(hd, ROPE_BASE)
+
+        def chunk_piece(item):
+            l, z0 = item
+            k = np.concatenate([oracle.synth(c0, kvd, 5, k_stream(l), 0, 2),
+                                oracle.synth(cn, kvd, 5, k_stream(l), c0, 2)])
+            v = np.concatenate([oracle.synth(c0, kvd, 5, v_stream(l), 0, 3),
+                                oracle.synth(cn, kvd, 5, v_stream(l), c0, 3)])
+            K = oracle.rope_rows(k[:c0 + z0 + 64], np.arange(c0 + z0 + 64), nkv, hd, inv_f)
+            q = oracle.synth(64, E_, 5, q_stream(l), c0 + z0, 1)
+            qr = oracle.rope_rows(q, np.arange(c0 + z0, c0 + z0 + 64), nh, hd, inv_f)
+            ref = oracle.attn_batch(qr, c0 + z0, K, v[:c0 + z0 + 64], nh, nkv, hd, avx2=True)
+            return _rel_err(chunk_outs[l][z0:z0 + 64], ref)
+
+        errs = _pool(chunk_piece, [(l, z0) for l in chunk_layers for z0 in range(0, cn, 64)], parity_threads)
+        par["c5_chunk_1p5b"] = {"max_rel_err": float(max(errs)), "layers": list(chunk_layers), "rows": cn}
+        par["c5_sliding_decode_1p5b"] = _parity_decode_layers(nl, c0 + cn, nh, nkv, hd, 5, W, outs,
+                                                              parity_threads, window=W)
     print("[bench] 1.5B chunk + sliding decode done", file=sys.stderr, flush=True)
-    return res
+    return res, par
 
 
 class _KqbOp(C.Structure):
@@ -675,7 +774,7 @@ def cpu_prompt(seconds: float, threads: int):
     if not os.path.exists(oracle.REF_LAYER_BIN):
         return None
     r = subprocess.run([oracle.REF_LAYER_BIN, "--time-batch", str(threads), str(seconds / CPU_RUNS), str(CPU_RUNS)],
-                       capture_output=True, text=True, check=True)
+                       capture_output=True, text=True, check=True, timeout=seconds + 300)
     j = json.loads(r.stdout)
     st = _runs([64 * c / t for c, t in zip(j["run_chunks"], j["run_seconds"])], "tokens/s")
     return {"value": round(st["median"], 3), "unit": "tokens/s", "cores": j["threads"], "kind": "reference",
@@ -718,7 +817,7 @@ def cpu_token(seconds: float, threads: int):
     if not os.path.exists(oracle.REF_LAYER_BIN):
         return None
     r = subprocess.run([oracle.REF_LAYER_BIN, "--time", str(threads), str(seconds / CPU_RUNS), str(DEC_POS0),
-                        str(CPU_RUNS)], capture_output=True, text=True, check=True)
+                        str(CPU_RUNS)], capture_output=True, text=True, check=True, timeout=seconds + 300)
     j = json.loads(r.stdout)
     st = _runs([n / t for n, t in zip(j["run_tokens"], j["run_seconds"])], "tokens/s")
     return {"value": round(st["median"], 3), "unit": "tokens/s", "cores": j["threads"], "kind": "reference",
@@ -741,7 +840,7 @@ def kore_token_dropin(seconds: float, threads: int):
     if not os.path.exists(oracle.REF_LAYER_GPU_BIN):
         return None
     r = subprocess.run([oracle.REF_LAYER_GPU_BIN, "--time", str(threads), str(seconds / CPU_RUNS), str(DEC_POS0),
-                        str(CPU_RUNS)], capture_output=True, text=True, check=True)
+                        str(CPU_RUNS)], capture_output=True, text=True, check=True, timeout=seconds + 300)
     j = json.loads(r.stdout)
     st = _runs([n / t for n, t in zip(j["run_tokens"], j["run_seconds"])], "tokens/s")
     return {"value": round(st["median"], 3), "unit": "tokens/s", "threads": j["threads"], "best": round(st["best"], 3),
@@ -875,7 +974,7 @@ def cpu_matvec(seconds: float, threads: int):
                 f.write(w.tobytes())
                 f.write(x.tobytes())
             r = subprocess.run([oracle.REF_QMV_BIN, "--time", str(threads), str(seconds / CPU_RUNS), "16", job,
-                                str(CPU_RUNS)], capture_output=True, text=True, check=True)
+                                str(CPU_RUNS)], capture_output=True, text=True, check=True, timeout=seconds + 300)
         j = json.loads(r.stdout)
         st = _runs([j["weight_bytes"] * n / t / 1e9 for n, t in zip(j["run_reps"], j["run_seconds"])], "GB/s")
         return {"value": round(st["median"], 2), "unit": "GB/s", "cores": j["threads"], "kind": "reference",
@@ -920,7 +1019,7 @@ def cpu_gemm(seconds: float, threads: int):
                 f.write(w.tobytes())
                 f.write(x.tobytes())
             r = subprocess.run([oracle.REF_QMV_BIN, "--time-batch", str(threads), str(seconds / CPU_RUNS), job,
-                                str(CPU_RUNS)], capture_output=True, text=True, check=True)
+                                str(CPU_RUNS)], capture_output=True, text=True, check=True, timeout=seconds + 300)
         j = json.loads(r.stdout)
         st = _runs([flop * n / t / 1e12 for n, t in zip(j["run_reps"], j["run_seconds"])], "TFLOP/s")
         return {"value": round(st["median"], 5), "unit": "TFLOP/s", "cores": j["threads"], "kind": "reference",
@@ -976,6 +1075,41 @@ def read_calibration():
     out["empty_launch_us"] = round(us.value, 3)
     buf.free()
     sink.free()
+    return out
+
+
+def decode_floor(nbytes: int, rounds: int):
+    """What the device allows for the decode layer's launch pattern, measured
+    in the same run: each round one launch that reads the layer's algorithmic
+    bytes once (every load issued up front; 1, 2, 4 or 8 16-byte loads per
+    thread, the fastest kept) and one dependent empty launch, back to back,
+    over NL rotated buffers as the decode rotates its layers (NL x 17 MB, more
+    than the 256 MB MALL).  Also the read launches alone."""
+    from kore_amd import hip, qmv
+    qmv.lib()
+    B = C.CDLL(os.path.join(ROOT, "kore_amd", "libkore_qmv_bench.so"))
+    B.kqb_floor_probe.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                  C.POINTER(C.c_float)]
+    nb = (int(nbytes) + 15) // 16 * 16
+    buf = hip.DeviceBuffer(nb * NL // 4)
+    hip.check(hip.lib().hipMemset(buf.ptr, 1, nb * NL), "hipMemset")
+    sink = hip.DeviceBuffer(nb // 16 + 256)
+    us = C.c_float(0)
+    out = {}
+    for with_launch, key in ((1, "read_plus_dependent_launch_us"), (0, "read_only_us")):
+        per_us = {}
+        for per in (1, 2, 4, 8):
+            rc = B.kqb_floor_probe(buf.ptr, nb, NL, per, with_launch, rounds, sink.ptr, C.byref(us))
+            if rc != 0:
+                raise RuntimeError(f"kqb_floor_probe failed ({rc})")
+            per_us[per] = round(us.value, 3)
+        best = min(per_us, key=per_us.get)
+        out[key] = per_us[best]
+        out[key.replace("_us", "_loads_per_thread")] = best
+    buf.free()
+    sink.free()
+    out["bytes"] = nb
+    out["rounds"] = rounds
     return out
 
 
@@ -1242,7 +1376,11 @@ def main(argv=None):
     if not args.no_prefill:
         pf = gpu_prefill(args.prefill_steps, args.prefill_warmup)
     dec = gpu_decode(args.steps, args.warmup)
-    other = None if args.no_other else gpu_other_workloads(quick=args.steps < 64)
+    mean_bytes = sum(decode_bytes(DEC_POS0 + s + 1) for s in range(args.steps)) / args.steps
+    print("[bench] decode floor: read of the layer's bytes + one dependent launch", file=sys.stderr, flush=True)
+    floor = decode_floor(mean_bytes, max(args.steps * NL, 64 * NL))
+    other, other_par = (None, {}) if args.no_other else gpu_other_workloads(
+        quick=args.steps < 64, parity_threads=0 if args.no_cpu else args.cpu_threads)
     qt = None if (args.no_matvec and args.no_gemm) else qmv_tensors()
     mv = None if args.no_matvec else gpu_matvec(qt, args.matvec_tokens, args.matvec_warmup)
     gm = None if args.no_gemm else gpu_gemm(qt, args.gemm_chunks, args.gemm_warmup)
@@ -1285,6 +1423,10 @@ def main(argv=None):
         "decode": {
             "us_per_layer_gpu": round(mean_launch_s * 1e6, 3),
             "us_per_layer_wall": round(dec["wall_ms"] / (K * NL) * 1e3, 3),
+            "warmup_steps_run": dec["warm_steps"], "warmup_seconds": round(dec["warm_s"], 3),
+            "floor": dict(floor, layer_over_floor=round(mean_launch_s * 1e6 / floor["read_plus_dependent_launch_us"], 3),
+                          note="same run: one launch reading the layer's mean algorithmic bytes once plus one "
+                               "dependent empty launch per round, 28 rotated buffers; the decode layer's time over it"),
             "launch_us_events": {k: round(v * 1e3, 3) for k, v in _stats(lm).items()},
             "bytes_per_launch_mean": int(bytes_per_launch),
             "host_pointer_us_per_layer": round(dec["host_us_per_layer"], 3),
@@ -1339,6 +1481,7 @@ def main(argv=None):
         print(f"[bench] parity: {DEC_STEPS} decode steps x {NL} layers against the oracle and float64, "
               f"{args.cpu_threads} host threads", file=sys.stderr, flush=True)
         res["parity"] = dict(decode_parity(dec["outs"], dec["attn"], args.cpu_threads), tolerance=1e-4)
+        res["parity"].update(other_par)
         print(f"[bench] cpu baseline: decode ({CPU_RUNS} runs, {args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
         cd = cpu_decode(args.cpu_seconds)
         host = _host()
@@ -1403,8 +1546,45 @@ def main(argv=None):
             res["parity"]["prefill_max_rel_err"] = cp["max_rel_err"]
             res["parity"]["prefill_layers_compared"] = CPU_RUNS
     dec["attn"].close()
+    res["summary"] = _summary(res)
     print(json.dumps(res), flush=True)
     return 0
+
+
+def _summary(res):
+    """The figures of every leg in a few hundred bytes, last on the line (a
+    truncated tail of the output still shows them)."""
+    def g(*path):
+        d = res
+        for k in path:
+            if not isinstance(d, dict) or k not in d:
+                return None
+            d = d[k]
+        return d
+    par = res.get("parity", {})
+    out = {
+        "c2_decode_7b_us_per_layer": g("decode", "us_per_layer_gpu"),
+        "c2_floor_us": g("decode", "floor", "read_plus_dependent_launch_us"),
+        "c2_over_floor": g("decode", "floor", "layer_over_floor"),
+        "c2_frac": g("roofline", "frac"),
+        "c3_prefill_7b_us_per_layer": g("prefill", "us_per_layer_gpu"),
+        "c3_frac": g("prefill", "roofline", "frac"),
+        "c1_decode_0p5b_us": g("other_workloads", "decode_0p5b_pos511", "us_per_layer_gpu"),
+        "c4_decode_3b_us_per_layer": g("other_workloads", "decode_3b_pos32767", "us_per_layer_gpu"),
+        "c4_frac": g("other_workloads", "decode_3b_pos32767", "roofline", "frac"),
+        "c5_chunk_1p5b_us_per_layer": g("other_workloads", "chunk_1p5b_1024_at_7168", "us_per_layer_gpu"),
+        "c5_chunk_frac": g("other_workloads", "chunk_1p5b_1024_at_7168", "roofline", "frac"),
+        "c5_sliding_decode_us_per_layer": g("other_workloads", "decode_1p5b_sliding_8192", "us_per_layer_gpu"),
+        "token_ms": g("token", "ms_per_token_gpu"),
+        "prompt_ms_per_chunk": g("prompt", "ms_per_chunk_gpu"),
+        "matvec_ms_per_token": g("matvec", "ms_per_token_gpu"),
+        "gemm_ms_per_chunk": g("gemm", "ms_per_chunk_gpu"),
+        "parity_max_rel_err": {k: (par[k].get("max_rel_err") if isinstance(par.get(k), dict) else None)
+                               for k in ("c1_decode_0p5b", "c4_decode_3b", "c5_chunk_1p5b", "c5_sliding_decode_1p5b")},
+    }
+    out["parity_max_rel_err"]["c2_decode_7b"] = par.get("decode_max_rel_err")
+    out["parity_max_rel_err"]["c3_prefill_7b"] = par.get("prefill_max_rel_err")
+    return out
 
 
 if __name__ == "__main__":

@@ -194,8 +194,10 @@ KORE_QMV_API int kore_qmv_matmul_batch_glu_split_dev(const kore_qmv_tensor_t *ga
                                                      float *out, float *tmp, void *stream);
 
 /* kore_qmv_matmul_batch_group_ex_dev on the split x16 of nb activations
- * (written by kore_qmv_rmsnorm_rows_split_dev, kept unchanged since) instead
- * of x: the same results, bit for bit. */
+ * (written by kore_qmv_rmsnorm_rows_split_dev for the same cols as the
+ * tensors', kept unchanged since) instead of x: the same results, bit for bit.
+ * KORE_QMV_E_UNSUPPORTED when the tensors' cols have no split
+ * (kore_qmv_split_bytes(cols) == 0); the same for the glu call above. */
 KORE_QMV_API int kore_qmv_matmul_batch_group_split_dev(int n, const kore_qmv_tensor_t *t, const void *x16, int nb,
                                                        const kore_qmv_mv_opts *opts, float *const *out, void *stream);
 

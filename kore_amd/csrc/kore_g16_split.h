@@ -15,12 +15,19 @@
 
 namespace kore_qmv_gpu {
 
-// The row's power of two s (max |y s| < 2^10 for amax = max |y|) and 1 / s.
-__device__ __forceinline__ void g16_split_scale(float amax, float &s, float &inv) {
-    int e;
-    (void)frexpf(amax, &e);                            // amax < 2^e (0 for amax = 0)
-    e = max(e, -100);
-    s = ldexpf(1.f, 10 - e);
+// The row's power of two s = s1 * s2 (max |y s| < 2^10 for amax = max |y|;
+// callers scale as (y * s1) * s2, both factors powers of two, so the product is
+// exact) and 1 / s.  s reaches 2^149 for rows whose maximum is a subnormal
+// float (s1 alone would overflow above 2^127; s2 is 1 for every row whose
+// maximum is at least 2^-117); 1 / s stays a float down to 2^-149.  A row with
+// an infinite or NaN value takes s = 2^10: its products are non-finite anyway.
+__device__ __forceinline__ void g16_split_scale(float amax, float &s1, float &s2, float &inv) {
+    int e = 0;
+    if (amax <= 3.40282347e38f) (void)frexpf(amax, &e);   // amax < 2^e (0 for amax = 0)
+    e = max(e, -139);
+    const int sh = 10 - e, sh1 = min(sh, 127);
+    s1 = ldexpf(1.f, sh1);
+    s2 = ldexpf(1.f, sh - sh1);
     inv = ldexpf(1.f, e - 10);
 }
 

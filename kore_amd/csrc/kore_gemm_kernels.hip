@@ -396,12 +396,12 @@ __global__ __launch_bounds__(kPrepThreads) void gemm16_prep_kernel(const float *
     amax = red[0];
 #pragma unroll
     for (int k = 1; k < kPrepThreads / 64; ++k) amax = fmaxf(amax, red[k]);
-    float s, inv;
-    g16_split_scale(amax, s, inv);
+    float s1, s2, inv;
+    g16_split_scale(amax, s1, s2, inv);
 #pragma unroll
     for (int j = 0; j < kPrepPer; ++j) {
         if (t + j * kPrepThreads >= n4) break;         // whole waves: n4 is a multiple of 64
-        const float ys[4] = {v[j].x * s, v[j].y * s, v[j].z * s, v[j].w * s};
+        const float ys[4] = {(v[j].x * s1) * s2, (v[j].y * s1) * s2, (v[j].z * s1) * s2, (v[j].w * s1) * s2};
         g16_split_group(x16, b, (t + j * kPrepThreads) >> 6, lane, ys, inv);
     }
 }

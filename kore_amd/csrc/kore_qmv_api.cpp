@@ -49,22 +49,23 @@ int hip_fail(kore_qmv_tensor *t, hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail((t), e_, #call);  \
     } while (0)
 
-// Per-device workspace of the batched matmul: the partial sums of split tiles,
-// sized for the largest grid at the first tensor creation, and the fp16 split
-// of the activations, sized for the widest tensor created so far (grown at a
-// tensor creation, after the device has finished its work, never inside a
-// call).  Calls on one device share it: they must not overlap.
+// Per-device workspace of the batched matmul, allocated once, at the first
+// tensor creation on the device, and kept until the process ends: the partial
+// sums of split tiles, sized for the largest grid, and the fp16 split of the
+// activations, sized for the widest tensor any call accepts (kMaxBlocks
+// blocks, 8.7 MB).  Neither is ever freed or regrown, so a launch enqueued
+// from any thread, or captured in a graph, never holds a stale pointer.
+// Calls on one device share it: they must not overlap.
 struct GemmScratch {
     std::mutex mu;
     float *partials = nullptr;
     uint8_t *x16 = nullptr;
-    int x16_nblk = 0;
 };
 GemmScratch g_gemm[64];
 
 int row_tiles(int64_t rows) { return (int)((rows + gemm_rows_per_tile() - 1) / gemm_rows_per_tile()); }
 
-hipError_t gemm_scratch_reserve(int dev, int num_cu, int nblk) {
+hipError_t gemm_scratch_reserve(int dev, int num_cu) {
     GemmScratch &g = g_gemm[dev];
     std::lock_guard<std::mutex> lock(g.mu);
     hipError_t e = hipSuccess;
@@ -75,15 +76,8 @@ hipError_t gemm_scratch_reserve(int dev, int num_cu, int nblk) {
         const size_t bytes = (size_t)2 * gemm_max_workers(num_cu) * kGemmSlotFloats * sizeof(float);
         if ((e = hipMalloc((void **)&g.partials, bytes)) != hipSuccess) return e;
     }
-    if (nblk > g.x16_nblk) {
-        if (g.x16) {
-            if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-            (void)hipFree(g.x16);
-            g.x16 = nullptr;
-            g.x16_nblk = 0;
-        }
-        if ((e = hipMalloc((void **)&g.x16, (size_t)nblk * kG16BlockBytes)) != hipSuccess) return e;
-        g.x16_nblk = nblk;
+    if (!g.x16) {
+        if ((e = hipMalloc((void **)&g.x16, (size_t)kMaxBlocks * kG16BlockBytes)) != hipSuccess) return e;
     }
     return hipSuccess;
 }
@@ -201,7 +195,7 @@ KORE_QMV_API int kore_qmv_tensor_create(kore_qmv_tensor_t *out, int type, int64_
     t->rows_per_wave = pick_rows_per_wave(rows, t->nblk, num_cu);
     if ((e = hipMalloc(&t->xq, (size_t)t->nblk * 308)) != hipSuccess) return bail(hip_fail(t, e, "hipMalloc"));
     if (t->device < 0 || t->device >= 64) return bail(fail(t, KORE_QMV_E_UNSUPPORTED, "device ordinal above 63"));
-    if ((e = gemm_scratch_reserve(t->device, num_cu, t->nblk)) != hipSuccess)
+    if ((e = gemm_scratch_reserve(t->device, num_cu)) != hipSuccess)
         return bail(hip_fail(t, e, "matmul workspace"));
 
     const int64_t nblocks = rows * t->nblk;
@@ -411,6 +405,10 @@ int matmul_group(int n, const kore_qmv_tensor_t *t, const float *x, const void *
             if (int rc = check_dev_ptr(t0, opts->bias[k], 4, "bias")) return rc;
     if (x16) {
         if (!gemm_fp16()) return fail(t0, KORE_QMV_E_UNSUPPORTED, "split activations need the fp16 matmul path");
+        // a caller's split holds kore_qmv_split_bytes(cols) bytes: only tensors
+        // whose cols have a split (at most 16 blocks) may read one
+        if (kore_qmv_split_bytes(t0->cols) == 0)
+            return fail(t0, KORE_QMV_E_UNSUPPORTED, "split activations exist only for cols 256..4096");
         if (int rc = check_dev_ptr(t0, x16, 16, "x16")) return rc;
     } else if (int rc = check_dev_ptr(t0, x, 16, "x")) {
         return rc;
@@ -438,7 +436,6 @@ int matmul_group(int n, const kore_qmv_tensor_t *t, const float *x, const void *
     a.partials = g.partials;
     a.x16 = x16 ? (uint8_t *)x16 : g.x16;
     a.presplit = x16 ? 1 : 0;
-    if (!x16 && g.x16_nblk < a.nblk) return fail(t0, KORE_QMV_E_INVALID, "matmul workspace narrower than the tensor");
     hipError_t e = launch_gemm(a, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(t0, e, "matmul launch");
     return KORE_QMV_OK;

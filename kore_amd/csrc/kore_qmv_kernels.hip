@@ -1028,12 +1028,12 @@ __device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, 
     if (lane == 0) fred[t >> 6] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
-    float s, inv;
-    g16_split_scale(amax, s, inv);
+    float s1, s2, inv;
+    g16_split_scale(amax, s1, s2, inv);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         if (t + j * kThreads >= n4) break;             // whole waves: n4 is a multiple of 64
-        const float ys[4] = {y[j].x * s, y[j].y * s, y[j].z * s, y[j].w * s};
+        const float ys[4] = {(y[j].x * s1) * s2, (y[j].y * s1) * s2, (y[j].z * s1) * s2, (y[j].w * s1) * s2};
         g16_split_group(x16, b, (t + j * kThreads) >> 6, lane, ys, inv);
     }
 }

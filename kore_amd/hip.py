@@ -104,10 +104,13 @@ class DeviceBuffer:
         assert a.size <= self.n
         check(lib().hipMemcpy(self.ptr, a.ctypes.data, a.nbytes, H2D), "hipMemcpy H2D")
 
-    def download(self, n: int | None = None) -> np.ndarray:
-        n = self.n if n is None else n
+    def download(self, n: int | None = None, offset: int = 0) -> np.ndarray:
+        """n floats (all from offset by default) starting `offset` floats in."""
+        n = self.n - offset if n is None else n
+        if offset < 0 or n < 0 or offset + n > self.n:
+            raise ValueError("download range outside the buffer")
         out = np.empty(n, np.float32)
-        check(lib().hipMemcpy(out.ctypes.data, self.ptr, n * 4, D2H), "hipMemcpy D2H")
+        check(lib().hipMemcpy(out.ctypes.data, self.ptr + 4 * offset, n * 4, D2H), "hipMemcpy D2H")
         return out
 
     def at(self, offset_floats: int) -> int:

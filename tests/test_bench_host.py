@@ -166,3 +166,62 @@ def test_reference_timing_runs():
     j = json.loads(out)
     assert len(j["run_reps"]) == 3 and len(j["run_seconds"]) == 3
     assert sum(j["run_reps"]) == j["reps"] and all(t >= 0.02 for t in j["run_seconds"])
+
+
+def _small_decode_outs(n_layer, rows, nh, nkv, hd, seed, pos_first, n_steps, window=0):
+    """The oracle's own outputs of a small decode workload laid out as the
+    bench's other-workload legs fill and decode it."""
+    import oracle
+    kvd, E_ = nkv * hd, nh * hd
+    inv_f = oracle.inv_freq(hd, bench.ROPE_BASE)
+    ctx = window if window else rows + n_steps
+    kv = oracle.KV(n_layer, ctx, nh, nkv, hd, bench.ROPE_BASE, window=window)
+    outs = np.zeros((n_steps, n_layer, E_), np.float32)
+    for l in range(n_layer):
+        k0 = oracle.synth(rows, kvd, seed, bench.k_stream(l), 0, 2)
+        kv.kcache()[l, :rows] = oracle.rope_rows(k0, np.arange(rows), nkv, hd, inv_f)
+        kv.vcache()[l, :rows] = oracle.synth(rows, kvd, seed, bench.v_stream(l), 0, 3)
+        for s in range(n_steps):
+            p = pos_first + s
+            outs[s, l] = kv.decode(l, p, oracle.synth(1, E_, seed, bench.q_stream(l), p, 1)[0],
+                                   oracle.synth(1, kvd, seed, bench.k_stream(l), p, 2)[0],
+                                   oracle.synth(1, kvd, seed, bench.v_stream(l), p, 3)[0])
+    k, v = kv.kcache().copy(), kv.vcache().copy()
+    kv.close()
+    return outs, k, v
+
+
+def test_other_workload_parity_finds_a_planted_error():
+    """_parity_decode_layers (the bench's C1 / C4 / C5 decode parity): zero on
+    the oracle's own outputs and cache rows, the planted difference and the
+    flipped cache bit found; the window ring (C5's sliding decode) too."""
+    nl, rows, nh, nkv, hd, seed = 2, 40, 4, 2, 64, 3
+    outs, k, v = _small_decode_outs(nl, rows, nh, nkv, hd, seed, rows, 1)
+    rows_of = lambda l: (k[l], v[l])   # noqa: E731
+    r = bench._parity_decode_layers(nl, rows, nh, nkv, hd, seed, rows, outs, 2, kv_rows=rows_of)
+    assert r["max_rel_err"] == 0.0 and r["kv_bitwise"] and r["layers"] == nl and r["steps"] == 1
+    bad = outs.copy()
+    bad[0, 1, 5] += 5e-4 * float(np.max(np.abs(outs[0, 1])))
+    assert bench._parity_decode_layers(nl, rows, nh, nkv, hd, seed, rows, bad, 2)["max_rel_err"] > 4e-4
+    k[1, 7, 3] += 1.0
+    assert not bench._parity_decode_layers(nl, rows, nh, nkv, hd, seed, rows, outs, 2, kv_rows=rows_of)["kv_bitwise"]
+    W = 32
+    outs_w, _, _ = _small_decode_outs(1, W, nh, nkv, hd, seed, W, 6, window=W)
+    r = bench._parity_decode_layers(1, W, nh, nkv, hd, seed, W, outs_w, 1, window=W)
+    assert r["max_rel_err"] == 0.0 and r["steps"] == 6
+    outs_w[4, 0, 0] += 1e-3 * float(np.max(np.abs(outs_w[4, 0])))
+    assert bench._parity_decode_layers(1, W, nh, nkv, hd, seed, W, outs_w, 1, window=W)["max_rel_err"] > 5e-4
+
+
+def test_summary_is_last_and_names_every_config():
+    res = {"decode": {"us_per_layer_gpu": 8.0, "floor": {"read_plus_dependent_launch_us": 6.5,
+                                                         "layer_over_floor": 1.23}},
+           "roofline": {"frac": 0.26}, "prefill": {"us_per_layer_gpu": 270.0, "roofline": {"frac": 0.71}},
+           "other_workloads": {"decode_3b_pos32767": {"us_per_layer_gpu": 19.0, "roofline": {"frac": 0.44}}},
+           "parity": {"decode_max_rel_err": 4e-5, "c4_decode_3b": {"max_rel_err": 1e-6}}}
+    s = bench._summary(res)
+    assert s["c2_decode_7b_us_per_layer"] == 8.0 and s["c2_over_floor"] == 1.23 and s["c4_frac"] == 0.44
+    assert s["c1_decode_0p5b_us"] is None
+    assert set(s["parity_max_rel_err"]) == {"c1_decode_0p5b", "c2_decode_7b", "c3_prefill_7b", "c4_decode_3b",
+                                            "c5_chunk_1p5b", "c5_sliding_decode_1p5b"}
+    assert s["parity_max_rel_err"]["c4_decode_3b"] == 1e-6

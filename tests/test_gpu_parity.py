@@ -186,30 +186,35 @@ def test_decode_7b_ctx4096_outliers():
 
 
 def test_decode_3b_long_context():
-    """Qwen2.5-3B shape, single decode at position 32767 over a full cache."""
-    nh, nkv, hd, ctx = 16, 2, 128, 32768
+    """Qwen2.5-3B shape, decode at position 32767 over a full cache, on two
+    layers with different inputs: every cache row bit for bit, the outputs
+    against the oracle."""
+    nh, nkv, hd, ctx, nl = 16, 2, 128, 32768, 2
     n0 = ctx - 1
-    _say("decode 3b pos 32767")
     seed = 9
-    q0 = oracle.synth(n0, nh * hd, seed, 1 << 32)
-    k0 = oracle.synth(n0, nkv * hd, seed, 2 << 32)
-    v0 = oracle.synth(n0, nkv * hd, seed, 3 << 32)
     inv_f = oracle.inv_freq(hd, 1e6)
-    with _attn(1, ctx, nh, nkv, hd, 1e6) as attn:
-        for p0 in range(0, n0, 8192):       # chunked prefill fills the cache
-            n = min(8192, n0 - p0)
-            attn.prefill(0, p0, q0[p0:p0 + n], k0[p0:p0 + n], v0[p0:p0 + n])
-        q = oracle.synth(1, nh * hd, seed, 1 << 32, row0=n0)[0]
-        k = oracle.synth(1, nkv * hd, seed, 2 << 32, row0=n0)[0]
-        v = oracle.synth(1, nkv * hd, seed, 3 << 32, row0=n0)[0]
-        out = attn.decode(0, n0, q, k, v)
-        kg, vg = attn.read_kv(0, 0, ctx)
-    K = oracle.rope_rows(np.concatenate([k0, k[None]]), np.arange(ctx), nkv, hd, inv_f)
-    V = np.concatenate([v0, v[None]])
-    np.testing.assert_array_equal(kg, K)
-    np.testing.assert_array_equal(vg, V)
-    qr = oracle.rope_rows(q[None], [n0], nh, hd, inv_f)[0]
-    _close(out, oracle.attn_decode(qr, K, V, n0, nh, nkv, hd), "3b decode pos 32767")
+    with _attn(nl, ctx, nh, nkv, hd, 1e6) as attn:
+        for l in range(nl):
+            _say(f"decode 3b pos 32767 layer {l}")
+            sq, sk, sv = (1 << 32) | l, (2 << 32) | l, (3 << 32) | l
+            q0 = oracle.synth(n0, nh * hd, seed, sq)
+            k0 = oracle.synth(n0, nkv * hd, seed, sk)
+            v0 = oracle.synth(n0, nkv * hd, seed, sv)
+            for p0 in range(0, n0, 8192):       # chunked prefill fills the cache
+                n = min(8192, n0 - p0)
+                attn.prefill(l, p0, q0[p0:p0 + n], k0[p0:p0 + n], v0[p0:p0 + n])
+            del q0
+            q = oracle.synth(1, nh * hd, seed, sq, row0=n0)[0]
+            k = oracle.synth(1, nkv * hd, seed, sk, row0=n0)[0]
+            v = oracle.synth(1, nkv * hd, seed, sv, row0=n0)[0]
+            out = attn.decode(l, n0, q, k, v)
+            kg, vg = attn.read_kv(l, 0, ctx)
+            K = oracle.rope_rows(np.concatenate([k0, k[None]]), np.arange(ctx), nkv, hd, inv_f)
+            V = np.concatenate([v0, v[None]])
+            np.testing.assert_array_equal(kg, K)
+            np.testing.assert_array_equal(vg, V)
+            qr = oracle.rope_rows(q[None], [n0], nh, hd, inv_f)[0]
+            _close(out, oracle.attn_decode(qr, K, V, n0, nh, nkv, hd), f"3b decode pos 32767 layer {l}")
 
 
 @pytest.mark.parametrize("nh,nkv,hd,n0", [(40, 8, 128, 2600), (40, 8, 128, 2700), (20, 4, 64, 5200)])
@@ -387,7 +392,12 @@ def test_prefill_7b_2048_rows_vs_brute_force():
 
 def test_prefill_chunk_then_window_decode_1p5b():
     """Qwen2.5-1.5B shape: 1024-row chunk at 7168 onto a cache holding 7168
-    positions, then decode steps sliding the window at 8192."""
+    positions, every row against the oracle's batched attention (kore's AVX2
+    hd_dot / hd_fma arithmetic, kore.cpp:1542-1563) and every K/V row bit for
+    bit; then all 256 decode steps sliding the window at 8192 (positions
+    8192..8447) against the oracle's window decode, the ring's rows bit for bit
+    after the last step."""
+    from concurrent.futures import ThreadPoolExecutor
     nh, nkv, hd, W = 12, 2, 128, 8192
     _say("1.5b chunk at 7168 then sliding decode")
     seed = 5
@@ -399,21 +409,32 @@ def test_prefill_chunk_then_window_decode_1p5b():
         attn.prefill(0, 0, q[:7168], k[:7168], v[:7168])
         kv_k, kv_v = kv.kcache(), kv.vcache()
         inv_f = oracle.inv_freq(hd, 1e6)
-        kv_k[0, :7168] = oracle.rope_rows(k[:7168], np.arange(7168), nkv, hd, inv_f)
-        kv_v[0, :7168] = v[:7168]
         out = attn.prefill(0, 7168, q[7168:], k[7168:], v[7168:])
         K = oracle.rope_rows(k, np.arange(8192), nkv, hd, inv_f)
+        kg, vg = attn.read_kv(0, 0, 8192)
+        np.testing.assert_array_equal(kg, K)
+        np.testing.assert_array_equal(vg, v)
         kv_k[0] = K
         kv_v[0] = v
         qr = oracle.rope_rows(q[7168:], np.arange(7168, 8192), nh, hd, inv_f)
-        for z in (0, 511, 1023):
-            ref = oracle.attn_ref64(qr[z], K, v, np.arange(7168 + z + 1), nh, nkv, hd)
-            _close(out[z], ref, f"chunk row {z}")
-        for p in range(8192, 8192 + 20):
+
+        def piece(z0):
+            return oracle.attn_batch(qr[z0:z0 + 64], 7168 + z0, K[:7168 + z0 + 64], v[:7168 + z0 + 64], nh, nkv, hd,
+                                     avx2=True)
+
+        with ThreadPoolExecutor(max_workers=8) as ex:
+            refs = list(ex.map(piece, range(0, 1024, 64)))
+        for z0, ref in zip(range(0, 1024, 64), refs):
+            _close(out[z0:z0 + 64], ref, f"chunk rows {z0}..{z0 + 63}")
+        for p in range(8192, 8192 + 256):
             qd = oracle.synth(1, nh * hd, seed, 1 << 32, row0=p)[0]
             kd = oracle.synth(1, nkv * hd, seed, 2 << 32, row0=p)[0]
             vd = oracle.synth(1, nkv * hd, seed, 3 << 32, row0=p)[0]
             _close(attn.decode(0, p, qd, kd, vd), kv.decode(0, p, qd, kd, vd), f"decode {p}")
+        kg, vg = attn.read_kv(0, 0, W)
+        np.testing.assert_array_equal(kg, kv.kcache()[0])
+        np.testing.assert_array_equal(vg, kv.vcache()[0])
+    kv.close()
 
 
 # --------------------------------------------------------- errors, misc

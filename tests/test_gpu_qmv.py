@@ -368,6 +368,99 @@ def test_matmul_batch_activation_ranges(wtype, B):
                         f"activation {b} (scale {np.max(np.abs(x[b])):.1e})")
 
 
+@pytest.mark.parametrize("wtype", [oracle.TYPE_Q4K, oracle.TYPE_Q6K])
+def test_matmul_batch_tiny_and_nonfinite_rows(wtype):
+    """Activations whose maximum is a subnormal or barely normal float (2^-118,
+    2^-130, 2^-145), and rows holding +inf, -inf or NaN, next to an ordinary
+    row.  Tiny rows: kore's fp32 chain itself runs on the subnormal grid
+    there (quantum 2^-149 per rounding), so each output is held to the exact
+    float64 product within 1e-4 of the row's maximum plus 64 quanta, and to
+    kore's own tolerance against kore.  Non-finite rows: every output is
+    non-finite, as every one of kore's is; the ordinary row is unaffected."""
+    from kore_amd import qmv
+    rows, nblk, B = 200, 14, 7
+    cols = nblk * 256
+    _say(f"qmm tiny and non-finite rows type {wtype}")
+    rng = np.random.default_rng(4242 + wtype)
+    w = _weights(wtype, rows, nblk, rng)
+    x = np.stack([_x(cols, rng) for _ in range(B)]).astype(np.float64)
+    for b, e in ((1, -118), (2, -130), (3, -145)):
+        x[b] = x[b] / np.max(np.abs(x[b])) * 2.0 ** e
+    x = x.astype(np.float32)
+    x[4, 17] = np.inf
+    x[5, 1000] = -np.inf
+    x[6, 3] = np.nan
+    assert np.max(np.abs(x[3])) > 0 and np.max(np.abs(x[3])) < 2.0 ** -126   # a subnormal maximum
+    with qmv.QMat(wtype, rows, cols, w) as m:
+        out = m.matmul_batch(x)
+    ref = oracle.matmul_batch(wtype, w, rows, cols, x, avx2=True)
+    deq = np.stack([oracle.dequant_row(wtype, w[r * nblk * oracle.BLOCK_BYTES[wtype]:
+                                                 (r + 1) * nblk * oracle.BLOCK_BYTES[wtype]], cols)
+                    for r in range(rows)]).astype(np.float64)
+    _close_kore(out[0], ref[0], "ordinary row vs kore")
+    quantum = 2.0 ** -149
+    for b in (1, 2, 3):
+        exact = deq @ x[b].astype(np.float64)
+        err = float(np.max(np.abs(out[b] - exact)))
+        bound = 1e-4 * float(np.max(np.abs(exact))) + 64 * quantum
+        assert np.max(np.abs(out[b])) > 0, f"tiny row {b}: all-zero outputs"
+        assert err <= bound, f"tiny row {b} (max |x| {np.max(np.abs(x[b])):.2e}): |d| {err:.3e} > {bound:.3e}"
+        _close_kore(out[b], ref[b], f"tiny row {b} vs kore")
+    for b in (4, 5, 6):
+        assert not np.any(np.isfinite(ref[b])), f"kore's row {b} has finite outputs"
+        assert not np.any(np.isfinite(out[b])), f"row {b}: finite outputs where kore's are not"
+
+
+def test_split_matmul_refuses_cols_without_a_split():
+    """A caller's split holds kore_qmv_split_bytes(cols) bytes: a tensor whose
+    cols have none (ffn_down's 18944) is refused before anything launches."""
+    from kore_amd import hip, qmv
+    _say("qmm split refusal for 18944 cols")
+    rng = np.random.default_rng(5)
+    cols = 18944
+    m = qmv.QMat(oracle.TYPE_Q4K, 8, cols, _weights(oracle.TYPE_Q4K, 8, cols // 256, rng))
+    try:
+        assert qmv.split_bytes(cols) == 0
+        x16, do = hip.DeviceBuffer(qmv.split_bytes(3584) // 4), hip.DeviceBuffer(64 * 8)
+        with pytest.raises(qmv.QmvError) as e:
+            qmv.matmul_batch_group_split_dev([m], x16.ptr, 4, [do.ptr])
+        assert e.value.code == qmv.KORE_QMV_E_UNSUPPORTED
+        hip.synchronize()
+        x16.free()
+        do.free()
+    finally:
+        m.close()
+
+
+def _fp32_path_cases():
+    """Run in a child process started with KORE_GEMM=fp32 (the fp32 matmul
+    kernel; the variable is read once per process)."""
+    from kore_amd import qmv
+    assert qmv.split_bytes(3584) == 0, "KORE_GEMM=fp32 did not select the fp32 path"
+    for wtype, rows, nblk, B in [(oracle.TYPE_Q4K, 257, 2, 16), (oracle.TYPE_Q6K, 200, 74, 33),
+                                 (oracle.TYPE_Q4K, 3584, 14, 64), (oracle.TYPE_Q6K, 64, 74, 64)]:
+        print(f"[gpu-case] fp32 path type {wtype}: {rows} x {nblk * 256}, B {B}", flush=True)
+        rng = np.random.default_rng(rows + nblk + B)
+        w = _weights(wtype, rows, nblk, rng)
+        x = np.stack([_x(nblk * 256, rng) for _ in range(B)])
+        with qmv.QMat(wtype, rows, nblk * 256, w) as m:
+            out = m.matmul_batch(x)
+            again = m.matmul_batch(x)
+        assert np.array_equal(_bits(out), _bits(again)), "repeated calls differ"
+        _close_kore(out, oracle.matmul_batch(wtype, w, rows, nblk * 256, x, avx2=True), "fp32 path vs oracle")
+    print("FP32_PATH_OK", flush=True)
+
+
+def test_matmul_batch_fp32_path_in_a_fresh_process():
+    import subprocess
+    _say("qmm fp32 path (KORE_GEMM=fp32) in a child process")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, KORE_GEMM="fp32")
+    r = subprocess.run([sys.executable, "-c", "import tests.test_gpu_qmv as t; t._fp32_path_cases()"], cwd=root,
+                       env=env, capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "FP32_PATH_OK" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
+
+
 def test_matmul_batch_device_api_and_rejections():
     from kore_amd import hip, qmv
     _say("qmm device API, Q4_K 600 x 2048, B 40")
