@@ -36,11 +36,6 @@ struct kore_attn {
     float *d_pf_part = nullptr;              // prefill key-segment partials
     size_t pf_part_floats = 0;
     float *d_scratch = nullptr;              // the device's fixed scratch (allocation-free decode)
-    uint32_t *d_part_t = nullptr;            // tagged split partials of the in-grid merge
-    int part_t_bytes = 0;
-    uint32_t dec_tag = 0;                    // tag of the last in-grid merge (0: none yet)
-    uint32_t wait_ticks = 0;                 // wall-clock ticks an in-grid merge waits at most
-    int *h_err = nullptr, *d_err = nullptr;  // pinned flag an in-grid merge sets when it gave up
     float *h_stage = nullptr;                // pinned staging of the host entry points
     size_t h_stage_floats = 0;
     float *d_io = nullptr;                   // device copies of q/k/v/out
@@ -161,8 +156,6 @@ void release(kore_attn *h) {
     if (h->d_part_o) (void)hipFree(h->d_part_o);
     if (h->d_pf_part) (void)hipFree(h->d_pf_part);
     if (h->d_io) (void)hipFree(h->d_io);
-    if (h->d_part_t) (void)hipFree(h->d_part_t);
-    if (h->h_err) (void)hipHostFree(h->h_err);
     if (h->h_stage) (void)hipHostFree(h->h_stage);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
@@ -206,23 +199,11 @@ int generic_decode_enqueue(kore_attn *h, int layer, int pos, const float *q, con
     return KORE_ATTN_OK;
 }
 
-// Whether a decode on stream s may merge its splits inside its own launch:
-// the handle has the tagged buffer and s is not being captured (a graph
-// replays its launches with their tags frozen, so captured decodes take the
-// two-launch merge, whose partials need no tag).
-bool in_grid_merge(kore_attn *h, hipStream_t s) {
-    if (!h->d_part_t) return false;
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
-    return st == hipStreamCaptureStatusNone;
-}
-
 // Enqueues a decode with its split partials in part (part_floats floats; a
 // decode needs n_head * splits * (head_dim + 2), the generic one n_head *
-// head_dim more), or (fused, 2..kMaxFusedSplits splits) in the handle's
-// tagged buffer, merged inside the same launch.
+// head_dim more).
 int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float *k, const float *v,
-                   float *out, hipStream_t s, float *part, size_t part_floats, bool fused) {
+                   float *out, hipStream_t s, float *part, size_t part_floats) {
     // Cache rows read besides the new one: positions 0..pos-1 (kore.cpp:1437),
     // or every slot of a ring that has wrapped (the new slot's stale copy is
     // masked by the kernel).
@@ -254,31 +235,8 @@ int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float
                     np * ((size_t)h->head_dim + 2), part_floats);
     a.part_o = part;
     a.part_ml = part + np * h->head_dim;
-    if (fused && a.n_split > 1 && a.n_split <= kMaxFusedSplits && in_grid_merge(h, s)) {
-        // Tags 1 .. 2^32 - 2 in call order: every record in the buffer carries
-        // an earlier call's tag or 0, never this call's.  Before the tags wrap
-        // the buffer is zeroed (calls on one handle are ordered on one stream).
-        if (h->dec_tag == 0xFFFFFFFEu) {
-            HIP_TRY(h, hipMemsetAsync(h->d_part_t, 0, (size_t)h->part_t_bytes, s));
-            h->dec_tag = 0;
-        }
-        a.part_t = h->d_part_t;
-        a.part_t_bytes = h->part_t_bytes;
-        a.tag = ++h->dec_tag;
-        a.wait_ticks = h->wait_ticks;
-        a.err = h->d_err;
-    }
     HIP_TRY(h, launch_decode(a, decode_row(h, pos), h->head_dim, s));
     return KORE_ATTN_OK;
-}
-
-// After a synchronisation: an in-grid merge that gave up waiting (it wrote
-// NaN) is reported once.
-int merge_status(kore_attn *h) {
-    if (!h->h_err || !__atomic_load_n(h->h_err, __ATOMIC_ACQUIRE)) return KORE_ATTN_OK;
-    __atomic_store_n(h->h_err, 0, __ATOMIC_RELEASE);
-    return fail(h, KORE_ATTN_E_HIP, "decode: an in-grid merge did not see every split's partials in time "
-                                   "(its outputs are NaN)");
 }
 
 int prefill_enqueue(kore_attn *h, int layer, int pos0, int n_tok, const float *q, const float *k,
@@ -409,7 +367,7 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
     h->head_dim = head_dim;
     h->window = window;
     h->rope_base = rope_base;
-    h->fast_decode = decode_supported(head_dim, n_rep) && decode_fits(ctx, n_head_kv);
+    h->fast_decode = decode_supported(head_dim, n_rep);
     h->fast_prefill = prefill_supported(head_dim, n_rep);
     auto bail = [&](hipError_t e, const char *what) {
         g_create_error = std::string(what) + ": " + hipGetErrorString(e);
@@ -458,24 +416,6 @@ int kore_attn_create(kore_attn_t *out, int n_layer, int ctx, int n_head, int n_h
         if ((e = hipMalloc(&h->d_pf_part, h->pf_part_floats * sizeof(float))) != hipSuccess)
             return bail(e, "hipMalloc");
     }
-    // The in-grid merge's tagged partials (zero: no call's tag), and its
-    // give-up flag in pinned host memory (read after a synchronisation).
-    if (h->fast_decode) {
-        const int fs = std::min(h->max_split, kMaxFusedSplits);
-        h->part_t_bytes = n_head * fs * decode_tagged_record_bytes(head_dim);
-        if ((e = hipMalloc((void **)&h->d_part_t, (size_t)h->part_t_bytes)) != hipSuccess) return bail(e, "hipMalloc");
-        if ((e = hipMemsetAsync(h->d_part_t, 0, (size_t)h->part_t_bytes, h->stream)) != hipSuccess)
-            return bail(e, "hipMemset");
-        if ((e = hipHostMalloc((void **)&h->h_err, sizeof(int), hipHostMallocMapped)) != hipSuccess)
-            return bail(e, "hipHostMalloc");
-        *h->h_err = 0;
-        if ((e = hipHostGetDevicePointer((void **)&h->d_err, h->h_err, 0)) != hipSuccess)
-            return bail(e, "hipHostGetDevicePointer");
-        int khz = 0;
-        if ((e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, h->device)) != hipSuccess)
-            return bail(e, "hipDeviceGetAttribute");
-        h->wait_ticks = (uint32_t)std::min<int64_t>((int64_t)std::max(khz, 1) * 500, 0xFFFFFFFFLL);   // 0.5 s
-    }
     // the device's fixed scratch of kore_attn_decode_noalloc_dev, resolved
     // once per device with that device current
     if ((e = static_scratch(h->device, &h->d_scratch)) != hipSuccess) return bail(e, "hipGetSymbolAddress");
@@ -491,7 +431,7 @@ int kore_attn_decode_dev(kore_attn_t h, int layer, int pos, int n_head, int n_he
     if (!h) return fail(nullptr, KORE_ATTN_E_INVALID, "null handle");
     if (int rc = check_decode(h, layer, pos, n_head, n_head_kv, head_dim, q, k, v, out)) return rc;
     HIP_TRY(h, hipSetDevice(h->device));
-    return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_part_o, h->part_floats, true);
+    return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_part_o, h->part_floats);
 }
 
 int kore_attn_decode_noalloc_dev(kore_attn_t h, int layer, int pos, int n_head, int n_head_kv, int head_dim,
@@ -500,7 +440,7 @@ int kore_attn_decode_noalloc_dev(kore_attn_t h, int layer, int pos, int n_head, 
     if (int rc = check_decode(h, layer, pos, n_head, n_head_kv, head_dim, q, k, v, out)) return rc;
     HIP_TRY(h, hipSetDevice(h->device));
     return decode_enqueue(h, layer, pos, q, k, v, out, pick_stream(h, stream), h->d_scratch,
-                          kStaticScratchFloats, false);
+                          kStaticScratchFloats);
 }
 
 int kore_attn_decode(kore_attn_t h, int layer, int pos, int n_head, int n_head_kv, int head_dim,
@@ -516,13 +456,13 @@ int kore_attn_decode(kore_attn_t h, int layer, int pos, int n_head, int n_head_k
     std::memcpy(hs + E + kvd, v, kvd * sizeof(float));
     HIP_TRY(h, hipMemcpyAsync(ds, hs, (E + 2 * kvd) * sizeof(float), hipMemcpyHostToDevice, h->stream));
     if (int rc = decode_enqueue(h, layer, pos, ds, ds + E, ds + E + kvd, ds + E + 2 * kvd, h->stream,
-                                h->d_part_o, h->part_floats, true))
+                                h->d_part_o, h->part_floats))
         return rc;
     HIP_TRY(h, hipMemcpyAsync(hs + E + 2 * kvd, ds + E + 2 * kvd, E * sizeof(float), hipMemcpyDeviceToHost,
                               h->stream));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
     std::memcpy(out, hs + E + 2 * kvd, E * sizeof(float));
-    return merge_status(h);
+    return KORE_ATTN_OK;
 }
 
 int kore_attn_prefill_dev(kore_attn_t h, int layer, int pos0, int n_tok, int n_head, int n_head_kv,
@@ -621,7 +561,7 @@ int kore_attn_sync(kore_attn_t h) {
     if (!h) return fail(nullptr, KORE_ATTN_E_INVALID, "null handle");
     HIP_TRY(h, hipSetDevice(h->device));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
-    return merge_status(h);
+    return KORE_ATTN_OK;
 }
 
 int kore_attn_get_info(kore_attn_t h, kore_attn_info *info) {

@@ -14,24 +14,13 @@
 
 namespace kore_attn_gpu {
 
-// Single-token decode.  The split kernel does RoPE of q and of the new k
-// row, the append of the new k/v row, and flash-decoding attention of every
-// (kv-head, split) over the cache slots [0, n_rows) in blocks of kDecodeBlock
-// rows plus the new row itself; with one split it writes `out`, otherwise
-// unnormalised split partials, merged either by workgroups at the end of the
-// same grid (part_t set: one launch) or by the combine kernel (a second
-// launch).
+// Single-token decode, two launches.  The split kernel does RoPE of q and of
+// the new k row, the append of the new k/v row, and flash-decoding attention
+// of every (kv-head, split) over the cache slots [0, n_rows) in blocks of
+// kDecodeBlock rows plus the new row itself; with one split it writes `out`,
+// otherwise unnormalised split partials that the combine kernel merges.
 constexpr int kDecodeBlock = 16;
 constexpr int kMaxDecodeSplits = 128;   // splits per kv-head the combine merges in one round
-constexpr int kMaxFusedSplits = 64;     // splits per kv-head the in-grid merge takes
-// The split kernel takes slots and n_head_kv in one argument dword (slots << 8
-// | n_head_kv): the MFMA decode needs ctx < 2^23 and n_head_kv < 256.
-constexpr int kMaxDecodeSlots = 1 << 23;
-constexpr int kMaxDecodeKvHeads = 255;
-
-// Bytes of one (q-head, split) record of the in-grid merge: head_dim
-// (value, tag) pairs, then (max, tag, sum, tag).
-constexpr int decode_tagged_record_bytes(int head_dim) { return 8 * head_dim + 16; }
 
 struct DecodeArgs {
     const float *q;       // [n_head][hd]        post-bias, pre-RoPE
@@ -41,7 +30,7 @@ struct DecodeArgs {
     float *out;           // [n_head][hd]
     float *part_o;        // [n_head][n_split][hd]   split partial outputs
     float *part_ml;       // [n_head][n_split][2]    split max / sum
-    int slots;            // rows per kv-head in the cache (ctx), below kMaxDecodeSlots
+    int slots;            // rows per kv-head in the cache (ctx)
     int n_rows;           // cache slots read: [0, n_rows), the new row excluded
                           // (a wrapped ring reads all slots and masks new_slot)
     int new_slot;         // slot receiving the new row
@@ -50,15 +39,6 @@ struct DecodeArgs {
     int n_head_kv;
     int n_rep;            // q heads per kv head
     float scale;          // 1/sqrt(hd) as kore computes it (kore.cpp:1411)
-    // In-grid merge (part_t set; n_split 2..kMaxFusedSplits): the split
-    // workgroups store their partials as (value, tag) pairs with device-scope
-    // stores, and the workgroups past them in the grid load the pairs with
-    // device-scope loads until every pair carries this call's tag.
-    uint32_t *part_t;     // [n_head][n_split] records of decode_tagged_record_bytes(hd)
-    int part_t_bytes;
-    uint32_t tag;         // nonzero, different from the tag of every record still in part_t
-    uint32_t wait_ticks;  // 100 MHz wall-clock ticks a merge waits before giving up
-    int *err;             // set to 1 by a merge that gave up (its outputs are NaN)
 };
 
 // (cos, sin) of dims 0 .. hd/2 - 1 at the decode position, interleaved,
@@ -186,8 +166,6 @@ int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu);
 // Geometries of the MFMA decode / prefill kernels; the others take the
 // generic kernels.
 bool decode_supported(int head_dim, int n_rep);
-// Whether the MFMA decode's packed argument holds the cache's geometry.
-bool decode_fits(int ctx, int n_head_kv);
 bool prefill_supported(int head_dim, int n_rep);
 
 hipError_t launch_decode(const DecodeArgs &a, const RopeRow &rr, int head_dim, hipStream_t s);

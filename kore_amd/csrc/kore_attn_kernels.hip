@@ -158,105 +158,6 @@ __device__ __forceinline__ double sum4rows_d(double x) {
     return a + b;
 }
 
-// Device-scope cache policy of the in-grid merge's buffer loads and stores
-// (sc1): a store writes through the XCD's L2, a load misses on lines another
-// XCD may have written, so partials cross XCDs inside one launch without a
-// cache write-back or invalidate.
-constexpr int kDevScope = 16;
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ unsigned fbits(float x) { return __builtin_bit_cast(unsigned, x); }
-__device__ __forceinline__ float bitsf(unsigned x) { return __builtin_bit_cast(float, x); }
-
-// The in-grid merge of a decode (workgroups past the split ones): wave w of
-// tail workgroup t takes 32 dims of one q-head; lane (sub, c) = (l / 8, l % 8)
-// takes splits sub + 8 i (i < 8, so n_split <= 64) and float4 c of the 32
-// dims, with decode_combine_kernel's arithmetic in its order (the results are
-// that kernel's bits).  Each split's record is (value, tag) pairs; the lane
-// loads its pairs again until every one carries the call's tag, at most
-// a.wait_ticks of the 100 MHz wall clock (the split workgroups were all
-// dispatched before this one, so they run whatever this one does); past that
-// it writes NaN and sets *a.err.
-template <int HD>
-__device__ __forceinline__ void decode_merge_tail(int t, const DecodeArgs &a) {
-    constexpr int kPer = kMaxFusedSplits / 8;
-    constexpr int CPH = HD / 32;   // 32-dim chunks per head
-    constexpr int kRec = decode_tagged_record_bytes(HD);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int task = t * kWaves + wave;
-    const int hq = task / CPH, chunk = task - hq * CPH;
-    if (hq >= a.n_head_kv * a.n_rep) return;
-    const int S = a.n_split, sub = lane >> 3, c = lane & 7;
-    const unsigned tag = a.tag;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.part_t, 0, a.part_t_bytes, 0x00020000);
-    const int base = hq * S * kRec, doff = 8 * (32 * chunk + 4 * c);
-    u32x4 ml[kPer], o0[kPer], o1[kPer];
-    unsigned todo = 0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        if (sub + 8 * i < S) todo |= 1u << i;
-        ml[i] = o0[i] = o1[i] = u32x4{0u, 0u, 0u, 0u};
-    }
-    const uint64_t t0 = wall_clock64();
-    bool late = false;
-    while (true) {
-        __asm__ volatile("" ::: "memory");   // the loads below read what other workgroups write
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if ((todo >> i) & 1u) {
-                const int off = base + (sub + 8 * i) * kRec;
-                ml[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 8 * HD, 0, kDevScope);
-                o0[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + doff, 0, kDevScope);
-                o1[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + doff + 16, 0, kDevScope);
-            }
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if (ml[i].y == tag && ml[i].w == tag && o0[i].y == tag && o0[i].w == tag && o1[i].y == tag &&
-                o1[i].w == tag)
-                todo &= ~(1u << i);
-        if (__all(todo == 0u)) break;
-        if (wall_clock64() - t0 > (uint64_t)a.wait_ticks) {
-            late = true;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i)
-        if (sub + 8 * i < S) m = fmaxf(m, bitsf(ml[i].x));
-    m = max4rows(row16_max(m));
-    float4 acc = zero4();
-    float den = 0.f;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const bool on = sub + 8 * i < S;
-        const float mi = bitsf(ml[i].x);
-        const float w = (on && mi != -INFINITY) ? fast_exp2(mi - m) : 0.f;
-        den = fmaf(w, on ? bitsf(ml[i].z) : 0.f, den);
-        acc.x = fmaf(w, on ? bitsf(o0[i].x) : 0.f, acc.x);
-        acc.y = fmaf(w, on ? bitsf(o0[i].z) : 0.f, acc.y);
-        acc.z = fmaf(w, on ? bitsf(o1[i].x) : 0.f, acc.z);
-        acc.w = fmaf(w, on ? bitsf(o1[i].z) : 0.f, acc.w);
-    }
-    acc.x += dpp<0x128>(acc.x); acc.y += dpp<0x128>(acc.y); acc.z += dpp<0x128>(acc.z); acc.w += dpp<0x128>(acc.w);
-    den += dpp<0x128>(den);
-    acc.x = sum4rows(acc.x);
-    acc.y = sum4rows(acc.y);
-    acc.z = sum4rows(acc.z);
-    acc.w = sum4rows(acc.w);
-    den = sum4rows(den);
-    if (__any(late)) {
-        acc = make_float4(NAN, NAN, NAN, NAN);
-        den = 1.f;
-        if (lane == 0) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-    if (sub == 0) {
-        const float inv = 1.f / den;
-        st4(a.out + (size_t)hq * HD + chunk * 32 + c * 4,
-            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
-    }
-}
-
 // Workgroup (split, kv-head g): cache slots [r0, r_end) of kv-head g for the
 // NR q-heads of g, so every K/V byte is read once per kv-head (kore's
 // head-outer loop, kore.cpp:1432, reads it once per q-head).  The slots are
@@ -300,23 +201,12 @@ __device__ __forceinline__ void decode_merge_tail(int t, const DecodeArgs &a) {
 // where its stale slot is masked.  The four wave states (and the extra and
 // new rows') are merged in LDS into one partial per q-head, or into `out`
 // when the kv-head has a single split.
-template <int HD, int NR, bool MULTI, bool FUSED>
+template <int HD, int NR, bool MULTI>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
                                                                 float *vc_in, const float *__restrict__ k_in,
                                                                 const float *__restrict__ v_in, int n_rows,
-                                                                int rows_per_split, int new_slot, int slots_kv,
+                                                                int rows_per_split, int new_slot, int slots,
                                                                 DecodeArgs a, RopeRow rr) {
-    // slots_kv = slots << 8 | n_head_kv: both in the preloaded argument
-    // dwords (a fifteenth dword would be fetched from memory ahead of the
-    // first loads)
-    const int slots = slots_kv >> 8;
-    if constexpr (FUSED) {   // grid rows n_head_kv ..: the in-grid merge
-        const int n_kv = slots_kv & 0xFF;
-        if ((int)blockIdx.y >= n_kv) {
-            decode_merge_tail<HD>(((int)blockIdx.y - n_kv) * (int)gridDim.x + (int)blockIdx.x, a);
-            return;
-        }
-    }
     constexpr int NT = HD / 16;    // K float4 per lane per block (MFMA k-steps / 4)
     constexpr int NJ = HD / 64;    // V float4 per lane per row
     constexpr int NMB = HD / 16;   // 16-dim output blocks
@@ -398,9 +288,6 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     // not preloaded)
     float *const out_p = a.out, *const part_o = a.part_o, *const part_ml = a.part_ml;
     const int n_split = a.n_split, n_rep = a.n_rep;
-    uint32_t *const part_t = a.part_t;
-    const int part_t_bytes = a.part_t_bytes;
-    const unsigned tag = a.tag;
 
     float4 kA[NT], vA[4][NJ];
     float4 kB[MULTI ? NT : 1], vB[MULTI ? 4 : 1][NJ];
@@ -424,7 +311,6 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     // first read after the block loop would wait for a kernel-argument fetch
     // at the end of the kernel
     asm volatile("" ::"s"(out_p), "s"(part_o), "s"(part_ml), "s"(n_split), "s"(n_rep));
-    if constexpr (FUSED) asm volatile("" ::"s"(part_t), "s"(part_t_bytes), "s"(tag));
 
     // RoPE of the staged pairs into the wave's LDS rows, then the B operand:
     // lane l holds heads jq and jq + 4 (jq = l % 4) at dims CH kq + 4t + e
@@ -448,14 +334,19 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             st4(&wq[row * QS + HALF + 4 * sc], make_float4(y1[0], y1[1], y1[2], y1[3]));
         }
         __builtin_amdgcn_wave_barrier();
+        // heads past NR read head NR - 1 and are zeroed by a bit mask: a
+        // select of the loaded value became a read under a lane mask, each
+        // waited for before the next
 #pragma unroll
         for (int hg = 0; hg < NHG; ++hg) {
             const int h = jq + 4 * hg;
+            const unsigned keep = h < NR ? 0xFFFFFFFFu : 0u;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const float4 qv = ld4(&wq[min(h, NR - 1) * QS + CH * kq + 4 * t]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) qb[hg][t][e] = h < NR ? comp(qv, e) : 0.f;
+                for (int e = 0; e < 4; ++e)
+                    qb[hg][t][e] = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
             }
         }
     }
@@ -676,24 +567,27 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
         float l = 0.f;
         float4 acc = zero4();
-        // the extra rows' and the new row's states: only those the workgroup
-        // has (uniform branches; the states of the others hold max -inf,
-        // sum 0 and a zero row, so reading them would add nothing)
+        // the extra rows' and the new row's states, every one read (each is
+        // written in every workgroup: the absent ones hold max -inf, sum 0 and
+        // a zero row) and the absent ones masked, so that all the LDS reads
+        // are issued together (reads under the per-state branches were each
+        // waited for before the next)
         float ms[kWaves + 1], ls[kWaves + 1];
         float4 xs[kWaves + 1];
 #pragma unroll
         for (int w = 0; w <= kWaves; ++w) {
+            const int st = kWaves + w;
+            ms[w] = s_m[st * 8 + h];
+            ls[w] = s_l[st * 8 + h];
+            xs[w] = ld4(w < kWaves ? &s_vx[w * HD + 4 * d4] : &s_vnew[4 * d4]);
+        }
+#pragma unroll
+        for (int w = 0; w <= kWaves; ++w) {
             const bool on = w < kWaves ? w < n_extra : is_owner;
-            ms[w] = -INFINITY;
-            ls[w] = 0.f;
-            xs[w] = zero4();
-            if (on) {
-                const int st = kWaves + w;
-                ms[w] = s_m[st * 8 + h];
-                ls[w] = s_l[st * 8 + h];
-                xs[w] = ld4(w < kWaves ? &s_vx[w * HD + 4 * d4] : &s_vnew[4 * d4]);
-                m = fmaxf(m, ms[w]);
-            }
+            ms[w] = on ? ms[w] : -INFINITY;
+            ls[w] = on ? ls[w] : 0.f;
+            xs[w] = on ? xs[w] : zero4();
+            m = fmaxf(m, ms[w]);
         }
 #pragma unroll
         for (int w = 0; w < 2 * kWaves + 1; ++w) {
@@ -715,17 +609,6 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         if (n_split == 1) {
             const float inv = 1.f / l;
             st4(out_p + hg * HD + 4 * d4, make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
-        } else if constexpr (FUSED) {
-            // (value, tag) pairs with device-scope stores, for the in-grid merge
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part_t, 0, part_t_bytes, 0x00020000);
-            const int off = (int)(hg * n_split + split) * decode_tagged_record_bytes(HD);
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{fbits(acc.x), tag, fbits(acc.y), tag}, rs, off + 32 * d4, 0,
-                                                   kDevScope);
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{fbits(acc.z), tag, fbits(acc.w), tag}, rs,
-                                                   off + 32 * d4 + 16, 0, kDevScope);
-            if (d4 == 0)
-                __builtin_amdgcn_raw_buffer_store_b128(u32x4{fbits(m), tag, fbits(l), tag}, rs, off + 8 * HD, 0,
-                                                       kDevScope);
         } else {
             st4(part_o + (hg * n_split + split) * HD + 4 * d4, acc);
             if (d4 == 0) {
@@ -1388,51 +1271,34 @@ static __device__ __align__(256) float scratch[kStaticScratchFloats];
 
 // --------------------------------------------------------------- dispatch
 
-// The split kernel's launch: grid (n_split, n_head_kv + tail rows), the tail
-// rows (FUSED) holding the in-grid merge's workgroups.
-template <int HD, int NR, bool MULTI, bool FUSED>
-void launch_split(const DecodeArgs &a, const RopeRow &rr, int tail_rows, hipStream_t s) {
+template <int HD, int NR>
+hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t s) {
     // The leading scalar arguments (everything before the first aggregate:
     // the pointers and sizes the first loads need, the new row's included)
     // are preloaded into SGPRs at wave launch (gfx950 kernel-argument
     // preload, at most 16 dwords), so no load is issued behind a
     // kernel-argument fetch.
-    // The grid never has more split workgroups than CUs.  The single-block
-    // kernel fits two workgroups per CU by registers, so it asks for enough
-    // (unused) dynamic LDS that a CU holds one: two on a CU would leave
-    // another idle.
-    const dim3 grid(a.n_split, a.n_head_kv + tail_rows);
-    unsigned dyn = 0;
-    if constexpr (!MULTI) {
-        static const unsigned pad = [] {
+    // Splits of at most kWaves blocks plus kWaves extra rows give every wave
+    // one block at most: that kernel has no prefetch registers or branches.
+    // The grid never has more workgroups than CUs.  The single-block kernel
+    // fits two workgroups per CU by registers, so it asks for enough (unused)
+    // dynamic LDS that a CU holds one: two on a CU would leave another idle.
+    const dim3 grid(a.n_split, a.n_head_kv);
+    if (a.rows_per_split > kWaves * kDecodeBlock + kWaves) {
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, true>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
+                           a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
+    } else {
+        static const unsigned dyn = [] {
             hipFuncAttributes fa{};
-            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR, false, FUSED>)) !=
+            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR, false>)) !=
                 hipSuccess)
                 return 0u;
             const size_t half_cu = kLdsPerCu / 2 + 256;
             return fa.sharedSizeBytes < half_cu ? (unsigned)(half_cu - fa.sharedSizeBytes) : 0u;
         }();
-        dyn = pad;
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, false>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc, a.k, a.v,
+                           a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     }
-    hipLaunchKernelGGL((decode_split_kernel<HD, NR, MULTI, FUSED>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc,
-                       a.k, a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots << 8 | a.n_head_kv, a, rr);
-}
-
-template <int HD, int NR>
-hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t s) {
-    // Splits of at most kWaves blocks plus kWaves extra rows give every wave
-    // one block at most: that kernel has no prefetch registers or branches.
-    const bool multi = a.rows_per_split > kWaves * kDecodeBlock + kWaves;
-    if (a.part_t && a.n_split > 1) {
-        // in-grid merge: 4 waves of 32 dims per tail workgroup
-        const int tail_wgs = (a.n_head_kv * a.n_rep * (HD / 32) + kWaves - 1) / kWaves;
-        const int tail_rows = (tail_wgs + a.n_split - 1) / a.n_split;
-        if (multi) launch_split<HD, NR, true, true>(a, rr, tail_rows, s);
-        else launch_split<HD, NR, false, true>(a, rr, tail_rows, s);
-        return hipGetLastError();
-    }
-    if (multi) launch_split<HD, NR, true, false>(a, rr, 0, s);
-    else launch_split<HD, NR, false, false>(a, rr, 0, s);
     static_assert(kMaxDecodeSplits <= 8 * 16, "the combine takes at most 16 splits per lane");
     const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 32);
     const float *po = a.part_o, *pml = a.part_ml;
@@ -1479,8 +1345,6 @@ hipError_t static_scratch(int device, float **ptr) {
 bool decode_supported(int head_dim, int n_rep) {
     return (head_dim == 64 || head_dim == 128) && n_rep >= 1 && n_rep <= 8;
 }
-
-bool decode_fits(int ctx, int n_head_kv) { return ctx < kMaxDecodeSlots && n_head_kv <= kMaxDecodeKvHeads; }
 
 bool prefill_supported(int head_dim, int n_rep) {
     return (head_dim == 64 || head_dim == 128) && n_rep >= 1;

@@ -1,14 +1,10 @@
-"""GPU tests of the decode's in-grid merge (kore_attn_decode_dev with 2..64
-splits per kv-head): the split workgroups write their partials as tagged
-pairs and workgroups at the end of the same grid merge them.  Its outputs and
-cache rows must equal, bit for bit, those of the two-launch merge (split
-kernel + combine kernel), which kore_attn_decode_noalloc_dev and decodes
-under HIP graph capture take, and the oracle's within 1e-4 of max|ref|.
-
-Covered: split counts 2 .. 64 (single-block and multi-block split kernels,
-head_dim 64 and 128, 1 .. 8 q-heads per kv-head), a sliding ring, many calls
-on one handle in a row (a new tag each), a captured 28-layer step replayed
-three times against the eager decodes, and two handles decoding on two
+"""GPU tests of the decode over the split counts it uses (1 .. 64 splits per
+kv-head; the single-block and the multi-block split kernel; head_dim 64 and
+128; 1 .. 8 q-heads per kv-head): kore_attn_decode_dev against the oracle
+within 1e-4 of max|ref| and against kore_attn_decode_noalloc_dev (the same
+kernels over the library's fixed array) bit for bit, the cache rows bit for
+bit; many calls on one handle over a sliding ring; a captured 28-layer step
+replayed three times against the eager decodes; two handles decoding on two
 streams at once."""
 import ctypes as C
 import sys
@@ -58,10 +54,10 @@ def _fill(attn, rows, kvd, rng):
     (8, 8, 128, 2000, 2),      # 1 q-head per kv-head, 32 splits
     (12, 2, 128, 900, 2),      # 6 q-heads per kv-head, 56 splits
 ])
-def test_in_grid_merge_equals_two_launch_merge(nh, nkv, hd, fill, steps):
+def test_decode_splits_vs_oracle_and_noalloc(nh, nkv, hd, fill, steps):
     from kore_amd import KoreAttn, hip
     E, kvd = nh * hd, nkv * hd
-    _say(f"in-grid merge {nh}/{nkv}/{hd} fill {fill} steps {steps}")
+    _say(f"decode splits {nh}/{nkv}/{hd} fill {fill} steps {steps}")
     rng = np.random.default_rng(fill + nh)
     ctx = fill + steps + 1
     with KoreAttn(1, ctx, nh, nkv, hd, 1e6) as A, KoreAttn(1, ctx, nh, nkv, hd, 1e6) as B:
@@ -83,7 +79,7 @@ def test_in_grid_merge_equals_two_launch_merge(nh, nkv, hd, fill, steps):
             A.sync()
             B.sync()
             ra, rb = oa.download(), ob.download()
-            assert np.array_equal(_bits(ra), _bits(rb)), f"position {pos}: in-grid and two-launch merges differ"
+            assert np.array_equal(_bits(ra), _bits(rb)), f"position {pos}: decode_dev and decode_noalloc_dev differ"
             _close(ra, kv.decode(0, pos, q, k, v), f"position {pos} vs oracle")
             for b in (dq, dk, dv):
                 b.free()
@@ -95,12 +91,13 @@ def test_in_grid_merge_equals_two_launch_merge(nh, nkv, hd, fill, steps):
     kv.close()
 
 
-def test_in_grid_merge_many_calls_and_a_ring():
-    """A 1.5B-shape ring of 1024 slots decoded 300 times past its end (every
-    call a new tag over the same buffer) against the oracle's window decode."""
+def test_decode_many_calls_over_a_ring():
+    """A 1.5B-shape ring of 1024 slots decoded 300 times past its end (the
+    same split partials reused by every call) against the oracle's window
+    decode."""
     from kore_amd import KoreAttn
     nh, nkv, hd, W = 12, 2, 128, 1024
-    _say("in-grid merge: 300 ring decodes")
+    _say("decode: 300 ring decodes past the end")
     rng = np.random.default_rng(11)
     kv = oracle.KV(1, W, nh, nkv, hd, 1e6, window=W)
     with KoreAttn(1, W, nh, nkv, hd, 1e6, window=W) as A:
@@ -132,10 +129,10 @@ def _graph_api():
 
 
 def test_captured_decodes_replay_the_eager_results():
-    """A 28-layer 7B decode step captured on the handle's stream (the decodes
-    take the two-launch merge there, no memset in the graph) and replayed three
-    times, with eager in-grid-merge decodes of the same step between the
-    replays: every replay's outputs equal the eager ones bit for bit."""
+    """A 28-layer 7B decode step captured on the handle's stream (no memset in
+    the graph) and replayed three times, with eager decodes of the same step
+    between the replays: every replay's outputs equal the eager ones bit for
+    bit."""
     from kore_amd import KoreAttn, hip
     nl, nh, nkv, hd, fill = 28, 28, 4, 128, 2048
     E, kvd = nh * hd, nkv * hd
@@ -172,7 +169,7 @@ def test_captured_decodes_replay_the_eager_results():
                 A.sync()
                 got = graphed.download()
                 assert np.array_equal(_bits(got), _bits(ref)), f"replay {rep} differs from the eager decodes"
-                step(eager)                # eager in-grid-merge decodes between the replays
+                step(eager)                # eager decodes between the replays
                 A.sync()
                 assert np.array_equal(_bits(eager.download()), _bits(ref)), f"eager step after replay {rep}"
         finally:
@@ -183,7 +180,7 @@ def test_captured_decodes_replay_the_eager_results():
 
 
 def test_two_handles_on_two_streams_at_once():
-    """Two handles (their own tagged buffers) decoding 28 layers each on their
+    """Two handles (their own split partials) decoding 28 layers each on their
     own streams without a synchronisation between them: both equal their
     serial results bit for bit."""
     from kore_amd import KoreAttn, hip
