@@ -13,9 +13,9 @@
  * reads: matrices [n_embd x n_embd], [kv_dim x n_embd], [n_ff x n_embd],
  * [n_embd x n_ff], token_embd and output.weight n_embd wide and 2-D, every norm
  * and attn_q.bias n_embd floats, attn_k.bias and attn_v.bias kv_dim floats.
- * The matvecs always sum in kore's AVX2 order (kore's forward() uses its scalar
- * order only on a CPU without AVX2, kore.cpp:1293; on such a host the logits
- * of kore and of this engine differ in the last bits).  Part of libkore_layer.so. */
+ * The matvecs sum in the order kore's engine_init picks (e.avx2,
+ * kore.cpp:1293): its AVX2 order on a host with AVX2 and FMA, its scalar order
+ * elsewhere; kore_model_load_ex sets either.  Part of libkore_layer.so. */
 #ifndef KORE_MODEL_H
 #define KORE_MODEL_H
 
@@ -47,9 +47,17 @@ typedef struct kore_model_info {
     int n_vocab;             /* rows of output.weight */
     int head_dim, kv_dim;
     size_t weight_bytes;     /* device bytes of all tensors */
+    int avx2;                /* 1: the matvecs sum in kore's AVX2 order, 0: its scalar order */
 } kore_model_info;
 
+/* engine_init(e, path, ctx_max) with the matvec order kore would pick on this
+ * host: e.avx2 = KORE_HAVE_AVX2 && cpu_has_avx2() (kore.cpp:1293, 512-519). */
 KORE_MODEL_API int kore_model_load(const char *gguf_path, int ctx_max, kore_model_t *out);
+
+/* The same with e.avx2 given: 1 kore's AVX2 order (kore.cpp:521-632), 0 its
+ * scalar order (kore.cpp:450-506), -1 kore's own choice on this host (as
+ * kore_model_load); any other value is KORE_MODEL_E_LOAD. */
+KORE_MODEL_API int kore_model_load_ex(const char *gguf_path, int ctx_max, int avx2, kore_model_t *out);
 KORE_MODEL_API void kore_model_destroy(kore_model_t m);
 KORE_MODEL_API int kore_model_get_info(kore_model_t m, kore_model_info *info);
 

@@ -15,6 +15,7 @@ struct kore_model {
     kore_gguf_hparams hp{};
     int ctx = 0, n_vocab = 0, head_dim = 0, kv_dim = 0;
     size_t weight_bytes = 0;
+    int avx2 = 1;                                 // kore's e.avx2: the matvecs' summation order
     std::vector<kore_layer_weights> layers;
     std::vector<kore_qmv_tensor_t> mats;          // every matrix, for destruction
     std::vector<float *> arrays;                  // every device F32 array
@@ -49,6 +50,18 @@ void release(kore_model *m) {
     if (m->attn) kore_attn_destroy(m->attn);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
+}
+
+// kore's e.avx2 = KORE_HAVE_AVX2 && cpu_has_avx2() (kore.cpp:512-519, 1293):
+// an x86-64 host whose CPU reports AVX2 and FMA (host code: the device pass of
+// this file does not know the CPU builtins)
+int host_avx2() {
+#if defined(__x86_64__) && !defined(__HIP_DEVICE_COMPILE__)
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") ? 1 : 0;
+#else
+    return 0;
+#endif
 }
 
 // engine_init (kore.cpp:1274-1365) with the tensors copied to the device
@@ -180,8 +193,13 @@ int build(kore_model *m, kore_gguf_t g, int ctx_max) {
 extern "C" {
 
 KORE_MODEL_API int kore_model_load(const char *gguf_path, int ctx_max, kore_model_t *out) {
+    return kore_model_load_ex(gguf_path, ctx_max, -1, out);
+}
+
+KORE_MODEL_API int kore_model_load_ex(const char *gguf_path, int ctx_max, int avx2, kore_model_t *out) {
     if (!out) return fail(nullptr, KORE_MODEL_E_LOAD, "out is NULL");
     *out = nullptr;
+    if (avx2 < -1 || avx2 > 1) return fail(nullptr, KORE_MODEL_E_LOAD, "avx2 must be -1, 0 or 1");
     kore_gguf_t g = nullptr;
     if (kore_gguf_open(gguf_path, &g) != KORE_GGUF_OK)
         return fail(nullptr, KORE_MODEL_E_LOAD, kore_gguf_last_error(nullptr));
@@ -190,6 +208,7 @@ KORE_MODEL_API int kore_model_load(const char *gguf_path, int ctx_max, kore_mode
         kore_gguf_close(g);
         return fail(nullptr, KORE_MODEL_E_LOAD, "out of host memory");
     }
+    m->avx2 = avx2 < 0 ? host_avx2() : avx2;
     const int rc = build(m, g, ctx_max);
     kore_gguf_close(g);                               // everything needed is on the device now
     if (rc != KORE_MODEL_OK) {
@@ -213,6 +232,7 @@ KORE_MODEL_API int kore_model_get_info(kore_model_t m, kore_model_info *info) {
     info->head_dim = m->head_dim;
     info->kv_dim = m->kv_dim;
     info->weight_bytes = m->weight_bytes;
+    info->avx2 = m->avx2;
     return KORE_MODEL_OK;
 }
 
@@ -225,13 +245,13 @@ KORE_MODEL_API int kore_model_decode_dev(kore_model_t m, int token, int pos, int
     if (kore_qmv_get_row_dev(m->embd_type, m->embd, token, E, m->x, s) != KORE_QMV_OK)
         return fail(m, KORE_MODEL_E_DEVICE, std::string("embedding: ") + kore_qmv_last_error(nullptr));
     for (int l = 0; l < (int)m->layers.size(); ++l)
-        if (kore_layer_decode_dev(m->layer, &m->layers[(size_t)l], m->attn, l, pos, m->x, 1, s) != KORE_LAYER_OK)
+        if (kore_layer_decode_dev(m->layer, &m->layers[(size_t)l], m->attn, l, pos, m->x, m->avx2, s) != KORE_LAYER_OK)
             return fail(m, KORE_MODEL_E_DEVICE, std::string("layer: ") + kore_layer_last_error(m->layer));
     if (want_logits) {                                 // kore.cpp:1474-1478
         kore_qmv_mv_opts o{};
         o.norm_w = m->out_norm;
         o.norm_eps = m->hp.rms_eps;
-        if (kore_qmv_mv_group_ex_dev(1, &m->head, m->x, &o, &m->logits, 1, s) != KORE_QMV_OK)
+        if (kore_qmv_mv_group_ex_dev(1, &m->head, m->x, &o, &m->logits, m->avx2, s) != KORE_QMV_OK)
             return fail(m, KORE_MODEL_E_DEVICE, std::string("logits: ") + kore_qmv_last_error(m->head));
     }
     return KORE_MODEL_OK;
@@ -258,7 +278,7 @@ KORE_MODEL_API int kore_model_prefill_dev(kore_model_t m, const int *tokens, int
         o.norm_w = m->out_norm;
         o.norm_eps = m->hp.rms_eps;
         const float *last = m->bx + (size_t)(n_tok - 1) * E;
-        if (kore_qmv_mv_group_ex_dev(1, &m->head, last, &o, &m->logits, 1, s) != KORE_QMV_OK)
+        if (kore_qmv_mv_group_ex_dev(1, &m->head, last, &o, &m->logits, m->avx2, s) != KORE_QMV_OK)
             return fail(m, KORE_MODEL_E_DEVICE, std::string("logits: ") + kore_qmv_last_error(m->head));
     }
     return KORE_MODEL_OK;

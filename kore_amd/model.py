@@ -19,7 +19,7 @@ KORE_MODEL_OK, KORE_MODEL_E_LOAD, KORE_MODEL_E_RANGE, KORE_MODEL_E_DEVICE = rang
 
 class Info(C.Structure):
     _fields_ = [("hp", Hparams), ("ctx", C.c_int), ("n_vocab", C.c_int), ("head_dim", C.c_int), ("kv_dim", C.c_int),
-                ("weight_bytes", C.c_size_t)]
+                ("weight_bytes", C.c_size_t), ("avx2", C.c_int)]
 
 
 _done = False
@@ -31,6 +31,7 @@ def lib() -> C.CDLL:
     if not _done:
         vp = C.c_void_p
         for name, res, args in (("kore_model_load", C.c_int, [C.c_char_p, C.c_int, C.POINTER(vp)]),
+                                ("kore_model_load_ex", C.c_int, [C.c_char_p, C.c_int, C.c_int, C.POINTER(vp)]),
                                 ("kore_model_destroy", None, [vp]),
                                 ("kore_model_get_info", C.c_int, [vp, C.POINTER(Info)]),
                                 ("kore_model_decode_dev", C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
@@ -54,9 +55,13 @@ class ModelError(RuntimeError):
 
 
 class Model:
-    def __init__(self, path: str, ctx_max: int = 4096):
+    """avx2: the matvecs' summation order, kore's e.avx2 (kore.cpp:1293): None
+    picks it as kore's engine_init does on this host, True / False force
+    kore's AVX2 / scalar order."""
+
+    def __init__(self, path: str, ctx_max: int = 4096, avx2: bool | None = None):
         h = C.c_void_p()
-        rc = lib().kore_model_load(path.encode(), ctx_max, C.byref(h))
+        rc = lib().kore_model_load_ex(path.encode(), ctx_max, -1 if avx2 is None else int(bool(avx2)), C.byref(h))
         if rc != KORE_MODEL_OK:
             raise ModelError(rc, lib().kore_model_last_error(None).decode())
         self._h = h

@@ -39,3 +39,16 @@ def test_rejections_without_a_gpu():
     assert L.kore_layer_decode_dev(None, None, None, 0, 0, None, 1, None) == layer.KORE_LAYER_E_INVALID
     assert L.kore_layer_prefill_dev(None, None, None, 0, 0, 1, None, None) == layer.KORE_LAYER_E_INVALID
     assert b"NULL" in L.kore_layer_last_error(None)
+
+
+def test_model_load_rejects_an_unknown_matvec_order():
+    # kore's e.avx2 is 0 or 1; -1 asks for kore's own choice on this host
+    import ctypes as C
+
+    from kore_amd import model
+    L = model.lib()
+    h = C.c_void_p()
+    path = os.path.join(ROOT, "tests", "golden", "gguf_tiny_qwen2.gguf").encode()
+    for bad in (2, -2):
+        assert L.kore_model_load_ex(path, 16, bad, C.byref(h)) == model.KORE_MODEL_E_LOAD and not h.value
+        assert b"avx2" in L.kore_model_last_error(None)

@@ -142,25 +142,26 @@ def _oracle_engine(path, ctx_max):
     return hp, ctx, layers, f32, emb, (ot, odims[1], ob), kv
 
 
-def _oracle_logits(hp, f32, head, x):
+def _oracle_logits(hp, f32, head, x, avx2=True):
     """forward()'s logits (kore.cpp:1474-1478)."""
     import oracle
     ot, rows, ob = head
     xq = oracle.quantize_q8K(oracle.rmsnorm(x, f32("output_norm.weight"), hp["rms_eps"]))
-    return oracle.qmatvec(ot, ob, rows, hp["n_embd"], xq, avx2=True)
+    return oracle.qmatvec(ot, ob, rows, hp["n_embd"], xq, avx2=avx2)
 
 
-def oracle_engine_logits(path, tokens, ctx_max=64):
+def oracle_engine_logits(path, tokens, ctx_max=64, avx2=True):
     """The oracle's kore engine over a GGUF file: engine_init, then per token
-    get_row (kore.cpp:384-407), every forward() layer and the logits."""
+    get_row (kore.cpp:384-407), every forward() layer and the logits; avx2 is
+    kore's e.avx2 (the matvecs' summation order)."""
     import oracle
     hp, ctx, layers, f32, emb, head, kv = _oracle_engine(path, ctx_max)
     out = []
     for pos, tok in enumerate(tokens):
         x = emb(tok)
         for l, lw in enumerate(layers):
-            x = oracle.layer_forward(kv, l, pos, x, lw, hp["n_ff"], hp["rms_eps"], avx2=True)
-        out.append(_oracle_logits(hp, f32, head, x))
+            x = oracle.layer_forward(kv, l, pos, x, lw, hp["n_ff"], hp["rms_eps"], avx2=avx2)
+        out.append(_oracle_logits(hp, f32, head, x, avx2))
     return ctx, np.stack(out), kv
 
 

@@ -40,6 +40,42 @@ def test_model_logits_against_kore_engine():
     assert np.array_equal(v.view(np.uint32), kv.vcache()[0, :n].view(np.uint32))
 
 
+def _host_avx2():
+    flags = set()
+    with open("/proc/cpuinfo") as f:
+        for line in f:
+            if line.startswith("flags"):
+                flags = set(line.split(":", 1)[1].split())
+                break
+    return int("avx2" in flags and "fma" in flags)
+
+
+def test_model_matvec_order_follows_avx2_choice():
+    """kore's e.avx2 (kore.cpp:1293) picks the matvecs' summation order.  With
+    the scalar order forced, layer 0's K/V rows (exact steps and the q/k/v
+    matvecs) equal the oracle's scalar-order engine bit for bit, and the logits
+    hold kore's tolerance against it; the two orders give different K/V rows on
+    this file (221 of 512 K values), so the check tells them apart.  Without the
+    argument the engine takes this host's choice, as kore does."""
+    from kore_amd.model import Model
+    man = json.load(open(os.path.join(GOLD, "gguf_tiny_qwen2_forward.json")))
+    path, toks, n = os.path.join(GOLD, man["file"]), man["tokens"], len(man["tokens"])
+    _, want, kv = oracle_engine_logits(path, toks, man["ctx_max"], avx2=False)
+    _, _, kv_avx2 = oracle_engine_logits(path, toks, man["ctx_max"], avx2=True)
+    assert not np.array_equal(kv.kcache()[0, :n], kv_avx2.kcache()[0, :n])
+    print("[gpu-model] tiny_qwen2 engine in kore's scalar order, 4 tokens", flush=True)
+    with Model(path, man["ctx_max"], avx2=False) as m:
+        assert m.info.avx2 == 0
+        for pos, tok in enumerate(toks):
+            got, ref = m.decode(tok, pos).astype(np.float64), want[pos].astype(np.float64)
+            assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref)), f"token {pos}"
+        k, v = m.read_kv(0, 0, n)
+    assert np.array_equal(k.view(np.uint32), kv.kcache()[0, :n].view(np.uint32))
+    assert np.array_equal(v.view(np.uint32), kv.vcache()[0, :n].view(np.uint32))
+    with Model(path, man["ctx_max"]) as m:
+        assert m.info.avx2 == _host_avx2()
+
+
 def test_embedding_rows_bitwise():
     from kore_amd import hip, qmv
     rng = np.random.default_rng(4)
