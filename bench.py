@@ -539,6 +539,36 @@ def _kqb_runner(B, ops, tensors):
     return run
 
 
+def _mv_key(mats, ts):
+    """Name of a grouped matvec launch: its matrices' roles and types."""
+    return "+".join(mats[ti][0].split(".")[-1] + ("" if mats[ti][0] == "output" else
+                                                   ("_q6k" if mats[ti][1] == QMV_Q6K else "_q4k")) for ti in ts)
+
+
+def _gemm_key(mats, ts):
+    return "+".join(mats[ti][0].split(".")[-1] + ("_q6k" if mats[ti][1] == QMV_Q6K else "_q4k") for ti in ts)
+
+
+def _class_passes(B, ops, keys, tensors, reps: int):
+    """GPU time per launch of each kind of launch (key): the launches of one
+    kind, in layer order, back to back between one HIP event pair on the
+    stream they run on, the kinds in turn, `reps` times.  Between two passes of
+    one kind the others stream far more than the 256 MB MALL, so each pass
+    reads its weights from HBM as the token does; the time per launch then
+    holds the kernel and the dependent-launch gap, as in the token, and no
+    per-launch event (which adds ~2.4 us to each launch it brackets)."""
+    kinds = list(dict.fromkeys(keys))
+    runners = {k: _kqb_runner(B, [o for o, kk in zip(ops, keys) if kk == k], tensors) for k in kinds}
+    count = {k: keys.count(k) for k in kinds}
+    out = {k: [] for k in kinds}
+    reg = C.c_float(0)
+    for _ in range(reps):
+        for k in kinds:
+            runners[k](1, reg=C.byref(reg))
+            out[k].append(reg.value / count[k])
+    return out
+
+
 def gpu_matvec(qt, tokens: int, warmup: int):
     """One 7B token's quant() + mv() sequence (kore.cpp:1418-1477) over 28
     distinct layers plus the output head, replayed `tokens` times from C++."""
@@ -568,15 +598,13 @@ def gpu_matvec(qt, tokens: int, warmup: int):
     print(f"[bench] matvec: {tokens} timed tokens x {len(ops)} launches", file=sys.stderr, flush=True)
     wall_ms = run(tokens, reg=C.byref(region))
     region_ms = region.value
-    # per-launch durations (a second pass with an event pair around every launch)
-    n_ev = min(tokens, 4)
-    op_ms = np.zeros(n_ev * len(ops), np.float32)
-    run(n_ev, op_ms=op_ms.ctypes.data)
+    # time per launch of each kind (one event pair around each kind's launches)
+    class_ms = _class_passes(B, ops, [_mv_key(mats, ts) for ts in op_mats], tensors, min(tokens, 4))
     got = outs[0].download()      # for the bitwise check of the first matrix against kore's arithmetic
     for b in dx + outs:
         b.free()
     return dict(mats=mats, op_mats=op_mats, wall_ms=wall_ms, region_ms=region_ms,
-                op_ms=op_ms.reshape(n_ev, len(ops)), first_raw=first_raw, first_x=xs[0], first_out=got)
+                class_ms=class_ms, first_raw=first_raw, first_x=xs[0], first_out=got)
 
 
 GEMM_B = 64      # kore's prefill chunk, KORE_BMAX (kore.cpp:690)
@@ -612,9 +640,7 @@ def gpu_gemm(qt, chunks: int, warmup: int):
     print(f"[bench] gemm: {chunks} timed {GEMM_B}-token chunks x {len(ops)} launches", file=sys.stderr, flush=True)
     wall_ms = run(chunks, reg=C.byref(region))
     region_ms = region.value
-    n_ev = min(chunks, 3)
-    op_ms = np.zeros(n_ev * len(ops), np.float32)
-    run(n_ev, op_ms=op_ms.ctypes.data)
+    class_ms = _class_passes(B, ops, [_gemm_key(mats, ts) for ts in op_mats], tensors, min(chunks, 3))
     # the last layer's attn_q output is overwritten by later layers: run layer 0's alone for the check
     one = _kqb_runner(B, ops[:1], tensors)
     one(1)
@@ -622,7 +648,7 @@ def gpu_gemm(qt, chunks: int, warmup: int):
     for b in [dxb, datt, dgate] + douts:
         b.free()
     return dict(mats=mats, op_mats=op_mats, wall_ms=wall_ms, region_ms=region_ms,
-                op_ms=op_ms.reshape(n_ev, len(ops)), first_raw=first_raw, first_x=xb, first_out=got)
+                class_ms=class_ms, first_raw=first_raw, first_x=xb, first_out=got)
 
 
 def _klb():
@@ -858,19 +884,18 @@ def gemm_report(g, chunks: int):
     flops = sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] for ts in op_mats for ti in ts)
     chunk_s = g["region_ms"] / 1e3 / chunks
     per = {}
-    for i, ts in enumerate(op_mats):
-        key = "+".join(mats[ti][0].split(".")[-1] + ("_q6k" if mats[ti][1] == QMV_Q6K else "_q4k") for ti in ts)
-        d = per.setdefault(key, {"launches_per_chunk": 0, "ms": [],
+    for ts in op_mats:
+        key = _gemm_key(mats, ts)
+        d = per.setdefault(key, {"launches_per_chunk": 0, "ms": g["class_ms"][key],
                                  "flop": sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] for ti in ts),
                                  "weight_bytes": sum(qmv_weight_bytes(*mats[ti][1:]) for ti in ts)})
         d["launches_per_chunk"] += 1
-        d["ms"].extend(g["op_ms"][:, i].tolist())
     # the fp16 path (default) is bound by the fp16 MFMA rate on its MFMA work (the algorithmic
     # flops times the passes); the fp32 path (KORE_GEMM=fp32) by the fp32 MFMA rate
     fp16 = os.environ.get("KORE_GEMM", "") != "fp32"
     table = {}
-    for i, ts in enumerate(op_mats):
-        key = "+".join(mats[ti][0].split(".")[-1] + ("_q6k" if mats[ti][1] == QMV_Q6K else "_q4k") for ti in ts)
+    for ts in op_mats:
+        key = _gemm_key(mats, ts)
         per[key]["mfma_flop"] = sum(2 * GEMM_B * mats[ti][2] * mats[ti][3] * (GEMM16_PASSES[mats[ti][1]] if fp16 else 1)
                                     for ti in ts)
     peak = FP16_MFMA_PEAK_TFLOPS if fp16 else FP32_MFMA_PEAK_TFLOPS
@@ -910,18 +935,12 @@ def matvec_report(g, tokens: int):
     wbytes = sum(qmv_weight_bytes(t, r, c) for _, t, r, c in mats)
     tok_s = g["region_ms"] / 1e3 / tokens
     per = {}
-    for i, ts in enumerate(op_mats):
-        parts = []
-        alg = 0
-        for ti in ts:
-            name, t, r, c = mats[ti]
-            parts.append(name.split(".")[-1] + ("" if name == "output" else ("_q6k" if t == QMV_Q6K else "_q4k")))
-            alg += qmv_weight_bytes(t, r, c) + r * 4
+    for ts in op_mats:
+        alg = sum(qmv_weight_bytes(*mats[ti][1:]) + mats[ti][2] * 4 for ti in ts)
         alg += mats[ts[0]][3] * 4          # the fp32 input, read once
-        key = "+".join(parts)
-        d = per.setdefault(key, {"launches_per_token": 0, "ms": [], "bytes": alg})
+        key = _mv_key(mats, ts)
+        d = per.setdefault(key, {"launches_per_token": 0, "ms": g["class_ms"][key], "bytes": alg})
         d["launches_per_token"] += 1
-        d["ms"].extend(g["op_ms"][:, i].tolist())
     table = {}
     for key, d in per.items():
         us = float(np.mean(d["ms"])) * 1e3

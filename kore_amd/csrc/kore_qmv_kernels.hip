@@ -907,8 +907,13 @@ hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int ma
     if (!fused && !a.xq) return hipErrorInvalidValue;
     if ((a.norm_w || a.up) && !fused) return hipErrorInvalidValue;   // pre-ops act on x
     if (a.norm_w && a.up) return hipErrorInvalidValue;
-    // workgroups per matrix: in proportion to its weight bytes, at least one,
-    // at most one per row tile, about max_wgs in all
+    // workgroups per matrix: one per row tile when the launch may have a
+    // workgroup per tile (max_wgs 0 or at least the tiles); else in proportion
+    // to its weight bytes, at least one, at most one per row tile, about
+    // max_wgs in all.  (Proportional shares at one tile per workgroup would
+    // give a Q4_K matrix grouped with a Q6_K one fewer workgroups than tiles:
+    // q+k+v with a Q6_K attn_v had 13 workgroups walking two tiles, which
+    // ended 3 us after the others.)
     int64_t tiles[kMaxGroup], bytes[kMaxGroup], all_tiles = 0, all_bytes = 0;
     for (int k = 0; k < a.n_mat; ++k) {
         const MatDesc &m = a.m[k];
@@ -919,11 +924,11 @@ hipError_t launch_matvec_group(bool avx2, GroupArgs a, int rows_per_wave, int ma
         all_tiles += tiles[k];
         all_bytes += bytes[k];
     }
-    const int64_t target = max_wgs > 0 ? std::min<int64_t>(max_wgs, all_tiles) : all_tiles;
+    const bool per_tile = max_wgs <= 0 || max_wgs >= all_tiles;
     int64_t wg = 0;
     for (int k = 0; k < a.n_mat; ++k) {
         MatDesc &m = a.m[k];
-        int64_t n = (target * bytes[k] + all_bytes / 2) / all_bytes;
+        int64_t n = per_tile ? tiles[k] : ((int64_t)max_wgs * bytes[k] + all_bytes / 2) / all_bytes;
         n = std::max<int64_t>(1, std::min<int64_t>(n, tiles[k]));
         m.wg_begin = (int)wg;
         m.wg_count = (int)n;

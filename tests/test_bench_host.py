@@ -1,6 +1,6 @@
 """Host-side logic of bench.py (no GPU): the report builders of the matvec
-and batched-matmul legs turn per-launch timings into the JSON fields the
-bench line carries, and the workload tables match the 7B shapes."""
+and batched-matmul legs turn the per-kind launch timings into the JSON fields
+the bench line carries, and the workload tables match the 7B shapes."""
 import os
 import sys
 
@@ -27,8 +27,12 @@ def test_token_matrices_are_the_7b_layout():
 def test_matvec_report_fields():
     mats = _mats()
     op_mats = [(0, 1, 2), (3,), (4, 5), (6,)] + [(7 * bench.NL,)]
-    g = dict(mats=mats, op_mats=op_mats, wall_ms=20.0, region_ms=16.0, op_ms=np.full((2, len(op_mats)), 0.01))
+    class_ms = {bench._mv_key(mats, ts): [0.01, 0.01] for ts in op_mats}
+    g = dict(mats=mats, op_mats=op_mats, wall_ms=20.0, region_ms=16.0, class_ms=class_ms)
     r = bench.matvec_report(g, 10)
+    assert set(r["per_matrix"]) == {"attn_q_q4k+attn_k_q4k+attn_v_q6k", "attn_output_q4k",
+                                    "ffn_gate_q4k+ffn_up_q4k", "ffn_down_q6k", "output"}
+    assert r["per_matrix"]["attn_output_q4k"]["us_mean"] == 10.0
     assert r["ms_per_token_gpu"] == 1.6 and r["launches_per_token"] == len(op_mats)
     assert r["roofline"]["bound"] == "hbm" and r["roofline"]["unit"] == "GB/s"
     assert 0 < r["roofline"]["frac"] < 1
@@ -42,7 +46,8 @@ def test_gemm_report_fields():
         op_mats += [(b, b + 1, b + 2), (b + 3,), (b + 4, b + 5), (b + 6,)]
     # launch times proportional to their flops: the dominant launch is gate+up
     per = np.array([sum(2 * bench.GEMM_B * mats[i][2] * mats[i][3] for i in ts) for ts in op_mats]) / 1e11
-    g = dict(mats=mats, op_mats=op_mats, wall_ms=50.0, region_ms=50.0, op_ms=np.tile(per, (3, 1)))
+    class_ms = {bench._gemm_key(mats, ts): [float(ms)] * 3 for ts, ms in zip(op_mats, per)}
+    g = dict(mats=mats, op_mats=op_mats, wall_ms=50.0, region_ms=50.0, class_ms=class_ms)
     r = bench.gemm_report(g, 5)
     flop = sum(2 * bench.GEMM_B * mats[i][2] * mats[i][3] for i in range(7 * bench.NL))
     assert r["flop_per_chunk"] == flop
