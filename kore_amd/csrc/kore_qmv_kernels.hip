@@ -246,53 +246,67 @@ __device__ __forceinline__ Q8Lane quantize_lane(const float *xb, int m, const Pr
     return quantize16(v, m);
 }
 
+// v_cvt_i32_f32: a NaN converts to 0 (the instruction's own rule; C's
+// conversion leaves it undefined)
+__device__ __forceinline__ int cvt_i32(float f) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
+    return r;
+}
+
 // The quantisation proper of quantize_lane: lane m of a DPP row holds values
 // 16m .. 16m+15 of the block (after any pre-op) in v.
 __device__ __forceinline__ Q8Lane quantize16(const float (&v)[16], int m) {
     // kore keeps the first value of largest magnitude, starting from amax = 0
     // with a strict comparison (kore.cpp:424-428): the largest |x| wins, ties
-    // go to the lowest index, NaN and zeros are never chosen.
-    float best = 0.f, bval = 0.f;
-    int bidx = 256;
+    // go to the lowest index, NaN and zeros are never chosen.  Here: the
+    // largest magnitude over the row (fmaxf passes over a NaN), then each
+    // lane's first value of that magnitude as the key 2 index + sign bit,
+    // whose minimum over the row names kore's value (its magnitude is amax).
+    float amax = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const float ax = fabsf(v[e]);
-        if (ax > best) {
-            best = ax;
-            bval = v[e];
-            bidx = 16 * m + e;
-        }
+    for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    amax = fmaxf(amax, __int_as_float(dpp<0xB1>(__float_as_int(amax))));
+    amax = fmaxf(amax, __int_as_float(dpp<0x4E>(__float_as_int(amax))));
+    amax = fmaxf(amax, __int_as_float(dpp<0x124>(__float_as_int(amax))));
+    amax = fmaxf(amax, __int_as_float(dpp<0x128>(__float_as_int(amax))));
+    int idx = 16;
+    float sv = 0.f;
+#pragma unroll
+    for (int e = 15; e >= 0; --e) {
+        const bool hit = fabsf(v[e]) == amax;
+        idx = hit ? e : idx;
+        sv = hit ? v[e] : sv;
     }
-    auto merge = [&](float ob, float ov, int oi) {
-        if (ob > best || (ob == best && oi < bidx)) {
-            best = ob;
-            bval = ov;
-            bidx = oi;
-        }
-    };
-    merge(__int_as_float(dpp<0xB1>(__float_as_int(best))), __int_as_float(dpp<0xB1>(__float_as_int(bval))),
-          dpp<0xB1>(bidx));
-    merge(__int_as_float(dpp<0x4E>(__float_as_int(best))), __int_as_float(dpp<0x4E>(__float_as_int(bval))),
-          dpp<0x4E>(bidx));
-    merge(__int_as_float(dpp<0x124>(__float_as_int(best))), __int_as_float(dpp<0x124>(__float_as_int(bval))),
-          dpp<0x124>(bidx));
-    merge(__int_as_float(dpp<0x128>(__float_as_int(best))), __int_as_float(dpp<0x128>(__float_as_int(bval))),
-          dpp<0x128>(bidx));
+    int key = idx < 16 ? (int)((uint32_t)(32 * m + 2 * idx) | (__float_as_uint(sv) >> 31)) : INT_MAX;
+    key = min(key, dpp<0xB1>(key));
+    key = min(key, dpp<0x4E>(key));
+    key = min(key, dpp<0x124>(key));
+    key = min(key, dpp<0x128>(key));
     uint32_t packed[4] = {0, 0, 0, 0};
     int bsum = 0;
     float d = 0.f;
-    if (best != 0.f) {
+    if (amax != 0.f) {
+        const float bval = (key & 1) ? -amax : amax;
         const float iscale = -127.0f / bval;
+        if (fabsf(iscale) < INFINITY) {
+            // |iscale x| <= 127 (1 + 2^-24)^2 for every |x| <= amax, so the
+            // round-half-even integer lies in [-127, 127] (kore's clamp at 127
+            // never acts) and its low byte is kore's int8; a NaN x gives 0,
+            // as kore's x86 conversion gives INT_MIN, whose low byte is 0
+            int q[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            // (int) of an out-of-range or NaN value is x86's 0x80000000 in kore
-            const float t = rintf(iscale * v[e]);
-            int q = fabsf(t) < 2147483648.0f ? (int)t : INT_MIN;
-            q = q > 127 ? 127 : q;
-            const int q8 = (int)(int8_t)(q & 0xFF);
-            packed[e >> 2] |= (uint32_t)(q8 & 0xFF) << (8 * (e & 3));
-            bsum += q8;
+            for (int e = 0; e < 16; ++e) q[e] = cvt_i32(rintf(iscale * v[e]));
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                packed[k] = __builtin_amdgcn_perm(__builtin_amdgcn_perm((uint32_t)q[4 * k + 3], (uint32_t)q[4 * k + 2], 0x0c0c0400u),
+                                                  __builtin_amdgcn_perm((uint32_t)q[4 * k + 1], (uint32_t)q[4 * k], 0x0c0c0400u),
+                                                  0x05040100u);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) bsum = __builtin_amdgcn_sdot4((int)packed[k], 0x01010101, bsum, false);
         }
+        // else iscale is infinite (amax < 127 / FLT_MAX): every product is
+        // infinite or NaN, kore's conversion gives INT_MIN and the int8 0
         d = 1.0f / iscale;
     }
     return Q8Lane{make_uint4(packed[0], packed[1], packed[2], packed[3]), bsum, d};
