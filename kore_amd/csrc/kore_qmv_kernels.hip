@@ -172,8 +172,10 @@ __device__ float block_rms_scale_sum(double ss, const float *x, int n, float eps
     const double g = (double)(n - 1) * 0x1p-53 / (1.0 - (double)(n - 1) * 0x1p-53);
     const double m = 4.0 * g + 0x1p-50;
     const float lo_s = kore_rms_scale(S * (1.0 - m), n, eps), hi_s = kore_rms_scale(S * (1.0 + m), n, eps);
-    __syncthreads();                       // red is reused below and by the caller
+    // every thread holds the same S, so the branch is uniform; its caller
+    // (the fused matvec prologue) writes red again only after its own barrier
     if (__float_as_uint(lo_s) == __float_as_uint(hi_s)) return lo_s;
+    __syncthreads();                       // every thread has read red before it is rewritten
     if (t == 0) {                          // kore's own loop
         double sk = 0.0;
         for (int i = 0; i < n; ++i) sk += (double)x[i] * x[i];
