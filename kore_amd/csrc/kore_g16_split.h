@@ -15,6 +15,33 @@
 
 namespace kore_qmv_gpu {
 
+// x of another lane of the same 16-lane row: lane i ^ 1 (0xB1), i ^ 2 (0x4E),
+// 7 - i within its 8 lanes (0x141, row_half_mirror), (i - 4) / (i - 8) mod 16
+// (0x124 / 0x128, row rotations).
+template <int CTRL>
+__device__ __forceinline__ float g16_dppf(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// The maximum of x over the wave, in every lane: the 16-lane rows by DPP, then
+// the four rows by lane swaps (v_permlane16_swap / v_permlane32_swap with x as
+// both operands return the two rows of each pair, the two halves, in their
+// results).
+__device__ __forceinline__ float g16_wave_max(float x) {
+    x = fmaxf(x, g16_dppf<0xB1>(x));
+    x = fmaxf(x, g16_dppf<0x4E>(x));
+    x = fmaxf(x, g16_dppf<0x124>(x));
+    x = fmaxf(x, g16_dppf<0x128>(x));
+    const uint32_t u = __float_as_uint(x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const uint32_t a0 = a[0], a1 = a[1];
+    x = fmaxf(__uint_as_float(a0), __uint_as_float(a1));
+    const uint32_t w = __float_as_uint(x);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    const uint32_t b0 = b[0], b1 = b[1];
+    return fmaxf(__uint_as_float(b0), __uint_as_float(b1));
+}
+
 // The row's power of two s = s1 * s2 (max |y s| < 2^10 for amax = max |y|;
 // callers scale as (y * s1) * s2, both factors powers of two, so the product is
 // exact) and 1 / s.  s reaches 2^149 for rows whose maximum is a subnormal
@@ -50,10 +77,12 @@ __device__ __forceinline__ void g16_split_group(uint8_t *__restrict__ x16, int b
     uint8_t *blkp = x16 + (int64_t)blk * kG16BlockBytes;
     *(uint2 *)(blkp + off) = __builtin_bit_cast(uint2, h);
     *(uint2 *)(blkp + kG16Lo + off) = __builtin_bit_cast(uint2, l);
+    // lanes ^ 1, ^ 2, then the other quad of the 8 (every lane of a quad holds
+    // the same sum after the first two steps, so the mirror lane's is its quad's)
     float S = (ys[0] + ys[1]) + (ys[2] + ys[3]);
-    S += __shfl_xor(S, 1);
-    S += __shfl_xor(S, 2);
-    S += __shfl_xor(S, 4);
+    S += g16_dppf<0xB1>(S);
+    S += g16_dppf<0x4E>(S);
+    S += g16_dppf<0x141>(S);
     if ((lane & 7) == 0) {
         const _Float16 sh = (_Float16)S, sl = (_Float16)(S - (float)sh);
         _Float16 *sx = (_Float16 *)(blkp + kG16Sx + b * 32);

@@ -389,8 +389,7 @@ __global__ __launch_bounds__(kPrepThreads) void gemm16_prep_kernel(const float *
 #pragma unroll
     for (int j = 0; j < kPrepPer; ++j)
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = g16_wave_max(amax);
     if (lane == 0) red[t >> 6] = amax;
     __syncthreads();
     amax = red[0];

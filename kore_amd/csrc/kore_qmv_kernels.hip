@@ -1007,7 +1007,7 @@ namespace {
 // them, so the bytes are the pre-pass's own).  Thread t takes float4 groups
 // t + 256 j: lane t % 64 of block 4 j + t / 64.
 __device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, int n, float eps, float *orow,
-                                  uint8_t *__restrict__ x16, double *red) {
+                                  uint8_t *__restrict__ x16, double *red, float *fred) {
     const int t = threadIdx.x, lane = t & 63, b = blockIdx.x, n4 = n / 4;
     const float4 *x4 = (const float4 *)xr, *w4 = (const float4 *)w;
     float4 v[4], wv[4];
@@ -1017,21 +1017,17 @@ __device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, 
         v[j] = x4[f];
         wv[j] = w4[f];
     }
-    double hi = 0.0, lo = 0.0;
+    // the certified scale of block_rms_scale_sum from each thread's plain
+    // double sum of its exact squares (four chains)
+    double sq[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const bool in = t + j * kThreads < n4;
         const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float xv = in ? e[k] : 0.0f;
-            double s, er;
-            two_sum(hi, (double)xv * (double)xv, s, er);
-            hi = s;
-            lo += er;
-        }
+        for (int k = 0; k < 4; ++k) sq[k] += in ? (double)e[k] * (double)e[k] : 0.0;
     }
-    const float scale = block_rms_scale_from(hi, lo, xr, n, eps, red);
+    const float scale = block_rms_scale_sum((sq[0] + sq[1]) + (sq[2] + sq[3]), xr, n, eps, red);
     float4 y[4];
     float amax = 0.f;
 #pragma unroll
@@ -1043,10 +1039,8 @@ __device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, 
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y[j].x), fabsf(y[j].y)), fmaxf(fabsf(y[j].z), fabsf(y[j].w))));
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    float *fred = (float *)red;                        // free again past block_rms_scale_from's last barrier
-    if (lane == 0) fred[t >> 6] = amax;
+    amax = g16_wave_max(amax);
+    if (lane == 0) fred[t >> 6] = amax;                // its own LDS words: red may still be read
     __syncthreads();
     amax = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
     float s1, s2, inv;
@@ -1064,11 +1058,12 @@ __device__ void rmsnorm_split_row(const float *xr, const float *__restrict__ w, 
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, const float *__restrict__ w, int n,
                                                                 float eps, float *out, uint8_t *__restrict__ x16) {
     __shared__ double red[2 * kThreads / 64];
+    __shared__ float fred[kThreads / 64];
     const float *xr = x + (int64_t)blockIdx.x * n;
     float *orow = out + (int64_t)blockIdx.x * n;
     constexpr int kPer = 16;
     if (x16) {
-        rmsnorm_split_row(xr, w, n, eps, orow, x16, red);
+        rmsnorm_split_row(xr, w, n, eps, orow, x16, red, fred);
         return;
     }
     if (n > kPer * kThreads) {
