@@ -127,6 +127,15 @@ def test_quantize_edge_cases():
     b = rng.standard_normal(256); b[8] = np.inf; blocks.append(b)  # inf wins: iscale -0
     b = np.round(rng.standard_normal(256) * 16) / 16; b[0] = -127 / 16; blocks.append(b)  # halves
     b = rng.standard_normal(256); b[:128] = -0.0; blocks.append(b)
+    # the largest magnitude twice inside one 16-value group, opposite signs: the first wins
+    b = rng.standard_normal(256); b[3], b[7] = -6.0, 6.0; blocks.append(b)
+    b = rng.standard_normal(256); b[3], b[7] = 6.0, -6.0; blocks.append(b)
+    b = rng.standard_normal(256); b[255] = -7.0; blocks.append(b)              # the last value
+    b = rng.standard_normal(256); b[40], b[200] = -np.inf, np.inf; blocks.append(b)   # -inf first: d = +inf
+    b = rng.standard_normal(256); b[40], b[200] = np.inf, -np.inf; blocks.append(b)
+    b = rng.standard_normal(256); b[16], b[17] = np.nan, 9.0; blocks.append(b)  # NaN beside the maximum
+    blocks.append(np.full(256, np.nan))                                        # all NaN: a zero block
+    b = np.zeros(256); b[::2] = -0.0; blocks.append(b)                         # signed zeros only
     x = np.concatenate(blocks).astype(np.float32)
     with np.errstate(all="ignore"):
         ref = oracle.quantize_q8K(x)
