@@ -65,7 +65,7 @@ TRAFFIC_DECODE_BYTES = 19_115_000
 TRAFFIC_PREFILL_BYTES = 141_000_000
 # the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
 # of weights, activations and outputs algorithmic)
-TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_478_000}
+TRAFFIC_MATVEC_BYTES = {"ffn_gate_q4k+ffn_up_q4k": 80_449_000}
 # the same for the batched matmul leg's dominant launch, ffn_gate + ffn_up of one layer on 64
 # activations (87.17 MB algorithmic), fp16 path: split pre-pass 1.93 MB, main kernel 124.3 MB
 # (the partials of split tiles included), fix-up 35.1 MB
