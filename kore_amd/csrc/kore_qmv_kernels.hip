@@ -531,11 +531,13 @@ __device__ __forceinline__ Rec part_q6(const Q6Raw &r, const Q8View &x, int i, i
         S[k] = mul24(s0, dot4(u0l, w4(q0l, k))) + mul24(s1, dot4(u0h, w4(q0h, k))) +
                mul24(s2, dot4(u1l, w4(q1l, k))) + mul24(s3, dot4(u1h, w4(q1h, k)));
     }
-    // bias sum over the 16 sub-blocks (kore.cpp:605): part j takes 4j .. 4j+3
+    // bias sum over the 16 sub-blocks (kore.cpp:605): part j takes 4j .. 4j+3,
+    // the scale word j chosen by two selects (a select tree on the lane's j
+    // was compiled as branches, each waiting for the loads)
+    const uint32_t scw = (j & 2) ? ((j & 1) ? r.sc.w : r.sc.z) : ((j & 1) ? r.sc.y : r.sc.x);
     int ibias = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-        ibias += mul24((int)(int8_t)((w4(r.sc, j) >> (8 * e)) & 0xFF), x.bsum(i, 4 * j + e));
+    for (int e = 0; e < 4; ++e) ibias += mul24((int)(int8_t)((scw >> (8 * e)) & 0xFF), x.bsum(i, 4 * j + e));
     ibias += quad_xor1(ibias);
     ibias += quad_xor2(ibias);
     const float d = f16_bits(r.d) * x.d(i);
