@@ -131,7 +131,9 @@ def _stats(ms):
 def _bench_lib():
     from kore_amd import _lib
     _lib.lib()
-    path = os.path.join(ROOT, "kore_amd", "libkore_attn_bench.so")
+    # the timing build's driver when the package was pointed at the timing library (--decode-timeline)
+    timing = os.path.basename(_lib.LIB_PATH) == "libkore_attn_tl.so"
+    path = os.path.join(ROOT, "kore_amd", "libkore_attn_bench_tl.so" if timing else "libkore_attn_bench.so")
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built; run `make -C kore_amd/csrc`")
     L = C.CDLL(path)
@@ -221,6 +223,80 @@ def gpu_decode(steps: int, warmup: int, extras: bool = True):
     return dict(attn=attn, outs=outs, launch_ms=launch_ms, wall_ms=wall.value, region_ms=region.value,
                 num_cu=info.num_cu, buffers=(dq, dk, dv), host_us_per_layer=wall_h.value * 1e3 / (host_steps * NL),
                 host_steps=host_steps, warm_steps=warm_steps, warm_s=warm_s)
+
+
+TL_SPLIT_STAMPS = ("start", "K requested", "q staged", "single rows scored", "V requested", "block done",
+                   "wave state in LDS", "past the barrier", "partial stored", "end")
+TL_COMB_STAMPS = ("start", "partials loaded", "end")
+
+
+def decode_timeline(steps: int, raw_path: str = "", samples: int = 16):
+    """The decode workload on the timing build of the attention library: libkore_attn_tl.so, whose
+    decode_split_kernel and decode_combine_kernel keep s_memrealtime stamps (100 MHz, one counter for
+    the whole device) per wave / per workgroup in registers and write them when each ends.  After the
+    timed warm-up and `steps` steps, the stamps of the last launch of each kernel (the last layer of
+    the last step) are read: per stamp the median, 10th percentile and maximum over the split
+    kernel's waves and the combine's workgroups, in us from the first split wave's start.  Then
+    `samples` more single steps, each read the same way, give per XCD (workgroup index mod 8, the
+    order in which the dispatcher deals workgroups to the XCDs) the median over samples of the
+    XCD's earliest workgroup start and latest workgroup end.  The stamps perturb the kernels a
+    little; use them for where the time goes, the plain bench for how long it takes."""
+    from kore_amd import _lib, hip
+    L = _lib.lib()   # main() pointed the package at the timing build before anything loaded it
+    read = L.kore_attn_tl_read
+    read.restype = C.c_int
+    read.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    dec = gpu_decode(steps, 0, extras=False)
+    per = dec["region_ms"] / 1e3 / (steps * NL)
+    info = dec["attn"].info()
+    n_split = max(1, min(info.num_cu // NKV, 128))
+    n_wg = n_split * NKV
+    waves = n_wg * 4
+    comb_wg = NH * (HD // 32)
+    ts = np.zeros((waves, len(TL_SPLIT_STAMPS)), np.uint64)
+    tc = np.zeros((comb_wg, len(TL_COMB_STAMPS)), np.uint64)
+
+    def grab():
+        if read(ts.ctypes.data, ts.size, tc.ctypes.data, tc.size) != 0:
+            raise RuntimeError("kore_attn_tl_read failed")
+        t0 = int(ts[:, 0].min())
+        return (ts.astype(np.int64) - t0) / 100.0, (tc.astype(np.int64) - t0) / 100.0
+
+    us_s, us_c = grab()
+    B = _bench_lib()
+    dq, dk, dv = dec["buffers"]
+    n_in = max(steps, DEC_STEPS)
+    out = hip.DeviceBuffer(NL * E)
+    wall = C.c_double(0)
+    xs, xe, spans, gaps = [], [], [], []
+    for i in range(samples):
+        _check(B.kab_decode_run(dec["attn"].handle, NL, DEC_POS0, 1, 1, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, 1,
+                                None, None, C.byref(wall)), "decode timeline sample")
+        s_i, c_i = grab()
+        wg_start = s_i[:, 0].reshape(n_wg, 4).min(1)
+        wg_end = s_i[:, -1].reshape(n_wg, 4).max(1)
+        xs.append([wg_start[x::8].min() for x in range(8)])
+        xe.append([wg_end[x::8].max() for x in range(8)])
+        spans.append(wg_end.max())
+        gaps.append(c_i[:, 0].min() - wg_end.max())
+    out.free()
+    dec["attn"].close()
+
+    def row(x):
+        return {"median": round(float(np.median(x)), 2), "p10": round(float(np.percentile(x, 10)), 2),
+                "max": round(float(np.max(x)), 2)}
+
+    if raw_path:
+        np.savez(raw_path, split=us_s, combine=us_c, xcd_start=np.asarray(xs), xcd_end=np.asarray(xe))
+    return {"us_per_layer_gpu": round(per * 1e6, 3), "steps": steps, "splits_per_kv_head": n_split,
+            "split_waves": waves, "combine_workgroups": comb_wg, "unit": "us from the first split wave's start",
+            "split": {name: row(us_s[:, i]) for i, name in enumerate(TL_SPLIT_STAMPS)},
+            "split_median_by_wave": {name: [round(float(np.median(us_s[w::4, i])), 2) for w in range(4)]
+                                     for i, name in enumerate(TL_SPLIT_STAMPS)},
+            "combine": {name: row(us_c[:, i]) for i, name in enumerate(TL_COMB_STAMPS)},
+            "samples": samples, "split_span": row(spans), "gap_to_combine": row(gaps),
+            "xcd_first_start_median": [round(float(v), 2) for v in np.median(np.asarray(xs), 0)],
+            "xcd_last_end_median": [round(float(v), 2) for v in np.median(np.asarray(xe), 0)]}
 
 
 def gpu_prefill(steps: int, warmup: int):
@@ -1328,6 +1404,11 @@ def main(argv=None):
     ap.add_argument("--prompt-chunks", type=int, default=8, help="64-token chunks of the whole-prompt leg")
     ap.add_argument("--cpu-threads", type=int, default=16,
                     help="threads of kore's own matvec in the CPU baseline (the GPU box's CPU share)")
+    ap.add_argument("--decode-timeline", action="store_true",
+                    help="only run the decode workload on the timing build (libkore_attn_tl.so) and report "
+                         "per-wave s_memrealtime stamps of the last layer's kernels")
+    ap.add_argument("--timeline-raw", default="", help="with --decode-timeline: also save every stamp (us) "
+                                                            "to this .npz file")
     ap.add_argument("--read-calibration", action="store_true",
                     help="only time a plain streaming read kernel per launch size (the yardstick of the "
                          "HBM-bound kernels) and an empty launch")
@@ -1344,6 +1425,9 @@ def main(argv=None):
         print("--steps must be in 1..4096 and --warmup <= --steps", file=sys.stderr)
         return 2
 
+    if args.decode_timeline:
+        from kore_amd import _lib
+        _lib.LIB_PATH = os.path.join(ROOT, "kore_amd", "libkore_attn_tl.so")
     from kore_amd import hip
     if args.copy_calibration:
         n = 64 << 20   # floats: 256 MiB
@@ -1383,13 +1467,19 @@ def main(argv=None):
                                       "tflops": round(F / per / 1e12, 3),
                                       "frac": round(F / per / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}}), flush=True)
         return 0
+    if args.decode_timeline:
+        print(json.dumps({"decode_timeline": decode_timeline(args.steps, args.timeline_raw)}), flush=True)
+        return 0
     if args.decode_only:
         dec = gpu_decode(args.steps, args.warmup, extras=False)
         per = dec["region_ms"] / 1e3 / (args.steps * NL)
         nbytes = sum(decode_bytes(DEC_POS0 + s + 1) for s in range(args.steps)) / args.steps
         dec["attn"].close()
+        floor = decode_floor(nbytes, max(args.steps * NL, 64 * NL))
         print(json.dumps({"decode": {"us_per_layer_gpu": round(per * 1e6, 3), "bytes_per_layer": int(nbytes),
-                                     "gbs": round(nbytes / per / 1e9, 1)}}), flush=True)
+                                     "gbs": round(nbytes / per / 1e9, 1), "floor_us": floor["read_plus_dependent_launch_us"],
+                                     "layer_over_floor": round(per * 1e6 / floor["read_plus_dependent_launch_us"],
+                                                               3)}}), flush=True)
         return 0
     pf = None
     if not args.no_prefill:

@@ -38,6 +38,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace kore_attn_gpu {
@@ -73,6 +74,38 @@ __device__ __forceinline__ float row16_max(float x) {
     return fmaxf(x, dpp<0x121>(x));
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Timing build only (libkore_attn_tl.so, compiled with -DKORE_DECODE_TIMELINE;
+// never the product library): every wave of the latest decode_split_kernel
+// launch and every workgroup of the latest decode_combine_kernel launch keep
+// s_memrealtime stamps (a 100 MHz counter shared by the whole device) in
+// scalar registers and write them when they end, so the stamps add no memory
+// operation between a kernel's loads and their uses.  kore_attn_tl_read()
+// copies them out.
+#ifdef KORE_DECODE_TIMELINE
+constexpr int kTlStamps = 10;     // per split wave
+constexpr int kTlWaves = 4096;
+constexpr int kTlCombStamps = 3;  // per combine workgroup
+constexpr int kTlComb = 2048;
+__device__ unsigned long long g_tl_split[kTlWaves * kTlStamps];
+__device__ unsigned long long g_tl_comb[kTlComb * kTlCombStamps];
+#define TL_DECL(n) unsigned long long tl_[n] = {}
+#define TL(i)                                      \
+    do {                                           \
+        __builtin_amdgcn_sched_barrier(0);         \
+        tl_[i] = __builtin_amdgcn_s_memrealtime(); \
+        __builtin_amdgcn_sched_barrier(0);         \
+    } while (0)
+#define TL_WRITE(buf, cap, id, n)                                                    \
+    do {                                                                             \
+        if ((threadIdx.x & 63) == 0 && (id) < (cap))                                 \
+            for (int i_ = 0; i_ < (n); ++i_) buf[(size_t)(id) * (n) + i_] = tl_[i_]; \
+    } while (0)
+#else
+#define TL_DECL(n) ((void)0)
+#define TL(i) ((void)0)
+#define TL_WRITE(buf, cap, id, n) ((void)0)
+#endif
 
 // NEOX rotation of the pair (x0, x1) = (x[i], x[i + hd/2]) by (c, s)
 // (kore.cpp:1379-1382): products rounded, then difference / sum rounded.
@@ -217,13 +250,14 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     constexpr int NEW_WAVE = kWaves - 1;  // the wave that takes the new row
     static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    TL_DECL(kTlStamps);
+    TL(0);
 
     constexpr int OST = HD + 4;    // LDS stride of a head's output (bank spread)
     __shared__ __align__(16) float s_o[kWaves * NR * OST];  // unnormalised wave outputs
-    __shared__ __align__(16) float s_knew[HD];              // the new row: roped k
-    __shared__ __align__(16) float s_vnew[HD];              // ... and v
-    __shared__ __align__(16) float s_kx[kWaves * HD];       // the extra rows: k
-    __shared__ __align__(16) float s_vx[kWaves * HD];       // ... and v
+    // single entries e = 0 .. kWaves: the extra rows, then the new row
+    __shared__ __align__(16) float s_kx[(kWaves + 1) * HD];  // k (roped)
+    __shared__ __align__(16) float s_vx[(kWaves + 1) * HD];  // v (zero where absent)
     __shared__ float s_m[NST * 8], s_l[NST * 8];
     __shared__ __align__(16) float s_p[kWaves * (8 * 16 + 8)];   // per wave: weights, rescale factors
 
@@ -307,6 +341,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     __builtin_amdgcn_sched_barrier(0);
     load_k(kA, wave);
     __builtin_amdgcn_sched_barrier(0);
+    TL(1);
     // the merge arguments are waited for here, behind the K rows' requests: a
     // first read after the block loop would wait for a kernel-argument fetch
     // at the end of the kernel
@@ -317,7 +352,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     // (heads past NR are zero); the dot products are widened to double and
     // scaled by kore's 1/sqrt(hd) and log2(e) there.
     const double qscale = (double)a.scale * 1.4426950408889634;
-    float qb[NHG][NT][4];
+    // the single-block kernel keeps q as doubles (no conversion per product);
+    // the multi-block kernel's second register set leaves no room for that
+    using QT = std::conditional_t<MULTI, float, double>;
+    QT qb[NHG][NT][4];
     {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -346,10 +384,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
                 const float4 qv = ld4(&wq[min(h, NR - 1) * QS + CH * kq + 4 * t]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    qb[hg][t][e] = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
+                    qb[hg][t][e] = (QT)__builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
             }
         }
     }
+    TL(2);
 
     // dot of q (operand layout) with a k row staged in LDS, for heads jq + 4hg:
     // lane l sums its dims CH kq + 4t + e, then the four lanes of its chunk
@@ -366,9 +405,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         for (int t = 0; t < NT; ++t) {
             const float4 kx = ld4(&kr[CH * kq + 4 * t]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+            for (int e = 0; e < 4; ++e) {
+                const double kd = (double)comp(kx, e);
 #pragma unroll
-                for (int hg = 0; hg < NHG; ++hg) sx[hg][e] = fma((double)qb[hg][t][e], (double)comp(kx, e), sx[hg][e]);
+                for (int hg = 0; hg < NHG; ++hg) sx[hg][e] = fma((double)qb[hg][t][e], kd, sx[hg][e]);
+            }
         }
 #pragma unroll
         for (int hg = 0; hg < NHG; ++hg)
@@ -377,57 +418,62 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     // A single row as a softmax state: max = its score rounded to fp32, sum
     // = 2^(score - max) with the difference in fp64 (about 1), output = that
     // sum times the row (the merge applies the sum to the stored v row).
-    // ---- the wave's extra row (state kWaves + wave; -inf and a zero row
-    // when the wave has none) and, in NEW_WAVE, the new row (state 2 kWaves,
-    // roped here; -inf and a zero row outside the owner workgroup).  Only
-    // LDS and register work: no memory operation under these branches.  The
-    // merge weighs each stored v row with the state's sum.
-    {
-        const bool x_on = wave < n_extra;
-        if (lane < HALF) {
-            s_kx[wave * HD + lane] = xk0;
-            s_kx[wave * HD + lane + HALF] = xk1;
-            s_vx[wave * HD + lane] = x_on ? xv0 : 0.f;
-            s_vx[wave * HD + lane + HALF] = x_on ? xv1 : 0.f;
-        }
-        __builtin_amdgcn_wave_barrier();
-        const bool on = x_on && xrow != new_slot;
-        double sxs[NHG];
-        row_scores(&s_kx[wave * HD], sxs);
+    // ---- single entry `wave` (state kWaves + wave): extra row `wave` (from
+    // the cache, roped already) while wave < n_extra, the new row (roped
+    // here; it counts in the owner workgroup only) at wave == n_extra, none
+    // after; entry kWaves (state 2 kWaves: the new row behind kWaves extra
+    // rows) in NEW_WAVE.  So a wave scores one single row, NEW_WAVE a second
+    // one only when the split ends in kWaves extra rows.  Absent entries hold
+    // max -inf, sum 0 and a zero v row.  Only LDS and register work: no
+    // memory operation under these branches.  The merge weighs each stored v
+    // row with the state's sum.
+    float nky0, nky1;
+    rope_pair(nk0, nk1, ncs, nky0, nky1);
+    auto single_state = [&](int st, bool on, const double (&sc)[NHG]) {
 #pragma unroll
         for (int hg = 0; hg < NHG; ++hg) {
-            const double sx = sxs[hg];
+            const double sx = sc[hg];
             const int h = jq + 4 * hg;
             if (lane < 4 && h < NR) {
                 const float mx = (float)sx;
-                s_m[(kWaves + wave) * 8 + h] = on ? mx : -INFINITY;
-                s_l[(kWaves + wave) * 8 + h] = on ? fast_exp2((float)(sx - (double)mx)) : 0.f;
+                s_m[st * 8 + h] = on ? mx : -INFINITY;
+                s_l[st * 8 + h] = on ? fast_exp2((float)(sx - (double)mx)) : 0.f;
             }
         }
-    }
-    float nky0, nky1;
-    rope_pair(nk0, nk1, ncs, nky0, nky1);
-    if (wave == NEW_WAVE) {
+    };
+    {
+        const bool x_is = wave < n_extra, n_is = wave == n_extra;
+        const bool on = (x_is && xrow != new_slot) || (n_is && is_owner);
         if (lane < HALF) {
-            s_knew[lane] = nky0;
-            s_knew[lane + HALF] = nky1;
-            s_vnew[lane] = is_owner ? nv0 : 0.f;
-            s_vnew[lane + HALF] = is_owner ? nv1 : 0.f;
+            s_kx[wave * HD + lane] = x_is ? xk0 : nky0;
+            s_kx[wave * HD + lane + HALF] = x_is ? xk1 : nky1;
+            s_vx[wave * HD + lane] = on ? (x_is ? xv0 : nv0) : 0.f;
+            s_vx[wave * HD + lane + HALF] = on ? (x_is ? xv1 : nv1) : 0.f;
         }
         __builtin_amdgcn_wave_barrier();
-        double sns[NHG];
-        row_scores(s_knew, sns);
-#pragma unroll
-        for (int hg = 0; hg < NHG; ++hg) {
-            const double sn = sns[hg];
-            const int h = jq + 4 * hg;
-            if (lane < 4 && h < NR) {
-                const float mn = (float)sn;
-                s_m[2 * kWaves * 8 + h] = is_owner ? mn : -INFINITY;
-                s_l[2 * kWaves * 8 + h] = is_owner ? fast_exp2((float)(sn - (double)mn)) : 0.f;
-            }
-        }
+        double sxs[NHG];
+        row_scores(&s_kx[wave * HD], sxs);
+        single_state(kWaves + wave, on, sxs);
     }
+    if (wave == NEW_WAVE) {
+        const bool on = n_extra == kWaves && is_owner;
+        if (lane < HALF) {
+            s_kx[kWaves * HD + lane] = nky0;
+            s_kx[kWaves * HD + lane + HALF] = nky1;
+            s_vx[kWaves * HD + lane] = on ? nv0 : 0.f;
+            s_vx[kWaves * HD + lane + HALF] = on ? nv1 : 0.f;
+        }
+        double sns[NHG];
+        if (n_extra == kWaves) {   // uniform in the workgroup
+            __builtin_amdgcn_wave_barrier();
+            row_scores(&s_kx[kWaves * HD], sns);
+        } else {
+#pragma unroll
+            for (int hg = 0; hg < NHG; ++hg) sns[hg] = 0.0;
+        }
+        single_state(2 * kWaves, on, sns);
+    }
+    TL(3);
     __builtin_amdgcn_sched_barrier(0);
     load_v(vA, wave);
     if constexpr (MULTI) {
@@ -437,6 +483,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    TL(4);
 
     floatx4 o[NMB];
 #pragma unroll
@@ -530,6 +577,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         }
     }
 
+    TL(5);
     // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
     // 64(mb / 4) + 16kq + 4v + mb % 4; the max and sum of head jq + 4hg
     // come from lane jq
@@ -549,7 +597,9 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             s_l[wave * 8 + h] = l_run[hg];
         }
     }
+    TL(6);
     __syncthreads();
+    TL(7);
 
     // ---- merge of the wave states (and the new row's) per (head, float4):
     // thread (h, d4) for h < NR, d4 < hd/4 (NR * hd/4 <= kThreads)
@@ -579,11 +629,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             const int st = kWaves + w;
             ms[w] = s_m[st * 8 + h];
             ls[w] = s_l[st * 8 + h];
-            xs[w] = ld4(w < kWaves ? &s_vx[w * HD + 4 * d4] : &s_vnew[4 * d4]);
+            xs[w] = ld4(&s_vx[w * HD + 4 * d4]);
         }
 #pragma unroll
         for (int w = 0; w <= kWaves; ++w) {
-            const bool on = w < kWaves ? w < n_extra : is_owner;
+            const bool on = w < n_extra || (w == n_extra && is_owner);
             ms[w] = on ? ms[w] : -INFINITY;
             ls[w] = on ? ls[w] : 0.f;
             xs[w] = on ? xs[w] : zero4();
@@ -591,7 +641,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         }
 #pragma unroll
         for (int w = 0; w < 2 * kWaves + 1; ++w) {
-            const bool on = w < kWaves ? true : (w < 2 * kWaves ? w - kWaves < n_extra : is_owner);
+            const bool on = w < kWaves ? true : (w - kWaves < n_extra || (w - kWaves == n_extra && is_owner));
             if (!on) continue;
             const float mx = w < kWaves ? mw[w] : ms[w - kWaves];
             const float e0 = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
@@ -617,6 +667,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             }
         }
     }
+    TL(8);
     // ---- append of the new row (owner workgroup), last: no load waits
     // behind these stores
     if (is_owner && wave == NEW_WAVE && lane < HALF) {
@@ -627,6 +678,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         vd[lane] = nv0;
         vd[lane + HALF] = nv1;
     }
+    TL(9);
+    TL_WRITE(g_tl_split, kTlWaves, (blockIdx.y * gridDim.x + blockIdx.x) * kWaves + wave, kTlStamps);
 }
 
 // Block (q-head h, 32-dim chunk): out[h][chunk] = sum_s w_s o_s / sum_s w_s l_s
@@ -638,6 +691,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
 template <int HD, int PER>
 __global__ __launch_bounds__(64) void decode_combine_kernel(const float *part_o, const float *part_ml, float *out,
                                                             int n_split) {
+    TL_DECL(kTlCombStamps);
+    TL(0);
     const int h = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
     const int S = n_split;
     const int sub = lane >> 3, c = lane & 7;
@@ -656,6 +711,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const float *part_o,
 #pragma unroll
     for (int i = 0; i < PER; ++i) m = fmaxf(m, st[i].x);
     m = max4rows(row16_max(m));
+    TL(1);
     float4 acc = zero4();
     float den = 0.f;
 #pragma unroll
@@ -681,6 +737,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const float *part_o,
         st4(out + (size_t)h * HD + chunk * 32 + c * 4,
             make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
     }
+    TL(2);
+    TL_WRITE(g_tl_comb, kTlComb, blockIdx.y * gridDim.x + blockIdx.x, kTlCombStamps);
 }
 
 // ------------------------------------------------------------------ append
@@ -1325,6 +1383,20 @@ hipError_t launch_decode_hd(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
 }
 
 }  // namespace
+
+#ifdef KORE_DECODE_TIMELINE
+// Timing build only: the stamps of the latest decode_split_kernel launch
+// ([workgroup * 4 + wave][kTlStamps]) and decode_combine_kernel launch
+// ([workgroup][kTlCombStamps]), after a device synchronisation.
+extern "C" __attribute__((visibility("default"))) int kore_attn_tl_read(unsigned long long *split, size_t split_words,
+                                                                        unsigned long long *comb, size_t comb_words) {
+    if (split_words > sizeof(g_tl_split) / 8 || comb_words > sizeof(g_tl_comb) / 8) return -1;
+    if (hipDeviceSynchronize() != hipSuccess) return -4;
+    if (split_words && hipMemcpyFromSymbol(split, HIP_SYMBOL(g_tl_split), split_words * 8) != hipSuccess) return -4;
+    if (comb_words && hipMemcpyFromSymbol(comb, HIP_SYMBOL(g_tl_comb), comb_words * 8) != hipSuccess) return -4;
+    return 0;
+}
+#endif
 
 hipError_t static_scratch(int device, float **ptr) {
     constexpr int kMaxDevices = 64;
