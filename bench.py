@@ -230,29 +230,55 @@ TL_SPLIT_STAMPS = ("start", "K requested", "q staged", "single rows scored", "V 
 TL_COMB_STAMPS = ("start", "partials loaded", "end")
 
 
-def decode_timeline(steps: int, raw_path: str = "", samples: int = 16):
+def decode_timeline(steps: int, raw_path: str = "", samples: int = 16, config: str = "7b"):
     """The decode workload on the timing build of the attention library: libkore_attn_tl.so, whose
     decode_split_kernel and decode_combine_kernel keep s_memrealtime stamps (100 MHz, one counter for
-    the whole device) per wave / per workgroup in registers and write them when each ends.  After the
-    timed warm-up and `steps` steps, the stamps of the last launch of each kernel (the last layer of
-    the last step) are read: per stamp the median, 10th percentile and maximum over the split
-    kernel's waves and the combine's workgroups, in us from the first split wave's start.  Then
-    `samples` more single steps, each read the same way, give per XCD (workgroup index mod 8, the
-    order in which the dispatcher deals workgroups to the XCDs) the median over samples of the
-    XCD's earliest workgroup start and latest workgroup end.  The stamps perturb the kernels a
-    little; use them for where the time goes, the plain bench for how long it takes."""
-    from kore_amd import _lib, hip
+    the whole device) per wave / per workgroup in registers and write them when each ends.  config
+    "7b": the headline workload (28 layers, cache filled to 4096, `steps` steps after the timed
+    warm-up); "3b": the 3B decode at position 32767 (36 layers, the same position repeated).  The
+    stamps of the last launch of each kernel (the last layer of the last step) are read: per stamp
+    the median, 10th percentile and maximum over the split kernel's waves and the combine's
+    workgroups, in us from the first split wave's start.  Then `samples` more single steps, each read
+    the same way, give per XCD (workgroup index mod 8, the order in which the dispatcher deals
+    workgroups to the XCDs) the median over samples of the XCD's earliest workgroup start and latest
+    workgroup end.  The stamps perturb the kernels a little; use them for where the time goes, the
+    plain bench for how long it takes."""
+    from kore_amd import KoreAttn, _lib, hip, synth_dev
     L = _lib.lib()   # main() pointed the package at the timing build before anything loaded it
     read = L.kore_attn_tl_read
     read.restype = C.c_int
     read.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
-    dec = gpu_decode(steps, 0, extras=False)
-    per = dec["region_ms"] / 1e3 / (steps * NL)
-    info = dec["attn"].info()
-    n_split = max(1, min(info.num_cu // NKV, 128))
-    n_wg = n_split * NKV
+    B = _bench_lib()
+    wall, region = C.c_double(0), C.c_float(0)
+    if config == "7b":
+        dec = gpu_decode(steps, 0, extras=False)
+        attn, (dq, dk, dv) = dec["attn"], dec["buffers"]
+        nl, nh, nkv, hd, pos, pos_step, n_in = NL, NH, NKV, HD, DEC_POS0, 1, max(steps, DEC_STEPS)
+        per = dec["region_ms"] / 1e3 / (steps * NL)
+    else:
+        nl, nh, nkv, hd, pos, pos_step, n_in = 36, 16, 2, 128, 32767, 0, 1
+        attn = KoreAttn(nl, 32768, nh, nkv, hd, ROPE_BASE)
+        _fill_cache(attn, nl, pos, nkv * hd, 9, attn.stream)
+        dq, dk, dv = hip.DeviceBuffer(nl * nh * hd), hip.DeviceBuffer(nl * nkv * hd), hip.DeviceBuffer(nl * nkv * hd)
+        for l in range(nl):
+            synth_dev(dq.at(l * nh * hd), 1, nh * hd, 9, q_stream(l), pos, 1, 0, 1.0, attn.stream)
+            synth_dev(dk.at(l * nkv * hd), 1, nkv * hd, 9, k_stream(l), pos, 2, 0, 1.0, attn.stream)
+            synth_dev(dv.at(l * nkv * hd), 1, nkv * hd, 9, v_stream(l), pos, 3, 0, 1.0, attn.stream)
+        attn.sync()
+        o = hip.DeviceBuffer(nl * nh * hd)
+        t_warm = time.perf_counter()
+        while time.perf_counter() - t_warm < WARM_SECONDS:
+            _check(B.kab_decode_run(attn.handle, nl, pos, 0, 4, dq.ptr, dk.ptr, dv.ptr, 1, o.ptr, 1, None, None,
+                                    C.byref(wall)), "decode warmup")
+        _check(B.kab_decode_run(attn.handle, nl, pos, 0, steps, dq.ptr, dk.ptr, dv.ptr, 1, o.ptr, 1, None,
+                                C.byref(region), C.byref(wall)), "decode timed")
+        o.free()
+        per = region.value / 1e3 / (steps * nl)
+    info = attn.info()
+    n_split = max(1, min(info.num_cu // nkv, 128))
+    n_wg = n_split * nkv
     waves = n_wg * 4
-    comb_wg = NH * (HD // 32)
+    comb_wg = nh * (hd // 32)
     ts = np.zeros((waves, len(TL_SPLIT_STAMPS)), np.uint64)
     tc = np.zeros((comb_wg, len(TL_COMB_STAMPS)), np.uint64)
 
@@ -263,14 +289,10 @@ def decode_timeline(steps: int, raw_path: str = "", samples: int = 16):
         return (ts.astype(np.int64) - t0) / 100.0, (tc.astype(np.int64) - t0) / 100.0
 
     us_s, us_c = grab()
-    B = _bench_lib()
-    dq, dk, dv = dec["buffers"]
-    n_in = max(steps, DEC_STEPS)
-    out = hip.DeviceBuffer(NL * E)
-    wall = C.c_double(0)
+    out = hip.DeviceBuffer(nl * nh * hd)
     xs, xe, spans, gaps = [], [], [], []
     for i in range(samples):
-        _check(B.kab_decode_run(dec["attn"].handle, NL, DEC_POS0, 1, 1, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, 1,
+        _check(B.kab_decode_run(attn.handle, nl, pos, pos_step, 1, dq.ptr, dk.ptr, dv.ptr, n_in, out.ptr, 1,
                                 None, None, C.byref(wall)), "decode timeline sample")
         s_i, c_i = grab()
         wg_start = s_i[:, 0].reshape(n_wg, 4).min(1)
@@ -280,7 +302,9 @@ def decode_timeline(steps: int, raw_path: str = "", samples: int = 16):
         spans.append(wg_end.max())
         gaps.append(c_i[:, 0].min() - wg_end.max())
     out.free()
-    dec["attn"].close()
+    for b in (dq, dk, dv):
+        b.free()
+    attn.close()
 
     def row(x):
         return {"median": round(float(np.median(x)), 2), "p10": round(float(np.percentile(x, 10)), 2),
@@ -288,8 +312,9 @@ def decode_timeline(steps: int, raw_path: str = "", samples: int = 16):
 
     if raw_path:
         np.savez(raw_path, split=us_s, combine=us_c, xcd_start=np.asarray(xs), xcd_end=np.asarray(xe))
-    return {"us_per_layer_gpu": round(per * 1e6, 3), "steps": steps, "splits_per_kv_head": n_split,
-            "split_waves": waves, "combine_workgroups": comb_wg, "unit": "us from the first split wave's start",
+    return {"config": config, "us_per_layer_gpu": round(per * 1e6, 3), "steps": steps,
+            "splits_per_kv_head": n_split, "split_waves": waves, "combine_workgroups": comb_wg,
+            "unit": "us from the first split wave's start",
             "split": {name: row(us_s[:, i]) for i, name in enumerate(TL_SPLIT_STAMPS)},
             "split_median_by_wave": {name: [round(float(np.median(us_s[w::4, i])), 2) for w in range(4)]
                                      for i, name in enumerate(TL_SPLIT_STAMPS)},
@@ -1407,6 +1432,8 @@ def main(argv=None):
     ap.add_argument("--decode-timeline", action="store_true",
                     help="only run the decode workload on the timing build (libkore_attn_tl.so) and report "
                          "per-wave s_memrealtime stamps of the last layer's kernels")
+    ap.add_argument("--timeline-config", default="7b", choices=("7b", "3b"),
+                    help="with --decode-timeline: the 7B decode at 4096.. (default) or the 3B decode at 32767")
     ap.add_argument("--timeline-raw", default="", help="with --decode-timeline: also save every stamp (us) "
                                                             "to this .npz file")
     ap.add_argument("--read-calibration", action="store_true",
@@ -1468,7 +1495,8 @@ def main(argv=None):
                                       "frac": round(F / per / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}}), flush=True)
         return 0
     if args.decode_timeline:
-        print(json.dumps({"decode_timeline": decode_timeline(args.steps, args.timeline_raw)}), flush=True)
+        print(json.dumps({"decode_timeline": decode_timeline(args.steps, args.timeline_raw,
+                                                             config=args.timeline_config)}), flush=True)
         return 0
     if args.decode_only:
         dec = gpu_decode(args.steps, args.warmup, extras=False)

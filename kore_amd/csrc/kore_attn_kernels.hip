@@ -244,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     constexpr int NJ = HD / 64;    // V float4 per lane per row
     constexpr int NMB = HD / 16;   // 16-dim output blocks
     constexpr int HALF = HD / 2;
-    constexpr int NST = 2 * kWaves + 1;   // wave states, extra-row states, new row
+    constexpr int NST = kWaves + 1;       // wave states, then single entry kWaves
     constexpr int CH = HD / 4;            // dims per lane of a K row (one k chunk)
     constexpr int NHG = NR > 4 ? 2 : 1;   // groups of 4 heads (score chains)
     constexpr int NEW_WAVE = kWaves - 1;  // the wave that takes the new row
@@ -441,19 +441,20 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             }
         }
     };
+    // the wave's own entry: its scores stay in registers and become the
+    // wave's initial softmax state below
+    const bool e_on = (wave < n_extra && xrow != new_slot) || (wave == n_extra && is_owner);
+    double sxs[NHG];
     {
-        const bool x_is = wave < n_extra, n_is = wave == n_extra;
-        const bool on = (x_is && xrow != new_slot) || (n_is && is_owner);
+        const bool x_is = wave < n_extra;
         if (lane < HALF) {
             s_kx[wave * HD + lane] = x_is ? xk0 : nky0;
             s_kx[wave * HD + lane + HALF] = x_is ? xk1 : nky1;
-            s_vx[wave * HD + lane] = on ? (x_is ? xv0 : nv0) : 0.f;
-            s_vx[wave * HD + lane + HALF] = on ? (x_is ? xv1 : nv1) : 0.f;
+            s_vx[wave * HD + lane] = e_on ? (x_is ? xv0 : nv0) : 0.f;
+            s_vx[wave * HD + lane + HALF] = e_on ? (x_is ? xv1 : nv1) : 0.f;
         }
         __builtin_amdgcn_wave_barrier();
-        double sxs[NHG];
         row_scores(&s_kx[wave * HD], sxs);
-        single_state(kWaves + wave, on, sxs);
     }
     if (wave == NEW_WAVE) {
         const bool on = n_extra == kWaves && is_owner;
@@ -471,7 +472,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
 #pragma unroll
             for (int hg = 0; hg < NHG; ++hg) sns[hg] = 0.0;
         }
-        single_state(2 * kWaves, on, sns);
+        single_state(kWaves, on, sns);
     }
     TL(3);
     __builtin_amdgcn_sched_barrier(0);
@@ -485,20 +486,33 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     __builtin_amdgcn_sched_barrier(0);
     TL(4);
 
-    floatx4 o[NMB];
-#pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
-    // softmax state of heads jq + 4hg (the same in every lane that holds them)
+    // ---- the wave's initial softmax state: its single entry (max = the
+    // score rounded to fp32, sum = 2^(score - max) with the difference in
+    // fp64, output = sum * v row), or the empty state (-inf, 0, 0).  Heads
+    // jq + 4hg are in every lane that holds them; the output goes into the
+    // value layout by one MFMA k-step per output block whose only nonzero
+    // weights are in lanes kq = 0: lane (m16, 0) takes head m16's sum.
     float m_run[NHG], l_run[NHG];
 #pragma unroll
     for (int hg = 0; hg < NHG; ++hg) {
-        m_run[hg] = -INFINITY;
-        l_run[hg] = 0.f;
+        const float mx = (float)sxs[hg];
+        m_run[hg] = e_on ? mx : -INFINITY;
+        l_run[hg] = e_on ? fast_exp2((float)(sxs[hg] - (double)mx)) : 0.f;
+    }
+    floatx4 o[NMB];
+    {
+        const float pw = (kq == 0 && m16 < NR) ? (m16 < 4 ? l_run[0] : l_run[NHG - 1]) : 0.f;
+        float4 xv[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) xv[j] = ld4(&s_vx[wave * HD + 64 * j + 4 * m16]);
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+            o[mb] = mfma16(comp(xv[mb / 4], mb % 4), pw, floatx4{0.f, 0.f, 0.f, 0.f});
     }
     float *wp = s_p + wave * (8 * 16 + 8);   // the wave's weights [head][k][s], then rescale factors [head]
     const int rD = 4 * bq + iq;              // this lane's row of the block in the score layout
 
-    auto process = [&](const float4 *kf, const float4 (*vf)[NJ], int b, bool first) {
+    auto process = [&](const float4 *kf, const float4 (*vf)[NJ], int b) {
         const int rb = r0 + 16 * b;
         double acc[NHG];
 #pragma unroll
@@ -512,7 +526,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
                 for (int hg = 0; hg < NHG; ++hg) acc[hg] = mfma4d(kv, (double)qb[hg][t][e], acc[hg]);
             }
         const int row = rb + rD;
-        const bool ok = row < r_end && row != new_slot;
+        const bool ok = b < n_blk && row < r_end && row != new_slot;
 #pragma unroll
         for (int hg = 0; hg < NHG; ++hg) {
             const double sc = acc[hg] * qscale;
@@ -535,7 +549,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         // to the value layout: lane (m16, kq) takes rows 4s + kq of head m16
         const bool hv = m16 < 4 * NHG;
         const float4 pv = hv ? ld4(&wp[min(m16, 4 * NHG - 1) * 16 + kq * 4]) : zero4();
-        if (!first) {
+        {
             const float al = hv ? wp[8 * 16 + min(m16, 4 * NHG - 1)] : 1.f;
 #pragma unroll
             for (int mb = 0; mb < NMB; ++mb) o[mb] *= al;
@@ -548,14 +562,14 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     };
     if constexpr (MULTI) {
         for (int b = wave; b < n_blk;) {
-            process(kA, vA, b, b == wave);
+            process(kA, vA, b);
             b += kWaves;
             if (b >= n_blk) break;
             if (b + kWaves < n_blk) {
                 load_k(kA, b + kWaves);
                 load_v(vA, b + kWaves);
             }
-            process(kB, vB, b, false);
+            process(kB, vB, b);
             b += kWaves;
             if (b + kWaves < n_blk) {
                 load_k(kB, b + kWaves);
@@ -564,17 +578,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         }
     } else {
         // at most one block per wave: the first block's loads are exact and
-        // the block runs unconditionally (a wave without one masks it out)
-        process(kA, vA, wave, true);
-        if (wave >= n_blk) {
-#pragma unroll
-            for (int hg = 0; hg < NHG; ++hg) {
-                m_run[hg] = -INFINITY;
-                l_run[hg] = 0.f;
-            }
-#pragma unroll
-            for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+        // the block runs unconditionally (a wave without one masks its rows)
+        process(kA, vA, wave);
     }
 
     TL(5);
@@ -601,8 +606,9 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     __syncthreads();
     TL(7);
 
-    // ---- merge of the wave states (and the new row's) per (head, float4):
-    // thread (h, d4) for h < NR, d4 < hd/4 (NR * hd/4 <= kThreads)
+    // ---- merge of the wave states (each holds its wave's single entry) and
+    // of entry kWaves per (head, float4): thread (h, d4) for h < NR, d4 <
+    // hd/4 (NR * hd/4 <= kThreads)
     static_assert(8 * (HD / 4) <= kThreads, "one merge thread per output float4");
     if (tid < NR * (HD / 4)) {
         const int h = tid / (HD / 4), d4 = tid - h * (HD / 4);
@@ -614,46 +620,33 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             lw[w] = s_l[w * 8 + h];
             xw[w] = ld4(&s_o[(w * NR + h) * OST + 4 * d4]);
         }
-        float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+        // entry kWaves (the new row behind kWaves extra rows), read in every
+        // workgroup (written in every one: absent, it holds max -inf, sum 0
+        // and a zero row) so that all the LDS reads are issued together; it
+        // holds the bare v row, weighed here with its sum
+        const bool on5 = n_extra == kWaves && is_owner;
+        const float m5 = on5 ? s_m[kWaves * 8 + h] : -INFINITY;
+        const float l5 = s_l[kWaves * 8 + h];
+        const float4 x5 = ld4(&s_vx[kWaves * HD + 4 * d4]);
+        const float m = fmaxf(fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3])), m5);
         float l = 0.f;
         float4 acc = zero4();
-        // the extra rows' and the new row's states, every one read (each is
-        // written in every workgroup: the absent ones hold max -inf, sum 0 and
-        // a zero row) and the absent ones masked, so that all the LDS reads
-        // are issued together (reads under the per-state branches were each
-        // waited for before the next)
-        float ms[kWaves + 1], ls[kWaves + 1];
-        float4 xs[kWaves + 1];
 #pragma unroll
-        for (int w = 0; w <= kWaves; ++w) {
-            const int st = kWaves + w;
-            ms[w] = s_m[st * 8 + h];
-            ls[w] = s_l[st * 8 + h];
-            xs[w] = ld4(&s_vx[w * HD + 4 * d4]);
+        for (int w = 0; w < kWaves; ++w) {
+            const float e = mw[w] == -INFINITY ? 0.f : fast_exp2(mw[w] - m);
+            l = fmaf(e, lw[w], l);
+            acc.x = fmaf(e, xw[w].x, acc.x);
+            acc.y = fmaf(e, xw[w].y, acc.y);
+            acc.z = fmaf(e, xw[w].z, acc.z);
+            acc.w = fmaf(e, xw[w].w, acc.w);
         }
-#pragma unroll
-        for (int w = 0; w <= kWaves; ++w) {
-            const bool on = w < n_extra || (w == n_extra && is_owner);
-            ms[w] = on ? ms[w] : -INFINITY;
-            ls[w] = on ? ls[w] : 0.f;
-            xs[w] = on ? xs[w] : zero4();
-            m = fmaxf(m, ms[w]);
-        }
-#pragma unroll
-        for (int w = 0; w < 2 * kWaves + 1; ++w) {
-            const bool on = w < kWaves ? true : (w - kWaves < n_extra || (w - kWaves == n_extra && is_owner));
-            if (!on) continue;
-            const float mx = w < kWaves ? mw[w] : ms[w - kWaves];
-            const float e0 = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
-            const float4 x = w < kWaves ? xw[w] : xs[w - kWaves];
-            // a wave state holds its weighted output; a single row's state
-            // holds the bare v row, weighed here with the state's sum
-            const float e = w < kWaves ? e0 : e0 * ls[w - kWaves];
-            l = w < kWaves ? fmaf(e, lw[w], l) : l + e;
-            acc.x = fmaf(e, x.x, acc.x);
-            acc.y = fmaf(e, x.y, acc.y);
-            acc.z = fmaf(e, x.z, acc.z);
-            acc.w = fmaf(e, x.w, acc.w);
+        if (on5) {   // uniform in the workgroup; no memory operation inside
+            const float e = fast_exp2(m5 - m) * l5;
+            l += e;
+            acc.x = fmaf(e, x5.x, acc.x);
+            acc.y = fmaf(e, x5.y, acc.y);
+            acc.z = fmaf(e, x5.z, acc.z);
+            acc.w = fmaf(e, x5.w, acc.w);
         }
         const size_t hg = (size_t)g * n_rep + h;
         if (n_split == 1) {
