@@ -456,23 +456,20 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         __builtin_amdgcn_wave_barrier();
         row_scores(&s_kx[wave * HD], sxs);
     }
-    if (wave == NEW_WAVE) {
-        const bool on = n_extra == kWaves && is_owner;
+    // entry kWaves exists only behind kWaves extra rows (uniform in the
+    // workgroup); absent, nothing of it is written: the merge reads it but
+    // uses it only when present
+    if (wave == NEW_WAVE && n_extra == kWaves) {
         if (lane < HALF) {
             s_kx[kWaves * HD + lane] = nky0;
             s_kx[kWaves * HD + lane + HALF] = nky1;
-            s_vx[kWaves * HD + lane] = on ? nv0 : 0.f;
-            s_vx[kWaves * HD + lane + HALF] = on ? nv1 : 0.f;
+            s_vx[kWaves * HD + lane] = is_owner ? nv0 : 0.f;
+            s_vx[kWaves * HD + lane + HALF] = is_owner ? nv1 : 0.f;
         }
+        __builtin_amdgcn_wave_barrier();
         double sns[NHG];
-        if (n_extra == kWaves) {   // uniform in the workgroup
-            __builtin_amdgcn_wave_barrier();
-            row_scores(&s_kx[kWaves * HD], sns);
-        } else {
-#pragma unroll
-            for (int hg = 0; hg < NHG; ++hg) sns[hg] = 0.0;
-        }
-        single_state(kWaves, on, sns);
+        row_scores(&s_kx[kWaves * HD], sns);
+        single_state(kWaves, is_owner, sns);
     }
     TL(3);
     __builtin_amdgcn_sched_barrier(0);
@@ -620,12 +617,15 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             lw[w] = s_l[w * 8 + h];
             xw[w] = ld4(&s_o[(w * NR + h) * OST + 4 * d4]);
         }
-        // entry kWaves (the new row behind kWaves extra rows), read in every
-        // workgroup (written in every one: absent, it holds max -inf, sum 0
-        // and a zero row) so that all the LDS reads are issued together; it
-        // holds the bare v row, weighed here with its sum
+        // entry kWaves (the new row behind kWaves extra rows; it holds the
+        // bare v row, weighed here with its sum): read in every workgroup so
+        // that all the LDS reads are issued together, used only where it was
+        // written and counts (its max masked by bits: a select of the loaded
+        // value would become a read under a branch)
         const bool on5 = n_extra == kWaves && is_owner;
-        const float m5 = on5 ? s_m[kWaves * 8 + h] : -INFINITY;
+        const unsigned keep5 = on5 ? 0xFFFFFFFFu : 0u;
+        const float m5 = __builtin_bit_cast(float, (__builtin_bit_cast(unsigned, s_m[kWaves * 8 + h]) & keep5) |
+                                                       (__builtin_bit_cast(unsigned, -INFINITY) & ~keep5));
         const float l5 = s_l[kWaves * 8 + h];
         const float4 x5 = ld4(&s_vx[kWaves * HD + 4 * d4]);
         const float m = fmaxf(fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3])), m5);
