@@ -226,7 +226,7 @@ def gpu_decode(steps: int, warmup: int, extras: bool = True):
 
 
 TL_SPLIT_STAMPS = ("start", "K requested", "q staged", "single rows scored", "V requested", "block done",
-                   "wave state in LDS", "past the barrier", "partial stored", "end")
+                   "wave state in LDS", "past the barrier", "partial stored", "end", "q requested")
 TL_COMB_STAMPS = ("start", "partials loaded", "end")
 
 
@@ -296,7 +296,7 @@ def decode_timeline(steps: int, raw_path: str = "", samples: int = 16, config: s
                                 None, None, C.byref(wall)), "decode timeline sample")
         s_i, c_i = grab()
         wg_start = s_i[:, 0].reshape(n_wg, 4).min(1)
-        wg_end = s_i[:, -1].reshape(n_wg, 4).max(1)
+        wg_end = s_i[:, TL_SPLIT_STAMPS.index("end")].reshape(n_wg, 4).max(1)
         xs.append([wg_start[x::8].min() for x in range(8)])
         xe.append([wg_end[x::8].max() for x in range(8)])
         spans.append(wg_end.max())

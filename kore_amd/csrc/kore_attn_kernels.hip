@@ -83,7 +83,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // operation between a kernel's loads and their uses.  kore_attn_tl_read()
 // copies them out.
 #ifdef KORE_DECODE_TIMELINE
-constexpr int kTlStamps = 10;     // per split wave
+constexpr int kTlStamps = 11;     // per split wave
 constexpr int kTlWaves = 4096;
 constexpr int kTlCombStamps = 3;  // per combine workgroup
 constexpr int kTlComb = 2048;
@@ -307,6 +307,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
         sx0[i] = ld4(qh);
         sx1[i] = ld4(qh + HALF);
     }
+    TL(10);
     // the new k/v row and this wave's extra row, pair (i, i + hd/2) in lane
     // i: loaded by every lane of every wave (clamped rows), so that no load
     // is conditional, and ahead of the K rows, so that their scores are taken
