@@ -38,7 +38,6 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
-#include <type_traits>
 #include <vector>
 
 namespace kore_attn_gpu {
@@ -225,16 +224,16 @@ __device__ __forceinline__ double sum4rows_d(double x) {
 // rows, then the V rows, so the score MFMAs run while V streams in.  Every
 // load before the first MFMA is unconditional (rows past the split's end
 // are clamped to its last row and masked): a load under a branch makes the
-// compiler's wait counts for everything after it conservative.  MULTI
-// kernels (splits of more than four blocks) keep the next block of a wave in
-// a second register set while the current one is processed.
+// compiler's wait counts for everything after it conservative.  This kernel
+// takes splits of at most one block per wave (plus kWaves extra rows);
+// decode_multi_kernel takes the longer ones.
 // The new token's row is not read from the cache: the owner workgroup ropes
 // it, appends it, and adds it as one more softmax state (its own score, sum
 // 1, output v).  Slots [0, n_rows) never include it except in a wrapped ring,
-// where its stale slot is masked.  The four wave states (and the extra and
-// new rows') are merged in LDS into one partial per q-head, or into `out`
-// when the kv-head has a single split.
-template <int HD, int NR, bool MULTI>
+// where its stale slot is masked.  The four wave states (each started from
+// the wave's single row) are merged in LDS into one partial per q-head, or
+// into `out` when the kv-head has a single split.
+template <int HD, int NR>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
                                                                 float *vc_in, const float *__restrict__ k_in,
                                                                 const float *__restrict__ v_in, int n_rows,
@@ -325,7 +324,6 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     const int n_split = a.n_split, n_rep = a.n_rep;
 
     float4 kA[NT], vA[4][NJ];
-    float4 kB[MULTI ? NT : 1], vB[MULTI ? 4 : 1][NJ];
     auto load_k = [&](float4 *kf, int b) {
         const float *kr = kg + (size_t)min(r0 + 16 * b + m16, last_row) * HD + CH * kq;
 #pragma unroll
@@ -353,10 +351,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     // (heads past NR are zero); the dot products are widened to double and
     // scaled by kore's 1/sqrt(hd) and log2(e) there.
     const double qscale = (double)a.scale * 1.4426950408889634;
-    // the single-block kernel keeps q as doubles (no conversion per product);
-    // the multi-block kernel's second register set leaves no room for that
-    using QT = std::conditional_t<MULTI, float, double>;
-    QT qb[NHG][NT][4];
+    // q is kept as doubles (no conversion per product)
+    double qb[NHG][NT][4];
     {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -385,7 +381,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
                 const float4 qv = ld4(&wq[min(h, NR - 1) * QS + CH * kq + 4 * t]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    qb[hg][t][e] = (QT)__builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
+                    qb[hg][t][e] = (double)__builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
             }
         }
     }
@@ -475,12 +471,6 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     TL(3);
     __builtin_amdgcn_sched_barrier(0);
     load_v(vA, wave);
-    if constexpr (MULTI) {
-        if (wave + kWaves < n_blk) {
-            load_k(kB, wave + kWaves);
-            load_v(vB, wave + kWaves);
-        }
-    }
     __builtin_amdgcn_sched_barrier(0);
     TL(4);
 
@@ -558,27 +548,9 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             for (int sk = 0; sk < 4; ++sk) o[mb] = mfma16(comp(vf[sk][mb / 4], mb % 4), comp(pv, sk), o[mb]);
         __builtin_amdgcn_wave_barrier();
     };
-    if constexpr (MULTI) {
-        for (int b = wave; b < n_blk;) {
-            process(kA, vA, b);
-            b += kWaves;
-            if (b >= n_blk) break;
-            if (b + kWaves < n_blk) {
-                load_k(kA, b + kWaves);
-                load_v(vA, b + kWaves);
-            }
-            process(kB, vB, b);
-            b += kWaves;
-            if (b + kWaves < n_blk) {
-                load_k(kB, b + kWaves);
-                load_v(vB, b + kWaves);
-            }
-        }
-    } else {
-        // at most one block per wave: the first block's loads are exact and
-        // the block runs unconditionally (a wave without one masks its rows)
-        process(kA, vA, wave);
-    }
+    // one block per wave at most: the block's loads are exact and it runs
+    // unconditionally (a wave without one masks its rows)
+    process(kA, vA, wave);
 
     TL(5);
     // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
@@ -648,6 +620,438 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
             acc.y = fmaf(e, x5.y, acc.y);
             acc.z = fmaf(e, x5.z, acc.z);
             acc.w = fmaf(e, x5.w, acc.w);
+        }
+        const size_t hg = (size_t)g * n_rep + h;
+        if (n_split == 1) {
+            const float inv = 1.f / l;
+            st4(out_p + hg * HD + 4 * d4, make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
+        } else {
+            st4(part_o + (hg * n_split + split) * HD + 4 * d4, acc);
+            if (d4 == 0) {
+                part_ml[(hg * n_split + split) * 2 + 0] = m;
+                part_ml[(hg * n_split + split) * 2 + 1] = l;
+            }
+        }
+    }
+    TL(8);
+    // ---- append of the new row (owner workgroup), last: no load waits
+    // behind these stores
+    if (is_owner && wave == NEW_WAVE && lane < HALF) {
+        float *kd = kc_in + head_base + (size_t)new_slot * HD;
+        float *vd = vc_in + head_base + (size_t)new_slot * HD;
+        kd[lane] = nky0;
+        kd[lane + HALF] = nky1;
+        vd[lane] = nv0;
+        vd[lane + HALF] = nv1;
+    }
+    TL(9);
+    TL_WRITE(g_tl_split, kTlWaves, (blockIdx.y * gridDim.x + blockIdx.x) * kWaves + wave, kTlStamps);
+}
+
+// Splits of more than kWaves blocks plus kWaves extra rows (3B at 32K: 256
+// rows, four blocks per wave): decode_split_kernel's layouts and arithmetic
+// with each wave's blocks in a loop that keeps the next block in a second
+// register set, the extra rows and the new row as nine softmax states merged
+// after the loop (wave 3 scores the new row besides its own extra row), and
+// q in float operands (the second register set leaves no room for doubles).
+// Kept apart from the single-block kernel: the single rows as wave initial
+// states and one row per wave measured 0.4-0.8 us slower here (a loop that
+// streams at the read rate, and a different register allocation).
+template <int HD, int NR>
+__global__ __launch_bounds__(kThreads) void decode_multi_kernel(const float *__restrict__ q_in, float *kc_in,
+                                                                float *vc_in, const float *__restrict__ k_in,
+                                                                const float *__restrict__ v_in, int n_rows,
+                                                                int rows_per_split, int new_slot, int slots,
+                                                                DecodeArgs a, RopeRow rr) {
+    constexpr int NT = HD / 16;    // K float4 per lane per block (MFMA k-steps / 4)
+    constexpr int NJ = HD / 64;    // V float4 per lane per row
+    constexpr int NMB = HD / 16;   // 16-dim output blocks
+    constexpr int HALF = HD / 2;
+    constexpr int NST = 2 * kWaves + 1;   // wave states, extra-row states, new row
+    constexpr int CH = HD / 4;            // dims per lane of a K row (one k chunk)
+    constexpr int NHG = NR > 4 ? 2 : 1;   // groups of 4 heads (score chains)
+    constexpr int NEW_WAVE = kWaves - 1;  // the wave that takes the new row
+    static_assert(NR >= 1 && NR <= 8, "at most 8 q-heads per workgroup");
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    TL_DECL(kTlStamps);
+    TL(0);
+
+    constexpr int OST = HD + 4;    // LDS stride of a head's output (bank spread)
+    __shared__ __align__(16) float s_o[kWaves * NR * OST];  // unnormalised wave outputs
+    __shared__ __align__(16) float s_knew[HD];              // the new row: roped k
+    __shared__ __align__(16) float s_vnew[HD];              // ... and v
+    __shared__ __align__(16) float s_kx[kWaves * HD];       // the extra rows: k
+    __shared__ __align__(16) float s_vx[kWaves * HD];       // ... and v
+    __shared__ float s_m[NST * 8], s_l[NST * 8];
+    __shared__ __align__(16) float s_p[kWaves * (8 * 16 + 8)];   // per wave: weights, rescale factors
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m16 = lane & 15, kq = lane >> 4;
+    const int jq = lane & 3, bq = (lane >> 2) & 3, iq = lane >> 4;   // score layout: head, row group, row
+    const int split = blockIdx.x, g = blockIdx.y;
+    const int r0 = split * rows_per_split;
+    const int r_end = min(r0 + rows_per_split, n_rows);
+    const int n_own = max(r_end - r0, 0);
+    // whole blocks, plus a last partial block of more than kWaves rows; a
+    // remainder of at most kWaves rows is taken as extra rows, one per wave
+    const int rem = n_own % kDecodeBlock;
+    const int n_blk = n_own / kDecodeBlock + (rem > kWaves ? 1 : 0);
+    const int n_extra = rem > kWaves ? 0 : rem;
+    const int last_row = max(r_end - 1, 0);
+    const int owner = n_rows == 0 ? 0 : min(new_slot, n_rows - 1) / rows_per_split;
+    const bool is_owner = split == owner;
+    const size_t head_base = (size_t)g * slots * HD;
+    const float *kg = kc_in + head_base;
+    const float *vg = vc_in + head_base;
+
+    // ---- q of the NR heads of kv-head g, roped and pre-scaled by every wave
+    // for itself and staged through the wave's own LDS rows, so no
+    // workgroup barrier stands between a wave's loads and its first MFMA.
+    // Pair p < NR * hd/8 of the wave is (q[h][4c..4c+3], q[h][hd/2 + 4c..])
+    // with h = p / NC, c = p % NC; lane l takes pairs l and l + 64, which
+    // share c = l % NC and so the four (cos, sin) pairs of dims 4c..4c+3.
+    // The MFMA operand layout repeats every q value in 16/NR lanes and every
+    // (cos, sin) pair in 16, so loading the operands directly would cost each
+    // wave as much vector-memory traffic as its cache rows.
+    constexpr int QS = HD + 4;                 // s_q row stride (bank spread)
+    constexpr int NC = HALF / 4;               // float4 per half row
+    constexpr int NP = (NR * NC + 63) / 64;    // pairs per lane
+    static_assert(64 % NC == 0 && NP <= 2, "a lane's pairs share their (cos, sin) values");
+    // per wave NR rows of roped q * 1/sqrt(hd) * log2(e), and one row that
+    // takes the stores of lanes without a pair (so the stores need no branch)
+    __shared__ __align__(16) float s_q[kWaves * (NR + 1) * QS];
+    float *wq = s_q + wave * (NR + 1) * QS;
+    const int sc = lane % NC;
+    float4 sx0[NP], sx1[NP];
+    const float4 scs01 = ld4(&rr.cs[8 * sc]), scs23 = ld4(&rr.cs[8 * sc + 4]);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int sh = min((lane + 64 * i) / NC, NR - 1);
+        const float *qh = q_in + (size_t)(g * NR + sh) * HD + 4 * sc;
+        sx0[i] = ld4(qh);
+        sx1[i] = ld4(qh + HALF);
+    }
+    TL(10);
+    // the new k/v row and this wave's extra row, pair (i, i + hd/2) in lane
+    // i: loaded by every lane of every wave (clamped rows), so that no load
+    // is conditional, and ahead of the K rows, so that their scores are taken
+    // while the cache rows stream in
+    const int ni = min(lane, HALF - 1);
+    const float nk0 = k_in[(size_t)g * HD + ni], nk1 = k_in[(size_t)g * HD + ni + HALF];
+    const float nv0 = v_in[(size_t)g * HD + ni], nv1 = v_in[(size_t)g * HD + ni + HALF];
+    const float2 ncs = *reinterpret_cast<const float2 *>(&rr.cs[2 * ni]);
+    const int xrow = min(r0 + (n_own - n_extra) + wave, last_row);
+    const float xk0 = kg[(size_t)xrow * HD + ni], xk1 = kg[(size_t)xrow * HD + ni + HALF];
+    const float xv0 = vg[(size_t)xrow * HD + ni], xv1 = vg[(size_t)xrow * HD + ni + HALF];
+    // the arguments the merge needs (read from the kernel-argument segment,
+    // not preloaded)
+    float *const out_p = a.out, *const part_o = a.part_o, *const part_ml = a.part_ml;
+    const int n_split = a.n_split, n_rep = a.n_rep;
+
+    float4 kA[NT], vA[4][NJ];
+    float4 kB[NT], vB[4][NJ];
+    auto load_k = [&](float4 *kf, int b) {
+        const float *kr = kg + (size_t)min(r0 + 16 * b + m16, last_row) * HD + CH * kq;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) kf[t] = ld4(kr + 4 * t);
+    };
+    auto load_v = [&](float4 (*vf)[NJ], int b) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float *vr = vg + (size_t)min(r0 + 16 * b + 4 * s + kq, last_row) * HD + 4 * m16;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) vf[s][j] = ld4(vr + 64 * j);
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(kA, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    TL(1);
+    // the merge arguments are waited for here, behind the K rows' requests: a
+    // first read after the block loop would wait for a kernel-argument fetch
+    // at the end of the kernel
+    asm volatile("" ::"s"(out_p), "s"(part_o), "s"(part_ml), "s"(n_split), "s"(n_rep));
+
+    // RoPE of the staged pairs into the wave's LDS rows, then the B operand:
+    // lane l holds heads jq and jq + 4 (jq = l % 4) at dims CH kq + 4t + e
+    // (heads past NR are zero); the dot products are widened to double and
+    // scaled by kore's 1/sqrt(hd) and log2(e) there.
+    const double qscale = (double)a.scale * 1.4426950408889634;
+    float qb[NHG][NT][4];
+    {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int p = lane + 64 * i;
+            const int row = p < NR * NC ? p / NC : NR;
+            float y0[4], y1[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 c4 = e < 2 ? scs01 : scs23;
+                const float2 cs = (e & 1) ? make_float2(c4.z, c4.w) : make_float2(c4.x, c4.y);
+                rope_pair(comp(sx0[i], e), comp(sx1[i], e), cs, y0[e], y1[e]);
+            }
+            st4(&wq[row * QS + 4 * sc], make_float4(y0[0], y0[1], y0[2], y0[3]));
+            st4(&wq[row * QS + HALF + 4 * sc], make_float4(y1[0], y1[1], y1[2], y1[3]));
+        }
+        __builtin_amdgcn_wave_barrier();
+        // heads past NR read head NR - 1 and are zeroed by a bit mask: a
+        // select of the loaded value became a read under a lane mask, each
+        // waited for before the next
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) {
+            const int h = jq + 4 * hg;
+            const unsigned keep = h < NR ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float4 qv = ld4(&wq[min(h, NR - 1) * QS + CH * kq + 4 * t]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    qb[hg][t][e] = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
+            }
+        }
+    }
+    TL(2);
+
+    // dot of q (operand layout) with a k row staged in LDS, for heads jq + 4hg:
+    // lane l sums its dims CH kq + 4t + e, then the four lanes of its chunk
+    // row (l, l ^ 16, l ^ 32, l ^ 48) add up; every lane ends with the scores
+    // (four independent partial sums per head group: a single chain of
+    // dependent fp64 FMAs would take most of a microsecond)
+    auto row_scores = [&](const float *kr, double (&out)[NHG]) {
+        double sx[NHG][4];
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sx[hg][e] = 0.0;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 kx = ld4(&kr[CH * kq + 4 * t]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int hg = 0; hg < NHG; ++hg) sx[hg][e] = fma((double)qb[hg][t][e], (double)comp(kx, e), sx[hg][e]);
+        }
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg)
+            out[hg] = sum4rows_d((sx[hg][0] + sx[hg][1]) + (sx[hg][2] + sx[hg][3])) * qscale;
+    };
+    // A single row as a softmax state: max = its score rounded to fp32, sum
+    // = 2^(score - max) with the difference in fp64 (about 1), output = that
+    // sum times the row (the merge applies the sum to the stored v row).
+    // ---- the wave's extra row (state kWaves + wave; -inf and a zero row
+    // when the wave has none) and, in NEW_WAVE, the new row (state 2 kWaves,
+    // roped here; -inf and a zero row outside the owner workgroup).  Only
+    // LDS and register work: no memory operation under these branches.  The
+    // merge weighs each stored v row with the state's sum.
+    {
+        const bool x_on = wave < n_extra;
+        if (lane < HALF) {
+            s_kx[wave * HD + lane] = xk0;
+            s_kx[wave * HD + lane + HALF] = xk1;
+            s_vx[wave * HD + lane] = x_on ? xv0 : 0.f;
+            s_vx[wave * HD + lane + HALF] = x_on ? xv1 : 0.f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const bool on = x_on && xrow != new_slot;
+        double sxs[NHG];
+        row_scores(&s_kx[wave * HD], sxs);
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) {
+            const double sx = sxs[hg];
+            const int h = jq + 4 * hg;
+            if (lane < 4 && h < NR) {
+                const float mx = (float)sx;
+                s_m[(kWaves + wave) * 8 + h] = on ? mx : -INFINITY;
+                s_l[(kWaves + wave) * 8 + h] = on ? fast_exp2((float)(sx - (double)mx)) : 0.f;
+            }
+        }
+    }
+    float nky0, nky1;
+    rope_pair(nk0, nk1, ncs, nky0, nky1);
+    if (wave == NEW_WAVE) {
+        if (lane < HALF) {
+            s_knew[lane] = nky0;
+            s_knew[lane + HALF] = nky1;
+            s_vnew[lane] = is_owner ? nv0 : 0.f;
+            s_vnew[lane + HALF] = is_owner ? nv1 : 0.f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        double sns[NHG];
+        row_scores(s_knew, sns);
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) {
+            const double sn = sns[hg];
+            const int h = jq + 4 * hg;
+            if (lane < 4 && h < NR) {
+                const float mn = (float)sn;
+                s_m[2 * kWaves * 8 + h] = is_owner ? mn : -INFINITY;
+                s_l[2 * kWaves * 8 + h] = is_owner ? fast_exp2((float)(sn - (double)mn)) : 0.f;
+            }
+        }
+    }
+    TL(3);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(vA, wave);
+    if (wave + kWaves < n_blk) {
+        load_k(kB, wave + kWaves);
+        load_v(vB, wave + kWaves);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    TL(4);
+
+    floatx4 o[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) o[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // softmax state of heads jq + 4hg (the same in every lane that holds them)
+    float m_run[NHG], l_run[NHG];
+#pragma unroll
+    for (int hg = 0; hg < NHG; ++hg) {
+        m_run[hg] = -INFINITY;
+        l_run[hg] = 0.f;
+    }
+    float *wp = s_p + wave * (8 * 16 + 8);   // the wave's weights [head][k][s], then rescale factors [head]
+    const int rD = 4 * bq + iq;              // this lane's row of the block in the score layout
+
+    auto process = [&](const float4 *kf, const float4 (*vf)[NJ], int b, bool first) {
+        const int rb = r0 + 16 * b;
+        double acc[NHG];
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) acc[hg] = 0.0;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double kv = (double)comp(kf[t], e);
+#pragma unroll
+                for (int hg = 0; hg < NHG; ++hg) acc[hg] = mfma4d(kv, (double)qb[hg][t][e], acc[hg]);
+            }
+        const int row = rb + rD;
+        const bool ok = row < r_end && row != new_slot;
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) {
+            const double sc = acc[hg] * qscale;
+            float mt = ok ? (float)sc : -INFINITY;
+            mt = fmaxf(mt, dpp<0x124>(mt));           // the four row groups of a 16-lane row
+            mt = fmaxf(mt, dpp<0x128>(mt));
+            const float m_new = fmaxf(m_run[hg], max4rows(mt));
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;   // a block with every row masked
+            const float alpha = fast_exp2(m_run[hg] - m_use);
+            const float p = ok ? fast_exp2((float)(sc - (double)m_use)) : 0.f;
+            float ps = p + dpp<0x124>(p);
+            ps += dpp<0x128>(ps);
+            l_run[hg] = fmaf(l_run[hg], alpha, sum4rows(ps));
+            m_run[hg] = m_new;
+            const int h = jq + 4 * hg;
+            wp[h * 16 + iq * 4 + bq] = p;
+            if (lane < 4) wp[8 * 16 + h] = alpha;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // to the value layout: lane (m16, kq) takes rows 4s + kq of head m16
+        const bool hv = m16 < 4 * NHG;
+        const float4 pv = hv ? ld4(&wp[min(m16, 4 * NHG - 1) * 16 + kq * 4]) : zero4();
+        if (!first) {
+            const float al = hv ? wp[8 * 16 + min(m16, 4 * NHG - 1)] : 1.f;
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) o[mb] *= al;
+        }
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+            for (int sk = 0; sk < 4; ++sk) o[mb] = mfma16(comp(vf[sk][mb / 4], mb % 4), comp(pv, sk), o[mb]);
+        __builtin_amdgcn_wave_barrier();
+    };
+    for (int b = wave; b < n_blk;) {
+        process(kA, vA, b, b == wave);
+        b += kWaves;
+        if (b >= n_blk) break;
+        if (b + kWaves < n_blk) {
+            load_k(kA, b + kWaves);
+            load_v(vA, b + kWaves);
+        }
+        process(kB, vB, b, false);
+        b += kWaves;
+        if (b + kWaves < n_blk) {
+            load_k(kB, b + kWaves);
+            load_v(vB, b + kWaves);
+        }
+    }
+    TL(5);
+    // ---- the wave's state to LDS: o[mb][v] is head m16 at dim
+    // 64(mb / 4) + 16kq + 4v + mb % 4; the max and sum of head jq + 4hg
+    // come from lane jq
+    if (m16 < NR) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                st4(&s_o[(wave * NR + m16) * OST + 64 * j + 16 * kq + 4 * v],
+                    make_float4(o[4 * j][v], o[4 * j + 1][v], o[4 * j + 2][v], o[4 * j + 3][v]));
+    }
+#pragma unroll
+    for (int hg = 0; hg < NHG; ++hg) {
+        const int h = jq + 4 * hg;
+        if (lane < 4 && h < NR) {
+            s_m[wave * 8 + h] = m_run[hg];
+            s_l[wave * 8 + h] = l_run[hg];
+        }
+    }
+    TL(6);
+    __syncthreads();
+    TL(7);
+
+    // ---- merge of the wave states (and the new row's) per (head, float4):
+    // thread (h, d4) for h < NR, d4 < hd/4 (NR * hd/4 <= kThreads)
+    static_assert(8 * (HD / 4) <= kThreads, "one merge thread per output float4");
+    if (tid < NR * (HD / 4)) {
+        const int h = tid / (HD / 4), d4 = tid - h * (HD / 4);
+        float mw[kWaves], lw[kWaves];
+        float4 xw[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            mw[w] = s_m[w * 8 + h];
+            lw[w] = s_l[w * 8 + h];
+            xw[w] = ld4(&s_o[(w * NR + h) * OST + 4 * d4]);
+        }
+        float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+        float l = 0.f;
+        float4 acc = zero4();
+        // the extra rows' and the new row's states, every one read (each is
+        // written in every workgroup: the absent ones hold max -inf, sum 0 and
+        // a zero row) and the absent ones masked, so that all the LDS reads
+        // are issued together (reads under the per-state branches were each
+        // waited for before the next)
+        float ms[kWaves + 1], ls[kWaves + 1];
+        float4 xs[kWaves + 1];
+#pragma unroll
+        for (int w = 0; w <= kWaves; ++w) {
+            const int st = kWaves + w;
+            ms[w] = s_m[st * 8 + h];
+            ls[w] = s_l[st * 8 + h];
+            xs[w] = ld4(w < kWaves ? &s_vx[w * HD + 4 * d4] : &s_vnew[4 * d4]);
+        }
+#pragma unroll
+        for (int w = 0; w <= kWaves; ++w) {
+            const bool on = w < kWaves ? w < n_extra : is_owner;
+            ms[w] = on ? ms[w] : -INFINITY;
+            ls[w] = on ? ls[w] : 0.f;
+            xs[w] = on ? xs[w] : zero4();
+            m = fmaxf(m, ms[w]);
+        }
+#pragma unroll
+        for (int w = 0; w < 2 * kWaves + 1; ++w) {
+            const bool on = w < kWaves ? true : (w < 2 * kWaves ? w - kWaves < n_extra : is_owner);
+            if (!on) continue;
+            const float mx = w < kWaves ? mw[w] : ms[w - kWaves];
+            const float e0 = mx == -INFINITY ? 0.f : fast_exp2(mx - m);
+            const float4 x = w < kWaves ? xw[w] : xs[w - kWaves];
+            // a wave state holds its weighted output; a single row's state
+            // holds the bare v row, weighed here with the state's sum
+            const float e = w < kWaves ? e0 : e0 * ls[w - kWaves];
+            l = w < kWaves ? fmaf(e, lw[w], l) : l + e;
+            acc.x = fmaf(e, x.x, acc.x);
+            acc.y = fmaf(e, x.y, acc.y);
+            acc.z = fmaf(e, x.z, acc.z);
+            acc.w = fmaf(e, x.w, acc.w);
         }
         const size_t hg = (size_t)g * n_rep + h;
         if (n_split == 1) {
@@ -1337,18 +1741,17 @@ hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
     // dynamic LDS that a CU holds one: two on a CU would leave another idle.
     const dim3 grid(a.n_split, a.n_head_kv);
     if (a.rows_per_split > kWaves * kDecodeBlock + kWaves) {
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR, true>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
+        hipLaunchKernelGGL((decode_multi_kernel<HD, NR>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     } else {
         static const unsigned dyn = [] {
             hipFuncAttributes fa{};
-            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR, false>)) !=
-                hipSuccess)
+            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR>)) != hipSuccess)
                 return 0u;
             const size_t half_cu = kLdsPerCu / 2 + 256;
             return fa.sharedSizeBytes < half_cu ? (unsigned)(half_cu - fa.sharedSizeBytes) : 0u;
         }();
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR, false>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc, a.k, a.v,
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     }
     static_assert(kMaxDecodeSplits <= 8 * 16, "the combine takes at most 16 splits per lane");
