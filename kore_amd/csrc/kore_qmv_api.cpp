@@ -118,13 +118,17 @@ size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 // more lanes, and every step's chain advances then run on fewer lanes.
 // Measured on the 7B shapes (us per launch, rows per wave 1 / 2 / 4 / 8):
 // attn_output 8.2 / 7.0 / 6.4 / 7.2, q+k+v 14.7 / 11.1 / 10.4 / 12.3,
-// ffn_down (Q4_K) 18.4 / 17.0 / 19.7 / 29.1.
+// ffn_down (Q4_K) 18.4 / 17.0 / 19.7 / 29.1.  A matrix tall enough for more
+// than eight such rounds at 16 rows per wave (the 152064-row output head)
+// takes 4: 79-83 us against 89 at 16 and 85 at 8 (gate+up, three rounds,
+// stays at 16: 20.6 us against 21.4 at 4).
 int pick_rows_per_wave(int64_t rows, int nblk, int num_cu) {
     if (const char *env = getenv("KORE_QMV_ROWS_PER_WAVE")) {
         const int r = atoi(env);
         if (r == 1 || r == 2 || r == 4 || r == 8 || r == 16) return r;
     }
     const int64_t want = (nblk > 16 ? 6LL : 3LL) * std::max(num_cu, 1);
+    if (rows / 16 > 8 * want) return 4;
     for (int r = 16; r > 1; r /= 2)
         if (rows / r >= want) return r;
     return 1;
