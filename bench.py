@@ -61,7 +61,7 @@ WARM_SECONDS = 0.5             # least decode work ahead of the timed region (st
 # kernels and workloads, each counter scaled by what it reads for a 256 MiB device copy
 # (fetch x 2.0, write x 1.0): decode layer = split + combine kernel, prefill layer =
 # append + prefill + prefill combine kernel.  Re-measure when a kernel changes.
-TRAFFIC_DECODE_BYTES = 19_115_000
+TRAFFIC_DECODE_BYTES = 19_082_000
 TRAFFIC_PREFILL_BYTES = 141_000_000
 # the same for the matvec leg's dominant launch, ffn_gate + ffn_up of one layer (76.55 MB
 # of weights, activations and outputs algorithmic)
