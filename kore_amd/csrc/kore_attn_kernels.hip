@@ -351,8 +351,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
     // (heads past NR are zero); the dot products are widened to double and
     // scaled by kore's 1/sqrt(hd) and log2(e) there.
     const double qscale = (double)a.scale * 1.4426950408889634;
-    // q is kept as doubles (no conversion per product)
-    double qb[NHG][NT][4];
+    float qb[NHG][NT][4];
     {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -381,7 +380,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
                 const float4 qv = ld4(&wq[min(h, NR - 1) * QS + CH * kq + 4 * t]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    qb[hg][t][e] = (double)__builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
+                    qb[hg][t][e] = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, comp(qv, e)) & keep);
             }
         }
     }
@@ -652,8 +651,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__r
 // rows, four blocks per wave): decode_split_kernel's layouts and arithmetic
 // with each wave's blocks in a loop that keeps the next block in a second
 // register set, the extra rows and the new row as nine softmax states merged
-// after the loop (wave 3 scores the new row besides its own extra row), and
-// q in float operands (the second register set leaves no room for doubles).
+// after the loop (wave 3 scores the new row besides its own extra row).
 // Kept apart from the single-block kernel: the single rows as wave initial
 // states and one row per wave measured 0.4-0.8 us slower here (a loop that
 // streams at the read rate, and a different register allocation).
