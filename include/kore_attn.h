@@ -119,13 +119,13 @@ KORE_ATTN_API int kore_attn_prefill_dev(kore_attn_t h, int layer, int pos0, int 
                           const float *v, float *out, void *stream);
 
 /* kore_attn_decode_dev with its split partials in a fixed device array of
- * the library (327,680 floats = 1.25 MiB per GPU, held until the process
+ * the library (655,360 floats = 2.5 MiB per GPU, held until the process
  * ends) instead of the handle's scratch: after kore_attn_create, the call
  * allocates nothing, synchronises nothing and calls no allocating routine.
  * No counterpart in kore; it is for callers that cannot allocate (HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  A decode
  * needs n_head x splits x (head_dim + 2) floats, on the MFMA kernels at most
- * 8 x CUs x 130 (266,240 on a 256-CU MI355X), on the generic kernels
+ * 16 x CUs x 130 (532,480 on a 256-CU MI355X), on the generic kernels
  * n_head x head_dim more; a larger need fails with KORE_ATTN_E_UNSUPPORTED.  Every call on one GPU shares the array (each call
  * writes every partial it reads, so nothing carries over): calls that overlap
  * on one GPU (other streams, other handles) race. */

@@ -226,6 +226,7 @@ int decode_enqueue(kore_attn *h, int layer, int pos, const float *q, const float
     a.n_head_kv = h->n_head_kv;
     a.n_rep = h->n_head / h->n_head_kv;
     a.scale = 1.0f / std::sqrt((float)h->head_dim);   // kore.cpp:1411
+    a.wg_per_cu = a.n_split * a.n_head_kv > h->num_cu ? 2 : 1;
     if (a.n_split > h->max_split)
         return fail(h, KORE_ATTN_E_UNSUPPORTED, "decode needs %d splits, scratch holds %d", a.n_split,
                     h->max_split);

@@ -20,7 +20,7 @@ namespace kore_attn_gpu {
 // kDecodeBlock rows plus the new row itself; with one split it writes `out`,
 // otherwise unnormalised split partials that the combine kernel merges.
 constexpr int kDecodeBlock = 16;
-constexpr int kMaxDecodeSplits = 128;   // splits per kv-head the combine merges in one round
+constexpr int kMaxDecodeSplits = 256;   // splits per kv-head the combine merges in one round
 
 struct DecodeArgs {
     const float *q;       // [n_head][hd]        post-bias, pre-RoPE
@@ -39,6 +39,7 @@ struct DecodeArgs {
     int n_head_kv;
     int n_rep;            // q heads per kv head
     float scale;          // 1/sqrt(hd) as kore computes it (kore.cpp:1411)
+    int wg_per_cu;        // split workgroups per CU: 1, or 2 when the grid has more than the CUs
 };
 
 // (cos, sin) of dims 0 .. hd/2 - 1 at the decode position, interleaved,
@@ -110,6 +111,7 @@ struct PrefillArgs {
 // (after a prep launch has roped q and appended the new row), or all keys
 // 0..pos of one prefill row.
 constexpr int kMaxGenericHeadDim = 2 * kMaxRopeHalf;
+constexpr int kMaxGenericSplits = 128;   // decode splits per kv-head of the generic kernels
 struct GenericArgs {
     const float *q;       // decode: roped q [n_head][hd]; prefill: pre-RoPE q [n_tok][n_head][hd]
     const float2 *cs;     // prefill: RoPE table (row p = position p); decode: null
@@ -150,14 +152,14 @@ struct SynthArgs {
 };
 
 // The device's fixed scratch (a file-scope __device__ array of
-// kStaticScratchFloats floats, 1.25 MiB): the split partials of the
-// allocation-free decode entry point.  A decode has at most one split
-// workgroup per CU and at most 8 q-heads per kv-head, so it needs at most
-// 8 x num_cu x (hd + 2) floats: 266,240 on a 256-CU MI355X at head_dim 128.
+// kStaticScratchFloats floats, 2.5 MiB): the split partials of the
+// allocation-free decode entry point.  A decode has at most two split
+// workgroups per CU and at most 8 q-heads per kv-head, so it needs at most
+// 16 x num_cu x (hd + 2) floats: 532,480 on a 256-CU MI355X at head_dim 128.
 // static_scratch() returns the array's address on `device` (made current by
 // the caller), resolved with hipGetSymbolAddress on the first call for that
 // device and remembered.
-constexpr size_t kStaticScratchFloats = (size_t)5 << 16;
+constexpr size_t kStaticScratchFloats = (size_t)5 << 17;
 hipError_t static_scratch(int device, float **ptr);
 
 // Rows per split the decode uses for n_rows cache rows (the host sizes the

@@ -232,9 +232,10 @@ __device__ __forceinline__ double sum4rows_d(double x) {
 // 1, output v).  Slots [0, n_rows) never include it except in a wrapped ring,
 // where its stale slot is masked.  The four wave states (each started from
 // the wave's single row) are merged in LDS into one partial per q-head, or
-// into `out` when the kv-head has a single split.
-template <int HD, int NR>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
+// into `out` when the kv-head has a single split.  OCC: workgroups per CU the
+// register allocation leaves room for (1: 280 registers, 2: at most 256).
+template <int HD, int NR, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
                                                                 float *vc_in, const float *__restrict__ k_in,
                                                                 const float *__restrict__ v_in, int n_rows,
                                                                 int rows_per_split, int new_slot, int slots,
@@ -1734,28 +1735,36 @@ hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
     // kernel-argument fetch.
     // Splits of at most kWaves blocks plus kWaves extra rows give every wave
     // one block at most: that kernel has no prefetch registers or branches.
-    // The grid never has more workgroups than CUs.  The single-block kernel
-    // fits two workgroups per CU by registers, so it asks for enough (unused)
-    // dynamic LDS that a CU holds one: two on a CU would leave another idle.
+    // With at most as many workgroups as CUs, the single-block kernel asks
+    // for enough (unused) dynamic LDS that a CU holds one (it fits two by
+    // registers, and two on a CU would leave another idle); with twice as
+    // many (wg_per_cu 2) its variant compiled for two per CU runs, every CU
+    // holding two.
     const dim3 grid(a.n_split, a.n_head_kv);
     if (a.rows_per_split > kWaves * kDecodeBlock + kWaves) {
         hipLaunchKernelGGL((decode_multi_kernel<HD, NR>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
+    } else if (a.wg_per_cu == 2) {
+        // twice the CUs' workgroups, two per CU (the registers allow no third)
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, 2>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k,
+                           a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     } else {
         static const unsigned dyn = [] {
             hipFuncAttributes fa{};
-            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR>)) != hipSuccess)
+            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR, 1>)) !=
+                hipSuccess)
                 return 0u;
             const size_t half_cu = kLdsPerCu / 2 + 256;
             return fa.sharedSizeBytes < half_cu ? (unsigned)(half_cu - fa.sharedSizeBytes) : 0u;
         }();
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc, a.k, a.v,
-                           a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR, 1>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc, a.k,
+                           a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     }
-    static_assert(kMaxDecodeSplits <= 8 * 16, "the combine takes at most 16 splits per lane");
+    static_assert(kMaxDecodeSplits <= 8 * 32, "the combine takes at most 32 splits per lane");
     const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 32);
     const float *po = a.part_o, *pml = a.part_ml;
-    if (a.n_split > 64) hipLaunchKernelGGL((decode_combine_kernel<HD, 16>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
+    if (a.n_split > 128) hipLaunchKernelGGL((decode_combine_kernel<HD, 32>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
+    else if (a.n_split > 64) hipLaunchKernelGGL((decode_combine_kernel<HD, 16>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
     else if (a.n_split > 32) hipLaunchKernelGGL((decode_combine_kernel<HD, 8>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
     else if (a.n_split > 16) hipLaunchKernelGGL((decode_combine_kernel<HD, 4>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
     else if (a.n_split > 1) hipLaunchKernelGGL((decode_combine_kernel<HD, 2>), cgrid, dim3(64), 0, s, po, pml, a.out, a.n_split);
@@ -1818,20 +1827,38 @@ bool prefill_supported(int head_dim, int n_rep) {
 }
 
 int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu) {
-    // S = num_cu / n_head_kv splits per kv-head (one workgroup per CU, since
-    // the split kernel's register use leaves room for only one per CU; at
+    // S = num_cu / n_head_kv splits per kv-head (one workgroup per CU; at
     // most kMaxDecodeSplits, and at least kDecodeBlock rows per split) of
     // ceil(n_rows / S) rows.  A split is processed as whole blocks of
     // kDecodeBlock rows (MFMA) plus up to kWaves extra rows (VALU, one per
     // wave), so a row count a little over a multiple of the blocks does not
     // cost a wave a second block; a larger remainder is rounded up to a
-    // whole block.
+    // whole block while that stays within one block per wave (fewer splits,
+    // the same blocks per wave).  Past that a wave takes a second block
+    // whether the last one is whole or not, and rounding up would leave CUs
+    // idle (4420 rows of a 4-kv-head model: 56 splits of 80 instead of 64
+    // of 70).  When one workgroup per CU would need a second block per wave
+    // (the multi-block kernel), twice the splits are taken if that brings
+    // every split back to one block per wave: the single-block kernel then
+    // runs two workgroups per CU (7B at 8191 rows: 11.7 against 13.7 us per
+    // layer; 3B at 16383: 12.3 against 13.6).  At the same row count one
+    // workgroup per CU is faster (the second workgroup's requests queue
+    // behind the first's; 7B at 4095 rows: 10.7 against 8.2 us), and the
+    // multi-block kernel at two per CU, without its second register set and
+    // with spills, lost (3B at 32767: 24.1 against 19.4 us).
     (void)head_dim;
-    const int S = std::max(1, std::min({num_cu / std::max(n_head_kv, 1), kMaxDecodeSplits,
-                                        n_rows / kDecodeBlock}));
-    int rps = std::max(1, (n_rows + S - 1) / S);
-    if (rps % kDecodeBlock > kWaves) rps = (rps + kDecodeBlock - 1) / kDecodeBlock * kDecodeBlock;
-    return rps;
+    auto rows_for = [&](int cus) {
+        const int S = std::max(1, std::min({cus / std::max(n_head_kv, 1), kMaxDecodeSplits, n_rows / kDecodeBlock}));
+        int rps = std::max(1, (n_rows + S - 1) / S);
+        const int up = (rps + kDecodeBlock - 1) / kDecodeBlock * kDecodeBlock;
+        if (rps % kDecodeBlock > kWaves && up <= kWaves * kDecodeBlock) rps = up;
+        return rps;
+    };
+    const int single = kWaves * kDecodeBlock + kWaves;
+    const int r1 = rows_for(num_cu);
+    if (r1 <= single) return r1;
+    const int r2 = rows_for(2 * num_cu);
+    return r2 <= single ? r2 : r1;
 }
 
 hipError_t launch_decode(const DecodeArgs &a, const RopeRow &rr, int head_dim, hipStream_t s) {
@@ -1943,7 +1970,7 @@ size_t generic_lds_bytes(int head_dim, int tile, int chunk) {
 int generic_max_split(int head_dim, int n_rep, int n_head_kv, int num_cu) {
     int T, ch, nc;
     generic_shape(head_dim, n_rep, &T, &ch, &nc);
-    return std::max(1, std::min(kMaxDecodeSplits, num_cu / std::max(1, n_head_kv * nc)));
+    return std::max(1, std::min(kMaxGenericSplits, num_cu / std::max(1, n_head_kv * nc)));
 }
 
 int generic_rows_per_split(int head_dim, int n_rep, int n_rows, int n_head_kv, int num_cu) {

@@ -1,6 +1,6 @@
-"""GPU tests of the decode over the split counts it uses (1 .. 64 splits per
-kv-head; the single-block and the multi-block split kernel; head_dim 64 and
-128; 1 .. 8 q-heads per kv-head): kore_attn_decode_dev against the oracle
+"""GPU tests of the decode over the split counts it uses (1 .. 128 splits per
+kv-head; the single-block split kernel at one and two workgroups per CU and
+the multi-block split kernel; head_dim 64 and 128; 1 .. 8 q-heads per kv-head): kore_attn_decode_dev against the oracle
 within 1e-4 of max|ref| and against kore_attn_decode_noalloc_dev (the same
 kernels over the library's fixed array) bit for bit, the cache rows bit for
 bit; many calls on one handle over a sliding ring; a captured 28-layer step
@@ -48,7 +48,12 @@ def _fill(attn, rows, kvd, rng):
     (28, 4, 128, 4096, 3),     # Qwen2.5-7B: 64 splits of 64 rows
     (28, 4, 128, 40, 2),       # 2 splits
     (28, 4, 128, 560, 2),      # 35 splits
-    (28, 4, 128, 8000, 2),     # 64 splits of 125 rows: the multi-block kernel
+    (28, 4, 128, 8000, 2),     # 125 splits of 64 rows: two single-block workgroups per CU, then a
+                               # last split of one row
+    (28, 4, 128, 4421, 2),     # 127 splits of 35 rows (two blocks and three extra rows), two per CU
+    (28, 4, 128, 9000, 2),     # 64 splits of 141 rows: the multi-block kernel
+    (28, 4, 128, 12351, 2),    # multi-block, 193 rows per split: one extra row
+    (16, 2, 128, 10623, 2),    # 8 q-heads per kv-head, multi-block, 83 rows per split: three extra rows
     (14, 2, 64, 511, 2),       # Qwen2.5-0.5B: 31 splits, head_dim 64
     (16, 2, 128, 1000, 2),     # 8 q-heads per kv-head
     (8, 8, 128, 2000, 2),      # 1 q-head per kv-head, 32 splits
