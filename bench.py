@@ -324,6 +324,31 @@ def decode_timeline(steps: int, raw_path: str = "", samples: int = 16, config: s
             "xcd_last_end_median": [round(float(v), 2) for v in np.median(np.asarray(xe), 0)]}
 
 
+SWEEP_7B = (256, 1024, 2048, 3072, 4096, 4352, 4420, 5000, 6144, 8192, 8704, 9000, 12288, 16384, 24576, 32767)
+SWEEP_3B = (2048, 4096, 8192, 16384, 17408, 20000, 32767)
+
+
+def decode_sweep():
+    """The decode across the context: Qwen2.5-7B shape (28 layers, cache of 32768 slots) and 3B
+    shape (36 layers, 32768 slots), each filled once through the append path; per position the
+    step's us per layer over 40 repeated steps at that position (HIP events, time-based warm-up)
+    and its fraction of 8 TB/s, with the kernel the split rule picks (one or two workgroups per
+    CU, single- or multi-block)."""
+    from kore_amd import KoreAttn
+    out = {}
+    for name, (nl, nh, nkv, hd), poss in (("7b", (28, 28, 4, 128), SWEEP_7B), ("3b", (36, 16, 2, 128), SWEEP_3B)):
+        rows = []
+        with KoreAttn(nl, 32768, nh, nkv, hd, ROPE_BASE) as a:
+            _fill_cache(a, nl, 32767, nkv * hd, 7, a.stream)
+            for pos in poss:
+                r, _ = _decode_leg(a, nl, pos, 0, 40, 2, nh, nkv, hd, 7, lambda s, p=pos: p + 1)
+                rows.append({"position": pos, "us_per_layer_gpu": r["us_per_layer_gpu"],
+                             "frac": r["roofline"]["frac"]})
+                print(f"[bench] sweep {name} {pos}: {r['us_per_layer_gpu']} us", file=sys.stderr, flush=True)
+        out[name] = rows
+    return out
+
+
 def gpu_prefill(steps: int, warmup: int):
     from kore_amd import KoreAttn, hip, synth_dev
     B = _bench_lib()
@@ -1436,6 +1461,8 @@ def main(argv=None):
                     help="with --decode-timeline: the 7B decode at 4096.. (default) or the 3B decode at 32767")
     ap.add_argument("--timeline-raw", default="", help="with --decode-timeline: also save every stamp (us) "
                                                             "to this .npz file")
+    ap.add_argument("--decode-sweep", action="store_true",
+                    help="only time the 7B and 3B decode at positions across the context (32768 slots)")
     ap.add_argument("--read-calibration", action="store_true",
                     help="only time a plain streaming read kernel per launch size (the yardstick of the "
                          "HBM-bound kernels) and an empty launch")
@@ -1493,6 +1520,9 @@ def main(argv=None):
         print(json.dumps({"prefill": {"us_per_layer_gpu": round(per * 1e6, 2), "flop_per_layer": F,
                                       "tflops": round(F / per / 1e12, 3),
                                       "frac": round(F / per / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}}), flush=True)
+        return 0
+    if args.decode_sweep:
+        print(json.dumps({"decode_sweep": decode_sweep()}), flush=True)
         return 0
     if args.decode_timeline:
         print(json.dumps({"decode_timeline": decode_timeline(args.steps, args.timeline_raw,
