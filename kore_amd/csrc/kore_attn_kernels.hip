@@ -1843,9 +1843,11 @@ int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu) {
     // runs two workgroups per CU (7B at 8191 rows: 11.7 against 13.7 us per
     // layer; 3B at 16383: 12.3 against 13.6).  At the same row count one
     // workgroup per CU is faster (the second workgroup's requests queue
-    // behind the first's; 7B at 4095 rows: 10.7 against 8.2 us), and the
-    // multi-block kernel at two per CU, without its second register set and
-    // with spills, lost (3B at 32767: 24.1 against 19.4 us).
+    // behind the first's; 7B at 4095 rows: 10.7 against 8.2 us).  The
+    // multi-block kernel at two per CU (one register set, q read from LDS per
+    // block, no spills) won only where every wave got the same two or three
+    // blocks (3B at 32767: 19.1 against 19.6 us) and lost elsewhere (3B at
+    // 24575: 17.4 against 16.1), so longer splits stay at one per CU.
     (void)head_dim;
     auto rows_for = [&](int cus) {
         const int S = std::max(1, std::min({cus / std::max(n_head_kv, 1), kMaxDecodeSplits, n_rows / kDecodeBlock}));
