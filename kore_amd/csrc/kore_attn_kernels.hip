@@ -233,7 +233,8 @@ __device__ __forceinline__ double sum4rows_d(double x) {
 // where its stale slot is masked.  The four wave states (each started from
 // the wave's single row) are merged in LDS into one partial per q-head, or
 // into `out` when the kv-head has a single split.  OCC: workgroups per CU the
-// register allocation leaves room for (1: 280 registers, 2: at most 256).
+// register allocation leaves room for (1: up to 512 registers a wave, 280 at
+// 7 q-heads per kv-head; 2: at most 256, 240 there, no spills).
 template <int HD, int NR, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
                                                                 float *vc_in, const float *__restrict__ k_in,
