@@ -1,4 +1,4 @@
-"""GPU tests of the decode over the split counts it uses (1 .. 128 splits per
+"""GPU tests of the decode over the split counts it uses (1 .. 256 splits per
 kv-head; the single-block split kernel at one and two workgroups per CU and
 the multi-block split kernel; head_dim 64 and 128; 1 .. 8 q-heads per kv-head): kore_attn_decode_dev against the oracle
 within 1e-4 of max|ref| and against kore_attn_decode_noalloc_dev (the same
@@ -54,6 +54,7 @@ def _fill(attn, rows, kvd, rng):
     (28, 4, 128, 9000, 2),     # 64 splits of 141 rows: the multi-block kernel
     (28, 4, 128, 12351, 2),    # multi-block, 193 rows per split: one extra row
     (16, 2, 128, 10623, 2),    # 8 q-heads per kv-head, multi-block, 83 rows per split: three extra rows
+    (16, 2, 128, 12000, 2),    # 250 splits of 48 rows, two per CU: the combine's 32 splits per lane
     (14, 2, 64, 511, 2),       # Qwen2.5-0.5B: 31 splits, head_dim 64
     (16, 2, 128, 1000, 2),     # 8 q-heads per kv-head
     (8, 8, 128, 2000, 2),      # 1 q-head per kv-head, 32 splits

@@ -20,6 +20,7 @@ def _say(msg):
 @pytest.mark.parametrize("nh,nkv,hd,fill,positions", [
     (28, 4, 128, 3000, (3000, 77)),     # Qwen2.5-7B geometry: 64 splits, then 4
     (28, 4, 128, 8190, (8190, 6000)),   # 128 splits of 64 rows (two workgroups per CU), then 125 of 48
+    (16, 2, 128, 12000, (12000, 9000)), # 250 splits of 48 rows: 520,000 floats of the array, then 250 of 36
     (16, 2, 128, 4200, (4200, 1500)),   # 3B geometry: 128 splits of 33 rows, then 93 splits
     (14, 2, 64, 600, (600, 16)),        # 0.5B geometry, head_dim 64
     (32, 8, 40, 2000, (2000, 50)),      # head_dim 40: the generic kernels (roped q in the array too)
