@@ -1843,8 +1843,9 @@ int decode_rows_per_split(int head_dim, int n_rows, int n_head_kv, int num_cu) {
     // every split back to one block per wave: the single-block kernel then
     // runs two workgroups per CU (7B at 8191 rows: 11.7 against 13.7 us per
     // layer; 3B at 16383: 12.3 against 13.6).  At the same row count one
-    // workgroup per CU is faster (the second workgroup's requests queue
-    // behind the first's; 7B at 4095 rows: 10.7 against 8.2 us).  The
+    // workgroup per CU is faster (the second wave on each SIMD stages its q
+    // and scores its single row on the same SIMD; 7B at 4095 rows: 10.7
+    // against 8.2 us).  The
     // multi-block kernel at two per CU (one register set, q read from LDS per
     // block, no spills) won only where every wave got the same two or three
     // blocks (3B at 32767: 19.1 against 19.6 us) and lost elsewhere (3B at
