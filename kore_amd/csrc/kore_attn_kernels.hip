@@ -232,11 +232,13 @@ __device__ __forceinline__ double sum4rows_d(double x) {
 // 1, output v).  Slots [0, n_rows) never include it except in a wrapped ring,
 // where its stale slot is masked.  The four wave states (each started from
 // the wave's single row) are merged in LDS into one partial per q-head, or
-// into `out` when the kv-head has a single split.  OCC: workgroups per CU the
-// register allocation leaves room for (1: up to 512 registers a wave, 280 at
-// 7 q-heads per kv-head; 2: at most 256, 240 there, no spills).
-template <int HD, int NR, int OCC>
-__global__ __launch_bounds__(kThreads, OCC) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
+// into `out` when the kv-head has a single split.  Compiled for two
+// workgroups per CU (at most 256 registers a wave: 240 at 7 q-heads per
+// kv-head, no spills), which also runs faster at one workgroup per CU than
+// the build with the whole register file (280 there): 7B at 4096 rows 8.14-
+// 8.20 against 8.32-8.34 us per layer.
+template <int HD, int NR>
+__global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(const float *__restrict__ q_in, float *kc_in,
                                                                 float *vc_in, const float *__restrict__ k_in,
                                                                 const float *__restrict__ v_in, int n_rows,
                                                                 int rows_per_split, int new_slot, int slots,
@@ -1739,27 +1741,24 @@ hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
     // With at most as many workgroups as CUs, the single-block kernel asks
     // for enough (unused) dynamic LDS that a CU holds one (it fits two by
     // registers, and two on a CU would leave another idle); with twice as
-    // many (wg_per_cu 2) its variant compiled for two per CU runs, every CU
-    // holding two.
+    // many (wg_per_cu 2) every CU holds two.
     const dim3 grid(a.n_split, a.n_head_kv);
     if (a.rows_per_split > kWaves * kDecodeBlock + kWaves) {
         hipLaunchKernelGGL((decode_multi_kernel<HD, NR>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
-    } else if (a.wg_per_cu == 2) {
-        // twice the CUs' workgroups, two per CU (the registers allow no third)
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR, 2>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k,
-                           a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     } else {
+        // one workgroup per CU: enough (unused) dynamic LDS that a CU holds
+        // one; two per CU (twice the CUs' workgroups): none, the registers
+        // allow no third
         static const unsigned dyn = [] {
             hipFuncAttributes fa{};
-            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR, 1>)) !=
-                hipSuccess)
+            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR>)) != hipSuccess)
                 return 0u;
             const size_t half_cu = kLdsPerCu / 2 + 256;
             return fa.sharedSizeBytes < half_cu ? (unsigned)(half_cu - fa.sharedSizeBytes) : 0u;
         }();
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR, 1>), grid, dim3(kThreads), dyn, s, a.q, a.kc, a.vc, a.k,
-                           a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR>), grid, dim3(kThreads), a.wg_per_cu == 2 ? 0u : dyn, s, a.q,
+                           a.kc, a.vc, a.k, a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     }
     static_assert(kMaxDecodeSplits <= 8 * 32, "the combine takes at most 32 splits per lane");
     const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 32);
