@@ -1729,6 +1729,14 @@ static __device__ __align__(256) float scratch[kStaticScratchFloats];
 
 // --------------------------------------------------------------- dispatch
 
+// Dynamic LDS that brings a kernel's static LDS up to `total` bytes (0 if it
+// is there already or the attributes cannot be read).
+unsigned dyn_lds_above(const void *kernel, size_t total) {
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return 0u;
+    return fa.sharedSizeBytes < total ? (unsigned)(total - fa.sharedSizeBytes) : 0u;
+}
+
 template <int HD, int NR>
 hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t s) {
     // The leading scalar arguments (everything before the first aggregate:
@@ -1747,18 +1755,18 @@ hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
         hipLaunchKernelGGL((decode_multi_kernel<HD, NR>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     } else {
-        // one workgroup per CU: enough (unused) dynamic LDS that a CU holds
-        // one; two per CU (twice the CUs' workgroups): none, the registers
-        // allow no third
-        static const unsigned dyn = [] {
-            hipFuncAttributes fa{};
-            if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(&decode_split_kernel<HD, NR>)) != hipSuccess)
-                return 0u;
-            const size_t half_cu = kLdsPerCu / 2 + 256;
-            return fa.sharedSizeBytes < half_cu ? (unsigned)(half_cu - fa.sharedSizeBytes) : 0u;
-        }();
-        hipLaunchKernelGGL((decode_split_kernel<HD, NR>), grid, dim3(kThreads), a.wg_per_cu == 2 ? 0u : dyn, s, a.q,
-                           a.kc, a.vc, a.k, a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
+        // enough (unused) dynamic LDS that a CU holds exactly the workgroups
+        // the grid plans for it: more than half the CU's LDS for one, more
+        // than a third for two (the instances with few registers, head_dim 64
+        // or 3 q-heads per kv-head, would otherwise fit three or more, and a
+        // CU holding three leaves another with one)
+        static const unsigned pad[2] = {[] {
+            return dyn_lds_above(reinterpret_cast<const void *>(&decode_split_kernel<HD, NR>), kLdsPerCu / 2 + 256);
+        }(), [] {
+            return dyn_lds_above(reinterpret_cast<const void *>(&decode_split_kernel<HD, NR>), kLdsPerCu / 3 + 256);
+        }()};
+        hipLaunchKernelGGL((decode_split_kernel<HD, NR>), grid, dim3(kThreads), pad[a.wg_per_cu == 2 ? 1 : 0], s,
+                           a.q, a.kc, a.vc, a.k, a.v, a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     }
     static_assert(kMaxDecodeSplits <= 8 * 32, "the combine takes at most 32 splits per lane");
     const dim3 cgrid(a.n_head_kv * a.n_rep, HD / 32);
