@@ -1752,7 +1752,10 @@ hipError_t launch_decode_nr(const DecodeArgs &a, const RopeRow &rr, hipStream_t 
     // many (wg_per_cu 2) every CU holds two.
     const dim3 grid(a.n_split, a.n_head_kv);
     if (a.rows_per_split > kWaves * kDecodeBlock + kWaves) {
-        hipLaunchKernelGGL((decode_multi_kernel<HD, NR>), grid, dim3(kThreads), 0, s, a.q, a.kc, a.vc, a.k, a.v,
+        // one per CU; the head_dim-64 instances would fit two by registers
+        static const unsigned pad_m =
+            dyn_lds_above(reinterpret_cast<const void *>(&decode_multi_kernel<HD, NR>), kLdsPerCu / 2 + 256);
+        hipLaunchKernelGGL((decode_multi_kernel<HD, NR>), grid, dim3(kThreads), pad_m, s, a.q, a.kc, a.vc, a.k, a.v,
                            a.n_rows, a.rows_per_split, a.new_slot, a.slots, a, rr);
     } else {
         // enough (unused) dynamic LDS that a CU holds exactly the workgroups

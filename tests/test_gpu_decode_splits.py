@@ -56,6 +56,7 @@ def _fill(attn, rows, kvd, rng):
     (16, 2, 128, 10623, 2),    # 8 q-heads per kv-head, multi-block, 83 rows per split: three extra rows
     (16, 2, 128, 12000, 2),    # 250 splits of 48 rows, two per CU: the combine's 32 splits per lane
     (14, 2, 64, 12000, 2),     # head_dim 64, two per CU (its registers would allow more: LDS-padded)
+    (14, 2, 64, 20000, 2),     # head_dim 64, multi-block, one per CU (LDS-padded)
     (14, 2, 64, 511, 2),       # Qwen2.5-0.5B: 31 splits, head_dim 64
     (16, 2, 128, 1000, 2),     # 8 q-heads per kv-head
     (8, 8, 128, 2000, 2),      # 1 q-head per kv-head, 32 splits
